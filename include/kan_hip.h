@@ -1,0 +1,146 @@
+/*
+ * kan_hip.h -- C-ABI of libkan_hip.so, the gfx950 (MI355X) kernels behind the
+ * KANLinear hot path of torch-spline-kan.
+ *
+ * Every entry point takes raw device pointers, int64 sizes, a dtype code and
+ * a hipStream_t (passed as void*; NULL = legacy default stream), launches its
+ * kernels asynchronously on that stream and returns a status code.  No entry
+ * point allocates device memory: outputs and workspaces are provided by the
+ * caller (the workspace-size queries say how large).  On a non-zero status,
+ * kan_hip_last_error() returns a message for the calling thread.  Invalid
+ * sizes are rejected before any launch, so an error never leaves a kernel
+ * behind.
+ *
+ * Layouts are row-major and contiguous:
+ *   x [n, I]; grid [I, G+2k+1]; base_weight [O, I]; spline_weight [O, I, R];
+ *   spline_scaler [O, I]; basis [n, I, R]; output [n, O]; with R = G + k.
+ * The "augmented basis" is [n, W] with W = kan_hip_aug_width(I, G, k, base):
+ *   row n = [ basis(n, 0, 0..R-1), ..., basis(n, I-1, ..), silu(x(n, 0..I-1)), pad ]
+ * (the silu block only when a base branch is present).  It is produced by the
+ * forward and consumed by the backward.
+ *
+ * Reference interfaces each entry point replaces are cited per function
+ * (paths relative to the torch-spline-kan source tree).
+ */
+#ifndef KAN_HIP_H_
+#define KAN_HIP_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* dtype codes */
+#define KAN_DTYPE_F32 0
+#define KAN_DTYPE_F64 1
+
+/* status codes */
+#define KAN_OK 0
+#define KAN_ERR_INVALID 1  /* bad argument (shape, dtype code, null pointer) */
+#define KAN_ERR_LIMIT 2    /* configuration outside the native kernel limits */
+#define KAN_ERR_HIP 3      /* HIP runtime error at launch */
+#define KAN_ERR_WORKSPACE 4 /* workspace too small */
+
+/* Message for the last non-zero status returned on this thread ("" if none). */
+const char* kan_hip_last_error(void);
+
+/* Limits query.  Replaces the module attributes CUDA_MAX_DEG0_BASIS and
+ * CUDA_MAX_IN_FEATURES (csrc/kan_ext.cpp:164-165, csrc/kan_ops.h:15-17). */
+int kan_hip_limits(int64_t* max_deg0_basis, int64_t* max_in_features);
+
+/* Basis implementation switch: 0 = dense Cox-de Boor recurrence, 1 = local
+ * (default).  Replaces _C.set_basis_impl / _C.get_basis_impl
+ * (csrc/kan_cuda.cu:274-279, csrc/kan_ext.cpp:373-375).  Any other value
+ * returns KAN_ERR_INVALID. */
+int kan_hip_set_basis_impl(int64_t impl);
+int64_t kan_hip_get_basis_impl(void);
+
+/* basis[n, I, R] = B-spline basis of x.  Replaces _C.basis / kan_basis_cuda
+ * (csrc/kan_ext.cpp:376-377, csrc/kan_cuda.cu:666-680). */
+int kan_hip_basis(int dtype, const void* x, const void* grid, void* basis, int64_t n,
+                  int64_t in_features, int64_t grid_size, int64_t spline_order, void* stream);
+
+/* grad_x[n, i] = sum_r grad_basis[n, i, r] * dB_r/dx(x[n, i]).  Replaces
+ * _C.basis_grad / kan_basis_grad_cuda (csrc/kan_ext.cpp:378-380,
+ * csrc/kan_cuda.cu:682-699). */
+int kan_hip_basis_grad(int dtype, const void* x, const void* grid, const void* grad_basis,
+                       void* grad_x, int64_t n, int64_t in_features, int64_t grid_size,
+                       int64_t spline_order, void* stream);
+
+/* Row width (elements) of the augmented basis and augmented weight buffers.
+ * Returns -1 for invalid sizes.  No reference counterpart: the reference keeps
+ * basis [n, I, R] and runs the SiLU branch as a second GEMM
+ * (csrc/kan_cuda.cu:521-531). */
+int64_t kan_hip_aug_width(int64_t in_features, int64_t grid_size, int64_t spline_order,
+                          int has_base);
+
+/* Forward: output = silu(x) base_weight^T + basis(x) (spline_weight*scaler)^T.
+ * base_weight may be NULL (no fused base branch), spline_scaler may be NULL
+ * (no scaler).  Writes output [n, O], basis_aug [n, W] (kept for backward) and
+ * uses weight_aug [O, W] as workspace.  Replaces kan_forward_cuda
+ * (csrc/kan_cuda.cu:469-532) behind _C.kan_forward / KANFunction::forward
+ * (csrc/kan_ext.cpp:10-33, csrc/kan_autograd.cpp:18-47). */
+int kan_hip_forward(int dtype, const void* x, const void* grid, const void* base_weight,
+                    const void* spline_weight, const void* spline_scaler, void* output,
+                    void* basis_aug, void* weight_aug, int64_t n, int64_t in_features,
+                    int64_t out_features, int64_t grid_size, int64_t spline_order,
+                    void* stream);
+
+/* Builds basis_aug [n, W] from a caller-held basis [n, I, R] and x (silu block
+ * only when has_base).  Used by the raw backward op, whose caller passes the
+ * basis returned by the forward (csrc/kan_ext.cpp:35-56). */
+int kan_hip_pack_basis(int dtype, const void* basis, const void* x, void* basis_aug, int64_t n,
+                       int64_t in_features, int64_t grid_size, int64_t spline_order,
+                       int has_base, void* stream);
+
+/* Workspace bytes kan_hip_backward needs for the given requests. */
+int kan_hip_backward_workspace(int dtype, int64_t n, int64_t in_features, int64_t out_features,
+                               int64_t grid_size, int64_t spline_order, int has_base,
+                               int need_x, int need_params, size_t* bytes);
+
+/* First-order backward.  Each output pointer may be NULL when not requested:
+ *   grad_x [n, I], grad_base_weight [O, I], grad_spline_weight [O, I, R],
+ *   grad_spline_scaler [O, I] (requires grad_spline_weight's GEMM, computed
+ *   together).  Replaces kan_backward_cuda_ex (csrc/kan_cuda.cu:537-630)
+ * behind _C.kan_backward and KANFunction::backward
+ * (csrc/kan_ext.cpp:35-56, csrc/kan_autograd.cpp:48-111). */
+int kan_hip_backward(int dtype, const void* grad_output, const void* x, const void* grid,
+                     const void* base_weight, const void* spline_weight,
+                     const void* spline_scaler, const void* basis_aug, void* grad_x,
+                     void* grad_base_weight, void* grad_spline_weight, void* grad_spline_scaler,
+                     void* workspace, size_t workspace_bytes, int64_t n, int64_t in_features,
+                     int64_t out_features, int64_t grid_size, int64_t spline_order,
+                     void* stream);
+
+/* Workspace bytes for the edge statistic (backward != 0: backward pass). */
+int kan_hip_edge_workspace(int dtype, int64_t n, int64_t in_features, int64_t out_features,
+                           int64_t num_basis, int backward, size_t* bytes);
+
+/* a[o, i] = (1/n) sum_m | s[m,i] bw[o,i] + sum_r basis[m,i,r] weight[o,i,r] |
+ * without materialising the [n, O, I] edge tensor.  s and base_weight may both
+ * be NULL (no base branch).  Replaces _C.edge_abs_mean / edge_abs_mean_cuda
+ * (csrc/kan_ext.cpp:381-383, csrc/kan_reg_cuda.cu:263-280). */
+int kan_hip_edge_abs_mean(int dtype, const void* s, const void* basis, const void* base_weight,
+                          const void* weight, void* a, void* workspace, size_t workspace_bytes,
+                          int64_t n, int64_t in_features, int64_t out_features,
+                          int64_t num_basis, void* stream);
+
+/* Backward of kan_hip_edge_abs_mean given grad_a [O, I]; each output may be
+ * NULL when not needed: grad_s [n, I], grad_basis [n, I, R],
+ * grad_base_weight [O, I], grad_weight [O, I, R].  Replaces
+ * _C.edge_abs_mean_backward / edge_abs_mean_backward_cuda
+ * (csrc/kan_ext.cpp:384-387, csrc/kan_reg_cuda.cu:284-312). */
+int kan_hip_edge_abs_mean_backward(int dtype, const void* grad_a, const void* s,
+                                   const void* basis, const void* base_weight,
+                                   const void* weight, void* grad_s, void* grad_basis,
+                                   void* grad_base_weight, void* grad_weight, void* workspace,
+                                   size_t workspace_bytes, int64_t n, int64_t in_features,
+                                   int64_t out_features, int64_t num_basis, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* KAN_HIP_H_ */

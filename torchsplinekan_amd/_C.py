@@ -1,0 +1,375 @@
+"""Drop-in replacement for the ``spline_kan._C`` extension module.
+
+Same surface as the reference's pybind module (csrc/kan_ext.cpp:161-222):
+attributes CUDA_MAX_DEG0_BASIS, CUDA_MAX_IN_FEATURES, HAS_FUSED_KERNELS and
+functions kan_forward, kan_backward, kan_apply, set_basis_impl,
+get_basis_impl, basis, basis_grad, edge_abs_mean, edge_abs_mean_backward,
+with the same argument names, return conventions (empty tensor = absent
+optional, None for gradients not computed) and error texts
+(RuntimeError from the validation, as TORCH_CHECK raises).
+
+Device tensors (ROCm tensors report ``is_cuda``) run on the gfx950 kernels
+of libkan_hip.so, called through its C-ABI on the current torch stream of
+the tensors' device.  CPU tensors dispatch to the ATen formulation, as the
+reference dispatches to csrc/kan_cpu.cpp.  Importing this module raises
+ImportError when libkan_hip.so has not been built.
+"""
+
+from typing import Optional, Tuple
+
+import torch
+
+from . import _lib
+from . import composite as _cmp
+from ._lib import LIB, check, dtype_code, ptr, stream_of
+
+CUDA_MAX_DEG0_BASIS, CUDA_MAX_IN_FEATURES = _lib.limits()
+HAS_FUSED_KERNELS = True
+
+_F = (torch.float32, torch.float64)
+
+
+def _req(cond: bool, *msg) -> None:
+    if not cond:
+        raise RuntimeError("".join(str(m) for m in msg))
+
+
+def _check_inputs(x, grid, base_weight, spline_weight, spline_scaler, spline_order, has_scaler):
+    """Validation of kan_check_inputs (csrc/kan_ops.h:27-78) with the same
+    messages.  The reference's 32-bit index guard (B*I*(G+2k) <= INT_MAX) is
+    not applied: every native kernel here uses 64-bit offsets."""
+    _req(x.dim() == 2, "x must be 2-D [B, I], got ", x.dim(), "-D")
+    _req(grid.dim() == 2, "grid must be 2-D [I, G+2k+1]")
+    _req(spline_weight.dim() == 3, "spline_weight must be 3-D [O, I, R]")
+    _req(1 <= spline_order <= 3, "spline_order must be 1, 2 or 3; got ", spline_order)
+    I, O, nk = x.shape[1], spline_weight.shape[0], grid.shape[1]
+    G = nk - 2 * spline_order - 1
+    _req(G >= 1, "grid has ", nk, " knots, too few for spline_order ", spline_order)
+    _req(grid.shape[0] == I, "grid.size(0)=", grid.shape[0], " must equal in_features=", I)
+    _req(spline_weight.shape[1] == I, "spline_weight.size(1) must equal in_features=", I)
+    _req(spline_weight.shape[2] == G + spline_order, "spline_weight.size(2)=",
+         spline_weight.shape[2], " but grid implies R=G+k=", G + spline_order)
+    _req(x.dtype in _F, "only FP32 and FP64 inputs are supported, got ", x.dtype)
+    _req(grid.dtype == x.dtype and spline_weight.dtype == x.dtype,
+         "x, grid and spline_weight must share a dtype")
+    _req(grid.device == x.device and spline_weight.device == x.device,
+         "x, grid and spline_weight must be on the same device")
+    if _cmp.has_base(base_weight):
+        _req(base_weight.dim() == 2 and tuple(base_weight.shape) == (O, I),
+             "base_weight must have shape [O, I] = [", O, ", ", I, "]")
+        _req(base_weight.dtype == x.dtype and base_weight.device == x.device,
+             "base_weight must match x in dtype and device")
+    if has_scaler:
+        _req(spline_scaler is not None and spline_scaler.dim() == 2
+             and tuple(spline_scaler.shape) == (O, I),
+             "spline_scaler must have shape [O, I] = [", O, ", ", I, "]")
+        _req(spline_scaler.dtype == x.dtype and spline_scaler.device == x.device,
+             "spline_scaler must match x in dtype and device")
+    if x.is_cuda:
+        _req(G + 2 * spline_order <= CUDA_MAX_DEG0_BASIS, "CUDA kernel supports G + 2k <= ",
+             CUDA_MAX_DEG0_BASIS, " (got G=", G, ", k=", spline_order,
+             "); use backend='reference' for larger grids")
+        _req(I <= CUDA_MAX_IN_FEATURES, "CUDA kernel supports in_features <= ",
+             CUDA_MAX_IN_FEATURES, ", got ", I)
+    return G
+
+
+def _contig(t: Optional[torch.Tensor]) -> Optional[torch.Tensor]:
+    return None if t is None else t.contiguous()
+
+
+# ---------------------------------------------------------------------------
+# device implementations
+# ---------------------------------------------------------------------------
+
+def _forward_device(x, grid, base_weight, spline_weight, spline_scaler, k, has_scaler):
+    """(y [B, O], basis_aug [B, W]) from the gfx950 forward."""
+    G = grid.shape[1] - 2 * k - 1
+    hb = _cmp.has_base(base_weight)
+    x, grid, sw = x.contiguous(), grid.contiguous(), spline_weight.contiguous()
+    bw = base_weight.contiguous() if hb else None
+    sc = spline_scaler.contiguous() if has_scaler else None
+    B, I = x.shape
+    O = sw.shape[0]
+    ld = int(LIB.kan_hip_aug_width(I, G, k, int(hb)))
+    y = torch.empty(B, O, dtype=x.dtype, device=x.device)
+    aug = torch.empty(B, ld, dtype=x.dtype, device=x.device)
+    waug = torch.empty(O, ld, dtype=x.dtype, device=x.device)
+    with torch.cuda.device(x.device):
+        check(LIB.kan_hip_forward(dtype_code(x.dtype), ptr(x), ptr(grid), ptr(bw), ptr(sw),
+                                  ptr(sc), ptr(y), ptr(aug), ptr(waug), B, I, O, G, k,
+                                  stream_of(x.device)))
+    return y, aug
+
+
+def _basis_view(aug: torch.Tensor, I: int, R: int) -> torch.Tensor:
+    """basis [B, I, R] as a view of the augmented rows (no copy)."""
+    return aug[:, :I * R].reshape(aug.shape[0], I, R)
+
+
+def _backward_device(D, x, grid, base_weight, spline_weight, spline_scaler, aug, k, has_scaler,
+                     need_x, need_base, need_spline):
+    G = grid.shape[1] - 2 * k - 1
+    hb = _cmp.has_base(base_weight)
+    need_base = need_base and hb
+    D, x, grid, sw = D.contiguous(), x.contiguous(), grid.contiguous(), spline_weight.contiguous()
+    bw = base_weight.contiguous() if hb else None
+    sc = spline_scaler.contiguous() if has_scaler else None
+    B, I = x.shape
+    O, _, R = sw.shape
+    opts = dict(dtype=x.dtype, device=x.device)
+    gx = torch.empty(B, I, **opts) if need_x else None
+    gbw = torch.empty(O, I, **opts) if need_base else None
+    gsw = torch.empty(O, I, R, **opts) if need_spline else None
+    gsc = torch.empty(O, I, **opts) if (need_spline and has_scaler) else None
+    if not (need_x or need_base or need_spline):
+        return gx, gbw, gsw, gsc
+    code = dtype_code(x.dtype)
+    nbytes = _lib.ctypes.c_size_t()
+    with torch.cuda.device(x.device):
+        check(LIB.kan_hip_backward_workspace(code, B, I, O, G, k, int(hb), int(need_x),
+                                             int(need_base or need_spline),
+                                             _lib.ctypes.byref(nbytes)))
+        ws = torch.empty(max(int(nbytes.value), 1), dtype=torch.uint8, device=x.device)
+        check(LIB.kan_hip_backward(code, ptr(D), ptr(x), ptr(grid), ptr(bw), ptr(sw), ptr(sc),
+                                   ptr(aug), ptr(gx), ptr(gbw), ptr(gsw), ptr(gsc), ptr(ws),
+                                   int(nbytes.value), B, I, O, G, k, stream_of(x.device)))
+    return gx, gbw, gsw, gsc
+
+
+def _pack_basis_device(basis, x, grid, k, hb):
+    G = grid.shape[1] - 2 * k - 1
+    B, I = x.shape
+    ld = int(LIB.kan_hip_aug_width(I, G, k, int(hb)))
+    basis = basis.contiguous().to(x.dtype)
+    xc = x.contiguous()
+    aug = torch.empty(B, ld, dtype=x.dtype, device=x.device)
+    with torch.cuda.device(x.device):
+        check(LIB.kan_hip_pack_basis(dtype_code(x.dtype), ptr(basis), ptr(xc), ptr(aug), B, I, G,
+                                     k, int(hb), stream_of(x.device)))
+    return aug
+
+
+# ---------------------------------------------------------------------------
+# raw ops (csrc/kan_ext.cpp:10-56)
+# ---------------------------------------------------------------------------
+
+def kan_forward(x, grid, base_weight, spline_weight, spline_scaler, spline_order: int,
+                has_scaler: bool) -> Tuple[torch.Tensor, torch.Tensor]:
+    """B-spline KAN forward (CPU/device dispatch) -> (output [B, O], basis [B, I, R])."""
+    _check_inputs(x, grid, base_weight, spline_weight, spline_scaler, spline_order, has_scaler)
+    if x.is_cuda:
+        y, aug = _forward_device(x, grid, base_weight, spline_weight, spline_scaler,
+                                 spline_order, has_scaler)
+        return y, _basis_view(aug, x.shape[1], spline_weight.shape[2])
+    return _cmp.kan_forward_cpu(x.contiguous(), grid.contiguous(), base_weight,
+                                spline_weight.contiguous(), spline_scaler, spline_order,
+                                has_scaler)
+
+
+def kan_backward(grad_output, x, grid, base_weight, spline_weight, spline_scaler, basis,
+                 spline_order: int, has_scaler: bool):
+    """B-spline KAN backward (CPU/device dispatch) ->
+    (grad_x, grad_base_weight | None, grad_spline_weight, grad_spline_scaler | None)."""
+    if x.is_cuda:
+        _check_inputs(x, grid, base_weight, spline_weight, spline_scaler, spline_order, has_scaler)
+        hb = _cmp.has_base(base_weight)
+        B, I = x.shape
+        R = spline_weight.shape[2]
+        _req(basis.numel() == B * I * R, "kan_backward_cuda: saved basis missing or wrong size")
+        aug = _pack_basis_device(basis.reshape(B, I, R), x, grid, spline_order, hb)
+        return _backward_device(grad_output, x, grid, base_weight, spline_weight, spline_scaler,
+                                aug, spline_order, has_scaler, True, True, True)
+    return _cmp.kan_backward_cpu(grad_output.contiguous(), x.contiguous(), grid.contiguous(),
+                                 base_weight, spline_weight.contiguous(), spline_scaler,
+                                 basis.contiguous(), spline_order, has_scaler)
+
+
+class KANFunction(torch.autograd.Function):
+    """Autograd function of kan_apply (csrc/kan_autograd.cpp:13-111).
+
+    Forward saves the augmented basis produced by the kernels.  Backward
+    computes only what autograd asks for (needs_input_grad); when the
+    backward itself is being recorded (create_graph=True) it switches to the
+    differentiable ATen formulation so that higher-order derivatives are
+    exact.
+    """
+
+    @staticmethod
+    def forward(ctx, x, grid, base_weight, spline_weight, spline_scaler, spline_order,
+                has_scaler):
+        if x.is_cuda:
+            y, saved = _forward_device(x, grid, base_weight, spline_weight, spline_scaler,
+                                       spline_order, has_scaler)
+        else:
+            y, saved = _cmp.kan_forward_cpu(x.contiguous(), grid.contiguous(), base_weight,
+                                            spline_weight.contiguous(), spline_scaler,
+                                            spline_order, has_scaler)
+        ctx.spline_order = spline_order
+        ctx.has_scaler = has_scaler
+        ctx.save_for_backward(x, grid, base_weight, spline_weight,
+                              spline_scaler if has_scaler else None, saved)
+        return y
+
+    @staticmethod
+    def backward(ctx, D):
+        x, grid, bw, sw, sc, saved = ctx.saved_tensors
+        k, has_scaler = ctx.spline_order, ctx.has_scaler
+        if torch.is_grad_enabled():
+            gx, gbw, gsw, gsc = _cmp.kan_backward_composite(D, x, grid, bw, sw, sc, k, has_scaler)
+        elif x.is_cuda:
+            nig = ctx.needs_input_grad
+            need_spline = bool(nig[3] or (has_scaler and nig[4]))
+            gx, gbw, gsw, gsc = _backward_device(D, x, grid, bw, sw, sc, saved, k, has_scaler,
+                                                 bool(nig[0]), bool(nig[2]), need_spline)
+        else:
+            gx, gbw, gsw, gsc = _cmp.kan_backward_cpu(D.contiguous(), x.contiguous(),
+                                                      grid.contiguous(), bw, sw.contiguous(), sc,
+                                                      saved, k, has_scaler)
+        return (gx, None, gbw if _cmp.has_base(bw) else None, gsw,
+                gsc if has_scaler else None, None, None)
+
+
+def kan_apply(x, grid, base_weight, spline_weight, spline_scaler, spline_order: int,
+              has_scaler: bool) -> torch.Tensor:
+    """B-spline KAN forward with autograd (KANFunction)."""
+    _check_inputs(x, grid, base_weight, spline_weight, spline_scaler, spline_order, has_scaler)
+    return KANFunction.apply(x, grid, base_weight, spline_weight, spline_scaler, spline_order,
+                             has_scaler)
+
+
+# ---------------------------------------------------------------------------
+# basis implementation switch (csrc/kan_cuda.cu:274-279)
+# ---------------------------------------------------------------------------
+
+def set_basis_impl(impl: int) -> None:
+    """Selects the native basis kernel: 0 = full Cox-de Boor recurrence, 1 = local (default)."""
+    if int(impl) != impl:
+        raise RuntimeError("basis impl must be 0 (recurrence) or 1 (local)")
+    check(LIB.kan_hip_set_basis_impl(int(impl)))
+
+
+def get_basis_impl() -> int:
+    return int(LIB.kan_hip_get_basis_impl())
+
+
+# ---------------------------------------------------------------------------
+# building blocks of the fused regularisation path
+# ---------------------------------------------------------------------------
+
+def _check_basis_args(x, grid, k):
+    """check_basis_args, csrc/kan_cuda.cu:649-664 (no 32-bit index guard)."""
+    _req(x.is_cuda and grid.is_cuda, "kan_basis: x and grid must be CUDA tensors")
+    _req(x.dim() == 2 and grid.dim() == 2 and grid.shape[0] == x.shape[1],
+         "kan_basis: x must be [B, I] and grid [I, G+2k+1]")
+    _req(1 <= k <= 3, "kan_basis: spline_order must be 1, 2 or 3")
+    _req(x.dtype == grid.dtype, "kan_basis: dtype mismatch")
+    _req(x.dtype in _F, "kan_basis: only FP32/FP64 supported")
+    G = grid.shape[1] - 2 * k - 1
+    _req(G >= 1, "kan_basis: grid too short")
+    _req(G + 2 * k <= CUDA_MAX_DEG0_BASIS, "CUDA kernel supports G + 2k <= ",
+         CUDA_MAX_DEG0_BASIS, " (got G=", G, ", k=", k, ")")
+    _req(x.shape[1] <= CUDA_MAX_IN_FEATURES, "kan_basis: too many input features")
+    return G
+
+
+def basis(x, grid, spline_order: int) -> torch.Tensor:
+    """B-spline basis H [B, I, R] (device)."""
+    G = _check_basis_args(x, grid, spline_order)
+    x, grid = x.contiguous(), grid.contiguous()
+    B, I = x.shape
+    H = torch.empty(B, I, G + spline_order, dtype=x.dtype, device=x.device)
+    if B == 0:
+        return H
+    with torch.cuda.device(x.device):
+        check(LIB.kan_hip_basis(dtype_code(x.dtype), ptr(x), ptr(grid), ptr(H), B, I, G,
+                                spline_order, stream_of(x.device)))
+    return H
+
+
+def basis_grad(x, grid, spline_order: int, grad_basis) -> torch.Tensor:
+    """gx[b, i] = sum_r grad_basis[b, i, r] dB_r/dx (device; dH/dx is never stored)."""
+    G = _check_basis_args(x, grid, spline_order)
+    B, I = x.shape
+    R = G + spline_order
+    _req(grad_basis.dim() == 3 and tuple(grad_basis.shape) == (B, I, R),
+         "kan_basis_grad: gH must be [B, I, G+k]")
+    x, grid = x.contiguous(), grid.contiguous()
+    gH = grad_basis.contiguous().to(x.dtype)
+    gx = torch.empty(B, I, dtype=x.dtype, device=x.device)
+    if B == 0:
+        return gx
+    with torch.cuda.device(x.device):
+        check(LIB.kan_hip_basis_grad(dtype_code(x.dtype), ptr(x), ptr(grid), ptr(gH), ptr(gx),
+                                     B, I, G, spline_order, stream_of(x.device)))
+    return gx
+
+
+def _check_edge_inputs(s, H, bw, W, hb):
+    """check_edge_inputs, csrc/kan_reg_cuda.cu:240-257."""
+    _req(H.is_cuda and W.is_cuda, "edge_abs_mean: H and W must be CUDA tensors")
+    _req(H.dim() == 3 and W.dim() == 3, "edge_abs_mean: H must be [N,I,R], W [O,I,R]")
+    _req(H.shape[1] == W.shape[1] and H.shape[2] == W.shape[2], "edge_abs_mean: H/W shape mismatch")
+    _req(H.shape[2] <= 72, "edge_abs_mean: R must be <= 72, got ", H.shape[2])
+    _req(H.shape[1] <= CUDA_MAX_IN_FEATURES, "edge_abs_mean: too many input features")
+    _req(H.shape[0] >= 1, "edge_abs_mean: need at least one sample")
+    _req(H.dtype == W.dtype, "edge_abs_mean: dtype mismatch")
+    _req(H.dtype in _F, "edge_abs_mean: only FP32/FP64 supported")
+    if hb:
+        _req(tuple(s.shape) == tuple(H.shape[:2]), "edge_abs_mean: s must be [N, I]")
+        _req(tuple(bw.shape) == tuple(W.shape[:2]), "edge_abs_mean: base_weight must be [O, I]")
+        _req(s.dtype == H.dtype and bw.dtype == H.dtype, "edge_abs_mean: dtype mismatch")
+
+
+def edge_abs_mean(s, H, base_weight, W) -> torch.Tensor:
+    """a[o,i] = mean_n |s*bw + sum_r H*W| without materialising [N, O, I] (device)."""
+    hb = _cmp.has_base(base_weight)
+    _check_edge_inputs(s, H, base_weight, W, hb)
+    H, W = H.contiguous(), W.contiguous()
+    sc = s.contiguous() if hb else None
+    bw = base_weight.contiguous() if hb else None
+    N, I, R = H.shape
+    O = W.shape[0]
+    a = torch.empty(O, I, dtype=W.dtype, device=W.device)
+    if O * I == 0:
+        return a
+    code = dtype_code(H.dtype)
+    nbytes = _lib.ctypes.c_size_t()
+    with torch.cuda.device(H.device):
+        check(LIB.kan_hip_edge_workspace(code, N, I, O, R, 0, _lib.ctypes.byref(nbytes)))
+        ws = torch.empty(max(int(nbytes.value), 1), dtype=torch.uint8, device=H.device)
+        check(LIB.kan_hip_edge_abs_mean(code, ptr(sc), ptr(H), ptr(bw), ptr(W), ptr(a), ptr(ws),
+                                        int(nbytes.value), N, I, O, R, stream_of(H.device)))
+    return a
+
+
+def edge_abs_mean_backward(grad_a, s, H, base_weight, W, need_s: bool, need_H: bool,
+                           need_bw: bool, need_W: bool):
+    """Backward of edge_abs_mean, recomputing phi ->
+    (ds | None, dH | None, dbw | None, dW | None)."""
+    hb = _cmp.has_base(base_weight)
+    _check_edge_inputs(s, H, base_weight, W, hb)
+    _req(tuple(grad_a.shape) == tuple(W.shape[:2]), "edge_abs_mean_backward: grad shape")
+    H, W = H.contiguous(), W.contiguous()
+    ga = grad_a.contiguous().to(W.dtype)
+    sc = s.contiguous() if hb else None
+    bw = base_weight.contiguous() if hb else None
+    N, I, R = H.shape
+    O = W.shape[0]
+    opts = dict(dtype=H.dtype, device=H.device)
+    ds = torch.empty(N, I, **opts) if (need_s and hb) else None
+    dH = torch.empty(N, I, R, **opts) if need_H else None
+    dbw = torch.empty(O, I, **opts) if (need_bw and hb) else None
+    dW = torch.empty(O, I, R, **opts) if need_W else None
+    if ds is None and dH is None and dbw is None and dW is None:
+        return ds, dH, dbw, dW
+    code = dtype_code(H.dtype)
+    nbytes = _lib.ctypes.c_size_t(0)
+    with torch.cuda.device(H.device):
+        if dbw is not None or dW is not None:
+            check(LIB.kan_hip_edge_workspace(code, N, I, O, R, 1, _lib.ctypes.byref(nbytes)))
+        ws = torch.empty(max(int(nbytes.value), 1), dtype=torch.uint8, device=H.device)
+        check(LIB.kan_hip_edge_abs_mean_backward(
+            code, ptr(ga), ptr(sc), ptr(H), ptr(bw), ptr(W), ptr(ds), ptr(dH), ptr(dbw), ptr(dW),
+            ptr(ws), int(nbytes.value), N, I, O, R, stream_of(H.device)))
+    return ds, dH, dbw, dW

@@ -1,0 +1,110 @@
+"""ctypes binding of libkan_hip.so (declarations in include/kan_hip.h).
+
+torch is imported before the library is opened so that the HIP runtime torch
+already loaded (same soname, libamdhip64.so.7) is the one the kernels use:
+streams and device pointers handed over from torch are then valid in the
+library.  Loading fails loudly (ImportError) when the library is missing.
+"""
+
+import ctypes
+import os
+
+import torch  # noqa: F401  (must precede the CDLL open, see module docstring)
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libkan_hip.so")
+
+KAN_DTYPE_F32 = 0
+KAN_DTYPE_F64 = 1
+KAN_OK = 0
+KAN_ERR_INVALID = 1
+KAN_ERR_LIMIT = 2
+KAN_ERR_HIP = 3
+KAN_ERR_WORKSPACE = 4
+
+_i64 = ctypes.c_int64
+_int = ctypes.c_int
+_vp = ctypes.c_void_p
+_sz = ctypes.c_size_t
+
+# name -> (restype, argtypes)
+SIGNATURES = {
+    "kan_hip_last_error": (ctypes.c_char_p, []),
+    "kan_hip_limits": (_int, [ctypes.POINTER(_i64), ctypes.POINTER(_i64)]),
+    "kan_hip_set_basis_impl": (_int, [_i64]),
+    "kan_hip_get_basis_impl": (_i64, []),
+    "kan_hip_basis": (_int, [_int, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp]),
+    "kan_hip_basis_grad": (_int, [_int, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp]),
+    "kan_hip_aug_width": (_i64, [_i64, _i64, _i64, _int]),
+    "kan_hip_forward": (_int, [_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
+                               _i64, _i64, _i64, _i64, _i64, _vp]),
+    "kan_hip_pack_basis": (_int, [_int, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _int, _vp]),
+    "kan_hip_backward_workspace": (_int, [_int, _i64, _i64, _i64, _i64, _i64, _int, _int, _int,
+                                          ctypes.POINTER(_sz)]),
+    "kan_hip_backward": (_int, [_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
+                                _vp, _sz, _i64, _i64, _i64, _i64, _i64, _vp]),
+    "kan_hip_edge_workspace": (_int, [_int, _i64, _i64, _i64, _i64, _int, ctypes.POINTER(_sz)]),
+    "kan_hip_edge_abs_mean": (_int, [_int, _vp, _vp, _vp, _vp, _vp, _vp, _sz,
+                                     _i64, _i64, _i64, _i64, _vp]),
+    "kan_hip_edge_abs_mean_backward": (_int, [_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
+                                              _vp, _sz, _i64, _i64, _i64, _i64, _vp]),
+}
+
+
+class KanHipError(RuntimeError):
+    """A non-zero status from libkan_hip.so (message from kan_hip_last_error)."""
+
+    def __init__(self, code: int, message: str):
+        super().__init__(message)
+        self.code = code
+
+
+def _load():
+    if not os.path.exists(LIB_PATH):
+        raise ImportError(
+            f"{LIB_PATH} is missing: build it with `python -m torchsplinekan_amd.build_lib` "
+            "(or __graft_entry__.build())")
+    lib = ctypes.CDLL(LIB_PATH)
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    return lib
+
+
+LIB = _load()
+
+
+def last_error() -> str:
+    msg = LIB.kan_hip_last_error()
+    return msg.decode("utf-8", "replace") if msg else ""
+
+
+def check(status: int) -> None:
+    if status != KAN_OK:
+        raise KanHipError(status, last_error())
+
+
+def dtype_code(dtype: torch.dtype) -> int:
+    if dtype == torch.float32:
+        return KAN_DTYPE_F32
+    if dtype == torch.float64:
+        return KAN_DTYPE_F64
+    raise RuntimeError(f"only FP32 and FP64 inputs are supported, got {dtype}")
+
+
+def ptr(t):
+    """Device pointer of a tensor, or None for an absent optional."""
+    if t is None:
+        return None
+    return t.data_ptr() if t.numel() > 0 else None
+
+
+def stream_of(device: torch.device) -> int:
+    """hipStream_t handle of the current torch stream on `device`."""
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def limits():
+    a, b = _i64(), _i64()
+    check(LIB.kan_hip_limits(ctypes.byref(a), ctypes.byref(b)))
+    return int(a.value), int(b.value)

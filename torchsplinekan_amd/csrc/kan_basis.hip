@@ -1,0 +1,512 @@
+// B-spline basis kernels for gfx950: the basis H[n, I, R], its input-gradient
+// contraction gx = sum_r gH * dB_r/dx, and the small packing kernels that
+// build the augmented operands of the contraction GEMMs.
+//
+// Conventions (identical to the reference's native path,
+// csrc/kan_cuda.cu:188-271, and to spline_kan/reference_backend.py:69-94 for
+// finite inputs):
+//   * spans are half-open [t_m, t_{m+1}); x == t_{nk-1} uses the last
+//     non-degenerate span;
+//   * x outside [t_0, t_{nk-1}] (and NaN) gives an all-zero row;
+//   * a zero knot difference contributes zero (repeated knots allowed).
+//
+// Work mapping: a workgroup owns a block of up to 64 consecutive features
+// (their knot rows are staged in LDS) and a range of samples.  A wave
+// computes 64 (sample, feature) items per step; each lane writes its dense
+// R-row into an LDS stage, and the wave then stores the stage with
+// consecutive lanes on consecutive addresses, so global stores of the
+// [n, I, R] rows are fully coalesced.  x reads are coalesced along features.
+
+#include "kan_common.h"
+
+namespace kan {
+namespace {
+
+constexpr int kBasisThreads = 256;  // upper bound; a block has sh.waves waves
+
+// Span index m with t[m] <= x < t[m+1] (x == t[nk-1]: last non-degenerate
+// span), or -1 when x lies outside [t[0], t[nk-1]] or is NaN.
+// Follows find_span, csrc/kan_cuda.cu:207-221.
+template <typename T>
+__device__ __forceinline__ int knot_span(const T* __restrict__ t, int nk, T x) {
+  const T lo_knot = t[0];
+  const T hi_knot = t[nk - 1];
+  if (!(x >= lo_knot) || x > hi_knot) return -1;
+  if (x == hi_knot) {
+    int m = nk - 2;
+    while (m > 0 && t[m] == hi_knot) --m;
+    return m;
+  }
+  int lo = 0, hi = nk - 1;  // t[lo] <= x < t[hi]
+  while (hi - lo > 1) {
+    const int mid = (lo + hi) >> 1;
+    if (t[mid] <= x) lo = mid;
+    else hi = mid;
+  }
+  return lo;
+}
+
+template <typename T>
+__device__ __forceinline__ T knot_at(const T* __restrict__ t, int nk, int idx) {
+  idx = idx < 0 ? 0 : (idx > nk - 1 ? nk - 1 : idx);
+  return t[idx];
+}
+
+// The D+1 degree-D functions that are non-zero on span m,
+//   v[j] = B_{m-D+j, D}(x),  j = 0..D,
+// by the triangular scheme of Piegl & Tiller (The NURBS Book, A2.2) with a
+// zero-denominator guard.  Window entries that are not real basis functions
+// (near the ends of the knot vector) read clamped knots and are discarded by
+// the caller; every real function only depends on in-range knots.
+// Same recurrence as local_basis, csrc/kan_cuda.cu:230-271.
+template <int D, typename T>
+__device__ __forceinline__ void span_values(const T* __restrict__ t, int nk, int m, T x,
+                                            T (&v)[D + 1]) {
+  T left[D + 1], right[D + 1];
+  v[0] = T(1);
+#pragma unroll
+  for (int j = 1; j <= D; ++j) {
+    left[j] = x - knot_at(t, nk, m + 1 - j);
+    right[j] = knot_at(t, nk, m + j) - x;
+    T saved = T(0);
+#pragma unroll
+    for (int r = 0; r < j; ++r) {
+      const T den = right[r + 1] + left[j - r];
+      const T tmp = den != T(0) ? v[r] / den : T(0);
+      v[r] = saved + right[r + 1] * tmp;
+      saved = left[j - r] * tmp;
+    }
+    v[j] = saved;
+  }
+}
+
+// First derivatives of the K+1 degree-K functions active on span m:
+//   dB_{r,K} = K * ( B_{r,K-1}/(t_{r+K}-t_r) - B_{r+1,K-1}/(t_{r+K+1}-t_{r+1}) ),
+// r = m-K+j, from the degree-(K-1) values on the same span.
+// Formula of csrc/kan_cuda.cu:238-255 / spline_kan/reference_backend.py:99-125.
+template <int K, typename T>
+__device__ __forceinline__ void span_derivs(const T* __restrict__ t, int nk, int m, T x,
+                                            T (&d)[K + 1]) {
+  T lower[K];
+  span_values<K - 1, T>(t, nk, m, x, lower);
+#pragma unroll
+  for (int j = 0; j <= K; ++j) {
+    const int r = m - K + j;
+    T a = T(0), b = T(0);
+    if (j >= 1) {
+      const T den = knot_at(t, nk, r + K) - knot_at(t, nk, r);
+      if (den != T(0)) a = lower[j - 1] / den;
+    }
+    if (j <= K - 1) {
+      const T den = knot_at(t, nk, r + K + 1) - knot_at(t, nk, r + 1);
+      if (den != T(0)) b = lower[j] / den;
+    }
+    d[j] = T(K) * (a - b);
+  }
+}
+
+// Dense Cox-de Boor recurrence over the whole knot row (legacy basis
+// implementation 0).  Operation order follows compute_basis
+// (spline_kan/reference_backend.py:69-94): alpha = (x - t_r)/dl,
+// beta = (t_{r+d+1} - x)/dr, B = alpha*B_r + beta*B_{r+1}, with contraction
+// into FMA disabled so that the rounding sequence is the same.
+// Writes the degree-`deg` values into out[0 .. nk-2-deg].
+template <typename T>
+__device__ void dense_recurrence(const T* __restrict__ t, int nk, T x, int deg, T* out) {
+#pragma clang fp contract(off)
+  T buf[kMaxKnots];
+  const int n0 = nk - 1;
+  for (int r = 0; r < n0; ++r) {
+    const bool in = (x >= t[r]) && (x < t[r + 1]);
+    const bool last = (r == n0 - 1) && (x >= t[r]) && (x <= t[r + 1]);
+    buf[r] = (in || last) ? T(1) : T(0);
+  }
+  int cur = n0;
+  for (int d = 1; d <= deg; ++d) {
+    const int nn = cur - 1;
+    for (int r = 0; r < nn; ++r) {
+      const T dl = t[r + d] - t[r];
+      const T dr = t[r + d + 1] - t[r + 1];
+      const T alpha = (dl != T(0)) ? (x - t[r]) / dl : T(0);
+      const T beta = (dr != T(0)) ? (t[r + d + 1] - x) / dr : T(0);
+      const T lhs = alpha * buf[r];
+      const T rhs = beta * buf[r + 1];
+      buf[r] = lhs + rhs;
+    }
+    cur = nn;
+  }
+  for (int r = 0; r < cur; ++r) out[r] = buf[r];
+}
+
+// Dense derivative (legacy implementation 0), compute_basis_derivative order
+// (spline_kan/reference_backend.py:115-125): k*(Hm_r/d1 - Hm_{r+1}/d2).
+template <typename T>
+__device__ void dense_derivative(const T* __restrict__ t, int nk, T x, int k, T* out) {
+#pragma clang fp contract(off)
+  T lower[kMaxKnots];
+  dense_recurrence<T>(t, nk, x, k - 1, lower);
+  const int R = nk - k - 1;
+  for (int r = 0; r < R; ++r) {
+    const T d1 = t[r + k] - t[r];
+    const T d2 = t[r + k + 1] - t[r + 1];
+    const T t1 = (d1 != T(0)) ? lower[r] / d1 : T(0);
+    const T t2 = (d2 != T(0)) ? lower[r + 1] / d2 : T(0);
+    out[r] = T(k) * (t1 - t2);
+  }
+}
+
+// c / R for small non-negative c (c < 2^16) via a float reciprocal; exact
+// because the fractional part of (c + 0.5)/R is at least 0.5/R away from an
+// integer while the product's error is below 1e-3.
+__device__ __forceinline__ int small_div(int c, float inv_r) {
+  return (int)(((float)c + 0.5f) * inv_r);
+}
+
+struct BasisShape {
+  int64_t n;
+  int I, G;
+  int fb;     // features per block (<= 64)
+  int subs;   // samples per wave step (64 / fb)
+  int iters;  // wave steps per block
+  int rs;     // LDS row stride per item (R rounded up to odd)
+  int waves;  // waves per block (fewer for wide fp64 rows, to bound LDS)
+};
+
+template <typename T>
+__device__ __forceinline__ T* stage_knots(unsigned char* smem, const T* __restrict__ grid,
+                                          int i0, int fbv, int nk) {
+  T* knots = reinterpret_cast<T*>(smem);
+  const T* src = grid + (int64_t)i0 * nk;
+  for (int e = threadIdx.x; e < fbv * nk; e += blockDim.x) knots[e] = src[e];
+  return knots;
+}
+
+// H rows (and optionally silu(x)) for a block of features x samples.
+template <int K, typename T, int IMPL>
+__global__ __launch_bounds__(kBasisThreads) void basis_kernel(
+    const T* __restrict__ x, const T* __restrict__ grid, T* __restrict__ out, int64_t ld,
+    T* __restrict__ silu_out, BasisShape sh) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int nk = sh.G + 2 * K + 1, R = sh.G + K;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int i0 = blockIdx.x * sh.fb;
+  const int fbv = min(sh.fb, sh.I - i0);
+  T* knots = stage_knots<T>(smem, grid, i0, fbv, nk);
+  T* stage = knots + round_up((int64_t)sh.fb * nk, 4) + wave * 64 * sh.rs;
+  __syncthreads();
+
+  const int sub = lane / sh.fb, fi = lane - sub * sh.fb;
+  const bool lane_ok = sub < sh.subs && fi < fbv;
+  const T* t = knots + fi * nk;
+  const float inv_r = 1.0f / (float)R;
+  const int64_t step = (int64_t)sh.waves * sh.subs;
+  int64_t nbase = (int64_t)blockIdx.y * sh.iters * step + (int64_t)wave * sh.subs;
+  T* row = stage + lane * sh.rs;
+
+  for (int it = 0; it < sh.iters; ++it, nbase += step) {
+    const int64_t nn = nbase + sub;
+    const bool ok = lane_ok && nn < sh.n;
+    const T xv = ok ? x[nn * sh.I + i0 + fi] : T(0);
+    if (IMPL == 1) {
+      for (int r = 0; r < R; ++r) row[r] = T(0);
+      const int m = ok ? knot_span(t, nk, xv) : -1;
+      if (m >= 0) {
+        T v[K + 1];
+        span_values<K, T>(t, nk, m, xv, v);
+#pragma unroll
+        for (int j = 0; j <= K; ++j) {
+          const int r = m - K + j;
+          if (r >= 0 && r < R) row[r] = v[j];
+        }
+      }
+    } else {
+      if (ok) {
+        dense_recurrence<T>(t, nk, xv, K, row);
+      } else {
+        for (int r = 0; r < R; ++r) row[r] = T(0);
+      }
+    }
+    __syncthreads();
+    // Coalesced store of the staged rows: sample by sample, the fbv*R
+    // values of features [i0, i0+fbv) are contiguous in the output.
+    for (int s = 0; s < sh.subs; ++s) {
+      const int64_t ns = nbase + s;
+      if (ns >= sh.n) break;
+      T* dst = out + ns * ld + (int64_t)i0 * R;
+      const T* src = stage + s * sh.fb * sh.rs;
+      for (int c = lane; c < fbv * R; c += 64) {
+        const int item = small_div(c, inv_r);
+        dst[c] = src[item * sh.rs + (c - item * R)];
+      }
+    }
+    if (silu_out != nullptr && ok) silu_out[nn * ld + i0 + fi] = silu_of<T>(xv);
+    __syncthreads();
+  }
+}
+
+// gx[n, i] = sum_r g[n, i*R + r] * dB_r/dx (+ gbase[n, i] * silu'(x)).
+template <int K, typename T, int IMPL>
+__global__ __launch_bounds__(kBasisThreads) void basis_grad_kernel(
+    const T* __restrict__ x, const T* __restrict__ grid, const T* __restrict__ g, int64_t ld,
+    const T* __restrict__ gbase, T* __restrict__ gx, BasisShape sh) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int nk = sh.G + 2 * K + 1, R = sh.G + K;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int i0 = blockIdx.x * sh.fb;
+  const int fbv = min(sh.fb, sh.I - i0);
+  T* knots = stage_knots<T>(smem, grid, i0, fbv, nk);
+  T* stage = knots + round_up((int64_t)sh.fb * nk, 4) + wave * 64 * sh.rs;
+  __syncthreads();
+
+  const int sub = lane / sh.fb, fi = lane - sub * sh.fb;
+  const bool lane_ok = sub < sh.subs && fi < fbv;
+  const T* t = knots + fi * nk;
+  const float inv_r = 1.0f / (float)R;
+  const int64_t step = (int64_t)sh.waves * sh.subs;
+  int64_t nbase = (int64_t)blockIdx.y * sh.iters * step + (int64_t)wave * sh.subs;
+  const T* row = stage + lane * sh.rs;
+
+  for (int it = 0; it < sh.iters; ++it, nbase += step) {
+    for (int s = 0; s < sh.subs; ++s) {
+      const int64_t ns = nbase + s;
+      if (ns >= sh.n) break;
+      const T* src = g + ns * ld + (int64_t)i0 * R;
+      T* dst = stage + s * sh.fb * sh.rs;
+      for (int c = lane; c < fbv * R; c += 64) {
+        const int item = small_div(c, inv_r);
+        dst[item * sh.rs + (c - item * R)] = src[c];
+      }
+    }
+    __syncthreads();
+    const int64_t nn = nbase + sub;
+    const bool ok = lane_ok && nn < sh.n;
+    if (ok) {
+      const T xv = x[nn * sh.I + i0 + fi];
+      T acc = T(0);
+      if (IMPL == 1) {
+        const int m = knot_span(t, nk, xv);
+        if (m >= 0) {
+          T d[K + 1];
+          span_derivs<K, T>(t, nk, m, xv, d);
+#pragma unroll
+          for (int j = 0; j <= K; ++j) {
+            const int r = m - K + j;
+            if (r >= 0 && r < R) acc += row[r] * d[j];
+          }
+        }
+      } else {
+        T d[kMaxKnots];
+        dense_derivative<T>(t, nk, xv, K, d);
+        for (int r = 0; r < R; ++r) acc += row[r] * d[r];
+      }
+      if (gbase != nullptr) acc += gbase[nn * ld + i0 + fi] * silu_grad_of<T>(xv);
+      gx[nn * sh.I + i0 + fi] = acc;
+    }
+    __syncthreads();
+  }
+}
+
+// aug[n, i*R + r] = basis[n, i, r]; aug[n, I*R + i] = silu(x[n, i]).
+template <typename T>
+__global__ void pack_basis_kernel(const T* __restrict__ basis, const T* __restrict__ x,
+                                  T* __restrict__ aug, int64_t ld, int64_t n, int64_t I,
+                                  int64_t R, bool has_base) {
+  const int64_t IR = I * R;
+  const int64_t row_len = IR + (has_base ? I : 0);
+  const int64_t total = n * row_len;
+  for (int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; e < total;
+       e += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t r = e / row_len, c = e - r * row_len;
+    aug[r * ld + c] = c < IR ? basis[r * IR + c] : silu_of<T>(x[r * I + (c - IR)]);
+  }
+}
+
+// waug[o, i*R + r] = sw[o,i,r] * scaler[o,i]; waug[o, I*R + i] = bw[o,i];
+// padding columns are zeroed.
+template <typename T>
+__global__ void build_waug_kernel(const T* __restrict__ sw, const T* __restrict__ scaler,
+                                  const T* __restrict__ bw, T* __restrict__ waug, int64_t ld,
+                                  int64_t O, int64_t I, int64_t R) {
+  const int64_t IR = I * R;
+  const int64_t total = O * ld;
+  for (int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; e < total;
+       e += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t o = e / ld, c = e - o * ld;
+    T v = T(0);
+    if (c < IR) {
+      v = sw[o * IR + c];
+      if (scaler != nullptr) v = v * scaler[o * I + c / R];
+    } else if (bw != nullptr && c < IR + I) {
+      v = bw[o * I + (c - IR)];
+    }
+    waug[e] = v;
+  }
+}
+
+// Parameter gradients from the (split) products G = D^T [H | s]:
+//   gsw = scaler * G_H, gscaler = sum_r sw * G_H, gbw = G_s
+// (csrc/kan_cuda.cu:576-598).  Split partials are summed in fixed order.
+template <typename T>
+__global__ void param_grads_kernel(const T* __restrict__ part, int splits, int64_t split_stride,
+                                   int64_t ld, const T* __restrict__ sw,
+                                   const T* __restrict__ scaler, T* __restrict__ gsw,
+                                   T* __restrict__ gscaler, T* __restrict__ gbw, int64_t O,
+                                   int64_t I, int64_t R) {
+  const int64_t total = O * I;
+  for (int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; e < total;
+       e += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t o = e / I, i = e - o * I;
+    const T* base = part + o * ld + i * R;
+    if (gsw != nullptr || gscaler != nullptr) {
+      const T sc = scaler != nullptr ? scaler[e] : T(1);
+      T dsc = T(0);
+      for (int64_t r = 0; r < R; ++r) {
+        T gv = base[r];
+        for (int s = 1; s < splits; ++s) gv += base[r + s * split_stride];
+        if (gsw != nullptr) gsw[e * R + r] = scaler != nullptr ? sc * gv : gv;
+        dsc += sw[e * R + r] * gv;
+      }
+      if (gscaler != nullptr) gscaler[e] = dsc;
+    }
+    if (gbw != nullptr) {
+      const T* bp = part + o * ld + I * R + i;
+      T gv = bp[0];
+      for (int s = 1; s < splits; ++s) gv += bp[s * split_stride];
+      gbw[e] = gv;
+    }
+  }
+}
+
+BasisShape make_shape(int64_t n, int64_t I, int G, int R, size_t elem, int64_t* blocks_y) {
+  BasisShape sh;
+  sh.n = n;
+  sh.I = (int)I;
+  sh.G = G;
+  sh.fb = (int)(I < 64 ? I : 64);
+  sh.subs = 64 / sh.fb;
+  sh.rs = (R % 2 == 1) ? R : R + 1;
+  sh.waves = 4;
+  while (sh.waves > 1 && (size_t)sh.waves * 64 * sh.rs * elem > 48 * 1024) sh.waves /= 2;
+  const int64_t per_step = (int64_t)sh.waves * sh.subs;
+  const int64_t steps = ceil_div(n, per_step);
+  // Aim for ~16 steps per block, but keep enough blocks to fill the chip.
+  const int64_t fblocks = ceil_div(I, sh.fb);
+  int64_t iters = 16;
+  while (iters > 1 && fblocks * ceil_div(steps, iters) < 4096) iters /= 2;
+  sh.iters = (int)iters;
+  *blocks_y = ceil_div(steps, iters);
+  return sh;
+}
+
+template <typename T>
+size_t basis_smem(const BasisShape& sh, int nk) {
+  return sizeof(T) * (round_up((int64_t)sh.fb * nk, 4) + (int64_t)sh.waves * 64 * sh.rs);
+}
+
+inline int gs_blocks(int64_t total) {
+  int64_t b = ceil_div(total, 256);
+  if (b > 65536) b = 65536;
+  return (int)(b < 1 ? 1 : b);
+}
+
+}  // namespace
+
+template <typename T>
+int launch_basis(const T* x, const T* grid, T* out, int64_t ld_out, T* silu_out, int64_t n,
+                 int64_t I, int G, int k, int impl, hipStream_t st) {
+  if (n == 0 || I == 0) return KAN_OK;
+  const int R = G + k, nk = G + 2 * k + 1;
+  int64_t by = 0;
+  BasisShape sh = make_shape(n, I, G, R, sizeof(T), &by);
+  if (by > 2147483647LL) return set_error(KAN_ERR_LIMIT, "basis: too many samples (%lld)", (long long)n);
+  dim3 grid_dim((unsigned)ceil_div(I, sh.fb), (unsigned)by);
+  const size_t smem = basis_smem<T>(sh, nk);
+#define KAN_BASIS_LAUNCH(KK, IM)                                                           \
+  hipLaunchKernelGGL((basis_kernel<KK, T, IM>), grid_dim, dim3(64 * sh.waves), smem, st, x, \
+                     grid, out, ld_out, silu_out, sh)
+  if (impl == 1) {
+    if (k == 1) KAN_BASIS_LAUNCH(1, 1);
+    else if (k == 2) KAN_BASIS_LAUNCH(2, 1);
+    else KAN_BASIS_LAUNCH(3, 1);
+  } else {
+    if (k == 1) KAN_BASIS_LAUNCH(1, 0);
+    else if (k == 2) KAN_BASIS_LAUNCH(2, 0);
+    else KAN_BASIS_LAUNCH(3, 0);
+  }
+#undef KAN_BASIS_LAUNCH
+  return check_launch("basis");
+}
+
+template <typename T>
+int launch_basis_grad(const T* x, const T* grid, const T* gH, int64_t ld_g, const T* gbase,
+                      T* gx, int64_t n, int64_t I, int G, int k, int impl, hipStream_t st) {
+  if (n == 0 || I == 0) return KAN_OK;
+  const int R = G + k, nk = G + 2 * k + 1;
+  int64_t by = 0;
+  BasisShape sh = make_shape(n, I, G, R, sizeof(T), &by);
+  if (by > 2147483647LL) return set_error(KAN_ERR_LIMIT, "basis_grad: too many samples");
+  dim3 grid_dim((unsigned)ceil_div(I, sh.fb), (unsigned)by);
+  const size_t smem = basis_smem<T>(sh, nk);
+#define KAN_BGRAD_LAUNCH(KK, IM)                                                             \
+  hipLaunchKernelGGL((basis_grad_kernel<KK, T, IM>), grid_dim, dim3(64 * sh.waves), smem, st, \
+                     x, grid, gH, ld_g, gbase, gx, sh)
+  if (impl == 1) {
+    if (k == 1) KAN_BGRAD_LAUNCH(1, 1);
+    else if (k == 2) KAN_BGRAD_LAUNCH(2, 1);
+    else KAN_BGRAD_LAUNCH(3, 1);
+  } else {
+    if (k == 1) KAN_BGRAD_LAUNCH(1, 0);
+    else if (k == 2) KAN_BGRAD_LAUNCH(2, 0);
+    else KAN_BGRAD_LAUNCH(3, 0);
+  }
+#undef KAN_BGRAD_LAUNCH
+  return check_launch("basis_grad");
+}
+
+template <typename T>
+int launch_pack_basis(const T* basis, const T* x, T* aug, int64_t ld_aug, int64_t n, int64_t I,
+                      int64_t R, bool has_base, hipStream_t st) {
+  const int64_t total = n * (I * R + (has_base ? I : 0));
+  if (total == 0) return KAN_OK;
+  hipLaunchKernelGGL((pack_basis_kernel<T>), dim3(gs_blocks(total)), dim3(256), 0, st, basis, x,
+                     aug, ld_aug, n, I, R, has_base);
+  return check_launch("pack_basis");
+}
+
+template <typename T>
+int launch_build_waug(const T* sw, const T* scaler, const T* bw, T* waug, int64_t ld, int64_t O,
+                      int64_t I, int64_t R, hipStream_t st) {
+  const int64_t total = O * ld;
+  if (total == 0) return KAN_OK;
+  hipLaunchKernelGGL((build_waug_kernel<T>), dim3(gs_blocks(total)), dim3(256), 0, st, sw,
+                     scaler, bw, waug, ld, O, I, R);
+  return check_launch("build_weight_aug");
+}
+
+template <typename T>
+int launch_param_grads(const T* part, int splits, int64_t split_stride, int64_t ld, const T* sw,
+                       const T* scaler, T* gsw, T* gscaler, T* gbw, int64_t O, int64_t I,
+                       int64_t R, hipStream_t st) {
+  const int64_t total = O * I;
+  if (total == 0) return KAN_OK;
+  hipLaunchKernelGGL((param_grads_kernel<T>), dim3(gs_blocks(total)), dim3(256), 0, st, part,
+                     splits, split_stride, ld, sw, scaler, gsw, gscaler, gbw, O, I, R);
+  return check_launch("param_grads");
+}
+
+#define KAN_INST(T)                                                                          \
+  template int launch_basis<T>(const T*, const T*, T*, int64_t, T*, int64_t, int64_t, int, int, \
+                               int, hipStream_t);                                            \
+  template int launch_basis_grad<T>(const T*, const T*, const T*, int64_t, const T*, T*,       \
+                                    int64_t, int64_t, int, int, int, hipStream_t);           \
+  template int launch_pack_basis<T>(const T*, const T*, T*, int64_t, int64_t, int64_t,        \
+                                    int64_t, bool, hipStream_t);                             \
+  template int launch_build_waug<T>(const T*, const T*, const T*, T*, int64_t, int64_t,       \
+                                    int64_t, int64_t, hipStream_t);                          \
+  template int launch_param_grads<T>(const T*, int, int64_t, int64_t, const T*, const T*, T*, \
+                                     T*, T*, int64_t, int64_t, int64_t, hipStream_t);
+KAN_INST(float)
+KAN_INST(double)
+#undef KAN_INST
+
+}  // namespace kan

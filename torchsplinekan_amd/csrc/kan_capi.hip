@@ -1,0 +1,406 @@
+// extern "C" entry points of libkan_hip.so (declared in include/kan_hip.h).
+// Every entry point validates its sizes and limits before any launch, so a
+// rejected call leaves nothing running on the device.  Launch errors are
+// reported through the status code and kan_hip_last_error().
+
+#include <atomic>
+#include <cstdarg>
+#include <cstdio>
+#include <mutex>
+
+#include "kan_common.h"
+
+namespace kan {
+
+namespace {
+thread_local std::string g_last_error;
+std::atomic<int> g_basis_impl{1};
+std::mutex g_cu_mutex;
+int g_cu_count[64] = {0};
+}  // namespace
+
+int set_error(int code, const char* fmt, ...) {
+  char buf[1024];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return code;
+}
+
+int check_launch(const char* what) {
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return set_error(KAN_ERR_HIP, "%s: launch failed: %s", what, hipGetErrorString(e));
+  return KAN_OK;
+}
+
+int device_cu_count() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
+    (void)hipGetLastError();
+    return 256;
+  }
+  std::lock_guard<std::mutex> lock(g_cu_mutex);
+  if (g_cu_count[dev] == 0) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) {
+      (void)hipGetLastError();
+      cus = 256;
+    }
+    g_cu_count[dev] = cus;
+  }
+  return g_cu_count[dev];
+}
+
+namespace {
+
+int check_dtype(int dtype, const char* who) {
+  if (dtype != KAN_DTYPE_F32 && dtype != KAN_DTYPE_F64)
+    return set_error(KAN_ERR_INVALID, "%s: only FP32 and FP64 inputs are supported (dtype code %d)", who, dtype);
+  return KAN_OK;
+}
+
+// Layer limits, mirroring kan_check_inputs (csrc/kan_ops.h:39-76) except the
+// 32-bit index guard: every kernel here indexes with 64-bit offsets.
+int check_layer(const char* who, int64_t n, int64_t I, int64_t O, int64_t G, int64_t k) {
+  if (k < 1 || k > 3) return set_error(KAN_ERR_INVALID, "spline_order must be 1, 2 or 3; got %lld", (long long)k);
+  if (G < 1) return set_error(KAN_ERR_INVALID, "%s: grid too short for spline_order %lld (G=%lld)", who, (long long)k, (long long)G);
+  if (n < 0 || I < 0 || O < 0) return set_error(KAN_ERR_INVALID, "%s: negative size", who);
+  if (G + 2 * k > kMaxDeg0Basis)
+    return set_error(KAN_ERR_LIMIT,
+                     "CUDA kernel supports G + 2k <= %lld (got G=%lld, k=%lld); use backend='reference' for larger grids",
+                     (long long)kMaxDeg0Basis, (long long)G, (long long)k);
+  if (I > kMaxInFeatures)
+    return set_error(KAN_ERR_LIMIT, "CUDA kernel supports in_features <= %lld, got %lld",
+                     (long long)kMaxInFeatures, (long long)I);
+  return KAN_OK;
+}
+
+int need_ptr(const void* p, const char* who, const char* name) {
+  if (p == nullptr) return set_error(KAN_ERR_INVALID, "%s: %s must not be NULL", who, name);
+  return KAN_OK;
+}
+
+#define KAN_TRY(expr)              \
+  do {                             \
+    const int kan_rc_ = (expr);    \
+    if (kan_rc_ != KAN_OK) return kan_rc_; \
+  } while (0)
+
+struct BackwardPlan {
+  int64_t R, ld, kaug;
+  bool need_x, need_params;
+  int splits;
+  size_t waug_elems, e_elems, part_elems;
+};
+
+template <typename T>
+BackwardPlan plan_backward(int64_t n, int64_t I, int64_t O, int64_t G, int64_t k, bool has_base,
+                           bool need_x, bool need_params) {
+  BackwardPlan p;
+  p.R = G + k;
+  p.ld = aug_width(I, p.R, has_base);
+  p.kaug = I * p.R + (has_base ? I : 0);
+  p.need_x = need_x;
+  p.need_params = need_params;
+  p.splits = need_params ? gemm_pick_splits<T>(O, p.kaug, n) : 1;
+  p.waug_elems = need_x ? (size_t)(O * p.ld) : 0;
+  p.e_elems = need_x ? (size_t)(n * p.ld) : 0;
+  p.part_elems = need_params ? (size_t)p.splits * (size_t)(O * p.ld) : 0;
+  return p;
+}
+
+template <typename T>
+int forward_impl(const void* x, const void* grid, const void* bw, const void* sw,
+                 const void* scaler, void* out, void* aug, void* waug, int64_t n, int64_t I,
+                 int64_t O, int64_t G, int64_t k, hipStream_t st) {
+  const int64_t R = G + k;
+  const bool has_base = bw != nullptr;
+  const int64_t ld = aug_width(I, R, has_base);
+  const int64_t kaug = I * R + (has_base ? I : 0);
+  const T* tx = static_cast<const T*>(x);
+  T* taug = static_cast<T*>(aug);
+  T* twaug = static_cast<T*>(waug);
+  KAN_TRY(launch_build_waug<T>(static_cast<const T*>(sw), static_cast<const T*>(scaler),
+                               static_cast<const T*>(bw), twaug, ld, O, I, R, st));
+  KAN_TRY(launch_basis<T>(tx, static_cast<const T*>(grid), taug, ld,
+                          has_base ? taug + I * R : nullptr, n, I, (int)G, (int)k,
+                          g_basis_impl.load(), st));
+  return launch_gemm<T>(kLayoutNT, n, O, kaug, taug, ld, twaug, ld, static_cast<T*>(out), O, 1,
+                        0, st);
+}
+
+template <typename T>
+int backward_impl(const void* D, const void* x, const void* grid, const void* bw,
+                  const void* sw, const void* scaler, const void* aug, void* gx, void* gbw,
+                  void* gsw, void* gscaler, void* ws, size_t ws_bytes, int64_t n, int64_t I,
+                  int64_t O, int64_t G, int64_t k, hipStream_t st) {
+  const bool has_base = bw != nullptr;
+  const bool need_x = gx != nullptr;
+  const bool need_params = gsw != nullptr || gscaler != nullptr || gbw != nullptr;
+  const BackwardPlan p = plan_backward<T>(n, I, O, G, k, has_base, need_x, need_params);
+  const size_t need_bytes = sizeof(T) * (p.waug_elems + p.e_elems + p.part_elems);
+  if (ws_bytes < need_bytes || (need_bytes > 0 && ws == nullptr))
+    return set_error(KAN_ERR_WORKSPACE, "kan_backward: workspace of %zu bytes is smaller than the %zu required",
+                     ws_bytes, need_bytes);
+  T* base = static_cast<T*>(ws);
+  T* waug = base;
+  T* E = waug + p.waug_elems;
+  T* part = E + p.e_elems;
+  const T* tD = static_cast<const T*>(D);
+  const T* taug = static_cast<const T*>(aug);
+  const int impl = g_basis_impl.load();
+  if (need_x) {
+    KAN_TRY(launch_build_waug<T>(static_cast<const T*>(sw), static_cast<const T*>(scaler),
+                                 static_cast<const T*>(bw), waug, p.ld, O, I, p.R, st));
+    // E[n, k'] = sum_o D[n, o] Waug[o, k']
+    KAN_TRY(launch_gemm<T>(kLayoutNN, n, p.kaug, O, tD, O, waug, p.ld, E, p.ld, 1, 0, st));
+    KAN_TRY(launch_basis_grad<T>(static_cast<const T*>(x), static_cast<const T*>(grid), E, p.ld,
+                                 has_base ? E + I * p.R : nullptr, static_cast<T*>(gx), n, I,
+                                 (int)G, (int)k, impl, st));
+  }
+  if (need_params) {
+    // G[o, k'] = sum_n D[n, o] Aug[n, k']  (split over n when the tile count is low)
+    KAN_TRY(launch_gemm<T>(kLayoutTN, O, p.kaug, n, tD, O, taug, p.ld, part, p.ld, p.splits,
+                           O * p.ld, st));
+    KAN_TRY(launch_param_grads<T>(part, p.splits, O * p.ld, p.ld, static_cast<const T*>(sw),
+                                  static_cast<const T*>(scaler), static_cast<T*>(gsw),
+                                  static_cast<T*>(gscaler), static_cast<T*>(gbw), O, I, p.R, st));
+  }
+  return KAN_OK;
+}
+
+int check_edge(const char* who, int dtype, const void* s, const void* H, const void* bw,
+               const void* W, int64_t n, int64_t I, int64_t O, int64_t R) {
+  KAN_TRY(check_dtype(dtype, who));
+  KAN_TRY(need_ptr(H, who, "H"));
+  KAN_TRY(need_ptr(W, who, "W"));
+  if ((s == nullptr) != (bw == nullptr))
+    return set_error(KAN_ERR_INVALID, "%s: s and base_weight must both be given or both be empty", who);
+  if (R < 1 || R > 72) return set_error(KAN_ERR_LIMIT, "edge_abs_mean: R must be <= 72, got %lld", (long long)R);
+  if (I > kMaxInFeatures) return set_error(KAN_ERR_LIMIT, "edge_abs_mean: too many input features");
+  if (n < 1) return set_error(KAN_ERR_INVALID, "edge_abs_mean: need at least one sample");
+  if (I < 0 || O < 0) return set_error(KAN_ERR_INVALID, "%s: negative size", who);
+  return KAN_OK;
+}
+
+size_t edge_ws_bytes(int dtype, int64_t n, int64_t I, int64_t O, int64_t R, bool backward) {
+  const int splits = edge_pick_splits(n, I, O);
+  if (splits <= 1) return 0;
+  const size_t elem = dtype == KAN_DTYPE_F64 ? 8 : 4;
+  return elem * (size_t)splits * (size_t)(O * I) * (size_t)(backward ? R + 1 : 1);
+}
+
+}  // namespace
+}  // namespace kan
+
+using namespace kan;
+
+extern "C" {
+
+const char* kan_hip_last_error(void) { return g_last_error.c_str(); }
+
+int kan_hip_limits(int64_t* max_deg0_basis, int64_t* max_in_features) {
+  if (max_deg0_basis != nullptr) *max_deg0_basis = kMaxDeg0Basis;
+  if (max_in_features != nullptr) *max_in_features = kMaxInFeatures;
+  return KAN_OK;
+}
+
+int kan_hip_set_basis_impl(int64_t impl) {
+  if (impl != 0 && impl != 1)
+    return set_error(KAN_ERR_INVALID, "basis impl must be 0 (recurrence) or 1 (local)");
+  g_basis_impl.store((int)impl);
+  return KAN_OK;
+}
+
+int64_t kan_hip_get_basis_impl(void) { return g_basis_impl.load(); }
+
+int kan_hip_basis(int dtype, const void* x, const void* grid, void* basis, int64_t n, int64_t I,
+                  int64_t G, int64_t k, void* stream) {
+  KAN_TRY(check_dtype(dtype, "kan_basis"));
+  KAN_TRY(check_layer("kan_basis", n, I, 0, G, k));
+  if (n == 0 || I == 0) return KAN_OK;
+  KAN_TRY(need_ptr(x, "kan_basis", "x"));
+  KAN_TRY(need_ptr(grid, "kan_basis", "grid"));
+  KAN_TRY(need_ptr(basis, "kan_basis", "basis"));
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int64_t R = G + k;
+  if (dtype == KAN_DTYPE_F32)
+    return launch_basis<float>(static_cast<const float*>(x), static_cast<const float*>(grid),
+                               static_cast<float*>(basis), I * R, nullptr, n, I, (int)G, (int)k,
+                               g_basis_impl.load(), st);
+  return launch_basis<double>(static_cast<const double*>(x), static_cast<const double*>(grid),
+                              static_cast<double*>(basis), I * R, nullptr, n, I, (int)G, (int)k,
+                              g_basis_impl.load(), st);
+}
+
+int kan_hip_basis_grad(int dtype, const void* x, const void* grid, const void* gH, void* gx,
+                       int64_t n, int64_t I, int64_t G, int64_t k, void* stream) {
+  KAN_TRY(check_dtype(dtype, "kan_basis_grad"));
+  KAN_TRY(check_layer("kan_basis_grad", n, I, 0, G, k));
+  if (n == 0 || I == 0) return KAN_OK;
+  KAN_TRY(need_ptr(x, "kan_basis_grad", "x"));
+  KAN_TRY(need_ptr(grid, "kan_basis_grad", "grid"));
+  KAN_TRY(need_ptr(gH, "kan_basis_grad", "grad_basis"));
+  KAN_TRY(need_ptr(gx, "kan_basis_grad", "grad_x"));
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int64_t R = G + k;
+  // The derivative contraction always uses the local kernel, as the
+  // reference's basis_grad does (csrc/kan_cuda.cu:459-464).
+  if (dtype == KAN_DTYPE_F32)
+    return launch_basis_grad<float>(static_cast<const float*>(x), static_cast<const float*>(grid),
+                                    static_cast<const float*>(gH), I * R, nullptr,
+                                    static_cast<float*>(gx), n, I, (int)G, (int)k, 1, st);
+  return launch_basis_grad<double>(static_cast<const double*>(x), static_cast<const double*>(grid),
+                                   static_cast<const double*>(gH), I * R, nullptr,
+                                   static_cast<double*>(gx), n, I, (int)G, (int)k, 1, st);
+}
+
+int64_t kan_hip_aug_width(int64_t I, int64_t G, int64_t k, int has_base) {
+  if (I < 0 || G < 1 || k < 1 || k > 3) return -1;
+  return aug_width(I, G + k, has_base != 0);
+}
+
+int kan_hip_forward(int dtype, const void* x, const void* grid, const void* bw, const void* sw,
+                    const void* scaler, void* out, void* aug, void* waug, int64_t n, int64_t I,
+                    int64_t O, int64_t G, int64_t k, void* stream) {
+  KAN_TRY(check_dtype(dtype, "kan_forward"));
+  KAN_TRY(check_layer("kan_forward", n, I, O, G, k));
+  // Pointers are only required for buffers of non-zero size.
+  const int64_t R = G + k;
+  const int64_t ld = aug_width(I, R, bw != nullptr);
+  if (O * I > 0) KAN_TRY(need_ptr(sw, "kan_forward", "spline_weight"));
+  if (O * ld > 0) KAN_TRY(need_ptr(waug, "kan_forward", "weight_aug"));
+  if (n * I > 0) {
+    KAN_TRY(need_ptr(x, "kan_forward", "x"));
+    KAN_TRY(need_ptr(grid, "kan_forward", "grid"));
+  }
+  if (n * ld > 0) KAN_TRY(need_ptr(aug, "kan_forward", "basis_aug"));
+  if (n * O > 0) KAN_TRY(need_ptr(out, "kan_forward", "output"));
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (dtype == KAN_DTYPE_F32)
+    return forward_impl<float>(x, grid, bw, sw, scaler, out, aug, waug, n, I, O, G, k, st);
+  return forward_impl<double>(x, grid, bw, sw, scaler, out, aug, waug, n, I, O, G, k, st);
+}
+
+int kan_hip_pack_basis(int dtype, const void* basis, const void* x, void* aug, int64_t n,
+                       int64_t I, int64_t G, int64_t k, int has_base, void* stream) {
+  KAN_TRY(check_dtype(dtype, "kan_pack_basis"));
+  KAN_TRY(check_layer("kan_pack_basis", n, I, 0, G, k));
+  if (n == 0 || I == 0) return KAN_OK;
+  KAN_TRY(need_ptr(basis, "kan_pack_basis", "basis"));
+  KAN_TRY(need_ptr(aug, "kan_pack_basis", "basis_aug"));
+  if (has_base) KAN_TRY(need_ptr(x, "kan_pack_basis", "x"));
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int64_t R = G + k;
+  const int64_t ld = aug_width(I, R, has_base != 0);
+  if (dtype == KAN_DTYPE_F32)
+    return launch_pack_basis<float>(static_cast<const float*>(basis), static_cast<const float*>(x),
+                                    static_cast<float*>(aug), ld, n, I, R, has_base != 0, st);
+  return launch_pack_basis<double>(static_cast<const double*>(basis), static_cast<const double*>(x),
+                                   static_cast<double*>(aug), ld, n, I, R, has_base != 0, st);
+}
+
+int kan_hip_backward_workspace(int dtype, int64_t n, int64_t I, int64_t O, int64_t G, int64_t k,
+                               int has_base, int need_x, int need_params, size_t* bytes) {
+  KAN_TRY(check_dtype(dtype, "kan_backward_workspace"));
+  KAN_TRY(check_layer("kan_backward_workspace", n, I, O, G, k));
+  KAN_TRY(need_ptr(bytes, "kan_backward_workspace", "bytes"));
+  BackwardPlan p;
+  size_t elem;
+  if (dtype == KAN_DTYPE_F32) {
+    p = plan_backward<float>(n, I, O, G, k, has_base != 0, need_x != 0, need_params != 0);
+    elem = 4;
+  } else {
+    p = plan_backward<double>(n, I, O, G, k, has_base != 0, need_x != 0, need_params != 0);
+    elem = 8;
+  }
+  *bytes = elem * (p.waug_elems + p.e_elems + p.part_elems);
+  return KAN_OK;
+}
+
+int kan_hip_backward(int dtype, const void* D, const void* x, const void* grid, const void* bw,
+                     const void* sw, const void* scaler, const void* aug, void* gx, void* gbw,
+                     void* gsw, void* gscaler, void* ws, size_t ws_bytes, int64_t n, int64_t I,
+                     int64_t O, int64_t G, int64_t k, void* stream) {
+  KAN_TRY(check_dtype(dtype, "kan_backward"));
+  KAN_TRY(check_layer("kan_backward", n, I, O, G, k));
+  if (gbw != nullptr && bw == nullptr)
+    return set_error(KAN_ERR_INVALID, "kan_backward: grad_base_weight requested without base_weight");
+  if (gscaler != nullptr && scaler == nullptr)
+    return set_error(KAN_ERR_INVALID, "kan_backward: grad_spline_scaler requested without spline_scaler");
+  const bool need_params = gsw != nullptr || gscaler != nullptr || gbw != nullptr;
+  if (O * I > 0) KAN_TRY(need_ptr(sw, "kan_backward", "spline_weight"));
+  if (n * O > 0) KAN_TRY(need_ptr(D, "kan_backward", "grad_output"));
+  if (n * I > 0 && gx != nullptr) {
+    KAN_TRY(need_ptr(x, "kan_backward", "x"));
+    KAN_TRY(need_ptr(grid, "kan_backward", "grid"));
+  }
+  if (n > 0 && I > 0 && need_params) KAN_TRY(need_ptr(aug, "kan_backward", "basis_aug"));
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (dtype == KAN_DTYPE_F32)
+    return backward_impl<float>(D, x, grid, bw, sw, scaler, aug, gx, gbw, gsw, gscaler, ws,
+                                ws_bytes, n, I, O, G, k, st);
+  return backward_impl<double>(D, x, grid, bw, sw, scaler, aug, gx, gbw, gsw, gscaler, ws,
+                               ws_bytes, n, I, O, G, k, st);
+}
+
+int kan_hip_edge_workspace(int dtype, int64_t n, int64_t I, int64_t O, int64_t R, int backward,
+                           size_t* bytes) {
+  KAN_TRY(check_dtype(dtype, "edge_workspace"));
+  KAN_TRY(need_ptr(bytes, "edge_workspace", "bytes"));
+  if (n < 0 || I < 0 || O < 0 || R < 0) return set_error(KAN_ERR_INVALID, "edge_workspace: negative size");
+  *bytes = edge_ws_bytes(dtype, n, I, O, R, backward != 0);
+  return KAN_OK;
+}
+
+int kan_hip_edge_abs_mean(int dtype, const void* s, const void* H, const void* bw, const void* W,
+                          void* a, void* ws, size_t ws_bytes, int64_t n, int64_t I, int64_t O,
+                          int64_t R, void* stream) {
+  KAN_TRY(check_edge("edge_abs_mean", dtype, s, H, bw, W, n, I, O, R));
+  KAN_TRY(need_ptr(a, "edge_abs_mean", "a"));
+  const size_t need = edge_ws_bytes(dtype, n, I, O, R, false);
+  if (ws_bytes < need || (need > 0 && ws == nullptr))
+    return set_error(KAN_ERR_WORKSPACE, "edge_abs_mean: workspace of %zu bytes is smaller than the %zu required", ws_bytes, need);
+  const int splits = need > 0 ? edge_pick_splits(n, I, O) : 1;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (dtype == KAN_DTYPE_F32)
+    return launch_edge_forward<float>(static_cast<const float*>(s), static_cast<const float*>(H),
+                                      static_cast<const float*>(bw), static_cast<const float*>(W),
+                                      static_cast<float*>(a), static_cast<float*>(ws), splits, n,
+                                      I, O, R, st);
+  return launch_edge_forward<double>(static_cast<const double*>(s), static_cast<const double*>(H),
+                                     static_cast<const double*>(bw), static_cast<const double*>(W),
+                                     static_cast<double*>(a), static_cast<double*>(ws), splits, n,
+                                     I, O, R, st);
+}
+
+int kan_hip_edge_abs_mean_backward(int dtype, const void* ga, const void* s, const void* H,
+                                   const void* bw, const void* W, void* gs, void* gH, void* gbw,
+                                   void* gW, void* ws, size_t ws_bytes, int64_t n, int64_t I,
+                                   int64_t O, int64_t R, void* stream) {
+  KAN_TRY(check_edge("edge_abs_mean_backward", dtype, s, H, bw, W, n, I, O, R));
+  KAN_TRY(need_ptr(ga, "edge_abs_mean_backward", "grad_a"));
+  if ((gs != nullptr || gbw != nullptr) && bw == nullptr)
+    return set_error(KAN_ERR_INVALID, "edge_abs_mean_backward: base gradients requested without a base branch");
+  const bool want_params = gbw != nullptr || gW != nullptr;
+  const size_t need = want_params ? edge_ws_bytes(dtype, n, I, O, R, true) : 0;
+  if (ws_bytes < need || (need > 0 && ws == nullptr))
+    return set_error(KAN_ERR_WORKSPACE, "edge_abs_mean_backward: workspace of %zu bytes is smaller than the %zu required", ws_bytes, need);
+  const int splits = need > 0 ? edge_pick_splits(n, I, O) : 1;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (dtype == KAN_DTYPE_F32)
+    return launch_edge_backward<float>(
+        static_cast<const float*>(ga), static_cast<const float*>(s), static_cast<const float*>(H),
+        static_cast<const float*>(bw), static_cast<const float*>(W), static_cast<float*>(gs),
+        static_cast<float*>(gH), static_cast<float*>(gbw), static_cast<float*>(gW),
+        static_cast<float*>(ws), splits, n, I, O, R, st);
+  return launch_edge_backward<double>(
+      static_cast<const double*>(ga), static_cast<const double*>(s), static_cast<const double*>(H),
+      static_cast<const double*>(bw), static_cast<const double*>(W), static_cast<double*>(gs),
+      static_cast<double*>(gH), static_cast<double*>(gbw), static_cast<double*>(gW),
+      static_cast<double*>(ws), splits, n, I, O, R, st);
+}
+
+}  // extern "C"

@@ -1,0 +1,119 @@
+// Shared definitions for the gfx950 KAN kernels: limits, dtype codes,
+// error reporting and small device helpers.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <string>
+
+#include "../../include/kan_hip.h"
+
+namespace kan {
+
+// Degree-0 basis count G + 2k accepted by the native path.  Mirrors
+// KAN_CUDA_MAX_DEG0_BASIS (csrc/kan_ops.h:15) so that backend selection in
+// the module layer is unchanged.
+constexpr int64_t kMaxDeg0Basis = 71;
+// in_features limit, mirroring KAN_CUDA_MAX_IN_FEATURES (csrc/kan_ops.h:17).
+constexpr int64_t kMaxInFeatures = 65535;
+// Knots per feature row at the limit (G + 2k + 1).
+constexpr int kMaxKnots = (int)kMaxDeg0Basis + 1;
+// Largest basis count R = G + k under the limit (k = 1, G = 69).
+constexpr int kMaxR = 70;
+
+// Records a formatted message as this thread's last error and returns code.
+int set_error(int code, const char* fmt, ...);
+// Checks hipGetLastError() after a launch; records and returns KAN_ERR_HIP.
+int check_launch(const char* what);
+// Number of compute units of the current device (cached per device).
+int device_cu_count();
+
+__host__ __device__ inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+__host__ __device__ inline int64_t round_up(int64_t a, int64_t b) { return ceil_div(a, b) * b; }
+
+// Width of one augmented basis row [H(n, 0..I*R-1) | silu(x(n, 0..I-1))],
+// padded to a multiple of 4 elements so that rows start 16-byte aligned.
+inline int64_t aug_width(int64_t I, int64_t R, bool has_base) {
+  return round_up(I * R + (has_base ? I : 0), 4);
+}
+
+template <typename T>
+struct alignas(4 * sizeof(T)) Vec4 {
+  T v[4];
+};
+
+template <typename T>
+__device__ __forceinline__ T silu_of(T x) {
+  return x / (T(1) + exp(-x));
+}
+
+template <typename T>
+__device__ __forceinline__ T silu_grad_of(T x) {
+  const T sg = T(1) / (T(1) + exp(-x));
+  return sg * (T(1) + x * (T(1) - sg));
+}
+
+template <>
+__device__ __forceinline__ float silu_of<float>(float x) {
+  return x / (1.0f + expf(-x));
+}
+
+template <>
+__device__ __forceinline__ float silu_grad_of<float>(float x) {
+  const float sg = 1.0f / (1.0f + expf(-x));
+  return sg * (1.0f + x * (1.0f - sg));
+}
+
+// ---- launchers implemented in the .hip translation units -----------------
+
+template <typename T>
+int launch_basis(const T* x, const T* grid, T* out, int64_t ld_out, T* silu_out, int64_t n,
+                 int64_t I, int G, int k, int impl, hipStream_t st);
+
+template <typename T>
+int launch_basis_grad(const T* x, const T* grid, const T* gH, int64_t ld_g, const T* gbase,
+                      T* gx, int64_t n, int64_t I, int G, int k, int impl, hipStream_t st);
+
+template <typename T>
+int launch_pack_basis(const T* basis, const T* x, T* aug, int64_t ld_aug, int64_t n, int64_t I,
+                      int64_t R, bool has_base, hipStream_t st);
+
+template <typename T>
+int launch_build_waug(const T* sw, const T* scaler, const T* bw, T* waug, int64_t ld,
+                      int64_t O, int64_t I, int64_t R, hipStream_t st);
+
+template <typename T>
+int launch_param_grads(const T* part, int splits, int64_t split_stride, int64_t ld,
+                       const T* sw, const T* scaler, T* gsw, T* gscaler, T* gbw, int64_t O,
+                       int64_t I, int64_t R, hipStream_t st);
+
+enum GemmLayout {
+  kLayoutNT = 0,  // C[m,n] = sum_k A[m*lda+k] * B[n*ldb+k]
+  kLayoutTN = 1,  // C[m,n] = sum_k A[k*lda+m] * B[k*ldb+n]
+  kLayoutNN = 2,  // C[m,n] = sum_k A[m*lda+k] * B[k*ldb+n]
+};
+
+// C (+ split * split_stride) = partial product over the split's K range.
+template <typename T>
+int launch_gemm(int layout, int64_t M, int64_t N, int64_t K, const T* A, int64_t lda,
+                const T* B, int64_t ldb, T* C, int64_t ldc, int splits, int64_t split_stride,
+                hipStream_t st);
+
+// Split count the GEMM scheduler would choose for a problem (1 = no split).
+template <typename T>
+int gemm_pick_splits(int64_t M, int64_t N, int64_t K);
+
+template <typename T>
+int launch_edge_forward(const T* s, const T* H, const T* bw, const T* W, T* a, T* part,
+                        int splits, int64_t n, int64_t I, int64_t O, int64_t R, hipStream_t st);
+
+template <typename T>
+int launch_edge_backward(const T* ga, const T* s, const T* H, const T* bw, const T* W, T* ds,
+                         T* dH, T* dbw, T* dW, T* part, int splits, int64_t n, int64_t I,
+                         int64_t O, int64_t R, hipStream_t st);
+
+int edge_pick_splits(int64_t n, int64_t I, int64_t O);
+
+}  // namespace kan

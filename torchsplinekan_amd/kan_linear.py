@@ -1,0 +1,294 @@
+"""KANLinear: one B-spline KAN layer with a native gfx950 backend
+(mirrors spline_kan/kan_linear.py: same constructor, backend selection,
+attributes, forward, regularisation API and state_dict keys).
+
+Backend selection (kan_linear.py:127-150, 193-213 of the reference):
+  "auto"      native kernels for device inputs when the configuration is
+              supported (grid_size + 2*spline_order <= 71, in_features <= 65535);
+              the reference backend for CPU inputs and unsupported shapes.
+  "cuda"      native kernels; raises if the library is missing, the shape is
+              unsupported or the input is on the CPU.
+  "reference" the pure-PyTorch backend.
+One deliberate difference: with "auto", a device input on a supported shape
+raises RuntimeError when libkan_hip.so is not built, instead of silently
+running the pure-PyTorch path on the device.
+"""
+
+import copy
+from typing import Optional, Tuple
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from . import fused as _fused
+from .reference_backend import (
+    ReferenceKANLayer,
+    compute_basis,
+    edge_abs_mean_dense,
+    regularization_from_edge_means,
+)
+
+_C = _fused._C
+_CUDA_EXT_LOADED: bool = _C is not None
+
+REG_IMPLS = ("auto", "dense", "fused", "checkpoint")
+
+CUDA_MAX_DEG0_BASIS = int(getattr(_C, "CUDA_MAX_DEG0_BASIS", 71)) if _C is not None else 71
+CUDA_MAX_IN_FEATURES = int(getattr(_C, "CUDA_MAX_IN_FEATURES", 65535)) if _C is not None else 65535
+
+
+def native_config_supported(in_features: int, grid_size: int, spline_order: int) -> Tuple[bool, str]:
+    """(ok, reason): whether the native kernels accept a layer shape."""
+    if grid_size + 2 * spline_order > CUDA_MAX_DEG0_BASIS:
+        return False, (f"grid_size + 2*spline_order = {grid_size + 2 * spline_order} exceeds the "
+                       f"CUDA kernel limit of {CUDA_MAX_DEG0_BASIS}")
+    if in_features > CUDA_MAX_IN_FEATURES:
+        return False, (f"in_features = {in_features} exceeds the CUDA kernel limit of "
+                       f"{CUDA_MAX_IN_FEATURES}")
+    return True, ""
+
+
+class KANLinear(nn.Module):
+    """B-spline KAN layer.
+
+    Attributes: base_weight [O, I], spline_weight [O, I, G+k],
+    spline_scaler [O, I] (if enabled), grid buffer [I, G+2k+1].  The
+    parameters are owned by an inner ReferenceKANLayer (``_ref``) and
+    re-exposed here, so state_dicts carry both key sets, as the reference's.
+    """
+
+    def __init__(self, in_features: int, out_features: int, grid_size: int = 5,
+                 spline_order: int = 3, scale_noise: float = 0.1, scale_base: float = 1.0,
+                 scale_spline: float = 1.0, enable_standalone_scale_spline: bool = True,
+                 base_activation=nn.SiLU, grid_eps: float = 0.02,
+                 grid_range: Tuple[float, float] = (-1.0, 1.0), backend: str = "auto") -> None:
+        super().__init__()
+        if grid_size < 1:
+            raise ValueError(f"grid_size must be >= 1, got {grid_size}")
+        if spline_order not in (1, 2, 3):
+            raise ValueError(f"spline_order must be 1, 2, or 3, got {spline_order}")
+        if backend not in ("auto", "cuda", "reference"):
+            raise ValueError(f"backend must be 'auto', 'cuda', or 'reference', got {backend!r}")
+        native_ok, reason = native_config_supported(in_features, grid_size, spline_order)
+        if backend == "cuda":
+            if not _CUDA_EXT_LOADED:
+                raise RuntimeError(
+                    "backend='cuda' requested but the native extension (libkan_hip.so) could not "
+                    "be loaded.  Build it first (python -m torchsplinekan_amd.build_lib) or use "
+                    "backend='reference'.")
+            if not native_ok:
+                raise ValueError(
+                    f"backend='cuda' does not support this configuration: {reason}. "
+                    "Use backend='reference' (or 'auto', which falls back automatically).")
+            self._use_cuda = True
+        elif backend == "reference":
+            self._use_cuda = False
+        else:
+            self._use_cuda = _CUDA_EXT_LOADED and native_ok
+        self._native_ok = native_ok
+        self.backend = backend
+        self.last_backend: Optional[str] = None
+
+        self._ref = ReferenceKANLayer(
+            in_features=in_features, out_features=out_features, grid_size=grid_size,
+            spline_order=spline_order, scale_noise=scale_noise, scale_base=scale_base,
+            scale_spline=scale_spline,
+            enable_standalone_scale_spline=enable_standalone_scale_spline,
+            base_activation=base_activation, grid_eps=grid_eps, grid_range=grid_range)
+        self.base_weight = self._ref.base_weight
+        self.spline_weight = self._ref.spline_weight
+        if enable_standalone_scale_spline:
+            self.spline_scaler = self._ref.spline_scaler
+        self.register_buffer("grid", self._ref.grid)
+
+        self.in_features = in_features
+        self.out_features = out_features
+        self.grid_size = grid_size
+        self.spline_order = spline_order
+        self.enable_standalone_scale_spline = enable_standalone_scale_spline
+
+    # ------------------------------------------------------------------ backends
+
+    @property
+    def selected_backend(self) -> str:
+        """Backend used for device inputs: "cuda" (native) or "reference"."""
+        return "cuda" if self._use_cuda else "reference"
+
+    def backend_for(self, x: torch.Tensor) -> str:
+        """Backend that :meth:`forward` uses for input ``x``."""
+        if not self._use_cuda:
+            if (x.is_cuda and self.backend == "auto" and self._native_ok
+                    and not _CUDA_EXT_LOADED):
+                raise RuntimeError(
+                    "KANLinear(backend='auto') received a device tensor but libkan_hip.so is "
+                    "not built; build it (python -m torchsplinekan_amd.build_lib) or choose "
+                    "backend='reference' explicitly.")
+            return "reference"
+        if self.backend == "cuda" or x.is_cuda:
+            return "cuda"
+        return "reference"
+
+    @property
+    def _native_fuses_base(self) -> bool:
+        # The kernels fuse SiLU; other activations run in PyTorch.
+        return type(self._ref.base_activation) is nn.SiLU
+
+    # ------------------------------------------------------------------ forward
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        backend = self.backend_for(x)
+        self.last_backend = backend
+        if backend == "cuda":
+            return self._cuda_forward(x)
+        return self._ref(x)
+
+    def _cuda_forward(self, x: torch.Tensor) -> torch.Tensor:
+        if not x.is_cuda:
+            raise RuntimeError(
+                "KANLinear with backend='cuda' received a CPU tensor. Move the input and model "
+                "to a CUDA device, or use backend='reference'.")
+        lead = x.shape[:-1]
+        xf = x.reshape(-1, self.in_features)
+        has_scaler = self.enable_standalone_scale_spline
+        empty = xf.new_empty(0)
+        fuse_base = self._native_fuses_base
+        out = _C.kan_apply(xf, self.grid, self.base_weight if fuse_base else empty,
+                           self.spline_weight, self.spline_scaler if has_scaler else empty,
+                           self.spline_order, has_scaler)
+        if not fuse_base:
+            out = out + F.linear(self._ref.base_activation(xf), self.base_weight)
+        return out.reshape(lead + (self.out_features,))
+
+    # ------------------------------------------------------------------ grid update
+
+    def update_grid(self, x: torch.Tensor, margin: float = 0.01) -> None:
+        """Moves the knots to the data and refits spline_weight
+        (ReferenceKANLayer.update_grid), keeping the top-level grid in sync."""
+        self._ref.update_grid(x, margin=margin)
+        with torch.no_grad():
+            self.grid.copy_(self._ref.grid)
+
+    # ------------------------------------------------------------------ regularisation
+
+    def regularization_loss(self, reg_act: float = 1.0, reg_entropy: float = 1.0, *,
+                            x: Optional[torch.Tensor] = None, mode: str = "activation",
+                            reg_impl: str = "auto", chunk_size: int = 1024) -> torch.Tensor:
+        """Scalar regulariser: activation-based (KAN paper; needs x) or the legacy
+        coefficient-based penalty (spline_kan/kan_linear.py:275-334)."""
+        if mode not in ("activation", "coefficient"):
+            raise ValueError(f"mode must be 'activation' or 'coefficient', got {mode!r}")
+        if mode == "coefficient":
+            return self._ref.regularization_loss(regularize_activation=reg_act,
+                                                 regularize_entropy=reg_entropy,
+                                                 mode="coefficient")
+        if x is None:
+            return self._ref.regularization_loss(reg_act, reg_entropy, x=None)
+        xf = x.reshape(-1, self.in_features)
+        s = self._ref.base_activation(xf)
+        impl = self._resolve_reg_impl(reg_impl, xf)
+        H = self._basis(xf, impl)
+        a = self._edge_abs_mean(xf, s, H, self._ref.effective_spline_weight(), impl, chunk_size)
+        return regularization_from_edge_means(a, reg_act, reg_entropy)
+
+    def forward_with_regularization(self, x: torch.Tensor, reg_act: float = 1.0,
+                                    reg_entropy: float = 1.0, *, mode: str = "activation",
+                                    reg_impl: str = "auto", chunk_size: int = 1024
+                                    ) -> Tuple[torch.Tensor, torch.Tensor]:
+        """(self(x), self.regularization_loss(reg_act, reg_entropy, x=x)) with the
+        base activation and the basis evaluated once.  reg_impl: "auto" (fused
+        when the native kernels run this layer on this input, else dense),
+        "dense", "fused" (phi never stored) or "checkpoint" (chunked recompute)
+        (spline_kan/kan_linear.py:340-389)."""
+        if mode == "coefficient":
+            return self(x), self.regularization_loss(reg_act, reg_entropy, mode="coefficient")
+        if mode != "activation":
+            raise ValueError(f"mode must be 'activation' or 'coefficient', got {mode!r}")
+        lead = x.shape[:-1]
+        xf = x.reshape(-1, self.in_features)
+        impl = self._resolve_reg_impl(reg_impl, xf)
+        s = self._ref.base_activation(xf)
+        H = self._basis(xf, impl)
+        W = self._ref.effective_spline_weight()
+        B, R = xf.shape[0], self.grid_size + self.spline_order
+        y = F.linear(s, self.base_weight) + F.linear(H.reshape(B, self.in_features * R),
+                                                     W.reshape(self.out_features, -1))
+        self.last_backend = "cuda" if impl == "fused" else "reference"
+        a = self._edge_abs_mean(xf, s, H, W, impl, chunk_size)
+        reg = regularization_from_edge_means(a, reg_act, reg_entropy)
+        return y.reshape(lead + (self.out_features,)), reg
+
+    def _resolve_reg_impl(self, reg_impl: str, x_flat: torch.Tensor) -> str:
+        if reg_impl not in REG_IMPLS:
+            raise ValueError(f"reg_impl must be one of {REG_IMPLS}, got {reg_impl!r}")
+        native_ok = (_fused.HAS_FUSED_KERNELS and x_flat.is_cuda
+                     and self.backend_for(x_flat) == "cuda")
+        if reg_impl == "auto":
+            return "fused" if native_ok else "dense"
+        if reg_impl == "fused" and not native_ok:
+            raise RuntimeError(
+                "reg_impl='fused' needs the native CUDA kernels, a CUDA input and a layer "
+                "configuration supported by backend='cuda'.  Use reg_impl='dense' or "
+                "'checkpoint' instead.")
+        return reg_impl
+
+    def _basis(self, x_flat: torch.Tensor, impl: str) -> torch.Tensor:
+        if impl == "fused":
+            return _fused.native_basis(x_flat, self.grid, self.spline_order)
+        return compute_basis(x_flat, self.grid, self.spline_order)
+
+    def _edge_abs_mean(self, x_flat, s, H, W, impl, chunk_size):
+        if impl == "fused":
+            return _fused.edge_abs_mean(s, H, self.base_weight, W)
+        if impl == "checkpoint":
+            if chunk_size < 1:
+                raise ValueError(f"chunk_size must be >= 1, got {chunk_size}")
+            return _fused.edge_abs_mean_chunked(s, x_flat, self.grid, self.spline_order,
+                                                self.base_weight, W, chunk_size)
+        return edge_abs_mean_dense(s, H, self.base_weight, W)
+
+    @torch.no_grad()
+    def edge_l1(self, x: torch.Tensor) -> torch.Tensor:
+        """Per-edge L1 norm mean_n |phi_{o,i}(x_n)| -> [O, I] (no grad)."""
+        xf = x.reshape(-1, self.in_features)
+        impl = self._resolve_reg_impl("auto", xf)
+        s = self._ref.base_activation(xf)
+        H = self._basis(xf, impl)
+        return self._edge_abs_mean(xf, s, H, self._ref.effective_spline_weight(), impl, 1024)
+
+    # ------------------------------------------------------------------ copies
+
+    def make_like(self, in_features: Optional[int] = None, out_features: Optional[int] = None,
+                  grid_size: Optional[int] = None,
+                  enable_standalone_scale_spline: Optional[bool] = None) -> "KANLinear":
+        """Freshly initialised layer with this layer's hyper-parameters, dtype and device."""
+        ref = self._ref
+        return KANLinear(
+            self.in_features if in_features is None else in_features,
+            self.out_features if out_features is None else out_features,
+            grid_size=self.grid_size if grid_size is None else grid_size,
+            spline_order=self.spline_order, scale_noise=ref.scale_noise,
+            scale_base=ref.scale_base, scale_spline=ref.scale_spline,
+            enable_standalone_scale_spline=(self.enable_standalone_scale_spline
+                                            if enable_standalone_scale_spline is None
+                                            else enable_standalone_scale_spline),
+            base_activation=copy.deepcopy(ref.base_activation), grid_eps=ref.grid_eps,
+            grid_range=ref.grid_range, backend=self.backend,
+        ).to(device=self.grid.device, dtype=self.grid.dtype)
+
+    @torch.no_grad()
+    def _copy_grid_(self, grid: torch.Tensor) -> None:
+        # .to()/.double() re-create buffers per module: keep both grids in sync.
+        self.grid.copy_(grid)
+        self._ref.grid.copy_(grid)
+
+    def export_inference(self, requires_grad: bool = False) -> "KANLinear":
+        """Independent layer computing the same function with spline_scaler
+        folded into spline_weight (enable_standalone_scale_spline=False)."""
+        new = self.make_like(enable_standalone_scale_spline=False)
+        with torch.no_grad():
+            new.base_weight.copy_(self.base_weight)
+            new.spline_weight.copy_(self._ref.effective_spline_weight())
+            new._copy_grid_(self.grid)
+        new.requires_grad_(requires_grad)
+        return new.train(self.training and requires_grad)
