@@ -1,0 +1,238 @@
+#!/usr/bin/env python3
+"""Throughput benchmark of the KANLinear hot path on one MI355X.
+
+Workload (the metric's config): a single
+KANLinear(in=1024, out=1024, grid_size=10, spline_order=3) in fp32 on the
+native gfx950 backend, N = 65536 samples, x ~ U(-1, 1) with
+requires_grad=True, coef ~ N(0, 0.1), base_weight ~ U(+-1/32),
+scaler ~ U(0.5, 1.5), target ~ N(0, 1); one step is
+zero_grad -> forward -> MSE loss -> backward (dx, dcoef, dscaler, dbase_w),
+so three dense-equivalent contractions of 2*N*O*I*(R+1) flops each.
+Inputs are generated on the CPU with a seeded torch.Generator and moved to
+the device before timing starts.
+
+Prints one JSON line (the benchmark contract): whole-job samples/s, the
+roofline of the dominant kernel (the MFMA contraction, timed live with HIP
+events recorded by the library on the launch stream) and a CPU baseline
+(the numpy oracle on a bounded sample of the same workload, rank 0 only).
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c3|c3-nodx]
+"""
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+METRIC = "fwd+bwd samples/s, KANLinear 1024→1024 G10 k3 N=64K; % MFMA/HBM roofline"
+PEAK_FP32_MFMA_TFLOPS = 157.3
+PEAK_HBM_GBS = 8000.0
+
+
+def parse():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--workload", default="c3", choices=["c3", "c3-nodx"])
+    ap.add_argument("--n", type=int, default=65536, help="samples per step (default: config's 65536)")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0,
+                    help="target CPU time of the baseline sample")
+    return ap.parse_args()
+
+
+def make_inputs(N, I, O, G, k, seed=0):
+    """Seeded CPU draws in a fixed order: x, coef, base_weight, scaler, target."""
+    import torch
+    g = torch.Generator().manual_seed(seed)
+    x = torch.rand(N, I, generator=g) * 2 - 1
+    coef = torch.randn(O, I, G + k, generator=g) * 0.1
+    bw = (torch.rand(O, I, generator=g) * 2 - 1) / (I ** 0.5)
+    scaler = torch.rand(O, I, generator=g) + 0.5
+    target = torch.randn(N, O, generator=g)
+    return x, coef, bw, scaler, target
+
+
+def cpu_baseline(x, coef, bw, scaler, target, grid, k, need_dx, seconds):
+    """The numpy oracle (restatement of the reference CPU path: basis
+    recurrence, BLAS GEMMs, analytic backward) timed on this host on
+    consecutive 1024-row chunks of the same workload until `seconds` of work
+    are done; returns samples/s, BLAS threads and the sample description."""
+    import numpy as np
+    from oracle import kan_oracle as ko
+    try:
+        from threadpoolctl import threadpool_info
+        threads = max([p.get("num_threads", 1) for p in threadpool_info()
+                       if p.get("user_api") == "blas"] or [1])
+    except Exception:  # threadpoolctl missing: report the env setting
+        threads = int(os.environ.get("OMP_NUM_THREADS", "1"))
+    N, O = target.shape
+    gridn = grid.numpy()
+    sw, bwn, sc = coef.numpy(), bw.numpy(), scaler.numpy()
+    chunk = 1024
+    done, t_total = 0, 0.0
+    for n0 in range(0, N, chunk):
+        xs = x[n0:n0 + chunk].numpy()
+        ts = target[n0:n0 + chunk].numpy()
+        t0 = time.perf_counter()
+        y, H = ko.kan_forward(xs, gridn, bwn, sw, sc, k)
+        D = (np.float32(2.0) / np.float32(N * O)) * (y - ts)
+        if need_dx:
+            ko.kan_backward(D, xs, gridn, bwn, sw, sc, k, basis=H)
+        else:
+            ko.kan_backward_params(D, xs, bwn, sw, sc, H)
+        t_total += time.perf_counter() - t0
+        done += xs.shape[0]
+        if t_total >= seconds:
+            break
+    return {
+        "value": done / t_total,
+        "unit": "samples/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"numpy oracle (oracle/kan_oracle.py) fp32 fwd+MSE+bwd of the first {done} of "
+                   f"{N} rows in {chunk}-row chunks, {t_total:.1f} s; BLAS threads={threads}, "
+                   f"elementwise work single-threaded; host {os.cpu_count()} logical CPUs"),
+    }
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
+              "(the sample axis would shard over GPUs with one all-reduce of the parameter "
+              "gradients; see DESIGN.md)", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    import torch.nn.functional as F
+    from torchsplinekan_amd import KANLinear, _lib
+
+    if not torch.cuda.is_available():
+        print("bench.py: no ROCm device visible", file=sys.stderr)
+        sys.exit(1)
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+
+    I = O = 1024
+    G, k = 10, 3
+    N = args.n
+    need_dx = args.workload == "c3"
+    x, coef, bw, scaler, target = make_inputs(N, I, O, G, k, seed=0)
+    L = KANLinear(I, O, grid_size=G, spline_order=k, backend="cuda")
+    with torch.no_grad():
+        L.spline_weight.copy_(coef)
+        L.base_weight.copy_(bw)
+        L.spline_scaler.copy_(scaler)
+    grid_cpu = L.grid.detach().clone()
+    L = L.to(dev)
+    xd = x.to(dev).requires_grad_(need_dx)
+    td = target.to(dev)
+    torch.cuda.synchronize()
+
+    def step():
+        for p in L.parameters():
+            p.grad = None
+        xd.grad = None
+        y = L(xd)
+        loss = F.mse_loss(y, td)
+        loss.backward()
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    assert L.last_backend == "cuda"
+
+    stream = torch.cuda.current_stream(dev)
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(args.steps)]
+    _lib.timing_enable(True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        ev[i][0].record(stream)
+        step()
+        ev[i][1].record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    step_ms = [a.elapsed_time(b) for a, b in ev]
+    kernels = {}
+    for cls in ("contraction", "basis", "basis_grad", "other"):
+        ms, cnt, work = _lib.timing_read(cls)
+        kernels[cls] = (ms, cnt, work)
+    _lib.timing_enable(False)
+
+    ms_per_step = wall * 1e3 / args.steps
+    value = N * args.steps / wall
+
+    c_ms, c_cnt, c_work = kernels["contraction"]
+    c_avg_ms = c_ms / max(c_cnt, 1)
+    c_flop = c_work / max(c_cnt, 1)
+    achieved = c_flop / (c_avg_ms * 1e-3) / 1e12 if c_cnt else 0.0
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", "contraction_c3_traffic.json")
+    if os.path.exists(tpath):
+        with open(tpath) as f:
+            traffic = json.load(f).get("hbm_bytes_per_launch")
+    b_ms, b_cnt, b_work = kernels["basis"]
+    g_ms, g_cnt, g_work = kernels["basis_grad"]
+
+    line = {
+        "metric": METRIC,
+        "value": value,
+        "unit": "samples/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded torch.Generator draws, random-init weights of the config)",
+        "config": {
+            "workload": ("c3: KANLinear(1024->1024, grid_size=10, spline_order=3) fp32, N=%d, "
+                         "fwd + MSE + bwd %s" % (N, "with dx (3 contractions)" if need_dx
+                                                 else "without dx (2 contractions)")),
+            "in_features": I, "out_features": O, "grid_size": G, "spline_order": k,
+            "samples_per_step": N, "x_requires_grad": need_dx,
+        },
+        "roofline": {
+            "bound": "mfma",
+            "kernel": "gemm_kernel (MFMA f32 16x16x4 contraction)",
+            "achieved": achieved,
+            "peak": PEAK_FP32_MFMA_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": achieved / PEAK_FP32_MFMA_TFLOPS,
+            "traffic": traffic,
+            "flop_per_launch": c_flop,
+            "avg_launch_ms": c_avg_ms,
+            "launches": c_cnt,
+        },
+        "step_ms_median_events": statistics.median(step_ms),
+        "kernels": {
+            "basis": {"avg_ms": b_ms / max(b_cnt, 1), "launches": b_cnt,
+                      "GB/s": (b_work / max(b_cnt, 1)) / (b_ms / max(b_cnt, 1) * 1e-3) / 1e9
+                      if b_cnt else None},
+            "basis_grad": {"avg_ms": g_ms / max(g_cnt, 1), "launches": g_cnt,
+                           "GB/s": (g_work / max(g_cnt, 1)) / (g_ms / max(g_cnt, 1) * 1e-3) / 1e9
+                           if g_cnt else None},
+            "contraction_ms_per_step": c_ms / args.steps,
+            "other_ms_per_step": kernels["other"][0] / args.steps,
+        },
+    }
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = cpu_baseline(x, coef, bw, scaler, target, grid_cpu, k, need_dx,
+                                            args.cpu_seconds)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

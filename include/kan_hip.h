@@ -139,6 +139,20 @@ int kan_hip_edge_abs_mean_backward(int dtype, const void* grad_a, const void* s,
                                    size_t workspace_bytes, int64_t n, int64_t in_features,
                                    int64_t out_features, int64_t num_basis, void* stream);
 
+/* Kernel-level timing (measurement support; no counterpart in the
+ * reference, whose benchmarks time with torch.profiler,
+ * benchmarks/bench_kan.py:288-301).  kan_hip_timing_enable(1) clears the
+ * record and starts recording a HIP-event pair around every kernel launch
+ * the library makes, on the launch's own stream, together with the launch's
+ * algorithmic work; kan_hip_timing_enable(0) clears and stops.
+ * kan_hip_timing_read waits for the recorded events of one kernel class and
+ * returns the summed duration (ms), the launch count and the summed work
+ * (flops for class 0, bytes for classes 1-2, flops for classes 3-4).
+ * Classes: 0 contraction GEMM, 1 basis, 2 basis_grad, 3 edge statistic,
+ * 4 edge statistic backward, 5 packing/finalize. */
+int kan_hip_timing_enable(int on);
+int kan_hip_timing_read(int kernel_class, double* total_ms, int64_t* launches, double* work);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,386 @@
+"""CPU oracle for the KANLinear hot path -- TEST INFRASTRUCTURE ONLY.
+
+This module restates, in numpy, the arithmetic of torch-spline-kan's
+KANLinear path (B-spline basis, its derivative, the SiLU + spline forward,
+the analytic first-order backward, the fused mean|phi| edge statistic and
+the entropy regulariser).  It is the checker the GPU kernels are compared
+with; it is never the thing measured or shipped.  Only ``tests/``,
+``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of ``bench.py`` may
+import it.  The product path (``torchsplinekan_amd``) never imports it.
+
+Each function cites the reference file:line it follows (paths relative to
+the torch-spline-kan source tree).  Every function computes in the dtype of
+its inputs (float32 or float64) with the same elementwise operation order
+as the reference, so float64 calls are the high-precision truth and float32
+calls reproduce the reference backend's rounding of elementwise work.
+
+How each function is pinned (tests/test_oracle.py):
+  basis_dense       exact rational Cox-de Boor (fractions.Fraction) on small
+                    grids; closed-form uniform B-splines for k = 1, 2, 3;
+                    partition of unity, non-negativity, support, zeros out
+                    of range; golden vectors written by the reference's own
+                    compute_basis (tests/golden/).
+  basis_local       agreement with basis_dense to 1e-13 in float64 over
+                    uniform, nonuniform and repeated-knot grids, including
+                    points on every knot and out of range.
+  basis_derivative  central finite differences of basis_dense in float64
+                    away from knots; exact cubic reproduction (x^3 - x).
+  kan_forward       brute-force per-(n,o) loop over the definition.
+  kan_backward      finite differences of kan_forward (all four gradients).
+  edge_abs_mean     brute-force per-(n,o,i) loop; golden vectors.
+  edge_abs_mean_backward
+                    finite differences of edge_abs_mean away from phi = 0.
+  regularization_from_edge_means (+ _grad)
+                    closed form on hand-computed inputs; finite differences;
+                    all-zero layer gives 0 with a finite zero gradient.
+"""
+
+from fractions import Fraction
+
+import numpy as np
+
+__all__ = [
+    "uniform_grid",
+    "basis_dense",
+    "basis_local",
+    "basis_derivative",
+    "silu",
+    "silu_grad",
+    "kan_forward",
+    "kan_backward",
+    "kan_backward_params",
+    "edge_abs_mean",
+    "edge_abs_mean_backward",
+    "regularization_from_edge_means",
+    "regularization_grad",
+    "basis_fraction",
+]
+
+
+# ---------------------------------------------------------------------------
+# knots
+# ---------------------------------------------------------------------------
+
+def uniform_grid(in_features, grid_size, spline_order, lo=-1.0, hi=1.0, dtype=np.float64):
+    """Extended uniform knot rows [I, G+2k+1]: t_r = lo + ((r - k)(hi - lo))/G,
+    evaluated in float32 in that order and then cast, as the reference builds
+    the grid buffer (_build_uniform_grid, spline_kan/reference_backend.py:327-332)."""
+    G, k = grid_size, spline_order
+    r = np.arange(G + 2 * k + 1, dtype=np.float32)
+    row = np.float32(lo) + ((r - np.float32(k)) * np.float32(hi - lo)) / np.float32(G)
+    return np.repeat(row[None, :], in_features, axis=0).astype(dtype)
+
+
+# ---------------------------------------------------------------------------
+# basis
+# ---------------------------------------------------------------------------
+
+def _guarded_div(num, den):
+    """num / den where den != 0, else 0 (den broadcast against num)."""
+    nz = den != 0
+    safe = np.where(nz, den, np.ones_like(den))
+    return np.where(nz, num / safe, np.zeros_like(num))
+
+
+def basis_dense(x, grid, k, chunk=1 << 14):
+    """B-spline basis [N, I, G+k] by the dense Cox-de Boor recurrence.
+
+    Follows compute_basis, spline_kan/reference_backend.py:62-94:
+    degree 0 is the half-open indicator [t_r, t_{r+1}) with the last interval
+    closed on the right; level d combines alpha*B_r + beta*B_{r+1} with
+    alpha = (x - t_r)/(t_{r+d} - t_r), beta = (t_{r+d+1} - x)/(t_{r+d+1} - t_{r+1}),
+    a zero denominator giving a zero coefficient.  The elementwise operation
+    order is the reference's, so results carry its rounding in the input
+    dtype.  Processed in sample chunks to bound memory.
+    """
+    x = np.asarray(x)
+    grid = np.asarray(grid)
+    dt = x.dtype
+    N, I = x.shape
+    nk = grid.shape[1]
+    R = nk - k - 1
+    out = np.empty((N, I, R), dtype=dt)
+    t = grid[None, :, :].astype(dt)
+    tl, tr = t[:, :, :-1], t[:, :, 1:]
+    for n0 in range(0, N, chunk):
+        xe = x[n0:n0 + chunk, :, None]
+        b = ((xe >= tl) & (xe < tr)).astype(dt)
+        last = ((xe >= tl[:, :, -1:]) & (xe <= tr[:, :, -1:])).astype(dt)
+        b = np.concatenate([b[:, :, :-1], last], axis=-1)
+        for d in range(1, k + 1):
+            n = b.shape[-1] - 1
+            t0, td = t[:, :, :n], t[:, :, d:d + n]
+            t1, td1 = t[:, :, 1:1 + n], t[:, :, d + 1:d + 1 + n]
+            den_l = td - t0
+            den_r = td1 - t1
+            alpha = _guarded_div(xe - t0, np.broadcast_to(den_l, (xe.shape[0],) + den_l.shape[1:]))
+            beta = _guarded_div(td1 - xe, np.broadcast_to(den_r, (xe.shape[0],) + den_r.shape[1:]))
+            b = alpha * b[:, :, :n] + beta * b[:, :, 1:n + 1]
+        out[n0:n0 + chunk] = b
+    return out
+
+
+def _find_span(t, x):
+    """Span m with t[m] <= x < t[m+1]; x == t[-1] gives the last span of
+    non-zero length; -1 for x outside [t[0], t[-1]] or NaN.
+    Follows find_span, csrc/kan_cuda.cu:207-221."""
+    nk = len(t)
+    if not (x >= t[0]) or x > t[nk - 1]:
+        return -1
+    if x == t[nk - 1]:
+        m = nk - 2
+        while m > 0 and t[m] == t[nk - 1]:
+            m -= 1
+        return m
+    lo, hi = 0, nk - 1
+    while hi - lo > 1:
+        mid = (lo + hi) >> 1
+        if t[mid] <= x:
+            lo = mid
+        else:
+            hi = mid
+    return lo
+
+
+def _local_values(t, m, x, deg):
+    """The deg+1 functions B_{m-deg+j, deg}(x), j = 0..deg, by the triangular
+    scheme of Piegl & Tiller (The NURBS Book, algorithm A2.2) with clamped knot
+    reads and zero-denominator guards.  Follows local_basis,
+    csrc/kan_cuda.cu:230-271."""
+    nk = len(t)
+    dt = type(x)
+
+    def T(idx):
+        return t[0 if idx < 0 else (nk - 1 if idx > nk - 1 else idx)]
+
+    v = [dt(1)] + [dt(0)] * deg
+    for d in range(1, deg + 1):
+        saved = dt(0)
+        for j in range(d):
+            rgt = T(m + j + 1) - x
+            lft = x - T(m + 1 - d + j)
+            dd = rgt + lft
+            tmp = v[j] / dd if dd != 0 else dt(0)
+            v[j] = saved + rgt * tmp
+            saved = lft * tmp
+        v[d] = saved
+    return v
+
+
+def basis_local(x, grid, k):
+    """B-spline basis [N, I, G+k] from the span search plus the k+1 active
+    values (csrc/kan_cuda.cu:207-312), zero rows out of range and for NaN.
+    Scalar loops: for small inputs only."""
+    x = np.asarray(x)
+    grid = np.asarray(grid).astype(x.dtype)
+    N, I = x.shape
+    nk = grid.shape[1]
+    R = nk - k - 1
+    out = np.zeros((N, I, R), dtype=x.dtype)
+    for n in range(N):
+        for i in range(I):
+            t = grid[i]
+            xv = x[n, i]
+            m = _find_span(t, xv)
+            if m < 0:
+                continue
+            v = _local_values(t, m, xv, k)
+            for j in range(k + 1):
+                r = m - k + j
+                if 0 <= r < R:
+                    out[n, i, r] = v[j]
+    return out
+
+
+def basis_derivative(x, grid, k, chunk=1 << 14):
+    """dB_{r,k}/dx [N, I, G+k] = k (B_{r,k-1}/(t_{r+k}-t_r) - B_{r+1,k-1}/(t_{r+k+1}-t_{r+1})),
+    zero-denominator terms dropped.  Follows compute_basis_derivative,
+    spline_kan/reference_backend.py:99-125 (and csrc/kan_cpu.cpp:88-131)."""
+    x = np.asarray(x)
+    dt = x.dtype
+    grid = np.asarray(grid).astype(dt)
+    nk = grid.shape[1]
+    R = nk - k - 1
+    lower = basis_dense(x, grid, k - 1, chunk=chunk)
+    t = grid[None]
+    d1 = t[:, :, k:k + R] - t[:, :, :R]
+    d2 = t[:, :, k + 1:k + 1 + R] - t[:, :, 1:1 + R]
+    shp = (x.shape[0],) + d1.shape[1:]
+    term1 = _guarded_div(lower[:, :, :R], np.broadcast_to(d1, shp))
+    term2 = _guarded_div(lower[:, :, 1:R + 1], np.broadcast_to(d2, shp))
+    return dt.type(k) * (term1 - term2)
+
+
+def basis_fraction(xv, knots, k):
+    """Exact rational B-spline values [B_{0,k}(x) .. B_{R-1,k}(x)] of one
+    point on one knot row by the Cox-de Boor definition (degree 0 half-open,
+    last interval closed; zero denominators give zero).  Brute force on
+    fractions.Fraction, used to pin basis_dense."""
+    xv = Fraction(xv)
+    t = [Fraction(v) for v in knots]
+    n0 = len(t) - 1
+    b = []
+    for r in range(n0):
+        inside = t[r] <= xv < t[r + 1]
+        if r == n0 - 1:
+            inside = t[r] <= xv <= t[r + 1]
+        b.append(Fraction(1) if inside else Fraction(0))
+    for d in range(1, k + 1):
+        nb = []
+        for r in range(len(b) - 1):
+            dl = t[r + d] - t[r]
+            dr = t[r + d + 1] - t[r + 1]
+            a = (xv - t[r]) / dl if dl != 0 else Fraction(0)
+            c = (t[r + d + 1] - xv) / dr if dr != 0 else Fraction(0)
+            nb.append(a * b[r] + c * b[r + 1])
+        b = nb
+    return b
+
+
+# ---------------------------------------------------------------------------
+# forward / backward
+# ---------------------------------------------------------------------------
+
+def silu(x):
+    """x * sigmoid(x) = x / (1 + exp(-x))."""
+    return x / (x.dtype.type(1) + np.exp(-x))
+
+
+def silu_grad(x):
+    """d silu/dx = sigma(x) (1 + x (1 - sigma(x))) (csrc/kan_cpu.cpp:245-246)."""
+    one = x.dtype.type(1)
+    sg = one / (one + np.exp(-x))
+    return sg * (one + x * (one - sg))
+
+
+def _eff_weight(sw, scaler):
+    return sw if scaler is None else sw * scaler[:, :, None]
+
+
+def kan_forward(x, grid, base_weight, spline_weight, spline_scaler, k, basis=None):
+    """(y [N, O], H [N, I, R]) with
+    y = silu(x) base_weight^T + H (spline_weight * spline_scaler)^T.
+    base_weight None: no base branch; spline_scaler None: no scaler.
+    Follows kan_forward_cpu, csrc/kan_cpu.cpp:136-188."""
+    N, I = x.shape
+    O, _, R = spline_weight.shape
+    H = basis_dense(x, grid, k) if basis is None else basis
+    W = _eff_weight(spline_weight, spline_scaler)
+    y = H.reshape(N, I * R) @ W.reshape(O, I * R).T
+    if base_weight is not None:
+        y = silu(x) @ base_weight.T + y
+    return y, H
+
+
+def kan_backward(D, x, grid, base_weight, spline_weight, spline_scaler, k, basis=None):
+    """Analytic first-order backward -> (gx, gbw | None, gsw, gscaler | None):
+      gbw     = D^T silu(x)
+      DtH     = D^T H;  gsw = scaler * DtH;  gscaler = sum_r sw * DtH
+      gx      = sum_r (D W)[n,i,r] dB_r/dx(x[n,i]) + (D bw) * silu'(x)
+    Follows kan_backward_cpu, csrc/kan_cpu.cpp:193-290."""
+    N, I = x.shape
+    O, _, R = spline_weight.shape
+    H = basis_dense(x, grid, k) if basis is None else basis
+    gbw = D.T @ silu(x) if base_weight is not None else None
+    DtH = (D.T @ H.reshape(N, I * R)).reshape(O, I, R)
+    if spline_scaler is not None:
+        gsw = spline_scaler[:, :, None] * DtH
+        gsc = (spline_weight * DtH).sum(axis=2)
+    else:
+        gsw, gsc = DtH, None
+    W = _eff_weight(spline_weight, spline_scaler)
+    DW = (D @ W.reshape(O, I * R)).reshape(N, I, R)
+    gx = (DW * basis_derivative(x, grid, k)).sum(axis=2)
+    if base_weight is not None:
+        gx = gx + (D @ base_weight) * silu_grad(x)
+    return gx, gbw, gsw, gsc
+
+
+def kan_backward_params(D, x, base_weight, spline_weight, spline_scaler, basis):
+    """Parameter gradients only (x without requires_grad) ->
+    (gbw | None, gsw, gscaler | None), the same formulas as kan_backward
+    (csrc/kan_cpu.cpp:219-241)."""
+    N, I = x.shape
+    O, _, R = spline_weight.shape
+    gbw = D.T @ silu(x) if base_weight is not None else None
+    DtH = (D.T @ basis.reshape(N, I * R)).reshape(O, I, R)
+    if spline_scaler is not None:
+        return gbw, spline_scaler[:, :, None] * DtH, (spline_weight * DtH).sum(axis=2)
+    return gbw, DtH, None
+
+
+# ---------------------------------------------------------------------------
+# edge statistic and regulariser
+# ---------------------------------------------------------------------------
+
+def _phi_chunk(s, H, bw, W):
+    """phi [n, O, I] = s[n,i] bw[o,i] + sum_r H[n,i,r] W[o,i,r] for a sample chunk."""
+    phi = np.einsum("nir,oir->noi", H, W, optimize=True)
+    if bw is not None:
+        phi = s[:, None, :] * bw[None, :, :] + phi
+    return phi
+
+
+def edge_abs_mean(s, H, bw, W, chunk=256):
+    """a[o,i] = (1/N) sum_n |s[n,i] bw[o,i] + sum_r H[n,i,r] W[o,i,r]| [O, I],
+    chunked over samples (s, bw None: no base branch).  Follows
+    edge_abs_mean_dense, spline_kan/reference_backend.py:128-146, and the
+    statistic of csrc/kan_reg_cuda.cu:1-10."""
+    N = H.shape[0]
+    acc = np.zeros(W.shape[:2], dtype=np.float64 if H.dtype == np.float64 else H.dtype)
+    for n0 in range(0, N, chunk):
+        sc = s[n0:n0 + chunk] if s is not None else None
+        acc += np.abs(_phi_chunk(sc, H[n0:n0 + chunk], bw, W)).sum(axis=0)
+    return acc / H.dtype.type(N)
+
+
+def edge_abs_mean_backward(ga, s, H, bw, W, chunk=256):
+    """Gradients of edge_abs_mean given grad_a [O, I] -> (ds | None, dH, dbw | None, dW),
+    with g[n,o,i] = ga[o,i] sign(phi[n,o,i]) / N and sign(0) = 0:
+      ds = sum_o g bw,  dH = sum_o g W,  dbw = sum_n g s,  dW = sum_n g H.
+    Follows csrc/kan_reg_cuda.cu:25-28, 81-107 and 113-176."""
+    N = H.shape[0]
+    dt = H.dtype
+    inv_n = dt.type(1) / dt.type(N)
+    dH = np.empty_like(H)
+    ds = np.empty_like(s) if s is not None else None
+    dW = np.zeros_like(W)
+    dbw = np.zeros_like(bw) if bw is not None else None
+    for n0 in range(0, N, chunk):
+        sc = s[n0:n0 + chunk] if s is not None else None
+        Hc = H[n0:n0 + chunk]
+        g = np.sign(_phi_chunk(sc, Hc, bw, W)) * (ga * inv_n)[None]
+        dH[n0:n0 + chunk] = np.einsum("noi,oir->nir", g, W, optimize=True)
+        dW += np.einsum("noi,nir->oir", g, Hc, optimize=True)
+        if bw is not None:
+            ds[n0:n0 + chunk] = (g * bw[None]).sum(axis=1)
+            dbw += (g * sc[:, None, :]).sum(axis=0)
+    return ds, dH, dbw, dW
+
+
+def regularization_from_edge_means(a, reg_act, reg_entropy):
+    """mu1 * A + mu2 * S with A = sum a, p = max(a / max(A, tiny), tiny),
+    S = -sum p log p; tiny = smallest normal number of a's dtype.
+    Follows spline_kan/reference_backend.py:149-170."""
+    tiny = np.finfo(a.dtype).tiny
+    A = a.sum()
+    p = np.maximum(a / max(A, tiny), tiny)
+    S = -(p * np.log(p)).sum()
+    return reg_act * A + reg_entropy * S
+
+
+def regularization_grad(a, reg_act, reg_entropy):
+    """d(regularization_from_edge_means)/da [O, I], the derivative of the
+    clamped formula (clamp passes gradient only where it is inactive)."""
+    tiny = np.finfo(a.dtype).tiny
+    A = a.sum()
+    A_safe = max(A, tiny)
+    q = a / A_safe
+    p = np.maximum(q, tiny)
+    dS_dp = -(np.log(p) + 1.0)
+    dS_dq = np.where(q >= tiny, dS_dp, 0.0)
+    # q = a / A_safe: dq_j/da_i = delta_ij / A_safe - a_j / A_safe^2 (when A > tiny)
+    g = dS_dq / A_safe
+    if A > tiny:
+        g = g - (dS_dq * a).sum() / (A_safe * A_safe)
+    return reg_act * np.ones_like(a) + reg_entropy * g

@@ -1,0 +1,106 @@
+"""CPU checks of the C-ABI library (no kernel launches): libkan_hip.so loads,
+exports every entry point include/kan_hip.h declares, and its host-side
+validation returns the documented status codes and messages before any
+launch (csrc/kan_ops.h:27-78 of the reference for the limits and texts)."""
+
+import ctypes
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "kan_hip.h")
+
+
+def _declared():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(kan_hip_\w+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from torchsplinekan_amd import _lib
+    return _lib
+
+
+def test_library_exports_every_declared_symbol(lib):
+    names = _declared()
+    assert len(names) >= 15
+    raw = ctypes.CDLL(lib.LIB_PATH)
+    for n in names:
+        assert hasattr(raw, n), n
+    # and the Python binding types every one of them
+    assert set(names) <= set(lib.SIGNATURES)
+
+
+def test_limits(lib):
+    assert lib.limits() == (71, 65535)
+    from torchsplinekan_amd import _C
+    assert _C.CUDA_MAX_DEG0_BASIS == 71 and _C.CUDA_MAX_IN_FEATURES == 65535
+    assert _C.HAS_FUSED_KERNELS is True
+
+
+def test_basis_impl_switch(lib):
+    L = lib.LIB
+    assert L.kan_hip_get_basis_impl() == 1
+    assert L.kan_hip_set_basis_impl(7) == lib.KAN_ERR_INVALID
+    assert "basis impl must be 0" in lib.last_error()
+    assert L.kan_hip_set_basis_impl(0) == lib.KAN_OK
+    assert L.kan_hip_get_basis_impl() == 0
+    assert L.kan_hip_set_basis_impl(1) == lib.KAN_OK
+
+
+def test_validation_before_launch(lib):
+    L = lib.LIB
+    # unsupported dtype code
+    assert L.kan_hip_basis(7, None, None, None, 4, 4, 5, 3, None) == lib.KAN_ERR_INVALID
+    assert "FP32 and FP64" in lib.last_error()
+    # grid beyond the kernel limit: G + 2k = 72
+    assert L.kan_hip_basis(0, None, None, None, 4, 4, 66, 3, None) == lib.KAN_ERR_LIMIT
+    assert "G + 2k <= 71" in lib.last_error()
+    # in_features beyond the limit
+    assert L.kan_hip_forward(0, None, None, None, None, None, None, None, None,
+                             4, 65536, 4, 5, 3, None) == lib.KAN_ERR_LIMIT
+    assert "in_features <= 65535" in lib.last_error()
+    # spline order
+    assert L.kan_hip_basis(0, None, None, None, 4, 4, 5, 4, None) == lib.KAN_ERR_INVALID
+    # null pointers of non-empty buffers
+    assert L.kan_hip_basis(0, None, None, None, 4, 4, 5, 3, None) == lib.KAN_ERR_INVALID
+    assert "must not be NULL" in lib.last_error()
+    # edge statistic: R beyond 72, and s without base_weight
+    assert L.kan_hip_edge_abs_mean(0, None, 1, None, 1, 1, None, 0, 4, 4, 4, 73,
+                                   None) == lib.KAN_ERR_LIMIT
+    assert L.kan_hip_edge_abs_mean(0, 1, 1, None, 1, 1, None, 0, 4, 4, 4, 8,
+                                   None) == lib.KAN_ERR_INVALID
+    # a gradient that needs an absent operand
+    assert L.kan_hip_backward(0, None, None, None, None, None, None, None, None, 1, None, None,
+                              None, 0, 4, 4, 4, 5, 3, None) == lib.KAN_ERR_INVALID
+    assert "without base_weight" in lib.last_error()
+    # timing class
+    assert L.kan_hip_timing_read(9, None, None, None) == lib.KAN_ERR_INVALID
+
+
+def test_aug_width(lib):
+    L = lib.LIB
+    # [H | silu(x)] row padded to a multiple of 4 elements
+    assert L.kan_hip_aug_width(1024, 10, 3, 1) == 1024 * 13 + 1024
+    assert L.kan_hip_aug_width(16, 5, 3, 1) == 16 * 8 + 16
+    assert L.kan_hip_aug_width(3, 4, 1, 0) == 16      # 15 -> 16
+    assert L.kan_hip_aug_width(3, 0, 1, 0) == -1
+
+
+def test_c_header_compiles_as_c(tmp_path):
+    """The header is plain C (no C++ or torch types in the signatures)."""
+    import shutil
+    import subprocess
+    gcc = shutil.which("gcc")
+    if gcc is None:
+        pytest.skip("gcc not available")
+    src = tmp_path / "t.c"
+    src.write_text('#include "kan_hip.h"\nint main(void){return KAN_OK;}\n')
+    r = subprocess.run([gcc, "-std=c99", "-Wall", "-Werror", "-I", os.path.dirname(HEADER),
+                        "-c", str(src), "-o", str(tmp_path / "t.o")], capture_output=True,
+                       text=True)
+    assert r.returncode == 0, r.stderr

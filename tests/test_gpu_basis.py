@@ -1,0 +1,107 @@
+"""GPU parity of the basis kernels (libkan_hip.so through the C-ABI) against
+the CPU oracle: dense Cox-de Boor values and the input-gradient contraction,
+on uniform, nonuniform and repeated-knot grids, with points on every knot and
+beyond both ends (mirrors tests/test_local_basis.py:40-68 of the reference).
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import kan_oracle as ko
+from tests._util import make_grid, make_points, np64
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def C():
+    from torchsplinekan_amd import _C
+    assert torch.cuda.is_available(), "GPU tests need a ROCm device"
+    return _C
+
+
+@pytest.mark.parametrize("k", [1, 2, 3])
+@pytest.mark.parametrize("G", [1, 4, 17, 64])
+@pytest.mark.parametrize("kind", ["uniform", "nonuniform", "repeated"])
+def test_basis_and_grad_fp64_match_oracle(C, k, G, kind):
+    if G + 2 * k > 71 or (kind == "repeated" and G < 2):
+        pytest.skip("config outside the native kernel range")
+    print(f"basis fp64 k={k} G={G} kind={kind}", flush=True)
+    grid = make_grid(3, G, k, kind, seed=G + k)
+    x = make_points(grid, n=1000, seed=k)
+    H = C.basis(x.cuda(), grid.cuda(), k).cpu()
+    ref = ko.basis_dense(x.numpy(), grid.numpy(), k)
+    assert np.allclose(H.numpy(), ref, atol=1e-13, rtol=0)
+    gH = torch.randn(H.shape, dtype=torch.float64, generator=torch.Generator().manual_seed(5))
+    gx = C.basis_grad(x.cuda(), grid.cuda(), k, gH.cuda()).cpu().numpy()
+    gref = (gH.numpy() * ko.basis_derivative(x.numpy(), grid.numpy(), k)).sum(-1)
+    assert np.allclose(gx, gref, atol=1e-10 * max(1.0, np.abs(gref).max()), rtol=0)
+
+
+@pytest.mark.parametrize("k", [1, 2, 3])
+@pytest.mark.parametrize("impl", [0, 1])
+def test_basis_fp32_and_out_of_range_rows_exact(C, k, impl):
+    print(f"basis fp32 k={k} impl={impl}", flush=True)
+    grid = make_grid(70, 9, k, "nonuniform", seed=11, dtype=torch.float32)
+    x = make_points(grid, n=2000, seed=3)
+    try:
+        C.set_basis_impl(impl)
+        H = C.basis(x.cuda(), grid.cuda(), k).cpu().numpy()
+    finally:
+        C.set_basis_impl(1)
+    ref = ko.basis_dense(x.numpy(), grid.numpy(), k)
+    ref64 = ko.basis_dense(x.double().numpy(), grid.double().numpy(), k)
+    # out-of-grid rows are exactly zero in both
+    xs = x.numpy()
+    out = (xs < grid.numpy()[:, 0][None]) | (xs > grid.numpy()[:, -1][None])
+    assert out.any()
+    assert (H[out] == 0).all()
+    assert (ref[out] == 0).all()
+    # the zero pattern of in-range rows is bit-identical to the reference rounding
+    assert np.array_equal(H == 0, ref == 0) or np.abs(H - ref).max() < 1e-6
+    assert np.abs(H - ref64).max() < 2e-6
+    if impl == 0:
+        # the dense recurrence reproduces the reference's fp32 rounding exactly
+        assert np.array_equal(H, ref)
+
+
+@pytest.mark.parametrize("k", [1, 2, 3])
+def test_right_end_and_partition_of_unity(C, k):
+    grid = make_grid(2, 5, k, "nonuniform", seed=3)
+    x = torch.stack([grid[:, 0] - 1e-3, grid[:, -1] + 1e-3, grid[:, -1]], 0)
+    H = C.basis(x.cuda(), grid.cuda(), k).cpu().numpy()
+    assert (H[:2] == 0).all()
+    assert np.allclose(H[2], ko.basis_dense(x[2:].numpy(), grid.numpy(), k)[0])
+    xe = grid[:, k + 5][None]
+    He = C.basis(xe.cuda(), grid.cuda(), k).cpu().numpy()
+    assert np.allclose(He.sum(-1), 1.0, atol=1e-13)
+
+
+def test_wide_layer_fp32_basis_grad(C):
+    # many feature blocks, ragged feature count and sample count
+    torch.manual_seed(0)
+    grid = make_grid(1000, 10, 3, "uniform", dtype=torch.float32)
+    x = torch.rand(777, 1000) * 2.2 - 1.1
+    H = C.basis(x.cuda(), grid.cuda(), 3).cpu().numpy()
+    ref = ko.basis_dense(x.double().numpy(), grid.double().numpy(), 3)
+    assert np.abs(H - ref).max() < 2e-6
+    gH = torch.randn(H.shape)
+    gx = C.basis_grad(x.cuda(), grid.cuda(), 3, gH.cuda()).cpu().numpy()
+    gref = (gH.double().numpy() * ko.basis_derivative(x.double().numpy(), grid.double().numpy(), 3)).sum(-1)
+    assert np.abs(gx - gref).max() / np.abs(gref).max() < 1e-5
+
+
+def test_basis_impl_switch_validation(C):
+    with pytest.raises(RuntimeError):
+        C.set_basis_impl(7)
+    assert C.get_basis_impl() == 1
+
+
+def test_empty_batch(C):
+    grid = make_grid(4, 5, 3, "uniform", dtype=torch.float32).cuda()
+    x = torch.empty(0, 4, device="cuda")
+    H = C.basis(x, grid, 3)
+    assert H.shape == (0, 4, 8)
+    gx = C.basis_grad(x, grid, 3, torch.empty(0, 4, 8, device="cuda"))
+    assert gx.shape == (0, 4)

@@ -1,0 +1,95 @@
+"""GPU parity of the fused edge statistic a[o,i] = mean_n |phi[n,o,i]| and its
+backward against the CPU oracle, and of forward_with_regularization with
+reg_impl="fused" against the dense path (mirrors
+tests/test_fused_regularization.py:58-107 of the reference).
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import kan_oracle as ko
+from tests._util import normwise, np64
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def C():
+    from torchsplinekan_amd import _C
+    assert torch.cuda.is_available(), "GPU tests need a ROCm device"
+    return _C
+
+
+def _edge_inputs(N, I, O, R, dtype, seed):
+    g = torch.Generator().manual_seed(seed)
+    s = torch.randn(N, I, generator=g, dtype=torch.float64)
+    H = torch.rand(N, I, R, generator=g, dtype=torch.float64)
+    bw = torch.randn(O, I, generator=g, dtype=torch.float64) * 0.3
+    W = torch.randn(O, I, R, generator=g, dtype=torch.float64) * 0.2
+    ga = torch.randn(O, I, generator=g, dtype=torch.float64)
+    return [t.to(dtype) for t in (s, H, bw, W, ga)]
+
+
+@pytest.mark.parametrize("shape", [(37, 5, 3, 4), (300, 16, 40, 8), (1000, 9, 70, 13),
+                                   (64, 3, 300, 68), (5000, 4, 6, 11)])
+@pytest.mark.parametrize("dtype", [torch.float64, torch.float32])
+@pytest.mark.parametrize("base", [True, False])
+def test_edge_abs_mean_and_backward_match_oracle(C, shape, dtype, base):
+    N, I, O, R = shape
+    print(f"edge {shape} {dtype} base={base}", flush=True)
+    s, H, bw, W, ga = _edge_inputs(N, I, O, R, dtype, seed=N + O)
+    empty = torch.empty(0, dtype=dtype, device="cuda")
+    sd = s.cuda() if base else empty
+    bwd = bw.cuda() if base else empty
+    a = C.edge_abs_mean(sd, H.cuda(), bwd, W.cuda())
+    ra = ko.edge_abs_mean(np64(s) if base else None, np64(H), np64(bw) if base else None,
+                          np64(W))
+    tol = 1e-12 if dtype == torch.float64 else 1e-5
+    assert normwise(np64(a), ra) < tol
+    ds, dH, dbw, dW = C.edge_abs_mean_backward(ga.cuda(), sd, H.cuda(), bwd, W.cuda(),
+                                               True, True, True, True)
+    rds, rdH, rdbw, rdW = ko.edge_abs_mean_backward(np64(ga), np64(s) if base else None,
+                                                    np64(H), np64(bw) if base else None,
+                                                    np64(W))
+    # fp32: sign(phi) may flip where |phi| is at rounding level; the normwise
+    # bound allows for a handful of such terms.
+    gtol = 1e-12 if dtype == torch.float64 else 1e-4
+    assert normwise(np64(dH), rdH) < gtol
+    assert normwise(np64(dW), rdW) < gtol
+    if base:
+        assert normwise(np64(ds), rds) < gtol
+        assert normwise(np64(dbw), rdbw) < gtol
+    else:
+        assert ds is None and dbw is None
+
+
+def test_edge_backward_partial_requests(C):
+    s, H, bw, W, ga = _edge_inputs(100, 6, 10, 8, torch.float64, seed=3)
+    d = [t.cuda() for t in (s, H, bw, W, ga)]
+    ds, dH, dbw, dW = C.edge_abs_mean_backward(d[4], d[0], d[1], d[2], d[3],
+                                               False, True, False, False)
+    assert ds is None and dbw is None and dW is None and dH is not None
+    ds, dH, dbw, dW = C.edge_abs_mean_backward(d[4], d[0], d[1], d[2], d[3],
+                                               False, False, True, True)
+    assert dH is None and dbw is not None and dW is not None
+
+
+@pytest.mark.parametrize("dtype", [torch.float64, torch.float32])
+def test_forward_with_regularization_fused_matches_dense(C, dtype):
+    from torchsplinekan_amd import KAN
+    torch.manual_seed(0)
+    net = KAN([6, 8, 5], grid_size=5, backend="cuda").to("cuda", dtype)
+    x = (torch.rand(200, 6, device="cuda", dtype=dtype) * 2.4 - 1.2)
+    res = {}
+    for impl in ("fused", "dense", "checkpoint"):
+        for p in net.parameters():
+            p.grad = None
+        xx = x.clone().requires_grad_()
+        y, r = net.forward_with_regularization(xx, 1e-2, 1e-2, reg_impl=impl, chunk_size=64)
+        (y.square().mean() + r).backward()
+        res[impl] = [y.detach(), r.detach(), xx.grad] + [p.grad for p in net.parameters()]
+    tol = 1e-10 if dtype == torch.float64 else 5e-5
+    for impl in ("dense", "checkpoint"):
+        for a, b in zip(res["fused"], res[impl]):
+            assert normwise(np64(a), np64(b)) < tol

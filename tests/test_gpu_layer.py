@@ -1,0 +1,242 @@
+"""GPU parity of the KANLinear forward and first-order backward (fused SiLU +
+spline contraction on MFMA, parameter and input gradients) against the CPU
+oracle, through the raw ops, the autograd function and the module API.
+
+Tolerances: fp64 1e-12 on outputs and 1e-10 on gradients (the reference's
+own bars, tests/test_math_correctness.py:284-306); fp32 normwise relative
+error <= 1e-5 against the fp64 oracle, measured as
+max|u - v| / max|v| per tensor.
+"""
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import kan_oracle as ko
+from tests._util import make_grid, normwise, np64
+
+pytestmark = pytest.mark.gpu
+
+FP32_TOL = 1e-5
+
+
+@pytest.fixture(scope="module")
+def C():
+    from torchsplinekan_amd import _C
+    assert torch.cuda.is_available(), "GPU tests need a ROCm device"
+    return _C
+
+
+def _layer_inputs(N, I, O, G, k, dtype, seed=0, kind="uniform", scaler=True, base=True,
+                  xrange=1.0):
+    g = torch.Generator().manual_seed(seed)
+    grid = make_grid(I, G, k, kind, seed=seed, dtype=dtype)
+    x = (torch.rand(N, I, generator=g, dtype=torch.float64) * 2 - 1) * xrange
+    sw = torch.randn(O, I, G + k, generator=g, dtype=torch.float64) * 0.1
+    bw = (torch.rand(O, I, generator=g, dtype=torch.float64) * 2 - 1) / np.sqrt(I)
+    sc = torch.rand(O, I, generator=g, dtype=torch.float64) + 0.5
+    D = torch.randn(N, O, generator=g, dtype=torch.float64)
+    cast = lambda t: t.to(dtype)
+    return (cast(x), grid, cast(bw) if base else None, cast(sw), cast(sc) if scaler else None,
+            cast(D))
+
+
+def _oracle(x, grid, bw, sw, sc, D, k):
+    a = lambda t: None if t is None else np64(t)
+    y, H = ko.kan_forward(a(x), a(grid), a(bw), a(sw), a(sc), k)
+    gx, gbw, gsw, gsc = ko.kan_backward(a(D), a(x), a(grid), a(bw), a(sw), a(sc), k, basis=H)
+    return y, gx, gbw, gsw, gsc
+
+
+def _dev(t):
+    return None if t is None else t.cuda()
+
+
+CASES = [
+    # N, I, O, G, k, kind
+    (64, 16, 8, 5, 3, "uniform"),
+    (257, 33, 19, 7, 2, "nonuniform"),
+    (130, 70, 129, 4, 1, "repeated"),
+    (300, 128, 160, 10, 3, "uniform"),
+]
+
+
+@pytest.mark.parametrize("case", CASES)
+@pytest.mark.parametrize("dtype", [torch.float64, torch.float32])
+@pytest.mark.parametrize("variant", ["full", "no_scaler", "no_base"])
+def test_raw_forward_backward_match_oracle(C, case, dtype, variant):
+    N, I, O, G, k, kind = case
+    print(f"raw fwd/bwd {case} {dtype} {variant}", flush=True)
+    x, grid, bw, sw, sc, D = _layer_inputs(N, I, O, G, k, dtype, seed=N, kind=kind,
+                                           scaler=variant != "no_scaler",
+                                           base=variant != "no_base", xrange=1.1)
+    empty = torch.empty(0, dtype=dtype, device="cuda")
+    y, H = C.kan_forward(x.cuda(), grid.cuda(), bw.cuda() if bw is not None else empty,
+                         sw.cuda(), sc.cuda() if sc is not None else empty, k, sc is not None)
+    gx, gbw, gsw, gsc = C.kan_backward(D.cuda(), x.cuda(), grid.cuda(),
+                                       bw.cuda() if bw is not None else empty, sw.cuda(),
+                                       sc.cuda() if sc is not None else empty, H, k,
+                                       sc is not None)
+    ry, rgx, rgbw, rgsw, rgsc = _oracle(x, grid, bw, sw, sc, D, k)
+    assert H.shape == (N, I, G + k)
+    assert np.allclose(np64(H), ko.basis_dense(np64(x), np64(grid), k),
+                       atol=1e-13 if dtype == torch.float64 else 2e-6, rtol=0)
+    pairs = [(y, ry), (gx, rgx), (gsw, rgsw)]
+    if bw is not None:
+        pairs.append((gbw, rgbw))
+    else:
+        assert gbw is None
+    if sc is not None:
+        pairs.append((gsc, rgsc))
+    else:
+        assert gsc is None
+    for got, ref in pairs:
+        err = normwise(np64(got), ref)
+        if dtype == torch.float64:
+            assert err < 1e-12, err
+        else:
+            assert err < FP32_TOL, err
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
+def test_module_autograd_matches_oracle(C, dtype):
+    from torchsplinekan_amd import KANLinear
+    torch.manual_seed(0)
+    N, I, O, G, k = 200, 24, 12, 6, 3
+    L = KANLinear(I, O, grid_size=G, spline_order=k, backend="cuda").to("cuda", dtype)
+    with torch.no_grad():
+        L.spline_scaler.uniform_(0.5, 1.5)
+        L.spline_weight.normal_(0, 0.1)
+    x = (torch.rand(N, I, device="cuda", dtype=dtype) * 2.2 - 1.1).requires_grad_()
+    tgt = torch.randn(N, O, device="cuda", dtype=dtype)
+    y = L(x)
+    assert L.last_backend == "cuda"
+    loss = F.mse_loss(y, tgt)
+    loss.backward()
+    D = 2.0 * (np64(y) - np64(tgt)) / (N * O)
+    ry, H = ko.kan_forward(np64(x), np64(L.grid), np64(L.base_weight), np64(L.spline_weight),
+                           np64(L.spline_scaler), k)
+    rgx, rgbw, rgsw, rgsc = ko.kan_backward(D, np64(x), np64(L.grid), np64(L.base_weight),
+                                            np64(L.spline_weight), np64(L.spline_scaler), k,
+                                            basis=H)
+    tol = 1e-12 if dtype == torch.float64 else FP32_TOL
+    for got, ref in [(y, ry), (x.grad, rgx), (L.base_weight.grad, rgbw),
+                     (L.spline_weight.grad, rgsw), (L.spline_scaler.grad, rgsc)]:
+        assert normwise(np64(got), ref) < tol
+
+
+def test_backward_skips_unneeded_grads(C):
+    from torchsplinekan_amd import KANLinear
+    torch.manual_seed(1)
+    L = KANLinear(8, 4, backend="cuda").cuda()
+    x = torch.rand(64, 8, device="cuda") * 2 - 1
+    L(x).sum().backward()
+    assert all(p.grad is not None for p in L.parameters())
+    L2 = KANLinear(8, 4, backend="cuda").cuda().requires_grad_(False)
+    xx = x.clone().requires_grad_()
+    L2(xx).sum().backward()
+    ref = KANLinear(8, 4, backend="reference").cuda()
+    ref.load_state_dict(L2.state_dict())
+    xr = x.clone().requires_grad_()
+    ref(xr).sum().backward()
+    assert torch.allclose(xx.grad, xr.grad, atol=1e-5)
+    assert all(p.grad is None for p in L2.parameters())
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
+def test_local_and_legacy_impl_give_same_layer_results(C, dtype):
+    from torchsplinekan_amd import KANLinear
+    torch.manual_seed(0)
+    L = KANLinear(16, 8, grid_size=9, backend="cuda").to("cuda", dtype)
+    x = torch.rand(512, 16, device="cuda", dtype=dtype) * 2.4 - 1.2
+    out = {}
+    try:
+        for impl in (0, 1):
+            C.set_basis_impl(impl)
+            for p in L.parameters():
+                p.grad = None
+            xx = x.clone().requires_grad_()
+            y = L(xx)
+            y.square().sum().backward()
+            out[impl] = [y.detach(), xx.grad] + [p.grad for p in L.parameters()]
+    finally:
+        C.set_basis_impl(1)
+    tol = 1e-12 if dtype == torch.float64 else 1e-4
+    for a, b in zip(out[0], out[1]):
+        assert torch.allclose(a, b, atol=tol, rtol=tol)
+
+
+def test_double_backward_uses_composite(C):
+    from torchsplinekan_amd import KANLinear
+    torch.manual_seed(2)
+    L = KANLinear(3, 2, grid_size=6, backend="cuda").to("cuda", torch.float64)
+    x = (torch.rand(20, 3, device="cuda", dtype=torch.float64) * 1.6 - 0.8).requires_grad_()
+    assert torch.autograd.gradcheck(lambda t: L(t), (x,), eps=1e-6, atol=1e-6)
+    assert torch.autograd.gradgradcheck(lambda t: L(t), (x,), eps=1e-6, atol=1e-5)
+
+
+def test_limits_and_errors(C):
+    from torchsplinekan_amd import KANLinear
+    # largest supported grid is exact
+    L = KANLinear(4, 3, grid_size=65, spline_order=3, backend="cuda").to("cuda", torch.float64)
+    Lr = KANLinear(4, 3, grid_size=65, spline_order=3, backend="reference").to("cuda", torch.float64)
+    Lr.load_state_dict(L.state_dict())
+    x = torch.rand(50, 4, device="cuda", dtype=torch.float64) * 2.2 - 1.1
+    assert torch.allclose(L(x), Lr(x), atol=1e-12)
+    with pytest.raises(ValueError, match="CUDA kernel limit"):
+        KANLinear(4, 3, grid_size=66, spline_order=3, backend="cuda")
+    La = KANLinear(4, 3, grid_size=66, spline_order=3, backend="auto").cuda()
+    assert La.backend_for(x.float()) == "reference"
+    grid = make_grid(4, 66, 3, "uniform", dtype=torch.float32).cuda()
+    sw = torch.zeros(3, 4, 69, device="cuda")
+    with pytest.raises(RuntimeError, match=r"G \+ 2k"):
+        C.kan_forward(x.float(), grid, torch.empty(0, device="cuda"), sw,
+                      torch.empty(0, device="cuda"), 3, False)
+    torch.cuda.synchronize()
+    grid = make_grid(4, 5, 3, "uniform", dtype=torch.float32).cuda()
+    with pytest.raises(RuntimeError, match=r"spline_weight.size\(2\)"):
+        C.kan_forward(x.float(), grid, torch.empty(0, device="cuda"),
+                      torch.zeros(3, 4, 7, device="cuda"), torch.empty(0, device="cuda"), 3,
+                      False)
+    with pytest.raises(RuntimeError):
+        C.kan_forward(x.half(), grid.half(), torch.empty(0, device="cuda"),
+                      torch.zeros(3, 4, 8, device="cuda").half(), torch.empty(0, device="cuda"),
+                      3, False)
+    with pytest.raises(RuntimeError):
+        KANLinear(4, 3, backend="cuda")(torch.rand(5, 4))
+
+
+def test_kernel_limit_layer_config5_shape(C):
+    """Config 5 shape class (G=65, k=3, R=68, 72 knots) with ~1% of inputs
+    outside the knot span: exact zero-basis extrapolation, and fwd/bwd parity
+    on a row subset at full width (the reference's 32-bit guard does not
+    apply: offsets are 64-bit)."""
+    from torchsplinekan_amd import KANLinear
+    torch.manual_seed(5)
+    N, I, O, G, k = 512, 4096, 256, 65, 3
+    L = KANLinear(I, O, grid_size=G, spline_order=k, backend="cuda").cuda()
+    with torch.no_grad():
+        L.spline_weight.normal_(0, 0.05)
+    x = (torch.rand(N, I, device="cuda") * 2.2 - 1.1).requires_grad_()
+    y = L(x)
+    D = torch.randn(N, O, device="cuda")
+    y.backward(D)
+    rows = slice(0, 48)
+    ry, H = ko.kan_forward(np64(x[rows]), np64(L.grid), np64(L.base_weight),
+                           np64(L.spline_weight), np64(L.spline_scaler), k)
+    assert normwise(np64(y[rows]), ry) < FP32_TOL
+    rgx, _, _, _ = ko.kan_backward(np64(D[rows]), np64(x[rows]), np64(L.grid),
+                                   np64(L.base_weight), np64(L.spline_weight),
+                                   np64(L.spline_scaler), k, basis=H)
+    assert normwise(np64(x.grad[rows]), rgx) < FP32_TOL
+    # parameter gradient on a few edges over all samples
+    for o, i in [(0, 0), (17, 4000), (255, 1234)]:
+        Hi = ko.basis_dense(np64(x[:, i:i + 1]), np64(L.grid[i:i + 1]), k)[:, 0, :]
+        ref = np64(L.spline_scaler)[o, i] * (np64(D)[:, o, None] * Hi).sum(0)
+        assert normwise(np64(L.spline_weight.grad[o, i]), ref) < FP32_TOL
+    # out-of-span samples have an all-zero basis row on the device
+    Hg = C.basis(x.detach(), L.grid, k)
+    out = (x.detach() < L.grid[:, 0][None]) | (x.detach() > L.grid[:, -1][None])
+    assert out.any()
+    assert (Hg[out] == 0).all()

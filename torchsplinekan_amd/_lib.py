@@ -47,6 +47,9 @@ SIGNATURES = {
                                      _i64, _i64, _i64, _i64, _vp]),
     "kan_hip_edge_abs_mean_backward": (_int, [_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                                               _vp, _sz, _i64, _i64, _i64, _i64, _vp]),
+    "kan_hip_timing_enable": (_int, [_int]),
+    "kan_hip_timing_read": (_int, [_int, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_i64),
+                                   ctypes.POINTER(ctypes.c_double)]),
 }
 
 
@@ -65,7 +68,10 @@ def _load():
             "(or __graft_entry__.build())")
     lib = ctypes.CDLL(LIB_PATH)
     for name, (res, args) in SIGNATURES.items():
-        fn = getattr(lib, name)
+        try:
+            fn = getattr(lib, name)
+        except AttributeError as exc:
+            raise ImportError(f"{LIB_PATH} does not export {name}: rebuild it") from exc
         fn.restype = res
         fn.argtypes = args
     return lib
@@ -108,3 +114,21 @@ def limits():
     a, b = _i64(), _i64()
     check(LIB.kan_hip_limits(ctypes.byref(a), ctypes.byref(b)))
     return int(a.value), int(b.value)
+
+
+# kernel classes of kan_hip_timing_read
+TIMING_CLASSES = {"contraction": 0, "basis": 1, "basis_grad": 2, "edge": 3, "edge_grad": 4,
+                  "other": 5}
+
+
+def timing_enable(on: bool) -> None:
+    """Starts (clearing earlier records) or stops HIP-event timing of launches."""
+    check(LIB.kan_hip_timing_enable(int(bool(on))))
+
+
+def timing_read(kernel_class: str):
+    """(total_ms, launches, total_work) recorded for one kernel class."""
+    ms, n, w = ctypes.c_double(), _i64(), ctypes.c_double()
+    check(LIB.kan_hip_timing_read(TIMING_CLASSES[kernel_class], ctypes.byref(ms), ctypes.byref(n),
+                                  ctypes.byref(w)))
+    return float(ms.value), int(n.value), float(w.value)

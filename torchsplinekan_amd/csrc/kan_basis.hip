@@ -421,6 +421,9 @@ int launch_basis(const T* x, const T* grid, T* out, int64_t ld_out, T* silu_out,
   if (by > 2147483647LL) return set_error(KAN_ERR_LIMIT, "basis: too many samples (%lld)", (long long)n);
   dim3 grid_dim((unsigned)ceil_div(I, sh.fb), (unsigned)by);
   const size_t smem = basis_smem<T>(sh, nk);
+  // algorithmic bytes: read x, write the R basis values (+ silu) per item
+  TimedLaunch timed(kClassBasis, st,
+                    (double)sizeof(T) * (double)n * (double)I * (1.0 + R + (silu_out ? 1 : 0)));
 #define KAN_BASIS_LAUNCH(KK, IM)                                                           \
   hipLaunchKernelGGL((basis_kernel<KK, T, IM>), grid_dim, dim3(64 * sh.waves), smem, st, x, \
                      grid, out, ld_out, silu_out, sh)
@@ -447,6 +450,9 @@ int launch_basis_grad(const T* x, const T* grid, const T* gH, int64_t ld_g, cons
   if (by > 2147483647LL) return set_error(KAN_ERR_LIMIT, "basis_grad: too many samples");
   dim3 grid_dim((unsigned)ceil_div(I, sh.fb), (unsigned)by);
   const size_t smem = basis_smem<T>(sh, nk);
+  // algorithmic bytes: read x and the R gradient values (+ base), write gx
+  TimedLaunch timed(kClassBasisGrad, st,
+                    (double)sizeof(T) * (double)n * (double)I * (2.0 + R + (gbase ? 1 : 0)));
 #define KAN_BGRAD_LAUNCH(KK, IM)                                                             \
   hipLaunchKernelGGL((basis_grad_kernel<KK, T, IM>), grid_dim, dim3(64 * sh.waves), smem, st, \
                      x, grid, gH, ld_g, gbase, gx, sh)
@@ -468,6 +474,7 @@ int launch_pack_basis(const T* basis, const T* x, T* aug, int64_t ld_aug, int64_
                       int64_t R, bool has_base, hipStream_t st) {
   const int64_t total = n * (I * R + (has_base ? I : 0));
   if (total == 0) return KAN_OK;
+  TimedLaunch timed(kClassOther, st, 0.0);
   hipLaunchKernelGGL((pack_basis_kernel<T>), dim3(gs_blocks(total)), dim3(256), 0, st, basis, x,
                      aug, ld_aug, n, I, R, has_base);
   return check_launch("pack_basis");
@@ -478,6 +485,7 @@ int launch_build_waug(const T* sw, const T* scaler, const T* bw, T* waug, int64_
                       int64_t I, int64_t R, hipStream_t st) {
   const int64_t total = O * ld;
   if (total == 0) return KAN_OK;
+  TimedLaunch timed(kClassOther, st, 0.0);
   hipLaunchKernelGGL((build_waug_kernel<T>), dim3(gs_blocks(total)), dim3(256), 0, st, sw,
                      scaler, bw, waug, ld, O, I, R);
   return check_launch("build_weight_aug");
@@ -489,6 +497,7 @@ int launch_param_grads(const T* part, int splits, int64_t split_stride, int64_t 
                        int64_t R, hipStream_t st) {
   const int64_t total = O * I;
   if (total == 0) return KAN_OK;
+  TimedLaunch timed(kClassOther, st, 0.0);
   hipLaunchKernelGGL((param_grads_kernel<T>), dim3(gs_blocks(total)), dim3(256), 0, st, part,
                      splits, split_stride, ld, sw, scaler, gsw, gscaler, gbw, O, I, R);
   return check_launch("param_grads");

@@ -7,6 +7,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <mutex>
+#include <vector>
 
 #include "kan_common.h"
 
@@ -51,6 +52,55 @@ int device_cu_count() {
     g_cu_count[dev] = cus;
   }
   return g_cu_count[dev];
+}
+
+// ---- HIP-event timing -------------------------------------------------------
+
+namespace {
+struct TimingRecord {
+  int cls;
+  hipEvent_t start, stop;
+  double work;
+};
+std::mutex g_timing_mutex;
+std::atomic<bool> g_timing_on{false};
+std::vector<TimingRecord> g_timing;
+constexpr size_t kMaxTimingRecords = 1 << 16;
+
+void timing_clear_locked() {
+  for (TimingRecord& r : g_timing) {
+    (void)hipEventDestroy(r.start);
+    (void)hipEventDestroy(r.stop);
+  }
+  g_timing.clear();
+}
+}  // namespace
+
+TimedLaunch::TimedLaunch(int cls, hipStream_t st, double work) : slot_(-1), st_(st) {
+  if (!g_timing_on.load(std::memory_order_relaxed)) return;
+  std::lock_guard<std::mutex> lock(g_timing_mutex);
+  if (g_timing.size() >= kMaxTimingRecords) return;
+  TimingRecord r;
+  r.cls = cls;
+  r.work = work;
+  if (hipEventCreate(&r.start) != hipSuccess) {
+    (void)hipGetLastError();
+    return;
+  }
+  if (hipEventCreate(&r.stop) != hipSuccess) {
+    (void)hipEventDestroy(r.start);
+    (void)hipGetLastError();
+    return;
+  }
+  (void)hipEventRecord(r.start, st);
+  slot_ = (int)g_timing.size();
+  g_timing.push_back(r);
+}
+
+TimedLaunch::~TimedLaunch() {
+  if (slot_ < 0) return;
+  std::lock_guard<std::mutex> lock(g_timing_mutex);
+  if ((size_t)slot_ < g_timing.size()) (void)hipEventRecord(g_timing[slot_].stop, st_);
 }
 
 namespace {
@@ -215,6 +265,36 @@ int kan_hip_set_basis_impl(int64_t impl) {
 }
 
 int64_t kan_hip_get_basis_impl(void) { return g_basis_impl.load(); }
+
+int kan_hip_timing_enable(int on) {
+  std::lock_guard<std::mutex> lock(g_timing_mutex);
+  timing_clear_locked();
+  g_timing_on.store(on != 0);
+  return KAN_OK;
+}
+
+int kan_hip_timing_read(int kernel_class, double* total_ms, int64_t* launches, double* work) {
+  if (kernel_class < 0 || kernel_class >= kNumKernelClasses)
+    return set_error(KAN_ERR_INVALID, "timing_read: unknown kernel class %d", kernel_class);
+  std::lock_guard<std::mutex> lock(g_timing_mutex);
+  double ms = 0.0, w = 0.0;
+  int64_t cnt = 0;
+  for (const TimingRecord& r : g_timing) {
+    if (r.cls != kernel_class) continue;
+    if (hipEventSynchronize(r.stop) != hipSuccess)
+      return set_error(KAN_ERR_HIP, "timing_read: %s", hipGetErrorString(hipGetLastError()));
+    float e = 0.0f;
+    if (hipEventElapsedTime(&e, r.start, r.stop) != hipSuccess)
+      return set_error(KAN_ERR_HIP, "timing_read: %s", hipGetErrorString(hipGetLastError()));
+    ms += e;
+    w += r.work;
+    ++cnt;
+  }
+  if (total_ms != nullptr) *total_ms = ms;
+  if (launches != nullptr) *launches = cnt;
+  if (work != nullptr) *work = w;
+  return KAN_OK;
+}
 
 int kan_hip_basis(int dtype, const void* x, const void* grid, void* basis, int64_t n, int64_t I,
                   int64_t G, int64_t k, void* stream) {

@@ -66,6 +66,31 @@ __device__ __forceinline__ float silu_grad_of<float>(float x) {
   return sg * (1.0f + x * (1.0f - sg));
 }
 
+// ---- optional HIP-event timing of kernel launches ---------------------------
+// When enabled (kan_hip_timing_enable), every launch below records a pair of
+// events on its stream together with the launch's algorithmic work (flops
+// for contractions, bytes for the memory-bound kernels), so that a caller can
+// read per-class average kernel durations without a profiler.
+enum KernelClass {
+  kClassContraction = 0,  // MFMA contraction GEMMs (forward, params, input)
+  kClassBasis = 1,        // basis evaluation (+ silu block)
+  kClassBasisGrad = 2,    // input-gradient contraction of the basis
+  kClassEdge = 3,         // edge statistic forward
+  kClassEdgeGrad = 4,     // edge statistic backward
+  kClassOther = 5,        // packing / finalize kernels
+  kNumKernelClasses = 6
+};
+
+class TimedLaunch {
+ public:
+  TimedLaunch(int cls, hipStream_t st, double work);
+  ~TimedLaunch();
+
+ private:
+  int slot_;
+  hipStream_t st_;
+};
+
 // ---- launchers implemented in the .hip translation units -----------------
 
 template <typename T>

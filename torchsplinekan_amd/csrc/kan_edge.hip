@@ -289,6 +289,7 @@ int launch_edge_forward(const T* s, const T* H, const T* bw, const T* W, T* a, T
   dim3 grid((unsigned)ceil_div(O, kEdgeThreads), (unsigned)I, (unsigned)splits);
   const bool fin = splits == 1;
   const int R1 = (int)R + 1;
+  TimedLaunch timed(kClassEdge, st, 2.0 * (double)n * (double)O * (double)I * (double)R1);
   KAN_EDGE_DISPATCH(R1, hipLaunchKernelGGL((edge_forward_kernel<T, RP>), grid,
                                            dim3(kEdgeThreads), 0, st, s, H, bw, W,
                                            fin ? a : part, n, (int)I, (int)O, (int)R, per_split,
@@ -311,6 +312,7 @@ int launch_edge_backward(const T* ga, const T* s, const T* H, const T* bw, const
     const int64_t per_split = round_up(ceil_div(n, splits), kEdgeTile);
     dim3 grid((unsigned)ceil_div(O, kEdgeThreads), (unsigned)I, (unsigned)splits);
     const bool fin = splits == 1;
+    TimedLaunch timed(kClassEdgeGrad, st, 4.0 * (double)n * (double)O * (double)I * (double)R1);
     KAN_EDGE_DISPATCH(R1, hipLaunchKernelGGL((edge_param_grad_kernel<T, RP>), grid,
                                              dim3(kEdgeThreads), 0, st, ga, s, H, bw, W, dbw, dW,
                                              part, n, (int)I, (int)O, (int)R, per_split, fin));
@@ -325,6 +327,7 @@ int launch_edge_backward(const T* ga, const T* s, const T* H, const T* bw, const
   }
   if ((ds != nullptr || dH != nullptr) && n > 0 && I > 0) {
     dim3 grid((unsigned)ceil_div(n, kEdgeThreads), (unsigned)I);
+    TimedLaunch timed(kClassEdgeGrad, st, 4.0 * (double)n * (double)O * (double)I * (double)R1);
     KAN_EDGE_DISPATCH(R1, hipLaunchKernelGGL((edge_input_grad_kernel<T, RP>), grid,
                                              dim3(kEdgeThreads), 0, st, ga, s, H, bw, W, ds, dH,
                                              n, (int)I, (int)O, (int)R));

@@ -326,6 +326,7 @@ int launch_gemm(int layout, int64_t M, int64_t N, int64_t K, const T* A, int64_t
   p.tiles_n = (int)tn;
   p.splits = splits;
   const bool vec = vec_ok(A, lda) && vec_ok(B, ldb);
+  TimedLaunch timed(kClassContraction, st, 2.0 * (double)M * (double)N * (double)K);
   switch (layout) {
     case kLayoutNT: launch_layout<T, true, true>(p, vec, (unsigned)blocks, st); break;
     case kLayoutTN: launch_layout<T, false, false>(p, vec, (unsigned)blocks, st); break;
