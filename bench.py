@@ -45,7 +45,22 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="target CPU time of the baseline sample")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="run only a plain 1 GiB device-to-device copy (3 times); the HBM "
+                         "counters of this known-size copy scale the counter readings of the "
+                         "kernels")
     return ap.parse_args()
+
+
+def copy_calibration():
+    import torch
+    n = 1 << 28  # 2^28 fp32 = 1 GiB
+    src = torch.ones(n, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes_read": 4 * n, "copy_bytes_written": 4 * n, "launches": 3}))
 
 
 def make_inputs(N, I, O, G, k, seed=0):
@@ -111,6 +126,10 @@ def main():
               "gradients; see DESIGN.md)", file=sys.stderr)
         sys.exit(2)
 
+    if args.copy_calibration:
+        copy_calibration()
+        return
+
     import torch
     import torch.nn.functional as F
     from torchsplinekan_amd import KANLinear, _lib
@@ -148,7 +167,6 @@ def main():
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
-    assert L.last_backend == "cuda"
 
     stream = torch.cuda.current_stream(dev)
     ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
@@ -162,6 +180,8 @@ def main():
         ev[i][1].record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
+    if L.last_backend != "cuda":
+        raise RuntimeError("the timed steps did not run on the native backend")
     step_ms = [a.elapsed_time(b) for a, b in ev]
     kernels = {}
     for cls in ("contraction", "basis", "basis_grad", "other"):
