@@ -19,15 +19,18 @@ How each function is pinned (tests/test_oracle.py):
                     grids; closed-form uniform B-splines for k = 1, 2, 3;
                     partition of unity, non-negativity, support, zeros out
                     of range; golden vectors written by the reference's own
-                    compute_basis (tests/golden/).
+                    compute_basis (tests/golden/), matched bit for bit in
+                    float32 and exactly in float64.
   basis_local       agreement with basis_dense to 1e-13 in float64 over
                     uniform, nonuniform and repeated-knot grids, including
                     points on every knot and out of range.
   basis_derivative  central finite differences of basis_dense in float64
                     away from knots; exact cubic reproduction (x^3 - x).
-  kan_forward       brute-force per-(n,o) loop over the definition.
-  kan_backward      finite differences of kan_forward (all four gradients).
-  edge_abs_mean     brute-force per-(n,o,i) loop; golden vectors.
+  kan_forward       brute-force per-(n,o) loop over the definition; config-1
+                    golden vectors of the reference (tests/test_golden.py).
+  kan_backward      finite differences of kan_forward (all four gradients);
+                    config-1 golden vectors.
+  edge_abs_mean     brute-force per-(n,o,i) loop.
   edge_abs_mean_backward
                     finite differences of edge_abs_mean away from phi = 0.
   regularization_from_edge_means (+ _grad)
