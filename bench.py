@@ -226,7 +226,7 @@ def main():
         },
         "roofline": {
             "bound": "mfma",
-            "kernel": "gemm_kernel (MFMA f32 16x16x4 contraction)",
+            "kernel": "gemm_kernel (fp32 MFMA contraction; average over the forward, parameter and input launches)",
             "achieved": achieved,
             "peak": PEAK_FP32_MFMA_TFLOPS,
             "unit": "TFLOP/s",

@@ -346,34 +346,48 @@ __global__ void build_waug_kernel(const T* __restrict__ sw, const T* __restrict_
 // Parameter gradients from the (split) products G = D^T [H | s]:
 //   gsw = scaler * G_H, gscaler = sum_r sw * G_H, gbw = G_s
 // (csrc/kan_cuda.cu:576-598).  Split partials are summed in fixed order.
+// A block owns kPairs consecutive (o, i) edges of one output row o: its
+// kPairs*R partial values are contiguous, so the loads are coalesced; the
+// per-edge sum over r goes through LDS.
+constexpr int kPairs = 128;
+
 template <typename T>
-__global__ void param_grads_kernel(const T* __restrict__ part, int splits, int64_t split_stride,
-                                   int64_t ld, const T* __restrict__ sw,
-                                   const T* __restrict__ scaler, T* __restrict__ gsw,
-                                   T* __restrict__ gscaler, T* __restrict__ gbw, int64_t O,
-                                   int64_t I, int64_t R) {
-  const int64_t total = O * I;
-  for (int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; e < total;
-       e += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t o = e / I, i = e - o * I;
-    const T* base = part + o * ld + i * R;
-    if (gsw != nullptr || gscaler != nullptr) {
-      const T sc = scaler != nullptr ? scaler[e] : T(1);
-      T dsc = T(0);
-      for (int64_t r = 0; r < R; ++r) {
-        T gv = base[r];
-        for (int s = 1; s < splits; ++s) gv += base[r + s * split_stride];
-        if (gsw != nullptr) gsw[e * R + r] = scaler != nullptr ? sc * gv : gv;
-        dsc += sw[e * R + r] * gv;
+__global__ __launch_bounds__(kPairs) void param_grads_kernel(
+    const T* __restrict__ part, int splits, int64_t split_stride, int64_t ld,
+    const T* __restrict__ sw, const T* __restrict__ scaler, T* __restrict__ gsw,
+    T* __restrict__ gscaler, T* __restrict__ gbw, int64_t O, int64_t I, int64_t R,
+    int64_t blocks_per_row) {
+  extern __shared__ __align__(16) unsigned char smem_pg[];
+  T* prod = reinterpret_cast<T*>(smem_pg);
+  const int64_t o = blockIdx.x / blocks_per_row;
+  const int64_t i0 = (blockIdx.x - o * blocks_per_row) * (int64_t)kPairs;
+  const int np = (int)min((int64_t)kPairs, I - i0);
+  const int cnt = np * (int)R;
+  const T* src = part + o * ld + i0 * R;
+  const int64_t ebase = (o * I + i0) * R;
+  const float inv_r = 1.0f / (float)R;
+  if (gsw != nullptr || gscaler != nullptr) {
+    for (int c = threadIdx.x; c < cnt; c += kPairs) {
+      T g = src[c];
+      for (int s = 1; s < splits; ++s) g += src[s * split_stride + c];
+      const int pr = small_div(c, inv_r);
+      if (gsw != nullptr) gsw[ebase + c] = scaler != nullptr ? scaler[o * I + i0 + pr] * g : g;
+      if (gscaler != nullptr) prod[c] = sw[ebase + c] * g;
+    }
+    if (gscaler != nullptr) {
+      __syncthreads();
+      if ((int)threadIdx.x < np) {
+        T acc = T(0);
+        for (int64_t r = 0; r < R; ++r) acc += prod[threadIdx.x * R + r];
+        gscaler[o * I + i0 + threadIdx.x] = acc;
       }
-      if (gscaler != nullptr) gscaler[e] = dsc;
     }
-    if (gbw != nullptr) {
-      const T* bp = part + o * ld + I * R + i;
-      T gv = bp[0];
-      for (int s = 1; s < splits; ++s) gv += bp[s * split_stride];
-      gbw[e] = gv;
-    }
+  }
+  if (gbw != nullptr && (int)threadIdx.x < np) {
+    const T* bp = part + o * ld + I * R + i0 + threadIdx.x;
+    T g = bp[0];
+    for (int s = 1; s < splits; ++s) g += bp[s * split_stride];
+    gbw[o * I + i0 + threadIdx.x] = g;
   }
 }
 
@@ -495,11 +509,14 @@ template <typename T>
 int launch_param_grads(const T* part, int splits, int64_t split_stride, int64_t ld, const T* sw,
                        const T* scaler, T* gsw, T* gscaler, T* gbw, int64_t O, int64_t I,
                        int64_t R, hipStream_t st) {
-  const int64_t total = O * I;
-  if (total == 0) return KAN_OK;
+  if (O * I == 0) return KAN_OK;
+  const int64_t per_row = ceil_div(I, kPairs);
+  const int64_t blocks = O * per_row;
+  if (blocks > 2147483647LL) return set_error(KAN_ERR_LIMIT, "param_grads: too many edges");
   TimedLaunch timed(kClassOther, st, 0.0);
-  hipLaunchKernelGGL((param_grads_kernel<T>), dim3(gs_blocks(total)), dim3(256), 0, st, part,
-                     splits, split_stride, ld, sw, scaler, gsw, gscaler, gbw, O, I, R);
+  hipLaunchKernelGGL((param_grads_kernel<T>), dim3((unsigned)blocks), dim3(kPairs),
+                     sizeof(T) * kPairs * R, st, part, splits, split_stride, ld, sw, scaler, gsw,
+                     gscaler, gbw, O, I, R, per_row);
   return check_launch("param_grads");
 }
 
