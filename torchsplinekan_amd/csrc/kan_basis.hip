@@ -168,8 +168,15 @@ struct BasisShape {
   int fb;     // features per block (<= 64)
   int subs;   // samples per wave step (64 / fb)
   int iters;  // wave steps per block
-  int rs;     // LDS row stride per item (R rounded up to odd)
-  int waves;  // waves per block (fewer for wide fp64 rows, to bound LDS)
+  int waves;  // waves per block
+  int vec;    // 16-byte vector path for the staged rows (alignment holds)
+};
+
+// 16-byte vector of T.
+template <typename T>
+struct V16 {
+  static constexpr int kN = 16 / sizeof(T);
+  typedef T type __attribute__((ext_vector_type(16 / sizeof(T))));
 };
 
 template <typename T>
@@ -181,7 +188,32 @@ __device__ __forceinline__ T* stage_knots(unsigned char* smem, const T* __restri
   return knots;
 }
 
+// Copies cnt elements between a staged row in LDS and global memory, with
+// 16-byte vectors when both sides are aligned (vec), element-wise otherwise.
+template <typename T, bool TO_GLOBAL>
+__device__ __forceinline__ void move_row(T* __restrict__ gmem, T* __restrict__ lds, int cnt,
+                                         int lane, bool vec) {
+  typedef typename V16<T>::type VT;
+  constexpr int kV = V16<T>::kN;
+  int done = 0;
+  if (vec) {
+    const int nv = cnt / kV;
+    for (int c = lane; c < nv; c += 64) {
+      if (TO_GLOBAL) reinterpret_cast<VT*>(gmem)[c] = reinterpret_cast<const VT*>(lds)[c];
+      else reinterpret_cast<VT*>(lds)[c] = reinterpret_cast<const VT*>(gmem)[c];
+    }
+    done = nv * kV;
+  }
+  for (int c = done + lane; c < cnt; c += 64) {
+    if (TO_GLOBAL) gmem[c] = lds[c];
+    else lds[c] = gmem[c];
+  }
+}
+
 // H rows (and optionally silu(x)) for a block of features x samples.
+// The per-wave LDS stage holds the subs sample segments exactly as they lie
+// in the output (item rows of R values back to back), so each segment is
+// written out with coalesced 16-byte stores.
 template <int K, typename T, int IMPL>
 __global__ __launch_bounds__(kBasisThreads) void basis_kernel(
     const T* __restrict__ x, const T* __restrict__ grid, T* __restrict__ out, int64_t ld,
@@ -192,16 +224,16 @@ __global__ __launch_bounds__(kBasisThreads) void basis_kernel(
   const int i0 = blockIdx.x * sh.fb;
   const int fbv = min(sh.fb, sh.I - i0);
   T* knots = stage_knots<T>(smem, grid, i0, fbv, nk);
-  T* stage = knots + round_up((int64_t)sh.fb * nk, 4) + wave * 64 * sh.rs;
+  T* stage = knots + round_up((int64_t)sh.fb * nk, 4) + wave * 64 * R;
   __syncthreads();
 
   const int sub = lane / sh.fb, fi = lane - sub * sh.fb;
   const bool lane_ok = sub < sh.subs && fi < fbv;
   const T* t = knots + fi * nk;
-  const float inv_r = 1.0f / (float)R;
   const int64_t step = (int64_t)sh.waves * sh.subs;
   int64_t nbase = (int64_t)blockIdx.y * sh.iters * step + (int64_t)wave * sh.subs;
-  T* row = stage + lane * sh.rs;
+  T* row = stage + lane * R;
+  const bool vec = sh.vec != 0;
 
   for (int it = 0; it < sh.iters; ++it, nbase += step) {
     const int64_t nn = nbase + sub;
@@ -226,25 +258,22 @@ __global__ __launch_bounds__(kBasisThreads) void basis_kernel(
         for (int r = 0; r < R; ++r) row[r] = T(0);
       }
     }
+    if (silu_out != nullptr && ok) silu_out[nn * ld + i0 + fi] = silu_of<T>(xv);
     __syncthreads();
-    // Coalesced store of the staged rows: sample by sample, the fbv*R
-    // values of features [i0, i0+fbv) are contiguous in the output.
     for (int s = 0; s < sh.subs; ++s) {
       const int64_t ns = nbase + s;
       if (ns >= sh.n) break;
-      T* dst = out + ns * ld + (int64_t)i0 * R;
-      const T* src = stage + s * sh.fb * sh.rs;
-      for (int c = lane; c < fbv * R; c += 64) {
-        const int item = small_div(c, inv_r);
-        dst[c] = src[item * sh.rs + (c - item * R)];
-      }
+      move_row<T, true>(out + ns * ld + (int64_t)i0 * R, stage + s * sh.fb * R, fbv * R, lane,
+                        vec);
     }
-    if (silu_out != nullptr && ok) silu_out[nn * ld + i0 + fi] = silu_of<T>(xv);
     __syncthreads();
   }
 }
 
 // gx[n, i] = sum_r g[n, i*R + r] * dB_r/dx (+ gbase[n, i] * silu'(x)).
+// The gradient segments are staged into LDS with coalesced 16-byte loads;
+// each lane then reads the k+1 values of its span window (impl 1) or its
+// whole row (impl 0).
 template <int K, typename T, int IMPL>
 __global__ __launch_bounds__(kBasisThreads) void basis_grad_kernel(
     const T* __restrict__ x, const T* __restrict__ grid, const T* __restrict__ g, int64_t ld,
@@ -255,33 +284,30 @@ __global__ __launch_bounds__(kBasisThreads) void basis_grad_kernel(
   const int i0 = blockIdx.x * sh.fb;
   const int fbv = min(sh.fb, sh.I - i0);
   T* knots = stage_knots<T>(smem, grid, i0, fbv, nk);
-  T* stage = knots + round_up((int64_t)sh.fb * nk, 4) + wave * 64 * sh.rs;
+  T* stage = knots + round_up((int64_t)sh.fb * nk, 4) + wave * 64 * R;
   __syncthreads();
 
   const int sub = lane / sh.fb, fi = lane - sub * sh.fb;
   const bool lane_ok = sub < sh.subs && fi < fbv;
   const T* t = knots + fi * nk;
-  const float inv_r = 1.0f / (float)R;
   const int64_t step = (int64_t)sh.waves * sh.subs;
   int64_t nbase = (int64_t)blockIdx.y * sh.iters * step + (int64_t)wave * sh.subs;
-  const T* row = stage + lane * sh.rs;
+  const T* row = stage + lane * R;
+  const bool vec = sh.vec != 0;
 
   for (int it = 0; it < sh.iters; ++it, nbase += step) {
     for (int s = 0; s < sh.subs; ++s) {
       const int64_t ns = nbase + s;
       if (ns >= sh.n) break;
-      const T* src = g + ns * ld + (int64_t)i0 * R;
-      T* dst = stage + s * sh.fb * sh.rs;
-      for (int c = lane; c < fbv * R; c += 64) {
-        const int item = small_div(c, inv_r);
-        dst[item * sh.rs + (c - item * R)] = src[c];
-      }
+      move_row<T, false>(const_cast<T*>(g) + ns * ld + (int64_t)i0 * R, stage + s * sh.fb * R,
+                         fbv * R, lane, vec);
     }
-    __syncthreads();
     const int64_t nn = nbase + sub;
     const bool ok = lane_ok && nn < sh.n;
+    const T xv = ok ? x[nn * sh.I + i0 + fi] : T(0);
+    const T gb = (ok && gbase != nullptr) ? gbase[nn * ld + i0 + fi] : T(0);
+    __syncthreads();
     if (ok) {
-      const T xv = x[nn * sh.I + i0 + fi];
       T acc = T(0);
       if (IMPL == 1) {
         const int m = knot_span(t, nk, xv);
@@ -299,7 +325,7 @@ __global__ __launch_bounds__(kBasisThreads) void basis_grad_kernel(
         dense_derivative<T>(t, nk, xv, K, d);
         for (int r = 0; r < R; ++r) acc += row[r] * d[r];
       }
-      if (gbase != nullptr) acc += gbase[nn * ld + i0 + fi] * silu_grad_of<T>(xv);
+      if (gbase != nullptr) acc += gb * silu_grad_of<T>(xv);
       gx[nn * sh.I + i0 + fi] = acc;
     }
     __syncthreads();
@@ -391,30 +417,35 @@ __global__ __launch_bounds__(kPairs) void param_grads_kernel(
   }
 }
 
-BasisShape make_shape(int64_t n, int64_t I, int G, int R, size_t elem, int64_t* blocks_y) {
+BasisShape make_shape(int64_t n, int64_t I, int G, int R, size_t elem, int64_t ld,
+                      const void* rows_ptr, int64_t* blocks_y) {
   BasisShape sh;
   sh.n = n;
   sh.I = (int)I;
   sh.G = G;
   sh.fb = (int)(I < 64 ? I : 64);
   sh.subs = 64 / sh.fb;
-  sh.rs = (R % 2 == 1) ? R : R + 1;
   sh.waves = 4;
-  while (sh.waves > 1 && (size_t)sh.waves * 64 * sh.rs * elem > 48 * 1024) sh.waves /= 2;
+  while (sh.waves > 1 && (size_t)sh.waves * 64 * R * elem > 48 * 1024) sh.waves /= 2;
+  // 16-byte vectors: the output rows, each block's feature offset and each
+  // staged sample segment must all start 16-byte aligned.
+  const int64_t v = 16 / (int64_t)elem;
+  sh.vec = ((reinterpret_cast<uintptr_t>(rows_ptr) % 16) == 0) && (ld % v == 0) &&
+           (((int64_t)sh.fb * R) % v == 0);
   const int64_t per_step = (int64_t)sh.waves * sh.subs;
   const int64_t steps = ceil_div(n, per_step);
-  // Aim for ~16 steps per block, but keep enough blocks to fill the chip.
+  // Aim for ~4 steps per block, but keep enough blocks to fill the chip.
   const int64_t fblocks = ceil_div(I, sh.fb);
-  int64_t iters = 16;
-  while (iters > 1 && fblocks * ceil_div(steps, iters) < 4096) iters /= 2;
+  int64_t iters = 4;
+  while (iters > 1 && fblocks * ceil_div(steps, iters) < 8192) iters /= 2;
   sh.iters = (int)iters;
   *blocks_y = ceil_div(steps, iters);
   return sh;
 }
 
 template <typename T>
-size_t basis_smem(const BasisShape& sh, int nk) {
-  return sizeof(T) * (round_up((int64_t)sh.fb * nk, 4) + (int64_t)sh.waves * 64 * sh.rs);
+size_t basis_smem(const BasisShape& sh, int nk, int R) {
+  return sizeof(T) * (round_up((int64_t)sh.fb * nk, 4) + (int64_t)sh.waves * 64 * R);
 }
 
 inline int gs_blocks(int64_t total) {
@@ -431,10 +462,10 @@ int launch_basis(const T* x, const T* grid, T* out, int64_t ld_out, T* silu_out,
   if (n == 0 || I == 0) return KAN_OK;
   const int R = G + k, nk = G + 2 * k + 1;
   int64_t by = 0;
-  BasisShape sh = make_shape(n, I, G, R, sizeof(T), &by);
+  BasisShape sh = make_shape(n, I, G, R, sizeof(T), ld_out, out, &by);
   if (by > 2147483647LL) return set_error(KAN_ERR_LIMIT, "basis: too many samples (%lld)", (long long)n);
   dim3 grid_dim((unsigned)ceil_div(I, sh.fb), (unsigned)by);
-  const size_t smem = basis_smem<T>(sh, nk);
+  const size_t smem = basis_smem<T>(sh, nk, R);
   // algorithmic bytes: read x, write the R basis values (+ silu) per item
   TimedLaunch timed(kClassBasis, st,
                     (double)sizeof(T) * (double)n * (double)I * (1.0 + R + (silu_out ? 1 : 0)));
@@ -460,10 +491,10 @@ int launch_basis_grad(const T* x, const T* grid, const T* gH, int64_t ld_g, cons
   if (n == 0 || I == 0) return KAN_OK;
   const int R = G + k, nk = G + 2 * k + 1;
   int64_t by = 0;
-  BasisShape sh = make_shape(n, I, G, R, sizeof(T), &by);
+  BasisShape sh = make_shape(n, I, G, R, sizeof(T), ld_g, gH, &by);
   if (by > 2147483647LL) return set_error(KAN_ERR_LIMIT, "basis_grad: too many samples");
   dim3 grid_dim((unsigned)ceil_div(I, sh.fb), (unsigned)by);
-  const size_t smem = basis_smem<T>(sh, nk);
+  const size_t smem = basis_smem<T>(sh, nk, R);
   // algorithmic bytes: read x and the R gradient values (+ base), write gx
   TimedLaunch timed(kClassBasisGrad, st,
                     (double)sizeof(T) * (double)n * (double)I * (2.0 + R + (gbase ? 1 : 0)));
