@@ -40,7 +40,10 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", default="c3", choices=["c3", "c3-nodx"])
+    ap.add_argument("--workload", default="c3", choices=["c3", "c3-nodx", "c4"],
+                    help="c3 (the metric's config, default), c3-nodx (x without grad, the "
+                         "reference benchmark's semantics) or c4 (KAN([256,512,512,64]) with "
+                         "forward_with_regularization; reported separately, not the metric)")
     ap.add_argument("--n", type=int, default=65536, help="samples per step (default: config's 65536)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
@@ -118,6 +121,74 @@ def cpu_baseline(x, coef, bw, scaler, target, grid, k, need_dx, seconds):
     }
 
 
+def bench_c4(args):
+    """KAN([256, 512, 512, 64], grid_size=8, spline_order=3) fp32, knots from
+    update_grid on x drawn from a 4-component Gaussian mixture (means +-0.5,
+    +-0.8, sd 0.1), N=16384; one step is forward_with_regularization(1e-2,
+    1e-2, reg_impl="auto") + MSE + backward (x without grad)."""
+    import torch
+    import torch.nn.functional as F
+    from torchsplinekan_amd import KAN, _lib
+    dev = torch.device("cuda", 0)
+    N, widths = args.n if args.n != 65536 else 16384, [256, 512, 512, 64]
+    g = torch.Generator().manual_seed(0)
+    means = torch.tensor([-0.8, -0.5, 0.5, 0.8])
+    comp = torch.randint(0, 4, (N, widths[0]), generator=g)
+    x = means[comp] + 0.1 * torch.randn(N, widths[0], generator=g)
+    target = torch.randn(N, widths[-1], generator=g)
+    torch.manual_seed(0)
+    net = KAN(widths, grid_size=8, spline_order=3, backend="cuda")
+    with torch.no_grad():
+        for layer in net.layers:
+            layer.spline_weight.normal_(0.0, 0.1, generator=g)
+    net = net.to(dev)
+    xd, td = x.to(dev), target.to(dev)
+    net.update_grid(xd)          # before timing (least squares on the host)
+
+    def step():
+        for p in net.parameters():
+            p.grad = None
+        y, reg = net.forward_with_regularization(xd, 1e-2, 1e-2, reg_impl="auto")
+        (F.mse_loss(y, td) + reg).backward()
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    _lib.timing_enable(True)
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    if any(l.last_backend != "cuda" for l in net.layers):
+        raise RuntimeError("c4 did not run the fused native path")
+    kern = {c: _lib.timing_read(c) for c in ("edge", "edge_grad", "basis", "basis_grad",
+                                             "contraction", "other")}
+    _lib.timing_enable(False)
+    e_ms, e_cnt, e_work = kern["edge"]
+    eg_ms, eg_cnt, eg_work = kern["edge_grad"]
+    ach = e_work / (e_ms * 1e-3) / 1e12 if e_cnt else 0.0
+    ach_g = eg_work / (eg_ms * 1e-3) / 1e12 if eg_cnt else 0.0
+    line = {
+        "metric": "fwd+bwd samples/s, KAN([256,512,512,64]) G8 k3 N=16K forward_with_regularization",
+        "value": N * args.steps / wall, "unit": "samples/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": wall * 1e3 / args.steps, "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic (Gaussian-mixture x, seeded; knots from update_grid)",
+        "config": {"workload": "c4: KAN([256,512,512,64], G=8, k=3) fp32, N=%d, "
+                               "forward_with_regularization(1e-2, 1e-2, 'auto') + MSE + backward" % N},
+        "roofline": {"bound": "valu", "kernel": "edge_forward_kernel (fused mean|phi|)",
+                     "achieved": ach, "peak": PEAK_FP32_MFMA_TFLOPS, "unit": "TFLOP/s",
+                     "frac": ach / PEAK_FP32_MFMA_TFLOPS, "traffic": None,
+                     "flop_per_launch": e_work / max(e_cnt, 1),
+                     "avg_launch_ms": e_ms / max(e_cnt, 1), "launches": e_cnt},
+        "kernels": {k_: {"ms_per_step": v[0] / args.steps, "launches_per_step": v[1] / args.steps}
+                    for k_, v in kern.items()},
+        "edge_grad_tflops": ach_g,
+    }
+    print(json.dumps(line), flush=True)
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -139,6 +210,9 @@ def main():
         sys.exit(1)
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
+    if args.workload == "c4":
+        bench_c4(args)
+        return
 
     I = O = 1024
     G, k = 10, 3

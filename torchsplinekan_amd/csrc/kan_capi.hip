@@ -236,7 +236,7 @@ int check_edge(const char* who, int dtype, const void* s, const void* H, const v
 }
 
 size_t edge_ws_bytes(int dtype, int64_t n, int64_t I, int64_t O, int64_t R, bool backward) {
-  const int splits = edge_pick_splits(n, I, O);
+  const int splits = edge_pick_splits(dtype, n, I, O, R);
   if (splits <= 1) return 0;
   const size_t elem = dtype == KAN_DTYPE_F64 ? 8 : 4;
   return elem * (size_t)splits * (size_t)(O * I) * (size_t)(backward ? R + 1 : 1);
@@ -443,7 +443,7 @@ int kan_hip_edge_abs_mean(int dtype, const void* s, const void* H, const void* b
   const size_t need = edge_ws_bytes(dtype, n, I, O, R, false);
   if (ws_bytes < need || (need > 0 && ws == nullptr))
     return set_error(KAN_ERR_WORKSPACE, "edge_abs_mean: workspace of %zu bytes is smaller than the %zu required", ws_bytes, need);
-  const int splits = need > 0 ? edge_pick_splits(n, I, O) : 1;
+  const int splits = need > 0 ? edge_pick_splits(dtype, n, I, O, R) : 1;
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (dtype == KAN_DTYPE_F32)
     return launch_edge_forward<float>(static_cast<const float*>(s), static_cast<const float*>(H),
@@ -468,7 +468,7 @@ int kan_hip_edge_abs_mean_backward(int dtype, const void* ga, const void* s, con
   const size_t need = want_params ? edge_ws_bytes(dtype, n, I, O, R, true) : 0;
   if (ws_bytes < need || (need > 0 && ws == nullptr))
     return set_error(KAN_ERR_WORKSPACE, "edge_abs_mean_backward: workspace of %zu bytes is smaller than the %zu required", ws_bytes, need);
-  const int splits = need > 0 ? edge_pick_splits(n, I, O) : 1;
+  const int splits = need > 0 ? edge_pick_splits(dtype, n, I, O, R) : 1;
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (dtype == KAN_DTYPE_F32)
     return launch_edge_backward<float>(

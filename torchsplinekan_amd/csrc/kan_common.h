@@ -139,6 +139,18 @@ int launch_edge_backward(const T* ga, const T* s, const T* H, const T* bw, const
                          T* dH, T* dbw, T* dW, T* part, int splits, int64_t n, int64_t I,
                          int64_t O, int64_t R, hipStream_t st);
 
-int edge_pick_splits(int64_t n, int64_t I, int64_t O);
+// Sample splits of the edge statistic (dtype code selects the fp32 MFMA or
+// the fp64 VALU kernels, which partition differently).
+int edge_pick_splits(int dtype, int64_t n, int64_t I, int64_t O, int64_t R);
+
+// fp32 MFMA kernels of the edge statistic (kan_edge_mfma.hip).
+int edge_mfma_splits(int64_t n, int64_t I, int64_t O, int64_t R);
+int launch_edge_forward_mfma(const float* s, const float* H, const float* bw, const float* W,
+                             float* a, float* part, int splits, int64_t n, int64_t I, int64_t O,
+                             int64_t R, hipStream_t st);
+int launch_edge_backward_mfma(const float* ga, const float* s, const float* H, const float* bw,
+                              const float* W, float* ds, float* dH, float* dbw, float* dW,
+                              float* part, int splits, int64_t n, int64_t I, int64_t O, int64_t R,
+                              hipStream_t st);
 
 }  // namespace kan

@@ -269,7 +269,8 @@ inline int fin_blocks(int64_t total) {
 
 }  // namespace
 
-int edge_pick_splits(int64_t n, int64_t I, int64_t O) {
+int edge_pick_splits(int dtype, int64_t n, int64_t I, int64_t O, int64_t R) {
+  if (dtype == KAN_DTYPE_F32) return edge_mfma_splits(n, I, O, R);
   const int64_t blocks = ceil_div(O, kEdgeThreads) * I;
   const int64_t target = 4LL * device_cu_count();
   int64_t s = ceil_div(target, blocks > 0 ? blocks : 1);
@@ -337,15 +338,25 @@ int launch_edge_backward(const T* ga, const T* s, const T* H, const T* bw, const
   return KAN_OK;
 }
 
-template int launch_edge_forward<float>(const float*, const float*, const float*, const float*,
-                                        float*, float*, int, int64_t, int64_t, int64_t, int64_t,
-                                        hipStream_t);
+template <>
+int launch_edge_forward<float>(const float* s, const float* H, const float* bw, const float* W,
+                               float* a, float* part, int splits, int64_t n, int64_t I,
+                               int64_t O, int64_t R, hipStream_t st) {
+  return launch_edge_forward_mfma(s, H, bw, W, a, part, splits, n, I, O, R, st);
+}
+
+template <>
+int launch_edge_backward<float>(const float* ga, const float* s, const float* H, const float* bw,
+                                const float* W, float* ds, float* dH, float* dbw, float* dW,
+                                float* part, int splits, int64_t n, int64_t I, int64_t O,
+                                int64_t R, hipStream_t st) {
+  return launch_edge_backward_mfma(ga, s, H, bw, W, ds, dH, dbw, dW, part, splits, n, I, O, R,
+                                   st);
+}
+
 template int launch_edge_forward<double>(const double*, const double*, const double*,
                                          const double*, double*, double*, int, int64_t, int64_t,
                                          int64_t, int64_t, hipStream_t);
-template int launch_edge_backward<float>(const float*, const float*, const float*, const float*,
-                                         const float*, float*, float*, float*, float*, float*,
-                                         int, int64_t, int64_t, int64_t, int64_t, hipStream_t);
 template int launch_edge_backward<double>(const double*, const double*, const double*,
                                           const double*, const double*, double*, double*,
                                           double*, double*, double*, int, int64_t, int64_t,

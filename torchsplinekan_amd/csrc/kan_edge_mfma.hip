@@ -1,0 +1,487 @@
+// fp32 edge statistic on MFMA.  For one input feature i the edge values of
+// a sample block are a small matrix product,
+//     phi_i[n, o] = sum_c Hc[n, c] Wc[o, c],   c = 0..R  (K = R + 1),
+// with the augmented rows Hc[n] = [s[n,i], H[n,i,0..R-1]] and
+// Wc[o] = [bw[o,i], W[o,i,0..R-1]], so phi never leaves registers:
+//   forward   a[o,i]   = (1/n) sum_n |phi[n,o]|
+//   params    dWc[o,c] = sum_n g[n,o] Hc[n,c]       g = ga[o,i] sign(phi) / n
+//   inputs    dHc[n,c] = sum_o g[n,o] Wc[o,c]
+// All products run v_mfma_f32_16x16x4f32 on 16x16 tiles.  Operand lane
+// (q = lane/16, r = lane%16) supplies row (or column) r at k = 4s + q of
+// step s; the accumulator of lane (q, r) holds column r, rows 4q + v
+// (v = 0..3).  The backward kernels feed that accumulator directly as the
+// operand of a second MFMA whose contraction index runs over those rows:
+// step v of the second product, lane group q, uses k = 4q + v -- exactly the
+// lane's own accumulator entry v -- and the other operand is loaded in the
+// same k order (a permutation of the sum, not of the result).  The small
+// dimension R + 1 is padded to whole k-steps of 4 and column tiles of 16.
+// Replaces csrc/kan_reg_cuda.cu:34-238 for float32 (float64 keeps the VALU
+// kernels of kan_edge.hip).  Sums over samples may be split across
+// workgroups; each split writes its own partial slice, added in a fixed order
+// by the finalize kernels, so results are deterministic.
+
+#include "kan_common.h"
+
+namespace kan {
+namespace {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kEdgeMfThreads = 256;  // 4 waves
+constexpr int kOT = 8;               // 16-wide output tiles per wave (128 outputs)
+constexpr int kBlockOut = 4 * kOT * 16;
+
+__device__ __forceinline__ f32x4 mfma16(float a, float b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ f32x4 zero4() {
+  f32x4 z;
+  z[0] = z[1] = z[2] = z[3] = 0.0f;
+  return z;
+}
+
+__device__ __forceinline__ float sign_f(float v) { return (float)((v > 0.0f) - (v < 0.0f)); }
+
+// augmented sample value Hc[n, c]
+__device__ __forceinline__ float hc_val(const float* __restrict__ s, const float* __restrict__ H,
+                                        int64_t n, int I, int i, int R, int c) {
+  const int64_t f = n * I + i;
+  if (c == 0) return s != nullptr ? s[f] : 0.0f;
+  return H[f * R + (c - 1)];
+}
+
+// augmented weight value Wc[o, c]
+__device__ __forceinline__ float wc_val(const float* __restrict__ bw, const float* __restrict__ W,
+                                        int64_t o, int I, int i, int R, int c) {
+  const int64_t e = o * I + i;
+  if (c == 0) return bw != nullptr ? bw[e] : 0.0f;
+  return W[e * R + (c - 1)];
+}
+
+struct EdgeGeom {
+  int64_t n;
+  int I, O, R;
+  int64_t per_split;  // samples per split (multiple of 16)
+  int ochunks;        // output chunks of kBlockOut
+  int splits;
+};
+
+// Forward: block (i, output chunk, split); wave w owns kOT output tiles.
+// KS = ceil((R+1)/4) k-steps.
+template <int KS>
+__global__ __launch_bounds__(kEdgeMfThreads) void edge_fwd_mfma_kernel(
+    const float* __restrict__ s, const float* __restrict__ H, const float* __restrict__ bw,
+    const float* __restrict__ W, float* __restrict__ out, EdgeGeom g, int final_out) {
+  const int64_t bid = blockIdx.x;
+  const int i = (int)(bid % g.I);
+  const int oc = (int)((bid / g.I) % g.ochunks);
+  const int split = (int)(bid / ((int64_t)g.I * g.ochunks));
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int q = lane >> 4, r = lane & 15;
+  const int obase = oc * kBlockOut + wave * kOT * 16;
+  if (obase >= g.O) return;
+  const int R1 = g.R + 1;
+
+  float w[kOT][KS];
+#pragma unroll
+  for (int t = 0; t < kOT; ++t) {
+    const int o = obase + t * 16 + r;
+#pragma unroll
+    for (int k = 0; k < KS; ++k) {
+      const int c = 4 * k + q;
+      w[t][k] = (o < g.O && c < R1) ? wc_val(bw, W, o, g.I, i, g.R, c) : 0.0f;
+    }
+  }
+  float tot[kOT];
+#pragma unroll
+  for (int t = 0; t < kOT; ++t) tot[t] = 0.0f;
+
+  const int64_t nb = (int64_t)split * g.per_split;
+  const int64_t ne = min(g.n, nb + g.per_split);
+  for (int64_t n0 = nb; n0 < ne; n0 += 16) {
+    const int64_t nn = n0 + r;
+    float a[KS];
+#pragma unroll
+    for (int k = 0; k < KS; ++k) {
+      const int c = 4 * k + q;
+      a[k] = (nn < ne && c < R1) ? hc_val(s, H, nn, g.I, i, g.R, c) : 0.0f;
+    }
+#pragma unroll
+    for (int t = 0; t < kOT; ++t) {
+      f32x4 acc = zero4();
+#pragma unroll
+      for (int k = 0; k < KS; ++k) acc = mfma16(a[k], w[t][k], acc);
+      tot[t] += (fabsf(acc[0]) + fabsf(acc[1])) + (fabsf(acc[2]) + fabsf(acc[3]));
+    }
+  }
+  // combine the four row groups of each column in a fixed order
+#pragma unroll
+  for (int t = 0; t < kOT; ++t) {
+    const float s1 = tot[t] + __shfl_xor(tot[t], 16);
+    const float s2 = s1 + __shfl_xor(s1, 32);
+    const int o = obase + t * 16 + r;
+    if (q == 0 && o < g.O) {
+      const int64_t e = (int64_t)o * g.I + i;
+      if (final_out) out[e] = s2 / (float)g.n;
+      else out[(int64_t)split * g.O * g.I + e] = s2;
+    }
+  }
+}
+
+// Parameter gradients: block (i, output chunk, split).  Per 16-sample tile:
+// phi (rows n, columns o) -> g in registers -> dWc[o, c] += sum_n g Hc with
+// the accumulator entries as the A operand.  CT column tiles of 16 cover c.
+template <int KS, int CT>
+__global__ __launch_bounds__(kEdgeMfThreads) void edge_param_mfma_kernel(
+    const float* __restrict__ ga, const float* __restrict__ s, const float* __restrict__ H,
+    const float* __restrict__ bw, const float* __restrict__ W, float* __restrict__ dbw,
+    float* __restrict__ dW, float* __restrict__ part, EdgeGeom g, int final_out) {
+  const int64_t bid = blockIdx.x;
+  const int i = (int)(bid % g.I);
+  const int oc = (int)((bid / g.I) % g.ochunks);
+  const int split = (int)(bid / ((int64_t)g.I * g.ochunks));
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int q = lane >> 4, r = lane & 15;
+  const int obase = oc * kBlockOut + wave * kOT * 16;
+  if (obase >= g.O) return;
+  const int R1 = g.R + 1;
+  const float inv_n = 1.0f / (float)g.n;
+
+  float w[kOT][KS], gav[kOT];
+#pragma unroll
+  for (int t = 0; t < kOT; ++t) {
+    const int o = obase + t * 16 + r;
+    gav[t] = o < g.O ? ga[(int64_t)o * g.I + i] * inv_n : 0.0f;
+#pragma unroll
+    for (int k = 0; k < KS; ++k) {
+      const int c = 4 * k + q;
+      w[t][k] = (o < g.O && c < R1) ? wc_val(bw, W, o, g.I, i, g.R, c) : 0.0f;
+    }
+  }
+  f32x4 dacc[kOT][CT];
+#pragma unroll
+  for (int t = 0; t < kOT; ++t)
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) dacc[t][ct] = zero4();
+
+  const int64_t nb = (int64_t)split * g.per_split;
+  const int64_t ne = min(g.n, nb + g.per_split);
+  for (int64_t n0 = nb; n0 < ne; n0 += 16) {
+    const int64_t nn = n0 + r;
+    float a[KS];
+#pragma unroll
+    for (int k = 0; k < KS; ++k) {
+      const int c = 4 * k + q;
+      a[k] = (nn < ne && c < R1) ? hc_val(s, H, nn, g.I, i, g.R, c) : 0.0f;
+    }
+    // B operand of the second product: Hc[n0 + 4q + v, 16ct + r]
+    float hb[CT][4];
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) {
+      const int c = ct * 16 + r;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int64_t nk = n0 + 4 * q + v;
+        hb[ct][v] = (nk < ne && c < R1) ? hc_val(s, H, nk, g.I, i, g.R, c) : 0.0f;
+      }
+    }
+#pragma unroll
+    for (int t = 0; t < kOT; ++t) {
+      f32x4 acc = zero4();
+#pragma unroll
+      for (int k = 0; k < KS; ++k) acc = mfma16(a[k], w[t][k], acc);
+      float gv[4];
+#pragma unroll
+      for (int v = 0; v < 4; ++v) gv[v] = gav[t] * sign_f(acc[v]);
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) dacc[t][ct] = mfma16(gv[v], hb[ct][v], dacc[t][ct]);
+    }
+  }
+  // dacc[t][ct]: lane (q, r) holds column c = 16ct + r, rows o = obase + 16t + 4q + v
+#pragma unroll
+  for (int t = 0; t < kOT; ++t) {
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) {
+      const int c = ct * 16 + r;
+      if (c >= R1) continue;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int o = obase + t * 16 + 4 * q + v;
+        if (o >= g.O) continue;
+        const int64_t e = (int64_t)o * g.I + i;
+        const float val = dacc[t][ct][v];
+        if (final_out) {
+          if (c == 0) {
+            if (dbw != nullptr) dbw[e] = val;
+          } else if (dW != nullptr) {
+            dW[e * g.R + (c - 1)] = val;
+          }
+        } else {
+          part[((int64_t)split * g.O * g.I + e) * R1 + c] = val;
+        }
+      }
+    }
+  }
+}
+
+// Input gradients: block (i, sample block of 4 waves x NTW tiles of 16).
+// The feature's weights and ga/n are staged in LDS one output chunk at a
+// time; each wave computes phi^T tiles (rows o, columns n) for its samples,
+// g in registers, and dHc^T[c, n] += sum_o Wc[o, c] g[n, o] with the
+// accumulator entries as the B operand.
+constexpr int kInChunkFloats = 8192;  // LDS floats for one staged weight chunk
+constexpr int kInMaxRows = 1024;
+
+template <int KS, int CT, int NTW>
+__global__ __launch_bounds__(kEdgeMfThreads) void edge_input_mfma_kernel(
+    const float* __restrict__ ga, const float* __restrict__ s, const float* __restrict__ H,
+    const float* __restrict__ bw, const float* __restrict__ W, float* __restrict__ ds,
+    float* __restrict__ dH, EdgeGeom g, int oc_rows) {
+  __shared__ float wl[kInChunkFloats];
+  __shared__ float gl[kInMaxRows];
+  const int i = (int)(blockIdx.x % g.I);
+  const int64_t nbk = blockIdx.x / g.I;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int q = lane >> 4, r = lane & 15;
+  const int R1 = g.R + 1;
+  const int stride = R1 | 1;  // odd row stride of the staged weights
+  const float inv_n = 1.0f / (float)g.n;
+
+  // this wave's sample tiles: n0 = nbase + (j*4 + wave)*16
+  const int64_t nbase = nbk * (int64_t)(64 * NTW);
+  float a[NTW][KS];
+#pragma unroll
+  for (int j = 0; j < NTW; ++j) {
+    const int64_t nn = nbase + (int64_t)(j * 4 + wave) * 16 + r;
+#pragma unroll
+    for (int k = 0; k < KS; ++k) {
+      const int c = 4 * k + q;
+      a[j][k] = (nn < g.n && c < R1) ? hc_val(s, H, nn, g.I, i, g.R, c) : 0.0f;
+    }
+  }
+  f32x4 dacc[NTW][CT];
+#pragma unroll
+  for (int j = 0; j < NTW; ++j)
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) dacc[j][ct] = zero4();
+
+  for (int o0 = 0; o0 < g.O; o0 += oc_rows) {
+    const int orows = min(oc_rows, g.O - o0);
+    __syncthreads();
+    for (int e = threadIdx.x; e < oc_rows * R1; e += kEdgeMfThreads) {
+      const int oo = e / R1, c = e - oo * R1;
+      wl[oo * stride + c] = oo < orows ? wc_val(bw, W, o0 + oo, g.I, i, g.R, c) : 0.0f;
+    }
+    for (int e = threadIdx.x; e < oc_rows; e += kEdgeMfThreads)
+      gl[e] = e < orows ? ga[(int64_t)(o0 + e) * g.I + i] * inv_n : 0.0f;
+    __syncthreads();
+    for (int ot = 0; ot < orows; ot += 16) {
+      // A operand of phi^T: Wc[o = ot + r, c = 4k + q]
+      float wa[KS];
+#pragma unroll
+      for (int k = 0; k < KS; ++k) {
+        const int c = 4 * k + q;
+        wa[k] = c < R1 ? wl[(ot + r) * stride + c] : 0.0f;
+      }
+      // g scale of the accumulator rows o = ot + 4q + v
+      float gs[4];
+#pragma unroll
+      for (int v = 0; v < 4; ++v) gs[v] = gl[ot + 4 * q + v];
+      // A operand of the second product: Wc[o = ot + 4q + v, c = 16ct + r]
+      float wb[CT][4];
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct) {
+        const int c = ct * 16 + r;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) wb[ct][v] = c < R1 ? wl[(ot + 4 * q + v) * stride + c] : 0.0f;
+      }
+#pragma unroll
+      for (int j = 0; j < NTW; ++j) {
+        f32x4 acc = zero4();
+#pragma unroll
+        for (int k = 0; k < KS; ++k) acc = mfma16(wa[k], a[j][k], acc);
+        float gv[4];
+#pragma unroll
+        for (int v = 0; v < 4; ++v) gv[v] = gs[v] * sign_f(acc[v]);
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+          for (int v = 0; v < 4; ++v) dacc[j][ct] = mfma16(wb[ct][v], gv[v], dacc[j][ct]);
+      }
+    }
+  }
+  // dacc[j][ct]: lane (q, r) holds column n = tile + r, rows c = 16ct + 4q + v
+#pragma unroll
+  for (int j = 0; j < NTW; ++j) {
+    const int64_t nn = nbase + (int64_t)(j * 4 + wave) * 16 + r;
+    if (nn >= g.n) continue;
+    const int64_t f = nn * g.I + i;
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) {
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int c = ct * 16 + 4 * q + v;
+        if (c >= R1) continue;
+        const float val = dacc[j][ct][v];
+        if (c == 0) {
+          if (ds != nullptr) ds[f] = val;
+        } else if (dH != nullptr) {
+          dH[f * g.R + (c - 1)] = val;
+        }
+      }
+    }
+  }
+}
+
+__global__ void edge_fwd_finalize_f32(const float* __restrict__ part, float* __restrict__ a,
+                                      int splits, int64_t count, int64_t n) {
+  for (int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; e < count;
+       e += (int64_t)gridDim.x * blockDim.x) {
+    float v = part[e];
+    for (int s = 1; s < splits; ++s) v += part[s * count + e];
+    a[e] = v / (float)n;
+  }
+}
+
+__global__ void edge_param_finalize_f32(const float* __restrict__ part, float* __restrict__ dbw,
+                                        float* __restrict__ dW, int splits, int64_t count, int R) {
+  const int R1 = R + 1;
+  const int64_t total = count * R1;
+  for (int64_t x = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; x < total;
+       x += (int64_t)gridDim.x * blockDim.x) {
+    float v = part[x];
+    for (int s = 1; s < splits; ++s) v += part[s * total + x];
+    const int64_t e = x / R1;
+    const int c = (int)(x - e * R1);
+    if (c == 0) {
+      if (dbw != nullptr) dbw[e] = v;
+    } else if (dW != nullptr) {
+      dW[e * R + (c - 1)] = v;
+    }
+  }
+}
+
+inline int fin_blocks_f32(int64_t total) {
+  int64_t b = ceil_div(total, 256);
+  if (b > 65536) b = 65536;
+  return (int)(b < 1 ? 1 : b);
+}
+
+// k-steps KS = ceil((R+1)/4) (exact up to 4, then by class) and column tiles
+// CT = ceil(4 KS / 16) of the backward products.
+#define KAN_EDGE_MF_DISPATCH(R1, ...)                           \
+  do {                                                          \
+    const int ks_ = ((R1) + 3) / 4;                             \
+    if (ks_ <= 1) { constexpr int KS = 1, CT = 1; __VA_ARGS__; }   \
+    else if (ks_ == 2) { constexpr int KS = 2, CT = 1; __VA_ARGS__; } \
+    else if (ks_ == 3) { constexpr int KS = 3, CT = 1; __VA_ARGS__; } \
+    else if (ks_ == 4) { constexpr int KS = 4, CT = 1; __VA_ARGS__; } \
+    else if (ks_ <= 6) { constexpr int KS = 6, CT = 2; __VA_ARGS__; } \
+    else if (ks_ <= 8) { constexpr int KS = 8, CT = 2; __VA_ARGS__; } \
+    else if (ks_ <= 12) { constexpr int KS = 12, CT = 3; __VA_ARGS__; } \
+    else { constexpr int KS = 19, CT = 5; __VA_ARGS__; }        \
+  } while (0)
+
+}  // namespace
+
+int edge_mfma_splits(int64_t n, int64_t I, int64_t O, int64_t R) {
+  (void)R;
+  const int64_t ochunks = ceil_div(O, kBlockOut);
+  const int64_t blocks = I * ochunks;
+  const int64_t target = 8LL * device_cu_count();
+  int64_t s = ceil_div(target, blocks > 0 ? blocks : 1);
+  const int64_t cap = ceil_div(n, 256);  // at least 16 sample tiles per split
+  if (s > cap) s = cap;
+  if (s > 64) s = 64;
+  if (s < 1) s = 1;
+  return (int)s;
+}
+
+int launch_edge_forward_mfma(const float* s, const float* H, const float* bw, const float* W,
+                             float* a, float* part, int splits, int64_t n, int64_t I, int64_t O,
+                             int64_t R, hipStream_t st) {
+  if (O == 0 || I == 0) return KAN_OK;
+  if (splits > 1 && part == nullptr)
+    return set_error(KAN_ERR_WORKSPACE, "edge_abs_mean: missing workspace");
+  const int R1 = (int)R + 1;
+  EdgeGeom g;
+  g.n = n;
+  g.I = (int)I;
+  g.O = (int)O;
+  g.R = (int)R;
+  g.splits = splits;
+  g.per_split = round_up(ceil_div(n, splits), 16);
+  g.ochunks = (int)ceil_div(O, kBlockOut);
+  const int64_t blocks = I * g.ochunks * (int64_t)splits;
+  if (blocks > 2147483647LL) return set_error(KAN_ERR_LIMIT, "edge_abs_mean: too many blocks");
+  const bool fin = splits == 1;
+  TimedLaunch timed(kClassEdge, st, 2.0 * (double)n * (double)O * (double)I * (double)R1);
+  KAN_EDGE_MF_DISPATCH(R1, (void)CT; hipLaunchKernelGGL((edge_fwd_mfma_kernel<KS>),
+                                                          dim3((unsigned)blocks),
+                                                          dim3(kEdgeMfThreads), 0, st, s, H, bw,
+                                                          W, fin ? a : part, g, fin ? 1 : 0));
+  int rc = check_launch("edge_abs_mean");
+  if (rc != KAN_OK || fin) return rc;
+  hipLaunchKernelGGL(edge_fwd_finalize_f32, dim3(fin_blocks_f32(O * I)), dim3(256), 0, st, part,
+                     a, splits, O * I, n);
+  return check_launch("edge_abs_mean_finalize");
+}
+
+int launch_edge_backward_mfma(const float* ga, const float* s, const float* H, const float* bw,
+                              const float* W, float* ds, float* dH, float* dbw, float* dW,
+                              float* part, int splits, int64_t n, int64_t I, int64_t O, int64_t R,
+                              hipStream_t st) {
+  const int R1 = (int)R + 1;
+  EdgeGeom g;
+  g.n = n;
+  g.I = (int)I;
+  g.O = (int)O;
+  g.R = (int)R;
+  g.splits = splits;
+  g.per_split = round_up(ceil_div(n, splits), 16);
+  g.ochunks = (int)ceil_div(O, kBlockOut);
+  if ((dbw != nullptr || dW != nullptr) && O > 0 && I > 0) {
+    if (splits > 1 && part == nullptr)
+      return set_error(KAN_ERR_WORKSPACE, "edge_abs_mean_backward: missing workspace");
+    const int64_t blocks = I * g.ochunks * (int64_t)splits;
+    if (blocks > 2147483647LL)
+      return set_error(KAN_ERR_LIMIT, "edge_abs_mean_backward: too many blocks");
+    const bool fin = splits == 1;
+    TimedLaunch timed(kClassEdgeGrad, st, 4.0 * (double)n * (double)O * (double)I * (double)R1);
+    KAN_EDGE_MF_DISPATCH(R1, hipLaunchKernelGGL((edge_param_mfma_kernel<KS, CT>),
+                                                dim3((unsigned)blocks), dim3(kEdgeMfThreads), 0,
+                                                st, ga, s, H, bw, W, dbw, dW, part, g,
+                                                fin ? 1 : 0));
+    int rc = check_launch("edge_abs_mean_backward(params)");
+    if (rc != KAN_OK) return rc;
+    if (!fin) {
+      hipLaunchKernelGGL(edge_param_finalize_f32, dim3(fin_blocks_f32(O * I * R1)), dim3(256), 0,
+                         st, part, dbw, dW, splits, O * I, (int)R);
+      rc = check_launch("edge_abs_mean_backward(finalize)");
+      if (rc != KAN_OK) return rc;
+    }
+  }
+  if ((ds != nullptr || dH != nullptr) && n > 0 && I > 0 && O > 0) {
+    constexpr int NTW = 4;
+    const int64_t nblk = ceil_div(n, 64 * NTW);
+    const int64_t blocks = I * nblk;
+    if (blocks > 2147483647LL)
+      return set_error(KAN_ERR_LIMIT, "edge_abs_mean_backward: too many blocks");
+    // staged output rows per chunk: a multiple of 16 that fits the LDS stage
+    int oc_rows = (int)(kInChunkFloats / (R1 | 1)) / 16 * 16;
+    if (oc_rows > kInMaxRows) oc_rows = kInMaxRows;
+    if ((int64_t)oc_rows > round_up(O, 16)) oc_rows = (int)round_up(O, 16);
+    TimedLaunch timed(kClassEdgeGrad, st, 4.0 * (double)n * (double)O * (double)I * (double)R1);
+    KAN_EDGE_MF_DISPATCH(R1, hipLaunchKernelGGL((edge_input_mfma_kernel<KS, CT, NTW>),
+                                                dim3((unsigned)blocks), dim3(kEdgeMfThreads), 0,
+                                                st, ga, s, H, bw, W, ds, dH, g, oc_rows));
+    int rc = check_launch("edge_abs_mean_backward(inputs)");
+    if (rc != KAN_OK) return rc;
+  }
+  return KAN_OK;
+}
+
+}  // namespace kan
