@@ -31,8 +31,15 @@ def _edge_inputs(N, I, O, R, dtype, seed):
     return [t.to(dtype) for t in (s, H, bw, W, ga)]
 
 
-@pytest.mark.parametrize("shape", [(37, 5, 3, 4), (300, 16, 40, 8), (1000, 9, 70, 13),
-                                   (64, 3, 300, 68), (5000, 4, 6, 11)])
+# (N, I, O, R): every k-step class of the fp32 MFMA kernels (R+1 = 2, 5, 9, 12, 14, 21,
+# 30, 45, 69), outputs beyond one 512-wide block and beyond one staged 1024-row
+# chunk, ragged sample counts and a sample count that is split across blocks.
+SHAPES = [(37, 5, 3, 4), (300, 16, 40, 8), (1000, 9, 70, 13), (64, 3, 300, 68),
+          (5000, 4, 6, 11), (77, 3, 5, 1), (513, 2, 33, 20), (129, 3, 17, 29), (70, 2, 9, 44),
+          (200, 2, 1300, 11), (3000, 3, 600, 7)]
+
+
+@pytest.mark.parametrize("shape", SHAPES)
 @pytest.mark.parametrize("dtype", [torch.float64, torch.float32])
 @pytest.mark.parametrize("base", [True, False])
 def test_edge_abs_mean_and_backward_match_oracle(C, shape, dtype, base):

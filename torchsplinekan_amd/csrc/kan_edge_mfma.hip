@@ -99,14 +99,22 @@ __global__ __launch_bounds__(kEdgeMfThreads) void edge_fwd_mfma_kernel(
 
   const int64_t nb = (int64_t)split * g.per_split;
   const int64_t ne = min(g.n, nb + g.per_split);
-  for (int64_t n0 = nb; n0 < ne; n0 += 16) {
+  // A fragments of the next sample tile are loaded while the current one runs
+  float an[KS];
+  auto load_a = [&](int64_t n0) {
     const int64_t nn = n0 + r;
-    float a[KS];
 #pragma unroll
     for (int k = 0; k < KS; ++k) {
       const int c = 4 * k + q;
-      a[k] = (nn < ne && c < R1) ? hc_val(s, H, nn, g.I, i, g.R, c) : 0.0f;
+      an[k] = (nn < ne && c < R1) ? hc_val(s, H, nn, g.I, i, g.R, c) : 0.0f;
     }
+  };
+  if (nb < ne) load_a(nb);
+  for (int64_t n0 = nb; n0 < ne; n0 += 16) {
+    float a[KS];
+#pragma unroll
+    for (int k = 0; k < KS; ++k) a[k] = an[k];
+    if (n0 + 16 < ne) load_a(n0 + 16);
 #pragma unroll
     for (int t = 0; t < kOT; ++t) {
       f32x4 acc = zero4();
@@ -167,25 +175,37 @@ __global__ __launch_bounds__(kEdgeMfThreads) void edge_param_mfma_kernel(
 
   const int64_t nb = (int64_t)split * g.per_split;
   const int64_t ne = min(g.n, nb + g.per_split);
-  for (int64_t n0 = nb; n0 < ne; n0 += 16) {
+  // operands of the next sample tile are loaded while the current one runs:
+  // A of phi (Hc[n0 + r, 4k + q]) and B of the second product
+  // (Hc[n0 + 4q + v, 16ct + r])
+  float an[KS], hn[CT][4];
+  auto load_tile = [&](int64_t n0) {
     const int64_t nn = n0 + r;
-    float a[KS];
 #pragma unroll
     for (int k = 0; k < KS; ++k) {
       const int c = 4 * k + q;
-      a[k] = (nn < ne && c < R1) ? hc_val(s, H, nn, g.I, i, g.R, c) : 0.0f;
+      an[k] = (nn < ne && c < R1) ? hc_val(s, H, nn, g.I, i, g.R, c) : 0.0f;
     }
-    // B operand of the second product: Hc[n0 + 4q + v, 16ct + r]
-    float hb[CT][4];
 #pragma unroll
     for (int ct = 0; ct < CT; ++ct) {
       const int c = ct * 16 + r;
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
         const int64_t nk = n0 + 4 * q + v;
-        hb[ct][v] = (nk < ne && c < R1) ? hc_val(s, H, nk, g.I, i, g.R, c) : 0.0f;
+        hn[ct][v] = (nk < ne && c < R1) ? hc_val(s, H, nk, g.I, i, g.R, c) : 0.0f;
       }
     }
+  };
+  if (nb < ne) load_tile(nb);
+  for (int64_t n0 = nb; n0 < ne; n0 += 16) {
+    float a[KS], hb[CT][4];
+#pragma unroll
+    for (int k = 0; k < KS; ++k) a[k] = an[k];
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) hb[ct][v] = hn[ct][v];
+    if (n0 + 16 < ne) load_tile(n0 + 16);
 #pragma unroll
     for (int t = 0; t < kOT; ++t) {
       f32x4 acc = zero4();
