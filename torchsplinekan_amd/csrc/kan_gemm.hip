@@ -1,39 +1,47 @@
 // Dense contraction engine for the KAN forward and backward on gfx950 MFMA.
 //
-// The three contractions of a KANLinear step all run through this kernel
-// with different operand layouts (A = augmented basis [H | silu(x)],
+// The three contractions of a KANLinear step all run through this file with
+// different operand layouts (A = augmented basis [H | silu(x)],
 // W = augmented weight [coef*scaler | base_weight], D = grad_output):
 //   forward  Y[n,o]  = sum_k A[n,k] W[o,k]     (NT: both K-contiguous)
 //   params   G[o,k]  = sum_n D[n,o] A[n,k]     (TN: both M/N-contiguous)
 //   input    E[n,k]  = sum_o D[n,o] W[o,k]     (NN)
 // They replace the cuBLAS calls of csrc/kan_cuda.cu:521-529, 579-604.
 //
-// One kernel template, configured per dtype and layout (tile, waves, MFMA
-// shape, pipelining), chosen by measurement on MI355X at the c3 shapes:
-//   fp32 NT   128x128 tile, BK 32, 2x2 waves of 64x64, v_mfma_f32_32x32x2f32,
-//             software-pipelined main loop;
-//   fp32 TN/NN 256x128 tile, BK 16, 4x2 waves of 64x64, v_mfma_f32_16x16x4f32;
-//   fp64      128x128 tile, BK 16, 2x2 waves, v_mfma_f64_16x16x4f64.
-// Operand slabs (BK wide) are staged through LDS with double buffering: the
-// next slab's global loads are in flight while the current slab feeds the
-// MFMAs.  Each operand keeps its global layout in LDS:
+// fp32 runs on gemm_pipe_kernel, a software-pipelined v_mfma_f32_32x32x2f32
+// main loop, in one of two tile configurations picked per problem by a cost
+// model (pick_cfg_f32):
+//   big    256x256 block tile, 4 waves of 128x128 (256 accumulator registers
+//          per lane), one block per CU;
+//   small  128x128 block tile, 4 waves of 64x64, two blocks per CU (for
+//          problems with too few big tiles to fill the chip).
+// fp64 runs on gemm_kernel: 128x128 tile, 2x2 waves, v_mfma_f64_16x16x4f64.
+//
+// Operand slabs (BK deep) are staged through LDS with double buffering.  Each
+// operand keeps its global layout in LDS:
 //   K-contiguous operand  -> LDS [rows][BK+4]; a lane reads 4 consecutive k
 //                            with one 16-byte ds_read.  Within each k-group
 //                            of the MFMA the k order is permuted identically
 //                            for A and B (step s, lane group q uses
 //                            k = KG*g + 4q + s), which leaves the sum unchanged;
 //   MN-contiguous operand -> LDS [BK][rows+4]; a lane reads one element.
-// Tiles whose rows and K range are entirely in bounds (and whose operands are
-// 16-byte aligned) take branch-free vector loads; edge tiles take a guarded
-// path.  The pipelined loop keeps two register sets of MFMA fragments: the
-// fragments of k-group g+1 are read from LDS while the MFMAs of group g run,
-// and the hand-over to the next slab (LDS store, barrier, first fragment
-// read) is issued ahead of the last group's MFMAs.
+// Pipeline of gemm_pipe_kernel, per K slab kt (NG k-groups of 8):
+//   group 0 issues the LDS stores of slab kt+1 (held in registers) and the
+//   global loads of slab kt+2, interleaved one-for-one with its MFMAs by
+//   scheduling-group barriers; every group reads the fragments of the next
+//   group from LDS while its own MFMAs run; the barrier that publishes slab
+//   kt+1 sits before the last group's MFMAs, which then cover the first
+//   fragment reads of slab kt+1.  The loop body is branch-free: whole tiles
+//   (every row, column and k in range, 16-byte aligned operands) take vector
+//   loads, edge tiles take a separately compiled loop with clamped scalar
+//   loads and zero fill.
 // Scheduling: the linear workgroup id is remapped so that each XCD (dispatch
 // is round-robin over 8 XCDs) receives a contiguous range of tiles, visited
 // in groups of 8 row-tiles so that tiles running together on one XCD share
 // operand slabs in its L2.  Optional split-K writes partial products to
 // separate slices of C (reduced by the caller in a fixed order).
+
+#include <type_traits>
 
 #include "kan_common.h"
 
@@ -52,21 +60,6 @@ typedef double f64x4 __attribute__((ext_vector_type(4)));
 // MFMA shapes: operand fragment of lane (row, kq) and accumulator layout.
 template <typename T, int MF>
 struct Mfma;
-
-template <>
-struct Mfma<float, 16> {  // v_mfma_f32_16x16x4f32
-  typedef f32x4 acc_t;
-  static constexpr int kKG = 16;    // k per fragment group (4 steps x 4)
-  static constexpr int kNAcc = 4;
-  __device__ static __forceinline__ acc_t mma(float a, float b, acc_t c) {
-    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
-  }
-  __device__ static __forceinline__ int row(int lane) { return lane & 15; }
-  __device__ static __forceinline__ int kq(int lane) { return lane >> 4; }
-  __device__ static __forceinline__ int kofs(int g, int q) { return 16 * g + 4 * q; }
-  __device__ static __forceinline__ int out_row(int lane, int v) { return 4 * (lane >> 4) + v; }
-  __device__ static __forceinline__ int out_col(int lane) { return lane & 15; }
-};
 
 template <>
 struct Mfma<float, 32> {  // v_mfma_f32_32x32x2f32
@@ -102,13 +95,11 @@ struct Mfma<double, 16> {  // v_mfma_f64_16x16x4f64
 };
 
 // Kernel configuration: block tile BM x BN, K slab BK, WM x WN waves,
-// MFMA shape MF, pipelined main loop, minimum resident blocks per CU.
-template <typename T_, int BM_, int BN_, int BK_, int WM_, int WN_, int MF_, bool PIPE_,
-          int MINB_>
+// MFMA shape MF, minimum resident blocks per CU.
+template <typename T_, int BM_, int BN_, int BK_, int WM_, int WN_, int MF_, int MINB_>
 struct Cfg {
   typedef T_ T;
   static constexpr int BM = BM_, BN = BN_, BK = BK_, WM = WM_, WN = WN_, MF = MF_;
-  static constexpr bool PIPE = PIPE_;
   static constexpr int MINB = MINB_;
   static constexpr int kThreads = 64 * WM * WN;
   static constexpr int TM = BM / WM, TN = BN / WN;
@@ -117,9 +108,9 @@ struct Cfg {
   static_assert(BK % Mfma<T, MF>::kKG == 0, "slab must be whole k-groups");
 };
 
-using CfgF32NT = Cfg<float, 128, 128, 32, 2, 2, 32, true, 2>;
-using CfgF32MN = Cfg<float, 256, 128, 16, 4, 2, 16, false, 1>;
-using CfgF64 = Cfg<double, 128, 128, 16, 2, 2, 16, false, 1>;
+using CfgF32Big = Cfg<float, 256, 256, 32, 2, 2, 32, 1>;
+using CfgF32Small = Cfg<float, 128, 128, 32, 2, 2, 32, 2>;
+using CfgF64 = Cfg<double, 128, 128, 16, 2, 2, 16, 1>;
 
 template <typename T>
 struct GemmParams {
@@ -147,6 +138,33 @@ __device__ __forceinline__ int xcd_remap(int pid, int total) {
   const int per = total / kNumXcd, rem = total % kNumXcd;
   const int xcd = pid % kNumXcd, idx = pid / kNumXcd;
   return xcd * per + min(xcd, rem) + idx;
+}
+
+// Tile owned by this block: output origin, split and K range.
+struct TileCoords {
+  int64_t m0, n0, kbeg, kend;
+  int split, nkt;
+};
+
+template <class C, typename T>
+__device__ __forceinline__ TileCoords tile_coords(const GemmParams<T>& p) {
+  const int total = p.tiles_m * p.tiles_n * p.splits;
+  const int pid = xcd_remap(blockIdx.x, total);
+  const int per_split = p.tiles_m * p.tiles_n;
+  TileCoords tc;
+  tc.split = pid / per_split;
+  const int t = pid - tc.split * per_split;
+  const int group = kGroupM * p.tiles_n;
+  const int first_m = (t / group) * kGroupM;
+  const int gm = min(p.tiles_m - first_m, kGroupM);
+  const int tm = first_m + (t % group) % gm;
+  const int tn = (t % group) / gm;
+  tc.m0 = (int64_t)tm * C::BM;
+  tc.n0 = (int64_t)tn * C::BN;
+  tc.kbeg = (int64_t)tc.split * p.k_per_split;
+  tc.kend = min(p.K, tc.kbeg + p.k_per_split);
+  tc.nkt = tc.kend > tc.kbeg ? (int)ceil_div(tc.kend - tc.kbeg, C::BK) : 0;
+  return tc;
 }
 
 // Global -> register staging of one operand slab (ROWS x BK), in chunks of 4
@@ -180,27 +198,24 @@ struct SlabLoader {
     }
   }
 
-  // Edge slab: element-wise bounds (rows < rows, k < kend), zero fill.
+  // Edge slab (rows < rows, k < kend; k0 < kend and rows >= 1): every lane
+  // loads from an address clamped into the operand and selects zero where
+  // the element lies outside it, so the loop has no divergent branches.
   __device__ __forceinline__ void load_guarded(const T* __restrict__ src, int64_t ld, int64_t row0,
-                                               int64_t rows, int64_t k0, int64_t kend, bool vec) {
+                                               int64_t rows, int64_t k0, int64_t kend) {
 #pragma unroll
     for (int p = 0; p < kPer; ++p) {
       int64_t r, kk;
       coords(threadIdx.x + p * NT, row0, k0, r, kk);
-      const bool full = KCONT ? ((r < rows) && (kk + 3 < kend)) : ((kk < kend) && (r + 3 < rows));
-      if (vec && full) {
-        reg[p] = *reinterpret_cast<const Vec4<T>*>(KCONT ? src + r * ld + kk : src + kk * ld + r);
-      } else {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          T v = T(0);
-          if (KCONT) {
-            if (r < rows && kk + j < kend) v = src[r * ld + kk + j];
-          } else {
-            if (kk < kend && r + j < rows) v = src[kk * ld + r + j];
-          }
-          reg[p].v[j] = v;
-        }
+      for (int j = 0; j < 4; ++j) {
+        const int64_t rr = KCONT ? r : r + j;
+        const int64_t kj = KCONT ? kk + j : kk;
+        const bool in = (rr < rows) && (kj < kend);
+        const int64_t rc = rr < rows ? rr : rows - 1;
+        const int64_t kc = kj < kend ? kj : kend - 1;
+        const T v = KCONT ? src[rc * ld + kc] : src[kc * ld + rc];
+        reg[p].v[j] = in ? v : T(0);
       }
     }
   }
@@ -231,6 +246,30 @@ __device__ __forceinline__ void read_frag(const T* __restrict__ lds, int row, in
   }
 }
 
+// Writes the wave's accumulators to C (+ split slice), bounds-checked.
+template <class C, typename Acc>
+__device__ __forceinline__ void store_tile(const GemmParams<typename C::T>& p, const TileCoords& tc,
+                                           const Acc (&acc)[C::FM][C::FN], int wm, int wn,
+                                           int lane) {
+  typedef Mfma<typename C::T, C::MF> M;
+  typename C::T* Cp = p.C + (int64_t)tc.split * p.split_stride;
+#pragma unroll
+  for (int i = 0; i < C::FM; ++i) {
+#pragma unroll
+    for (int j = 0; j < C::FN; ++j) {
+      const int64_t col = tc.n0 + wn * C::TN + j * C::MF + M::out_col(lane);
+      if (col >= p.N) continue;
+#pragma unroll
+      for (int v = 0; v < M::kNAcc; ++v) {
+        const int64_t row = tc.m0 + wm * C::TM + i * C::MF + M::out_row(lane, v);
+        if (row < p.M) Cp[row * p.ldc + col] = acc[i][j][v];
+      }
+    }
+  }
+}
+
+// ---- fp64: double-buffered LDS slabs, one fragment set per k-group --------
+
 template <class C, bool AK, bool BKC>
 __global__ __launch_bounds__(C::kThreads, C::MINB) void gemm_kernel(GemmParams<typename C::T> p) {
   typedef typename C::T T;
@@ -242,23 +281,7 @@ __global__ __launch_bounds__(C::kThreads, C::MINB) void gemm_kernel(GemmParams<t
   __shared__ __align__(16) T lds_a[2][SA::kElems];
   __shared__ __align__(16) T lds_b[2][SB::kElems];
 
-  const int total = p.tiles_m * p.tiles_n * p.splits;
-  const int pid = xcd_remap(blockIdx.x, total);
-  const int per_split = p.tiles_m * p.tiles_n;
-  const int split = pid / per_split;
-  const int t = pid - split * per_split;
-  const int group = kGroupM * p.tiles_n;
-  const int first_m = (t / group) * kGroupM;
-  const int gm = min(p.tiles_m - first_m, kGroupM);
-  const int tm = first_m + (t % group) % gm;
-  const int tn = (t % group) / gm;
-
-  const int64_t m0 = (int64_t)tm * BM;
-  const int64_t n0 = (int64_t)tn * BN;
-  const int64_t kbeg = (int64_t)split * p.k_per_split;
-  const int64_t kend = min(p.K, kbeg + p.k_per_split);
-  const int nkt = kend > kbeg ? (int)ceil_div(kend - kbeg, BK) : 0;
-
+  const TileCoords tc = tile_coords<C>(p);
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int wm = wave / C::WN, wn = wave % C::WN;
   const int rl = M::row(lane), q = M::kq(lane);
@@ -273,25 +296,134 @@ __global__ __launch_bounds__(C::kThreads, C::MINB) void gemm_kernel(GemmParams<t
 
   SlabLoader<T, BM, BK, AK, NT> la;
   SlabLoader<T, BN, BK, BKC, NT> lb;
-  const bool full = p.vec && (m0 + BM <= p.M) && (n0 + BN <= p.N) && ((kend - kbeg) % BK == 0);
+  const bool full = p.vec && (tc.m0 + BM <= p.M) && (tc.n0 + BN <= p.N) &&
+                    ((tc.kend - tc.kbeg) % BK == 0);
   auto gload = [&](int slab) {
-    const int64_t k0 = kbeg + (int64_t)slab * BK;
+    const int64_t k0 = tc.kbeg + (int64_t)slab * BK;
     if (full) {
-      la.load_full(p.A, p.lda, m0, k0);
-      lb.load_full(p.B, p.ldb, n0, k0);
+      la.load_full(p.A, p.lda, tc.m0, k0);
+      lb.load_full(p.B, p.ldb, tc.n0, k0);
     } else {
-      la.load_guarded(p.A, p.lda, m0, p.M, k0, kend, p.vec != 0);
-      lb.load_guarded(p.B, p.ldb, n0, p.N, k0, kend, p.vec != 0);
+      la.load_guarded(p.A, p.lda, tc.m0, p.M, k0, tc.kend);
+      lb.load_guarded(p.B, p.ldb, tc.n0, p.N, k0, tc.kend);
     }
   };
-  T fa[2][FM][4], fb[2][FN][4];
-  auto fread = [&](int buf, int g, int slot) {
+  T fa[FM][4], fb[FN][4];
+
+  if (tc.nkt > 0) {
+    gload(0);
+    la.store(lds_a[0]);
+    lb.store(lds_b[0]);
+    __syncthreads();
+    for (int kt = 0; kt < tc.nkt; ++kt) {
+      const int cur = kt & 1;
+      const bool more = kt + 1 < tc.nkt;
+      if (more) gload(kt + 1);
 #pragma unroll
-    for (int i = 0; i < FM; ++i)
-      read_frag<T, BM, BK, AK>(lds_a[buf], wm * C::TM + i * C::MF + rl, M::kofs(g, q), fa[slot][i]);
+      for (int g = 0; g < NG; ++g) {
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+          read_frag<T, BM, BK, AK>(lds_a[cur], wm * C::TM + i * C::MF + rl, M::kofs(g, q), fa[i]);
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+          read_frag<T, BN, BK, BKC>(lds_b[cur], wn * C::TN + j * C::MF + rl, M::kofs(g, q), fb[j]);
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+#pragma unroll
+          for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int j = 0; j < FN; ++j) acc[i][j] = M::mma(fa[i][s], fb[j][s], acc[i][j]);
+      }
+      if (more) {
+        la.store(lds_a[cur ^ 1]);
+        lb.store(lds_b[cur ^ 1]);
+      }
+      __syncthreads();
+    }
+  }
+  store_tile<C>(p, tc, acc, wm, wn, lane);
+}
+
+// ---- fp32: software-pipelined main loop ------------------------------------
+
+template <int N_>
+struct IC {
+  static constexpr int value = N_;
+};
+
+// max(0, |[A, B) intersect [LO, HI)|)
+template <int A, int B, int LO, int HI>
+struct Overlap {
+  static constexpr int lo = A > LO ? A : LO;
+  static constexpr int hi = B < HI ? B : HI;
+  static constexpr int v = hi > lo ? hi - lo : 0;
+};
+
+// Scheduling-group barriers that spread R fragment reads, W LDS stores and L
+// global loads (in that order) evenly over KMF MFMAs: MFMA i is followed by
+// the memory operations [i*T/KMF, (i+1)*T/KMF) of the T = R+W+L.
+template <int I, int KMF, int R, int W, int L>
+struct SchedSeq {
+  static __device__ __forceinline__ void run() {
+    constexpr int T = R + W + L;
+    constexpr int a = I * T / KMF, b = (I + 1) * T / KMF;
+    constexpr int nr = Overlap<a, b, 0, R>::v;
+    constexpr int nw = Overlap<a, b, R, R + W>::v;
+    constexpr int nl = Overlap<a, b, R + W, T>::v;
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+    if constexpr (nr > 0) __builtin_amdgcn_sched_group_barrier(0x100, nr, 0);  // DS read
+    if constexpr (nw > 0) __builtin_amdgcn_sched_group_barrier(0x200, nw, 0);  // DS write
+    if constexpr (nl > 0) __builtin_amdgcn_sched_group_barrier(0x020, nl, 0);  // VMEM read
+    SchedSeq<I + 1, KMF, R, W, L>::run();
+  }
+};
+template <int KMF, int R, int W, int L>
+struct SchedSeq<KMF, KMF, R, W, L> {
+  static __device__ __forceinline__ void run() {}
+};
+
+template <class C, bool AK, bool BKC>
+__global__ __launch_bounds__(C::kThreads, C::MINB) void gemm_pipe_kernel(GemmParams<float> p) {
+  typedef float T;
+  typedef Mfma<float, C::MF> M;
+  constexpr int BM = C::BM, BN = C::BN, BK = C::BK, NT = C::kThreads;
+  constexpr int FM = C::FM, FN = C::FN, NG = BK / M::kKG;
+  static_assert(NG % 2 == 0, "slab must hold an even number of k-groups");
+  typedef Slab<BM, BK, AK> SA;
+  typedef Slab<BN, BK, BKC> SB;
+  typedef SlabLoader<T, BM, BK, AK, NT> LA;
+  typedef SlabLoader<T, BN, BK, BKC, NT> LB;
+  // memory operations per slab (stores, loads) and per k-group (fragment reads)
+  constexpr int kDSW = LA::kPer + LB::kPer;
+  constexpr int kGLD = LA::kPer + LB::kPer;
+  constexpr int kDSR = (AK ? FM : 4 * FM) + (BKC ? FN : 4 * FN);
+  constexpr int kMF = 4 * FM * FN;  // MFMAs per k-group
+  __shared__ __align__(16) T lds_a[2][SA::kElems];
+  __shared__ __align__(16) T lds_b[2][SB::kElems];
+
+  const TileCoords tc = tile_coords<C>(p);
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int wm = wave / C::WN, wn = wave % C::WN;
+  const int rl = M::row(lane), q = M::kq(lane);
+
+  typename M::acc_t acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
 #pragma unroll
     for (int j = 0; j < FN; ++j)
-      read_frag<T, BN, BK, BKC>(lds_b[buf], wn * C::TN + j * C::MF + rl, M::kofs(g, q), fb[slot][j]);
+#pragma unroll
+      for (int v = 0; v < M::kNAcc; ++v) acc[i][j][v] = T(0);
+
+  LA la;
+  LB lb;
+  T fa[2][FM][4], fb[2][FN][4];
+  auto fread = [&](const T* a_lds, const T* b_lds, int g, int slot) {
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+      read_frag<T, BM, BK, AK>(a_lds, wm * C::TM + i * C::MF + rl, M::kofs(g, q), fa[slot][i]);
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+      read_frag<T, BN, BK, BKC>(b_lds, wn * C::TN + j * C::MF + rl, M::kofs(g, q), fb[slot][j]);
   };
   auto mfmas = [&](int slot) {
 #pragma unroll
@@ -301,69 +433,66 @@ __global__ __launch_bounds__(C::kThreads, C::MINB) void gemm_kernel(GemmParams<t
 #pragma unroll
         for (int j = 0; j < FN; ++j) acc[i][j] = M::mma(fa[slot][i][s], fb[slot][j][s], acc[i][j]);
   };
-
-  if (nkt > 0) {
-    gload(0);
-    la.store(lds_a[0]);
-    lb.store(lds_b[0]);
-    if (C::PIPE) {
-      if (nkt > 1) gload(1);
-      __syncthreads();
-      fread(0, 0, 0);
-      int slot = 0;
-      for (int kt = 0; kt < nkt; ++kt) {
-        const int cur = kt & 1;
-#pragma unroll
-        for (int g = 0; g < NG; ++g) {
-          if (g + 1 < NG) {
-            fread(cur, g + 1, slot ^ 1);
-          } else if (kt + 1 < nkt) {
-            // hand-over: slab kt+1 into the other buffer (last read during
-            // slab kt-1, before the previous barrier), loads of slab kt+2
-            la.store(lds_a[cur ^ 1]);
-            lb.store(lds_b[cur ^ 1]);
-            if (kt + 2 < nkt) gload(kt + 2);
-            __syncthreads();
-            fread(cur ^ 1, 0, slot ^ 1);
-          }
-          mfmas(slot);
-          slot ^= 1;
-        }
-      }
+  auto gload = [&](int slab, auto full_c) {
+    const int64_t k0 = tc.kbeg + (int64_t)slab * BK;
+    if (decltype(full_c)::value) {
+      la.load_full(p.A, p.lda, tc.m0, k0);
+      lb.load_full(p.B, p.ldb, tc.n0, k0);
     } else {
-      __syncthreads();
-      for (int kt = 0; kt < nkt; ++kt) {
-        const int cur = kt & 1;
-        const bool more = kt + 1 < nkt;
-        if (more) gload(kt + 1);
+      la.load_guarded(p.A, p.lda, tc.m0, p.M, k0, tc.kend);
+      lb.load_guarded(p.B, p.ldb, tc.n0, p.N, k0, tc.kend);
+    }
+  };
+  // One slab.  STORE: registers of slab kt+1 -> the other LDS buffer;
+  // LOAD: global loads of slab kt+2; NEXT: barrier + first fragments of kt+1.
+  auto slab = [&](int kt, auto store_c, auto load_c, auto next_c, auto full_c) {
+    constexpr bool STORE = decltype(store_c)::value != 0;
+    constexpr bool LOAD = decltype(load_c)::value != 0;
+    constexpr bool NEXT = decltype(next_c)::value != 0;
+    const int cur = kt & 1;
 #pragma unroll
-        for (int g = 0; g < NG; ++g) {
-          fread(cur, g, 0);
-          mfmas(0);
-        }
-        if (more) {
+    for (int g = 0; g < NG; ++g) {
+      if (g == 0) {
+        if (STORE) {
           la.store(lds_a[cur ^ 1]);
           lb.store(lds_b[cur ^ 1]);
         }
+        if (LOAD) gload(kt + 2, full_c);
+      }
+      if (g + 1 < NG) {
+        fread(lds_a[cur], lds_b[cur], g + 1, (g + 1) & 1);
+      } else if (NEXT) {
         __syncthreads();
+        fread(lds_a[cur ^ 1], lds_b[cur ^ 1], 0, 0);
       }
+      mfmas(g & 1);
+      if (g == 0 && STORE && LOAD) SchedSeq<0, kMF, kDSR, kDSW, kGLD>::run();
+      else if (g == 0 && STORE) SchedSeq<0, kMF, kDSR, kDSW, 0>::run();
+      else if (g + 1 < NG || NEXT) SchedSeq<0, kMF, kDSR, 0, 0>::run();
     }
-  }
-
-  T* Cp = p.C + (int64_t)split * p.split_stride;
-#pragma unroll
-  for (int i = 0; i < FM; ++i) {
-#pragma unroll
-    for (int j = 0; j < FN; ++j) {
-      const int64_t col = n0 + wn * C::TN + j * C::MF + M::out_col(lane);
-      if (col >= p.N) continue;
-#pragma unroll
-      for (int v = 0; v < M::kNAcc; ++v) {
-        const int64_t row = m0 + wm * C::TM + i * C::MF + M::out_row(lane, v);
-        if (row < p.M) Cp[row * p.ldc + col] = acc[i][j][v];
-      }
+  };
+  auto run = [&](auto full_c) {
+    gload(0, full_c);
+    la.store(lds_a[0]);
+    lb.store(lds_b[0]);
+    if (tc.nkt > 1) gload(1, full_c);
+    __syncthreads();
+    fread(lds_a[0], lds_b[0], 0, 0);
+    int kt = 0;
+    for (; kt + 2 < tc.nkt; ++kt) slab(kt, IC<1>(), IC<1>(), IC<1>(), full_c);
+    if (kt + 1 < tc.nkt) {
+      slab(kt, IC<1>(), IC<0>(), IC<1>(), full_c);
+      ++kt;
     }
+    slab(kt, IC<0>(), IC<0>(), IC<0>(), full_c);
+  };
+  if (tc.nkt > 0) {
+    const bool full = p.vec && (tc.m0 + BM <= p.M) && (tc.n0 + BN <= p.N) &&
+                      ((tc.kend - tc.kbeg) % BK == 0);
+    if (full) run(IC<1>());
+    else run(IC<0>());
   }
+  store_tile<C>(p, tc, acc, wm, wn, lane);
 }
 
 template <typename T>
@@ -371,60 +500,97 @@ bool vec_ok(const T* ptr, int64_t ld) {
   return ((reinterpret_cast<uintptr_t>(ptr) % (4 * sizeof(T))) == 0) && (ld % 4 == 0);
 }
 
-template <typename T>
-struct Select;
-template <>
-struct Select<float> {
-  typedef CfgF32NT NT;
-  typedef CfgF32MN TN;
-  typedef CfgF32MN NN;
-};
-template <>
-struct Select<double> {
-  typedef CfgF64 NT;
-  typedef CfgF64 TN;
-  typedef CfgF64 NN;
-};
+// ---- planning ----------------------------------------------------------------
 
-template <class C>
-void tiles_of(int64_t M, int64_t N, int64_t* tm, int64_t* tn) {
-  *tm = ceil_div(M, C::BM);
-  *tn = ceil_div(N, C::BN);
+// Tile configuration as seen by the cost model: block tile, slab depth,
+// resident blocks per CU and the measured fraction of the MFMA peak that one
+// CU sustains on whole tiles of this configuration (MI355X, c3 shapes).
+struct CfgModel {
+  int bm, bn, bk, blocks_per_cu;
+  double eff;
+};
+constexpr CfgModel kModelF32[2] = {{256, 256, 32, 1, 0.89}, {128, 128, 32, 2, 0.85}};
+constexpr CfgModel kModelF64 = {128, 128, 16, 1, 0.80};
+constexpr double kPeakPerCuF32 = 157.3e12 / 256.0;  // FP32 MFMA flop/s per CU
+constexpr double kPeakPerCuF64 = 78.6e12 / 256.0;
+constexpr double kStreamBytesPerS = 5.0e12;          // split-K partial-sum traffic
+
+// Estimated seconds for M x N x K with `splits` K-slices: whole waves of
+// resident blocks times the duration of one block, plus the split-K partial
+// traffic (written once, read once by the caller's reduction).
+double est_seconds(const CfgModel& c, double peak_per_cu, int64_t M, int64_t N, int64_t K,
+                   int splits, size_t elem) {
+  const int64_t cus = device_cu_count();
+  const int64_t tiles = ceil_div(M, c.bm) * ceil_div(N, c.bn) * splits;
+  const int64_t waves = ceil_div(tiles, cus * c.blocks_per_cu);
+  const int64_t kper = round_up(ceil_div(K > 0 ? K : 1, splits), c.bk);
+  const double block_s = 2.0 * c.bm * c.bn * (double)kper * c.blocks_per_cu / (peak_per_cu * c.eff);
+  double t = (double)waves * block_s;
+  if (splits > 1) t += 2.0 * (double)splits * (double)(M * N) * (double)elem / kStreamBytesPerS;
+  return t;
+}
+
+// fp32 configuration (0 = big, 1 = small) for a given split count.
+int pick_cfg_f32(int64_t M, int64_t N, int64_t K, int splits) {
+  const double t0 = est_seconds(kModelF32[0], kPeakPerCuF32, M, N, K, splits, 4);
+  const double t1 = est_seconds(kModelF32[1], kPeakPerCuF32, M, N, K, splits, 4);
+  return t1 < t0 ? 1 : 0;
 }
 
 template <class C, bool AK, bool BKC>
 int launch_cfg(GemmParams<typename C::T> p, int splits, hipStream_t st) {
   if (splits < 1) splits = 1;
   p.k_per_split = round_up(ceil_div(p.K > 0 ? p.K : 1, splits), C::BK);
-  int64_t tm, tn;
-  tiles_of<C>(p.M, p.N, &tm, &tn);
+  const int64_t tm = ceil_div(p.M, C::BM), tn = ceil_div(p.N, C::BN);
   const int64_t blocks = tm * tn * splits;
   if (blocks > 2147483647LL)
     return set_error(KAN_ERR_LIMIT, "gemm: problem too large (%lld tiles)", (long long)blocks);
   p.tiles_m = (int)tm;
   p.tiles_n = (int)tn;
   p.splits = splits;
-  hipLaunchKernelGGL((gemm_kernel<C, AK, BKC>), dim3((unsigned)blocks), dim3(C::kThreads), 0, st,
-                     p);
+  if constexpr (std::is_same<typename C::T, float>::value)
+    hipLaunchKernelGGL((gemm_pipe_kernel<C, AK, BKC>), dim3((unsigned)blocks), dim3(C::kThreads), 0,
+                       st, p);
+  else
+    hipLaunchKernelGGL((gemm_kernel<C, AK, BKC>), dim3((unsigned)blocks), dim3(C::kThreads), 0,
+                       st, p);
   return KAN_OK;
+}
+
+template <class C>
+int launch_layout(int layout, const GemmParams<typename C::T>& p, int splits, hipStream_t st) {
+  switch (layout) {
+    case kLayoutNT: return launch_cfg<C, true, true>(p, splits, st);
+    case kLayoutTN: return launch_cfg<C, false, false>(p, splits, st);
+    case kLayoutNN: return launch_cfg<C, true, false>(p, splits, st);
+    default: return set_error(KAN_ERR_INVALID, "gemm: unknown layout %d", layout);
+  }
 }
 
 }  // namespace
 
-// Split-K factor for a TN (parameter-gradient) product: the smallest split
-// that gives at least three waves of resident blocks, keeping >= 64 slabs
-// of K per split; at most 8.
+// Split-K factor for a TN (parameter-gradient) product: the split count in
+// {1, 2, 4, 8, 16} with the smallest estimated time (whole waves of resident
+// blocks plus partial-sum traffic), keeping at least 8 slabs per split.
 template <typename T>
 int gemm_pick_splits(int64_t M, int64_t N, int64_t K) {
-  typedef typename Select<T>::TN C;
-  int64_t tm, tn;
-  tiles_of<C>(M, N, &tm, &tn);
-  const int64_t tiles = tm * tn;
-  if (tiles <= 0) return 1;
-  const int64_t slots = (int64_t)device_cu_count() * 2;
-  int s = 1;
-  while (s < 8 && tiles * s < 3 * slots && K / (2 * s) >= 64 * C::BK) s *= 2;
-  return s;
+  int best = 1;
+  double best_t = 0.0;
+  for (int s = 1; s <= 16; s *= 2) {
+    double t;
+    if (std::is_same<T, float>::value) {
+      if (s > 1 && K / s < 8 * kModelF32[0].bk) break;
+      t = est_seconds(kModelF32[pick_cfg_f32(M, N, K, s)], kPeakPerCuF32, M, N, K, s, sizeof(T));
+    } else {
+      if (s > 1 && K / s < 8 * kModelF64.bk) break;
+      t = est_seconds(kModelF64, kPeakPerCuF64, M, N, K, s, sizeof(T));
+    }
+    if (s == 1 || t < best_t) {
+      best = s;
+      best_t = t;
+    }
+  }
+  return best;
 }
 
 template <typename T>
@@ -446,11 +612,13 @@ int launch_gemm(int layout, int64_t M, int64_t N, int64_t K, const T* A, int64_t
   p.vec = vec_ok(A, lda) && vec_ok(B, ldb);
   TimedLaunch timed(kClassContraction, st, 2.0 * (double)M * (double)N * (double)K);
   int rc;
-  switch (layout) {
-    case kLayoutNT: rc = launch_cfg<typename Select<T>::NT, true, true>(p, splits, st); break;
-    case kLayoutTN: rc = launch_cfg<typename Select<T>::TN, false, false>(p, splits, st); break;
-    case kLayoutNN: rc = launch_cfg<typename Select<T>::NN, true, false>(p, splits, st); break;
-    default: return set_error(KAN_ERR_INVALID, "gemm: unknown layout %d", layout);
+  if constexpr (std::is_same<T, float>::value) {
+    if (pick_cfg_f32(M, N, K, splits < 1 ? 1 : splits) == 0)
+      rc = launch_layout<CfgF32Big>(layout, p, splits, st);
+    else
+      rc = launch_layout<CfgF32Small>(layout, p, splits, st);
+  } else {
+    rc = launch_layout<CfgF64>(layout, p, splits, st);
   }
   if (rc != KAN_OK) return rc;
   return check_launch("gemm");
