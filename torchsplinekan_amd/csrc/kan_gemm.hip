@@ -41,6 +41,8 @@
 // operand slabs in its L2.  Optional split-K writes partial products to
 // separate slices of C (reduced by the caller in a fixed order).
 
+#include <cstdlib>
+#include <cstring>
 #include <type_traits>
 
 #include "kan_common.h"
@@ -530,8 +532,22 @@ double est_seconds(const CfgModel& c, double peak_per_cu, int64_t M, int64_t N, 
   return t;
 }
 
+// Test override of the fp32 tile configuration: KAN_HIP_GEMM_TILE=256 or
+// 128 forces the big or the small configuration (read at every launch, so a
+// test can switch it between calls); unset or any other value leaves the
+// choice to the cost model.
+int forced_cfg_f32() {
+  const char* v = std::getenv("KAN_HIP_GEMM_TILE");
+  if (v == nullptr) return -1;
+  if (std::strcmp(v, "256") == 0) return 0;
+  if (std::strcmp(v, "128") == 0) return 1;
+  return -1;
+}
+
 // fp32 configuration (0 = big, 1 = small) for a given split count.
 int pick_cfg_f32(int64_t M, int64_t N, int64_t K, int splits) {
+  const int forced = forced_cfg_f32();
+  if (forced >= 0) return forced;
   const double t0 = est_seconds(kModelF32[0], kPeakPerCuF32, M, N, K, splits, 4);
   const double t1 = est_seconds(kModelF32[1], kPeakPerCuF32, M, N, K, splits, 4);
   return t1 < t0 ? 1 : 0;
