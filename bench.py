@@ -300,7 +300,7 @@ def main():
         },
         "roofline": {
             "bound": "mfma",
-            "kernel": "gemm_kernel (fp32 MFMA contraction; average over the forward, parameter and input launches)",
+            "kernel": "gemm_pipe_kernel (fp32 MFMA contraction; average over the forward, parameter and input launches)",
             "achieved": achieved,
             "peak": PEAK_FP32_MFMA_TFLOPS,
             "unit": "TFLOP/s",
