@@ -210,10 +210,25 @@ __device__ __forceinline__ void move_row(T* __restrict__ gmem, T* __restrict__ l
   }
 }
 
+// Wave-scope barrier: orders this wave's LDS writes before its following
+// LDS reads (and vice versa) at the compiler level; LDS instructions of one
+// wave complete in issue order.
+__device__ __forceinline__ void wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Wave steps per block are bounded so that a wave's x values for all of its
+// steps are loaded into registers before the first step is computed.
+constexpr int kMaxIters = 8;
+
 // H rows (and optionally silu(x)) for a block of features x samples.
-// The per-wave LDS stage holds the subs sample segments exactly as they lie
-// in the output (item rows of R values back to back), so each segment is
-// written out with coalesced 16-byte stores.
+// Each wave loads the x values of all of its steps up front, then per step
+// fills its own LDS stage (the subs sample segments exactly as they lie in
+// the output, item rows of R values back to back) and writes each segment
+// out with coalesced 16-byte stores.  Only the knot staging needs a block
+// barrier; the stages are private to their waves.
 template <int K, typename T, int IMPL>
 __global__ __launch_bounds__(kBasisThreads) void basis_kernel(
     const T* __restrict__ x, const T* __restrict__ grid, T* __restrict__ out, int64_t ld,
@@ -223,22 +238,29 @@ __global__ __launch_bounds__(kBasisThreads) void basis_kernel(
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int i0 = blockIdx.x * sh.fb;
   const int fbv = min(sh.fb, sh.I - i0);
-  T* knots = stage_knots<T>(smem, grid, i0, fbv, nk);
-  T* stage = knots + round_up((int64_t)sh.fb * nk, 4) + wave * 64 * R;
-  __syncthreads();
-
   const int sub = lane / sh.fb, fi = lane - sub * sh.fb;
   const bool lane_ok = sub < sh.subs && fi < fbv;
-  const T* t = knots + fi * nk;
   const int64_t step = (int64_t)sh.waves * sh.subs;
-  int64_t nbase = (int64_t)blockIdx.y * sh.iters * step + (int64_t)wave * sh.subs;
+  const int64_t nbase = (int64_t)blockIdx.y * sh.iters * step + (int64_t)wave * sh.subs;
+  T xs[kMaxIters];
+#pragma unroll
+  for (int it = 0; it < kMaxIters; ++it) {
+    const int64_t nn = nbase + it * step + sub;
+    xs[it] = (it < sh.iters && lane_ok && nn < sh.n) ? x[nn * sh.I + i0 + fi] : T(0);
+  }
+  T* knots = stage_knots<T>(smem, grid, i0, fbv, nk);
+  T* stage = knots + round_up((int64_t)sh.fb * nk, 4) + wave * 64 * R;
+  const T* t = knots + fi * nk;
+  __syncthreads();
   T* row = stage + lane * R;
   const bool vec = sh.vec != 0;
-
-  for (int it = 0; it < sh.iters; ++it, nbase += step) {
-    const int64_t nn = nbase + sub;
+#pragma unroll
+  for (int it = 0; it < kMaxIters; ++it) {
+    if (it >= sh.iters) break;
+    const int64_t nb = nbase + it * step;
+    const int64_t nn = nb + sub;
     const bool ok = lane_ok && nn < sh.n;
-    const T xv = ok ? x[nn * sh.I + i0 + fi] : T(0);
+    const T xv = xs[it];
     if (IMPL == 1) {
       for (int r = 0; r < R; ++r) row[r] = T(0);
       const int m = ok ? knot_span(t, nk, xv) : -1;
@@ -259,14 +281,14 @@ __global__ __launch_bounds__(kBasisThreads) void basis_kernel(
       }
     }
     if (silu_out != nullptr && ok) silu_out[nn * ld + i0 + fi] = silu_of<T>(xv);
-    __syncthreads();
+    wave_sync();
     for (int s = 0; s < sh.subs; ++s) {
-      const int64_t ns = nbase + s;
+      const int64_t ns = nb + s;
       if (ns >= sh.n) break;
       move_row<T, true>(out + ns * ld + (int64_t)i0 * R, stage + s * sh.fb * R, fbv * R, lane,
                         vec);
     }
-    __syncthreads();
+    wave_sync();
   }
 }
 
@@ -434,9 +456,11 @@ BasisShape make_shape(int64_t n, int64_t I, int G, int R, size_t elem, int64_t l
            (((int64_t)sh.fb * R) % v == 0);
   const int64_t per_step = (int64_t)sh.waves * sh.subs;
   const int64_t steps = ceil_div(n, per_step);
-  // Aim for ~4 steps per block, but keep enough blocks to fill the chip.
+  // Aim for ~4 steps per block (at most kMaxIters), but keep enough blocks
+  // to fill the chip.
   const int64_t fblocks = ceil_div(I, sh.fb);
   int64_t iters = 4;
+  static_assert(kMaxIters >= 4, "basis_kernel holds up to kMaxIters steps of x per wave");
   while (iters > 1 && fblocks * ceil_div(steps, iters) < 8192) iters /= 2;
   sh.iters = (int)iters;
   *blocks_y = ceil_div(steps, iters);
