@@ -391,6 +391,41 @@ __global__ void build_waug_kernel(const T* __restrict__ sw, const T* __restrict_
   }
 }
 
+// Transposed augmented weight, waug_t[c, o] = waug[o, c] for the kaug
+// columns c of [coef*scaler | base_weight], so that the input-side product
+// E = D waug runs with both operands K-contiguous.  The product is formed as
+// in build_waug_kernel (same rounding).  64x64 tiles are transposed through
+// LDS so that reads (along c) and writes (along o) are both coalesced.
+template <typename T>
+__global__ __launch_bounds__(256) void build_waug_t_kernel(
+    const T* __restrict__ sw, const T* __restrict__ scaler, const T* __restrict__ bw,
+    T* __restrict__ waug_t, int64_t O, int64_t I, int64_t R, int64_t kaug) {
+  __shared__ T tile[64][65];
+  const int64_t c0 = (int64_t)blockIdx.x * 64, o0 = (int64_t)blockIdx.y * 64;
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  const int64_t IR = I * R;
+#pragma unroll 4
+  for (int j = 0; j < 16; ++j) {
+    const int64_t o = o0 + ty + 4 * j, c = c0 + tx;
+    T v = T(0);
+    if (o < O && c < kaug) {
+      if (c < IR) {
+        v = sw[o * IR + c];
+        if (scaler != nullptr) v = v * scaler[o * I + c / R];
+      } else if (bw != nullptr) {
+        v = bw[o * I + (c - IR)];
+      }
+    }
+    tile[ty + 4 * j][tx] = v;
+  }
+  __syncthreads();
+#pragma unroll 4
+  for (int j = 0; j < 16; ++j) {
+    const int64_t c = c0 + ty + 4 * j, o = o0 + tx;
+    if (c < kaug && o < O) waug_t[c * O + o] = tile[tx][ty + 4 * j];
+  }
+}
+
 // Parameter gradients from the (split) products G = D^T [H | s]:
 //   gsw = scaler * G_H, gscaler = sum_r sw * G_H, gbw = G_s
 // (csrc/kan_cuda.cu:576-598).  Split partials are summed in fixed order.
@@ -561,6 +596,18 @@ int launch_build_waug(const T* sw, const T* scaler, const T* bw, T* waug, int64_
 }
 
 template <typename T>
+int launch_build_waug_t(const T* sw, const T* scaler, const T* bw, T* waug_t, int64_t kaug,
+                        int64_t O, int64_t I, int64_t R, hipStream_t st) {
+  if (kaug * O == 0) return KAN_OK;
+  const int64_t bx = ceil_div(kaug, 64), by = ceil_div(O, 64);
+  if (bx > 2147483647LL || by > 65535) return set_error(KAN_ERR_LIMIT, "build_waug_t: too large");
+  TimedLaunch timed(kClassOther, st, 0.0);
+  hipLaunchKernelGGL((build_waug_t_kernel<T>), dim3((unsigned)bx, (unsigned)by), dim3(256), 0, st,
+                     sw, scaler, bw, waug_t, O, I, R, kaug);
+  return check_launch("build_weight_aug_t");
+}
+
+template <typename T>
 int launch_param_grads(const T* part, int splits, int64_t split_stride, int64_t ld, const T* sw,
                        const T* scaler, T* gsw, T* gscaler, T* gbw, int64_t O, int64_t I,
                        int64_t R, hipStream_t st) {
@@ -584,6 +631,8 @@ int launch_param_grads(const T* part, int splits, int64_t split_stride, int64_t 
                                     int64_t, bool, hipStream_t);                             \
   template int launch_build_waug<T>(const T*, const T*, const T*, T*, int64_t, int64_t,       \
                                     int64_t, int64_t, hipStream_t);                          \
+  template int launch_build_waug_t<T>(const T*, const T*, const T*, T*, int64_t, int64_t,     \
+                                      int64_t, int64_t, hipStream_t);                        \
   template int launch_param_grads<T>(const T*, int, int64_t, int64_t, const T*, const T*, T*, \
                                      T*, T*, int64_t, int64_t, int64_t, hipStream_t);
 KAN_INST(float)

@@ -155,7 +155,7 @@ BackwardPlan plan_backward(int64_t n, int64_t I, int64_t O, int64_t G, int64_t k
   p.need_x = need_x;
   p.need_params = need_params;
   p.splits = need_params ? gemm_pick_splits<T>(O, p.kaug, n) : 1;
-  p.waug_elems = need_x ? (size_t)(O * p.ld) : 0;
+  p.waug_elems = need_x ? (size_t)(p.kaug * O) : 0;  // transposed weight [kaug, O]
   p.e_elems = need_x ? (size_t)(n * p.ld) : 0;
   p.part_elems = need_params ? (size_t)p.splits * (size_t)(O * p.ld) : 0;
   return p;
@@ -202,10 +202,10 @@ int backward_impl(const void* D, const void* x, const void* grid, const void* bw
   const T* taug = static_cast<const T*>(aug);
   const int impl = g_basis_impl.load();
   if (need_x) {
-    KAN_TRY(launch_build_waug<T>(static_cast<const T*>(sw), static_cast<const T*>(scaler),
-                                 static_cast<const T*>(bw), waug, p.ld, O, I, p.R, st));
-    // E[n, k'] = sum_o D[n, o] Waug[o, k']
-    KAN_TRY(launch_gemm<T>(kLayoutNN, n, p.kaug, O, tD, O, waug, p.ld, E, p.ld, 1, 0, st));
+    KAN_TRY(launch_build_waug_t<T>(static_cast<const T*>(sw), static_cast<const T*>(scaler),
+                                   static_cast<const T*>(bw), waug, p.kaug, O, I, p.R, st));
+    // E[n, k'] = sum_o D[n, o] Waug[o, k'] = sum_o D[n, o] WaugT[k', o]  (both K-contiguous)
+    KAN_TRY(launch_gemm<T>(kLayoutNT, n, p.kaug, O, tD, O, waug, O, E, p.ld, 1, 0, st));
     KAN_TRY(launch_basis_grad<T>(static_cast<const T*>(x), static_cast<const T*>(grid), E, p.ld,
                                  has_base ? E + I * p.R : nullptr, static_cast<T*>(gx), n, I,
                                  (int)G, (int)k, impl, st));

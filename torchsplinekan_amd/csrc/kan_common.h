@@ -109,6 +109,11 @@ template <typename T>
 int launch_build_waug(const T* sw, const T* scaler, const T* bw, T* waug, int64_t ld,
                       int64_t O, int64_t I, int64_t R, hipStream_t st);
 
+// waug_t [kaug, O] = transpose of the first kaug columns of waug.
+template <typename T>
+int launch_build_waug_t(const T* sw, const T* scaler, const T* bw, T* waug_t, int64_t kaug,
+                        int64_t O, int64_t I, int64_t R, hipStream_t st);
+
 template <typename T>
 int launch_param_grads(const T* part, int splits, int64_t split_stride, int64_t ld,
                        const T* sw, const T* scaler, T* gsw, T* gscaler, T* gbw, int64_t O,
