@@ -7,7 +7,8 @@ same API, backed by ``torchsplinekan_amd._C`` (the replacement of
 
 from .kan_linear import KANLinear
 from .kan import KAN
+from .pruning import PruneResult, prune_nodes
 
 __version__ = "0.1.0"
 
-__all__ = ["KANLinear", "KAN", "__version__"]
+__all__ = ["KANLinear", "KAN", "PruneResult", "prune_nodes", "__version__"]

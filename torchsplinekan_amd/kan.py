@@ -77,6 +77,12 @@ class KAN(nn.Module):
         new = KAN.from_layers([l.export_inference(requires_grad) for l in self.layers])
         return new.train(self.training and requires_grad)
 
+    def prune(self, x_calib: torch.Tensor, threshold: float = 1e-2, **kw):
+        """Physical node pruning (paper eq. 23); see pruning.prune_nodes
+        (spline_kan/kan.py:204-207)."""
+        from .pruning import prune_nodes
+        return prune_nodes(self, x_calib, threshold, **kw)
+
     @classmethod
     def from_layers(cls, layers: List[KANLinear]) -> "KAN":
         """KAN around existing KANLinear layers (widths must chain)."""
