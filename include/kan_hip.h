@@ -139,6 +139,23 @@ int kan_hip_edge_abs_mean_backward(int dtype, const void* grad_a, const void* s,
                                    size_t workspace_bytes, int64_t n, int64_t in_features,
                                    int64_t out_features, int64_t num_basis, void* stream);
 
+/* Gram matrices of the least-squares spline refit used by update_grid and
+ * extend_grid, per input feature i, accumulated in float64:
+ *   gram[i]  = sum_b bn(x[b,i]) bn(x[b,i])^T   [I, Rn, Rn]  (A^T A on the new grid)
+ *   cross[i] = sum_b bn(x[b,i]) bo(x[b,i])^T   [I, Rn, Ro]  (new basis x old basis)
+ * with bn / bo the order-k bases on grid_new [I, G_new+2k+1] and grid_old
+ * [I, G_old+2k+1] (Rn = G_new + k, Ro = G_old + k), and x_t the samples in
+ * feature-major layout [I, n].  cross[i] times the old coefficients gives the
+ * refit right-hand side A^T y_old, so this replaces the [O, B, I] curve
+ * einsum and the normal-equation inputs of update_grid / curve2coeff and
+ * extend_grid / fit_spline_coeffs (spline_kan/reference_backend.py:199-202,
+ * 483-489; spline_kan/kan_linear.py:580-582).  Deterministic (fixed-order
+ * sums, no atomics). */
+int kan_hip_refit_gram(int dtype, const void* x_t, const void* grid_old, const void* grid_new,
+                       double* gram, double* cross, int64_t n, int64_t in_features,
+                       int64_t grid_size_old, int64_t grid_size_new, int64_t spline_order,
+                       void* stream);
+
 /* Kernel-level timing (measurement support; no counterpart in the
  * reference, whose benchmarks time with torch.profiler,
  * benchmarks/bench_kan.py:288-301).  kan_hip_timing_enable(1) clears the

@@ -36,6 +36,17 @@ How each function is pinned (tests/test_oracle.py):
   regularization_from_edge_means (+ _grad)
                     closed form on hand-computed inputs; finite differences;
                     all-zero layer gives 0 with a finite zero gradient.
+  grid_from_samples golden vectors of the reference's update_grid knots
+                    (float32 bit-exact, float64); interior knots against the
+                    quantile/uniform closed form; strictly increasing rows.
+  curve2coeff       exact recovery of coefficients of curves that lie in the
+                    new spline space; minimum-norm optimality conditions
+                    (A^T(Ac - y) = 0, c orthogonal to null(A)) on a
+                    rank-deficient case; golden vectors of update_grid.
+  fit_spline_coeffs exact recovery (ridge -> 0) and the regularised normal
+                    equations' residual; golden vectors of the reference's
+                    fit_spline_coeffs.
+  refit_gram        C coef^T against A^T y_old formed from the dense old curves.
 """
 
 from fractions import Fraction
@@ -57,6 +68,11 @@ __all__ = [
     "regularization_from_edge_means",
     "regularization_grad",
     "basis_fraction",
+    "grid_from_samples",
+    "refit_gram",
+    "curve2coeff",
+    "fit_spline_coeffs",
+    "update_grid",
 ]
 
 
@@ -387,3 +403,104 @@ def regularization_grad(a, reg_act, reg_entropy):
     if A > tiny:
         g = g - (dS_dq * a).sum() / (A_safe * A_safe)
     return reg_act * np.ones_like(a) + reg_entropy * g
+
+
+# ---------------------------------------------------------------------------
+# knot update and least-squares refit (update_grid, extend_grid)
+# ---------------------------------------------------------------------------
+
+def grid_from_samples(x, G, k, grid_eps, margin=0.01):
+    """Knot rows [I, G+2k+1] adapted to samples x [B, I]: G+1 interior knots
+    (1 - grid_eps) * quantile + grid_eps * uniform over the margin-widened
+    range, then k outer knots per side spaced (range)/G.  Quantiles are the
+    linear interpolation between sorted samples at positions
+    q * (B - 1), q = clamp(j (1 - grid_eps)/G + grid_eps/2, 0, 1).
+    Follows spline_kan/reference_backend.py:384-439 (elementwise operation
+    order kept; in the dtype of x)."""
+    dt = x.dtype.type
+    B = x.shape[0]
+    xs = np.sort(x, axis=0)
+    lo = xs[0] - dt(margin)
+    hi = xs[-1] + dt(margin)
+    # torch.linspace(0, 1, G+1): first half start + i*step, second half end - (n-1-i)*step
+    step = dt(1.0) / dt(G)
+    u = np.array([dt(i) * step if i < (G + 1) // 2 else dt(1.0) - dt(G - i) * step
+                  for i in range(G + 1)], dtype=x.dtype)
+    uniform = lo[None] + u[:, None] * (hi - lo)[None]
+    q = (np.arange(G + 1, dtype=x.dtype) * dt((1.0 - grid_eps) / G) + dt(grid_eps / 2.0))
+    q = np.clip(q, dt(0.0), dt(1.0))
+    pos = q * dt(B - 1)
+    i_lo = np.clip(pos.astype(np.int64), 0, B - 1)
+    i_hi = np.clip(i_lo + 1, 0, B - 1)
+    w = (pos - i_lo.astype(x.dtype))[:, None]
+    quant = (dt(1.0) - w) * xs[i_lo] + w * xs[i_hi]
+    inner = dt(1.0 - grid_eps) * quant + dt(grid_eps) * uniform
+    ext = (hi - lo) / dt(G)
+    left = inner[0][None] - np.arange(k, 0, -1, dtype=x.dtype)[:, None] * ext[None]
+    right = inner[-1][None] + np.arange(1, k + 1, dtype=x.dtype)[:, None] * ext[None]
+    return np.ascontiguousarray(np.concatenate([left, inner, right], axis=0).T)
+
+
+def refit_gram(x, grid_old, grid_new, k):
+    """Per-feature normal matrix G[i] = A_i^T A_i [I, Rn, Rn] and cross term
+    C[i] = A_i^T Bold_i [I, Rn, Ro] in float64, with A / Bold the bases of
+    x on grid_new / grid_old.  C[i] coef[o, i, :] equals the reference's
+    A_i^T y_old for y_old[o, b, i] = sum_s coef[o, i, s] Bold[b, i, s]
+    (spline_kan/reference_backend.py:199-202, 483-484)."""
+    A = basis_dense(x, grid_new, k).astype(np.float64)
+    Bo = basis_dense(x, grid_old, k).astype(np.float64)
+    return np.einsum("bir,bis->irs", A, A), np.einsum("bir,bis->irs", A, Bo)
+
+
+def curve2coeff(x, y, grid, k):
+    """Minimum-norm least-squares coefficients [O, I, R] of the curves
+    y [O, B, I] at x [B, I] on `grid`, per feature in float64, with the
+    basis evaluated in the dtype of x (spline_kan/reference_backend.py:218-265;
+    numpy's lstsq returns the same minimum-norm solution as torch's gelsy
+    driver, with rank cut eps * max(B, R))."""
+    A = basis_dense(x, grid, k).astype(np.float64)
+    Y = y.astype(np.float64)
+    O, I, R = Y.shape[0], A.shape[1], A.shape[2]
+    out = np.zeros((O, I, R), dtype=np.float64)
+    for i in range(I):
+        sol = np.linalg.lstsq(A[:, i, :], Y[:, :, i].T, rcond=None)[0]    # [R, O]
+        out[:, i, :] = sol.T
+    return out.astype(x.dtype)
+
+
+def fit_spline_coeffs(x, y, grid, k, ridge=1e-12):
+    """Ridge-regularised normal-equation coefficients [O, I, R] with the
+    basis in float64: Cholesky of A^T A + lam * (tr(A^T A)/R) I, lam = ridge,
+    raised 1e3-fold (up to three times) while the factorisation fails, then a
+    general solve (spline_kan/reference_backend.py:173-215)."""
+    A = basis_dense(x.astype(np.float64), grid.astype(np.float64), k)
+    Y = y.astype(np.float64)
+    R = A.shape[-1]
+    AtA = np.einsum("bir,bis->irs", A, A)
+    Aty = np.einsum("bir,obi->iro", A, Y)
+    scale = np.maximum(np.trace(AtA, axis1=1, axis2=2), 1e-300) / R
+    lam = ridge
+    sol = None
+    for _ in range(4):
+        M = AtA + (lam * scale)[:, None, None] * np.eye(R)[None]
+        try:
+            L = np.linalg.cholesky(M)
+        except np.linalg.LinAlgError:
+            lam *= 1e3
+            continue
+        z = np.linalg.solve(L, Aty)
+        sol = np.linalg.solve(np.transpose(L, (0, 2, 1)), z)
+        break
+    if sol is None:
+        sol = np.stack([np.linalg.lstsq(M[i], Aty[i], rcond=None)[0] for i in range(M.shape[0])])
+    return np.transpose(sol, (2, 0, 1)).astype(x.dtype)
+
+
+def update_grid(x, grid, spline_weight, G, k, grid_eps, margin=0.01):
+    """(new_grid, new_spline_weight) of ReferenceKANLayer.update_grid: the
+    old unscaled curves y_old = sum_r coef * H_old at x, refitted on
+    grid_from_samples by curve2coeff (spline_kan/reference_backend.py:443-493)."""
+    H_old = basis_dense(x, grid, k)
+    y_old = np.einsum("oir,bir->obi", spline_weight, H_old).astype(x.dtype)
+    new_grid = grid_from_samples(x, G, k, grid_eps, margin)
+    return new_grid, curve2coeff(x, y_old, new_grid, k)

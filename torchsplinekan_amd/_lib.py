@@ -47,6 +47,8 @@ SIGNATURES = {
                                      _i64, _i64, _i64, _i64, _vp]),
     "kan_hip_edge_abs_mean_backward": (_int, [_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                                               _vp, _sz, _i64, _i64, _i64, _i64, _vp]),
+    "kan_hip_refit_gram": (_int, [_int, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64,
+                                  _vp]),
     "kan_hip_timing_enable": (_int, [_int]),
     "kan_hip_timing_read": (_int, [_int, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_i64),
                                    ctypes.POINTER(ctypes.c_double)]),

@@ -16,7 +16,8 @@ CSRC = os.path.join(PKG_DIR, "csrc")
 BUILD_DIR = os.path.join(PKG_DIR, "_build")
 LIB_NAME = "libkan_hip.so"
 LIB_PATH = os.path.join(PKG_DIR, LIB_NAME)
-SOURCES = ["kan_capi.hip", "kan_basis.hip", "kan_gemm.hip", "kan_edge.hip", "kan_edge_mfma.hip"]
+SOURCES = ["kan_capi.hip", "kan_basis.hip", "kan_gemm.hip", "kan_edge.hip", "kan_edge_mfma.hip",
+           "kan_refit.hip"]
 ARCH = "gfx950"
 
 COMMON_FLAGS = [

@@ -483,4 +483,28 @@ int kan_hip_edge_abs_mean_backward(int dtype, const void* ga, const void* s, con
       static_cast<double*>(ws), splits, n, I, O, R, st);
 }
 
+int kan_hip_refit_gram(int dtype, const void* x_t, const void* grid_old, const void* grid_new,
+                       double* gram, double* cross, int64_t n, int64_t I, int64_t G_old,
+                       int64_t G_new, int64_t k, void* stream) {
+  KAN_TRY(check_dtype(dtype, "refit_gram"));
+  KAN_TRY(check_layer("refit_gram", n, I, 0, G_old, k));
+  KAN_TRY(check_layer("refit_gram", n, I, 0, G_new, k));
+  if (I == 0) return KAN_OK;
+  KAN_TRY(need_ptr(grid_old, "refit_gram", "grid_old"));
+  KAN_TRY(need_ptr(grid_new, "refit_gram", "grid_new"));
+  KAN_TRY(need_ptr(gram, "refit_gram", "gram"));
+  KAN_TRY(need_ptr(cross, "refit_gram", "cross"));
+  if (n > 0) KAN_TRY(need_ptr(x_t, "refit_gram", "x_t"));
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (dtype == KAN_DTYPE_F32)
+    return launch_refit_gram<float>(static_cast<const float*>(x_t),
+                                    static_cast<const float*>(grid_old),
+                                    static_cast<const float*>(grid_new), gram, cross, n, I,
+                                    (int)G_old, (int)G_new, (int)k, st);
+  return launch_refit_gram<double>(static_cast<const double*>(x_t),
+                                   static_cast<const double*>(grid_old),
+                                   static_cast<const double*>(grid_new), gram, cross, n, I,
+                                   (int)G_old, (int)G_new, (int)k, st);
+}
+
 }  // extern "C"

@@ -119,6 +119,13 @@ int launch_param_grads(const T* part, int splits, int64_t split_stride, int64_t 
                        const T* sw, const T* scaler, T* gsw, T* gscaler, T* gbw, int64_t O,
                        int64_t I, int64_t R, hipStream_t st);
 
+// Refit Gram matrices per feature (kan_refit.hip): gram [I, Rn, Rn] and
+// cross [I, Rn, Ro] in float64 from feature-major samples xt [I, n].
+template <typename T>
+int launch_refit_gram(const T* xt, const T* grid_old, const T* grid_new, double* gram,
+                      double* cross, int64_t n, int64_t I, int Go, int Gn, int k,
+                      hipStream_t st);
+
 enum GemmLayout {
   kLayoutNT = 0,  // C[m,n] = sum_k A[m*lda+k] * B[n*ldb+k]
   kLayoutTN = 1,  // C[m,n] = sum_k A[k*lda+m] * B[k*ldb+n]

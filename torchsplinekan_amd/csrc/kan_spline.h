@@ -1,0 +1,92 @@
+// Device helpers of the local B-spline evaluation, shared by the basis
+// kernels (kan_basis.hip) and the refit kernels (kan_refit.hip): span search
+// and the non-zero values / first derivatives of the order-K functions on a
+// span, read from a knot row t[0..nk-1] (normally staged in LDS).
+#pragma once
+
+#include "kan_common.h"
+
+namespace kan {
+
+// Span index m with t[m] <= x < t[m+1] (x == t[nk-1]: last non-degenerate
+// span), or -1 when x lies outside [t[0], t[nk-1]] or is NaN.
+// Follows find_span, csrc/kan_cuda.cu:207-221.
+template <typename T>
+__device__ __forceinline__ int knot_span(const T* __restrict__ t, int nk, T x) {
+  const T lo_knot = t[0];
+  const T hi_knot = t[nk - 1];
+  if (!(x >= lo_knot) || x > hi_knot) return -1;
+  if (x == hi_knot) {
+    int m = nk - 2;
+    while (m > 0 && t[m] == hi_knot) --m;
+    return m;
+  }
+  int lo = 0, hi = nk - 1;  // t[lo] <= x < t[hi]
+  while (hi - lo > 1) {
+    const int mid = (lo + hi) >> 1;
+    if (t[mid] <= x) lo = mid;
+    else hi = mid;
+  }
+  return lo;
+}
+
+template <typename T>
+__device__ __forceinline__ T knot_at(const T* __restrict__ t, int nk, int idx) {
+  idx = idx < 0 ? 0 : (idx > nk - 1 ? nk - 1 : idx);
+  return t[idx];
+}
+
+// The D+1 degree-D functions that are non-zero on span m,
+//   v[j] = B_{m-D+j, D}(x),  j = 0..D,
+// by the triangular scheme of Piegl & Tiller (The NURBS Book, A2.2) with a
+// zero-denominator guard.  Window entries that are not real basis functions
+// (near the ends of the knot vector) read clamped knots and are discarded by
+// the caller; every real function only depends on in-range knots.
+// Same recurrence as local_basis, csrc/kan_cuda.cu:230-271.
+template <int D, typename T>
+__device__ __forceinline__ void span_values(const T* __restrict__ t, int nk, int m, T x,
+                                            T (&v)[D + 1]) {
+  T left[D + 1], right[D + 1];
+  v[0] = T(1);
+#pragma unroll
+  for (int j = 1; j <= D; ++j) {
+    left[j] = x - knot_at(t, nk, m + 1 - j);
+    right[j] = knot_at(t, nk, m + j) - x;
+    T saved = T(0);
+#pragma unroll
+    for (int r = 0; r < j; ++r) {
+      const T den = right[r + 1] + left[j - r];
+      const T tmp = den != T(0) ? v[r] / den : T(0);
+      v[r] = saved + right[r + 1] * tmp;
+      saved = left[j - r] * tmp;
+    }
+    v[j] = saved;
+  }
+}
+
+// First derivatives of the K+1 degree-K functions active on span m:
+//   dB_{r,K} = K * ( B_{r,K-1}/(t_{r+K}-t_r) - B_{r+1,K-1}/(t_{r+K+1}-t_{r+1}) ),
+// r = m-K+j, from the degree-(K-1) values on the same span.
+// Formula of csrc/kan_cuda.cu:238-255 / spline_kan/reference_backend.py:99-125.
+template <int K, typename T>
+__device__ __forceinline__ void span_derivs(const T* __restrict__ t, int nk, int m, T x,
+                                            T (&d)[K + 1]) {
+  T lower[K];
+  span_values<K - 1, T>(t, nk, m, x, lower);
+#pragma unroll
+  for (int j = 0; j <= K; ++j) {
+    const int r = m - K + j;
+    T a = T(0), b = T(0);
+    if (j >= 1) {
+      const T den = knot_at(t, nk, r + K) - knot_at(t, nk, r);
+      if (den != T(0)) a = lower[j - 1] / den;
+    }
+    if (j <= K - 1) {
+      const T den = knot_at(t, nk, r + K + 1) - knot_at(t, nk, r + 1);
+      if (den != T(0)) b = lower[j] / den;
+    }
+    d[j] = T(K) * (a - b);
+  }
+}
+
+}  // namespace kan

@@ -77,6 +77,17 @@ class KAN(nn.Module):
         new = KAN.from_layers([l.export_inference(requires_grad) for l in self.layers])
         return new.train(self.training and requires_grad)
 
+    @torch.no_grad()
+    def extend_grid(self, new_grid_size: int, x: torch.Tensor, **kw) -> "KAN":
+        """New KAN with every layer refined to new_grid_size
+        (KANLinear.extend_grid), each fitted on the input that layer sees in
+        this network (spline_kan/kan.py:209-222)."""
+        layers, h = [], x
+        for layer in self.layers:
+            layers.append(layer.extend_grid(new_grid_size, h, **kw))
+            h = layer(h)
+        return KAN.from_layers(layers).train(self.training)
+
     def prune(self, x_calib: torch.Tensor, threshold: float = 1e-2, **kw):
         """Physical node pruning (paper eq. 23); see pruning.prune_nodes
         (spline_kan/kan.py:204-207)."""

@@ -26,6 +26,7 @@ from .reference_backend import (
     ReferenceKANLayer,
     compute_basis,
     edge_abs_mean_dense,
+    fit_spline_coeffs,
     regularization_from_edge_means,
 )
 
@@ -162,12 +163,85 @@ class KANLinear(nn.Module):
 
     # ------------------------------------------------------------------ grid update
 
+    @torch.no_grad()
     def update_grid(self, x: torch.Tensor, margin: float = 0.01) -> None:
-        """Moves the knots to the data and refits spline_weight
-        (ReferenceKANLayer.update_grid), keeping the top-level grid in sync."""
-        self._ref.update_grid(x, margin=margin)
-        with torch.no_grad():
+        """Moves the knots to the data and refits spline_weight to the old
+        (unscaled) curves by least squares, keeping both grid buffers in sync
+        (spline_kan/kan_linear.py:260-269, reference_backend.py:443-493).
+
+        On the native backend the refit runs on the device: the per-feature
+        Gram matrices come from libkan_hip.so in one pass over the samples
+        and the minimum-norm solve runs in float64 (refit.solve_min_norm);
+        the [O, B, I] curve tensor is never formed.  Otherwise the reference
+        path (CPU least squares) runs."""
+        if self.backend_for(x) != "cuda":
+            self._ref.update_grid(x, margin=margin)
             self.grid.copy_(self._ref.grid)
+            return
+        from . import refit as _refit
+        xf = self._ref.check_update_grid_args(x, margin).to(self.grid)
+        new_grid = self._ref.grid_from_samples(xf, self.grid_size, margin)
+        gram, cross = _refit.refit_gram(xf, self.grid, new_grid, self.spline_order)
+        coef = _refit.solve_min_norm(gram, cross, self.spline_weight)
+        self._copy_grid_(new_grid)
+        self.spline_weight.copy_(coef.to(self.spline_weight.dtype))
+
+    @torch.no_grad()
+    def extend_grid(self, new_grid_size: int, x: torch.Tensor, *, margin: float = 0.01,
+                    adapt_knots: bool = False, ridge: float = 1e-12,
+                    n_dense: int = 0) -> "KANLinear":
+        """New layer with `new_grid_size` intervals whose spline coefficients
+        are the ridge-regularised least-squares fit of this layer's current
+        (unscaled) spline curves; base_weight, spline_scaler and the base
+        activation are copied (spline_kan/kan_linear.py:503-587).
+
+        Knots: uniform over the current interior [t_k, t_{k+G}] widened to the
+        samples (+margin) where they fall outside it, clipped to the old knot
+        span; or, with adapt_knots, from the sample quantile/uniform mix as in
+        update_grid.  n_dense adds that many uniformly spaced fit points per
+        feature over the new interior.  On the native backend, the fit's
+        normal equations come from libkan_hip.so (refit.refit_gram on float64
+        samples, as fit_spline_coeffs evaluates its basis in float64) and are
+        solved on the device (refit.solve_ridge)."""
+        if new_grid_size < 1:
+            raise ValueError(f"new_grid_size must be >= 1, got {new_grid_size}")
+        x_flat = x.reshape(-1, self.in_features).to(self.grid)
+        if x_flat.shape[0] < 2:
+            raise ValueError("extend_grid needs at least 2 samples")
+        k = self.spline_order
+        new = self.make_like(grid_size=new_grid_size)
+        if adapt_knots:
+            new_grid = new._ref.grid_from_samples(x_flat, new_grid_size, margin)
+        else:
+            lo0, hi0 = self.grid[:, k], self.grid[:, k + self.grid_size]
+            xmin, xmax = x_flat.amin(0), x_flat.amax(0)
+            lo = torch.where(xmin < lo0, xmin - margin, lo0)
+            hi = torch.where(xmax > hi0, xmax + margin, hi0)
+            lo = torch.maximum(lo, self.grid[:, 0])     # the old spline is 0 beyond its support
+            hi = torch.minimum(hi, self.grid[:, -1])
+            r = torch.arange(new_grid_size + 2 * k + 1, device=lo.device, dtype=lo.dtype) - k
+            new_grid = lo[:, None] + r[None] * ((hi - lo) / new_grid_size)[:, None]
+        xs = x_flat
+        if n_dense > 0:
+            lo, hi = new_grid[:, k], new_grid[:, k + new_grid_size]
+            t = torch.linspace(0, 1, n_dense, device=lo.device, dtype=lo.dtype)
+            xs = torch.cat([x_flat, lo[None] + t[:, None] * (hi - lo)[None]], 0)
+        native = (self.backend_for(x) == "cuda"
+                  and native_config_supported(self.in_features, new_grid_size, k)[0])
+        if native:
+            from . import refit as _refit
+            gram, cross = _refit.refit_gram(xs.double(), self.grid.double(), new_grid.double(), k)
+            coeffs = _refit.solve_ridge(gram, cross, self.spline_weight, ridge)
+        else:
+            H_old = compute_basis(xs, self.grid, k)
+            y_old = torch.einsum("oir,bir->obi", self.spline_weight, H_old)   # unscaled curves
+            coeffs = fit_spline_coeffs(xs, y_old, new_grid, k, ridge=ridge)
+        new.base_weight.copy_(self.base_weight)
+        new.spline_weight.copy_(coeffs.to(new.spline_weight.dtype))
+        if self.enable_standalone_scale_spline:
+            new.spline_scaler.copy_(self.spline_scaler)
+        new._copy_grid_(new_grid)
+        return new.train(self.training)
 
     # ------------------------------------------------------------------ regularisation
 

@@ -110,6 +110,36 @@ def curve2coeff(x_samples: torch.Tensor, y_samples: torch.Tensor, grid: torch.Te
     return out.to(dtype=x_samples.dtype, device=x_samples.device)
 
 
+def fit_spline_coeffs(x_samples: torch.Tensor, y_samples: torch.Tensor, grid: torch.Tensor,
+                      k: int, ridge: float = 1e-12) -> torch.Tensor:
+    """Ridge-regularised least-squares coefficients [O, I, R] of the curves
+    y [O, B, I] at x [B, I] on `grid`, per feature through the normal
+    equations in float64 on the samples' device: Cholesky of
+    A^T A + lam * (tr(A^T A)/R) I with lam = ridge, raised 1e3-fold (up to
+    three times) while the factorisation fails, then a general solve
+    (spline_kan/reference_backend.py:173-215)."""
+    if ridge <= 0:
+        raise ValueError(f"ridge must be positive, got {ridge}")
+    A = compute_basis(x_samples.double(), grid.double(), k)                 # [B, I, R]
+    y = y_samples.double()                                                   # [O, B, I]
+    R = A.shape[-1]
+    AtA = torch.einsum("bir,bis->irs", A, A)
+    Aty = torch.einsum("bir,obi->iro", A, y)                                 # [I, R, O]
+    scale = AtA.diagonal(dim1=-2, dim2=-1).sum(-1).clamp(min=1e-300) / R
+    eye = torch.eye(R, dtype=torch.float64, device=A.device)
+    lam = ridge
+    for _ in range(4):
+        M = AtA + (lam * scale)[:, None, None] * eye
+        L, info = torch.linalg.cholesky_ex(M)
+        if not bool((info != 0).any()):
+            sol = torch.cholesky_solve(Aty, L)
+            break
+        lam *= 1e3
+    else:
+        sol = torch.linalg.lstsq(M, Aty).solution
+    return sol.permute(2, 0, 1).to(dtype=x_samples.dtype)
+
+
 class ReferenceKANLayer(nn.Module):
     """Pure-PyTorch B-spline KAN layer (owns all parameters and the knot grid).
 
@@ -203,11 +233,9 @@ class ReferenceKANLayer(nn.Module):
         right = inner[-1][None] + torch.arange(1, k + 1, device=dev, dtype=dt)[:, None] * step[None]
         return torch.cat([left, inner, right], dim=0).t().contiguous()
 
-    @torch.no_grad()
-    def update_grid(self, x: torch.Tensor, margin: float = 0.01) -> None:
-        """Moves the knots to the sample distribution and refits the unscaled
-        spline coefficients to the old curves by least squares; grid and
-        coefficients are replaced together (spline_kan/reference_backend.py:442-493)."""
+    def check_update_grid_args(self, x: torch.Tensor, margin: float) -> torch.Tensor:
+        """Argument checks of update_grid in the reference's order
+        (spline_kan/reference_backend.py:464-477); returns x as [B, I]."""
         if margin <= 0:
             raise ValueError(f"margin must be positive, got {margin}")
         if not (0.0 < self.grid_eps < 1.0):
@@ -215,6 +243,14 @@ class ReferenceKANLayer(nn.Module):
         xf = x.reshape(-1, self.in_features)
         if xf.shape[0] < 2:
             raise ValueError(f"update_grid requires at least 2 samples, got {xf.shape[0]}")
+        return xf
+
+    @torch.no_grad()
+    def update_grid(self, x: torch.Tensor, margin: float = 0.01) -> None:
+        """Moves the knots to the sample distribution and refits the unscaled
+        spline coefficients to the old curves by least squares; grid and
+        coefficients are replaced together (spline_kan/reference_backend.py:442-493)."""
+        xf = self.check_update_grid_args(x, margin)
         k = self.spline_order
         H_old = compute_basis(xf, self.grid, k)
         y_old = torch.einsum("oir,bir->obi", self.spline_weight, H_old)
