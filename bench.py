@@ -40,10 +40,11 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", default="c3", choices=["c3", "c3-nodx", "c4"],
+    ap.add_argument("--workload", default="c3", choices=["c3", "c3-nodx", "c4", "refit"],
                     help="c3 (the metric's config, default), c3-nodx (x without grad, the "
-                         "reference benchmark's semantics) or c4 (KAN([256,512,512,64]) with "
-                         "forward_with_regularization; reported separately, not the metric)")
+                         "reference benchmark's semantics), c4 (KAN([256,512,512,64]) with "
+                         "forward_with_regularization) or refit (update_grid of c4's 512->512 "
+                         "layer); c4 and refit are reported separately, not the metric")
     ap.add_argument("--n", type=int, default=65536, help="samples per step (default: config's 65536)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
@@ -189,6 +190,64 @@ def bench_c4(args):
     print(json.dumps(line), flush=True)
 
 
+def bench_refit(args):
+    """KANLinear(512 -> 512, G=8, k=3) fp32 update_grid on N=16384 samples
+    from c4's Gaussian mixture: device refit (native Gram kernel + float64
+    device solve) timed over `steps` calls; the reference's CPU path
+    (dense curve tensor + per-feature lstsq) timed on a subset of the
+    features, with the subset stated."""
+    import torch
+    from torchsplinekan_amd import KANLinear
+    from torchsplinekan_amd.reference_backend import ReferenceKANLayer
+    N, I, O, G, k = (args.n if args.n != 65536 else 16384), 512, 512, 8, 3
+    g = torch.Generator().manual_seed(0)
+    means = torch.tensor([-0.8, -0.5, 0.5, 0.8])
+    x = means[torch.randint(0, 4, (N, I), generator=g)] + 0.1 * torch.randn(N, I, generator=g)
+    coef = torch.randn(O, I, G + k, generator=g) * 0.1
+    L = KANLinear(I, O, grid_size=G, spline_order=k, backend="cuda")
+    xd = x.cuda()
+
+    def fresh():
+        with torch.no_grad():
+            L.spline_weight.copy_(coef)
+            L._copy_grid_(L._ref._uniform_grid(*L._ref.grid_range).to(L.grid.device))
+
+    L = L.cuda()
+    for _ in range(max(args.warmup, 1)):
+        fresh()
+        L.update_grid(xd)
+    torch.cuda.synchronize()
+    times = []
+    for _ in range(args.steps):
+        fresh()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        L.update_grid(xd)
+        torch.cuda.synchronize()
+        times.append(time.perf_counter() - t0)
+    dev_ms = statistics.median(times) * 1e3
+    # reference path on the CPU: update_grid of a layer holding the first i_sub features
+    i_sub = 16
+    ref = ReferenceKANLayer(i_sub, O, grid_size=G, spline_order=k)
+    with torch.no_grad():
+        ref.spline_weight.copy_(coef[:, :i_sub])
+    t0 = time.perf_counter()
+    ref.update_grid(x[:, :i_sub])
+    cpu_s = time.perf_counter() - t0
+    line = {
+        "metric": "update_grid ms, KANLinear 512->512 G8 k3 fp32, N=16384 (c4 middle layer)",
+        "value": dev_ms, "unit": "ms", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "higher_is_better": False, "dtype": "f32 (refit solves in f64)",
+        "data": "synthetic (c4 Gaussian mixture, seeded)",
+        "config": {"workload": "refit: KANLinear(512->512, G=8, k=3).update_grid(x[16384, 512])"},
+        "cpu_reference": {"seconds": cpu_s, "features": i_sub, "per_feature_ms": cpu_s * 1e3 / i_sub,
+                          "est_full_layer_s": cpu_s * I / i_sub, "threads": torch.get_num_threads(),
+                          "sample": f"ReferenceKANLayer.update_grid on the first {i_sub} of {I} "
+                                    "features (dense [O, B, I] curves + per-feature CPU lstsq)"},
+    }
+    print(json.dumps(line), flush=True)
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -212,6 +271,9 @@ def main():
     torch.cuda.set_device(dev)
     if args.workload == "c4":
         bench_c4(args)
+        return
+    if args.workload == "refit":
+        bench_refit(args)
         return
 
     I = O = 1024
