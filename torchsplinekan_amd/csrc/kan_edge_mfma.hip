@@ -41,7 +41,13 @@ __device__ __forceinline__ f32x4 zero4() {
   return z;
 }
 
-__device__ __forceinline__ float sign_f(float v) { return (float)((v > 0.0f) - (v < 0.0f)); }
+// g * sign(v) with sign(0) = 0, formed by flipping g's sign bit with v's
+// (a copysign and a zero test instead of two compares, a subtraction, a
+// conversion and a multiply); bit-identical to g * sign(v).
+__device__ __forceinline__ float g_sign(float g, float v) {
+  const unsigned bits = __float_as_uint(g) ^ (__float_as_uint(v) & 0x80000000u);
+  return v != 0.0f ? __uint_as_float(bits) : 0.0f;
+}
 
 // augmented sample value Hc[n, c]
 __device__ __forceinline__ float hc_val(const float* __restrict__ s, const float* __restrict__ H,
@@ -68,11 +74,14 @@ struct EdgeGeom {
 };
 
 // Forward: block (i, output chunk, split); wave w owns kOT output tiles.
-// KS = ceil((R+1)/4) k-steps.
+// KS = ceil((R+1)/4) k-steps.  The A fragments of the next P sample tiles are
+// in flight while the current tile runs (P = 4 for KS <= 4, fewer for wider
+// K to bound registers).
 template <int KS>
 __global__ __launch_bounds__(kEdgeMfThreads) void edge_fwd_mfma_kernel(
     const float* __restrict__ s, const float* __restrict__ H, const float* __restrict__ bw,
     const float* __restrict__ W, float* __restrict__ out, EdgeGeom g, int final_out) {
+  constexpr int P = KS <= 4 ? 4 : (KS <= 8 ? 2 : 1);
   const int64_t bid = blockIdx.x;
   const int i = (int)(bid % g.I);
   const int oc = (int)((bid / g.I) % g.ochunks);
@@ -99,28 +108,33 @@ __global__ __launch_bounds__(kEdgeMfThreads) void edge_fwd_mfma_kernel(
 
   const int64_t nb = (int64_t)split * g.per_split;
   const int64_t ne = min(g.n, nb + g.per_split);
-  // A fragments of the next sample tile are loaded while the current one runs
-  float an[KS];
-  auto load_a = [&](int64_t n0) {
+  float an[P][KS];
+  auto load_a = [&](int64_t n0, float (&dst)[KS]) {
     const int64_t nn = n0 + r;
 #pragma unroll
     for (int k = 0; k < KS; ++k) {
       const int c = 4 * k + q;
-      an[k] = (nn < ne && c < R1) ? hc_val(s, H, nn, g.I, i, g.R, c) : 0.0f;
+      dst[k] = (nn < ne && c < R1) ? hc_val(s, H, nn, g.I, i, g.R, c) : 0.0f;
     }
   };
-  if (nb < ne) load_a(nb);
-  for (int64_t n0 = nb; n0 < ne; n0 += 16) {
-    float a[KS];
 #pragma unroll
-    for (int k = 0; k < KS; ++k) a[k] = an[k];
-    if (n0 + 16 < ne) load_a(n0 + 16);
+  for (int p = 0; p < P; ++p) load_a(nb + 16 * p, an[p]);
+  for (int64_t n0 = nb; n0 < ne; n0 += 16 * P) {
 #pragma unroll
-    for (int t = 0; t < kOT; ++t) {
-      f32x4 acc = zero4();
+    for (int p = 0; p < P; ++p) {
+      const int64_t nt = n0 + 16 * p;
+      if (nt >= ne) break;
+      float a[KS];
 #pragma unroll
-      for (int k = 0; k < KS; ++k) acc = mfma16(a[k], w[t][k], acc);
-      tot[t] += (fabsf(acc[0]) + fabsf(acc[1])) + (fabsf(acc[2]) + fabsf(acc[3]));
+      for (int k = 0; k < KS; ++k) a[k] = an[p][k];
+      load_a(nt + 16 * P, an[p]);
+#pragma unroll
+      for (int t = 0; t < kOT; ++t) {
+        f32x4 acc = zero4();
+#pragma unroll
+        for (int k = 0; k < KS; ++k) acc = mfma16(a[k], w[t][k], acc);
+        tot[t] += (fabsf(acc[0]) + fabsf(acc[1])) + (fabsf(acc[2]) + fabsf(acc[3]));
+      }
     }
   }
   // combine the four row groups of each column in a fixed order
@@ -196,7 +210,7 @@ __global__ __launch_bounds__(kEdgeMfThreads) void edge_param_mfma_kernel(
       }
     }
   };
-  if (nb < ne) load_tile(nb);
+  load_tile(nb);
   for (int64_t n0 = nb; n0 < ne; n0 += 16) {
     float a[KS], hb[CT][4];
 #pragma unroll
@@ -205,7 +219,7 @@ __global__ __launch_bounds__(kEdgeMfThreads) void edge_param_mfma_kernel(
     for (int ct = 0; ct < CT; ++ct)
 #pragma unroll
       for (int v = 0; v < 4; ++v) hb[ct][v] = hn[ct][v];
-    if (n0 + 16 < ne) load_tile(n0 + 16);
+    load_tile(n0 + 16);
 #pragma unroll
     for (int t = 0; t < kOT; ++t) {
       f32x4 acc = zero4();
@@ -213,7 +227,7 @@ __global__ __launch_bounds__(kEdgeMfThreads) void edge_param_mfma_kernel(
       for (int k = 0; k < KS; ++k) acc = mfma16(a[k], w[t][k], acc);
       float gv[4];
 #pragma unroll
-      for (int v = 0; v < 4; ++v) gv[v] = gav[t] * sign_f(acc[v]);
+      for (int v = 0; v < 4; ++v) gv[v] = g_sign(gav[t], acc[v]);
 #pragma unroll
       for (int ct = 0; ct < CT; ++ct)
 #pragma unroll
@@ -325,7 +339,7 @@ __global__ __launch_bounds__(kEdgeMfThreads) void edge_input_mfma_kernel(
         for (int k = 0; k < KS; ++k) acc = mfma16(wa[k], a[j][k], acc);
         float gv[4];
 #pragma unroll
-        for (int v = 0; v < 4; ++v) gv[v] = gs[v] * sign_f(acc[v]);
+        for (int v = 0; v < 4; ++v) gv[v] = g_sign(gs[v], acc[v]);
 #pragma unroll
         for (int ct = 0; ct < CT; ++ct)
 #pragma unroll
