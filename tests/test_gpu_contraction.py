@@ -1,8 +1,11 @@
 """GPU parity of the fp32 contraction engine in both tile configurations
 (256x256 with 128x128 per wave, and 128x128 with 64x64 per wave), each
 forced through KAN_HIP_GEMM_TILE, on layer shapes chosen so that the
-forward (NT), input-gradient (NN) and parameter-gradient (TN, split over
-samples) products see whole tiles, ragged row and column edges, K tails that
+forward (NT), input-gradient (NT against the transposed weight; both the
+two-pass route and, with KAN_HIP_FUSED_DX=1, dx contracted in the GEMM
+epilogue, where the spline columns of one feature straddle two wave blocks
+when R does not divide the block width) and parameter-gradient (TN, split
+over samples) products see whole tiles, ragged row and column edges, K tails that
 are not a multiple of the 32-deep slab, unaligned leading dimensions
 (out_features not a multiple of 4) and several split-K counts.
 
@@ -43,20 +46,24 @@ def C():
 
 @pytest.fixture
 def tile_env():
-    old = os.environ.get("KAN_HIP_GEMM_TILE")
+    names = ("KAN_HIP_GEMM_TILE", "KAN_HIP_FUSED_DX")
+    old = {n: os.environ.get(n) for n in names}
     yield
-    if old is None:
-        os.environ.pop("KAN_HIP_GEMM_TILE", None)
-    else:
-        os.environ["KAN_HIP_GEMM_TILE"] = old
+    for n, v in old.items():
+        if v is None:
+            os.environ.pop(n, None)
+        else:
+            os.environ[n] = v
 
 
+@pytest.mark.parametrize("fused_dx", ["0", "1"])
 @pytest.mark.parametrize("tile", ["256", "128"])
 @pytest.mark.parametrize("shape", SHAPES)
-def test_contraction_configs_match_oracle(C, tile_env, tile, shape):
+def test_contraction_configs_match_oracle(C, tile_env, tile, shape, fused_dx):
     N, I, O, G, k, kind = shape
-    print(f"contraction tile={tile} shape={shape}", flush=True)
+    print(f"contraction tile={tile} fused_dx={fused_dx} shape={shape}", flush=True)
     os.environ["KAN_HIP_GEMM_TILE"] = tile
+    os.environ["KAN_HIP_FUSED_DX"] = fused_dx
     g = torch.Generator().manual_seed(N + I)
     grid = make_grid(I, G, k, kind, seed=N)
     x = torch.rand(N, I, generator=g, dtype=torch.float64) * 2.2 - 1.1
@@ -75,5 +82,31 @@ def test_contraction_configs_match_oracle(C, tile_env, tile, shape):
                                             basis=rH)
     for name, got, ref in [("y", y, ry), ("dx", gx, rgx), ("dbase_w", gbw, rgbw),
                            ("dcoef", gsw, rgsw), ("dscaler", gsc, rgsc)]:
+        err = normwise(np64(got), ref)
+        assert err < FP32_TOL, (name, err)
+
+
+@pytest.mark.parametrize("shape", [(300, 37, 96, 7, 3, "uniform"), (257, 33, 19, 4, 1, "repeated")])
+def test_fused_dx_without_base_branch(C, tile_env, shape):
+    """The fused input gradient with two partial slots per feature (no base
+    columns), spline features straddling wave blocks (R = 10 and R = 5)."""
+    N, I, O, G, k, kind = shape
+    print(f"fused dx, no base branch, shape={shape}", flush=True)
+    os.environ["KAN_HIP_FUSED_DX"] = "1"
+    g = torch.Generator().manual_seed(N)
+    grid = make_grid(I, G, k, kind, seed=N)
+    x = torch.rand(N, I, generator=g, dtype=torch.float64) * 2.2 - 1.1
+    sw = torch.randn(O, I, G + k, generator=g, dtype=torch.float64) * 0.1
+    D = torch.randn(N, O, generator=g, dtype=torch.float64)
+    f = lambda t: t.float().cuda()
+    empty = torch.empty(0, device="cuda")
+    y, H = C.kan_forward(f(x), f(grid), empty, f(sw), empty, k, False)
+    gx, gbw, gsw, gsc = C.kan_backward(f(D), f(x), f(grid), empty, f(sw), empty, H, k, False)
+    torch.cuda.synchronize()
+    a = lambda t: np64(t.float())
+    ry, rH = ko.kan_forward(a(x), a(grid), None, a(sw), None, k)
+    rgx, _, rgsw, _ = ko.kan_backward(a(D), a(x), a(grid), None, a(sw), None, k, basis=rH)
+    assert gbw is None and gsc is None
+    for name, got, ref in [("y", y, ry), ("dx", gx, rgx), ("dcoef", gsw, rgsw)]:
         err = normwise(np64(got), ref)
         assert err < FP32_TOL, (name, err)

@@ -6,7 +6,9 @@
 #include <atomic>
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
 #include <mutex>
+#include <type_traits>
 #include <vector>
 
 #include "kan_common.h"
@@ -18,6 +20,16 @@ thread_local std::string g_last_error;
 std::atomic<int> g_basis_impl{1};
 std::mutex g_cu_mutex;
 int g_cu_count[64] = {0};
+
+// KAN_HIP_FUSED_DX=1 contracts dx inside the input-side GEMM (no E buffer:
+// the workspace shrinks by n * (ld - 3 I) floats, at about 10% more time for
+// that GEMM, whose epilogue then evaluates dB/dx at one wave per SIMD).
+// Unset or any other value keeps the two-pass route (E, then basis_grad).
+// Read at every plan, so a caller can switch it between calls.
+bool fused_dx_enabled() {
+  const char* v = std::getenv("KAN_HIP_FUSED_DX");
+  return v != nullptr && v[0] == '1';
+}
 }  // namespace
 
 int set_error(int code, const char* fmt, ...) {
@@ -140,7 +152,7 @@ int need_ptr(const void* p, const char* who, const char* name) {
 
 struct BackwardPlan {
   int64_t R, ld, kaug;
-  bool need_x, need_params;
+  bool need_x, need_params, fused_dx;
   int splits;
   size_t waug_elems, e_elems, part_elems;
 };
@@ -156,7 +168,11 @@ BackwardPlan plan_backward(int64_t n, int64_t I, int64_t O, int64_t G, int64_t k
   p.need_params = need_params;
   p.splits = need_params ? gemm_pick_splits<T>(O, p.kaug, n) : 1;
   p.waug_elems = need_x ? (size_t)(p.kaug * O) : 0;  // transposed weight [kaug, O]
-  p.e_elems = need_x ? (size_t)(n * p.ld) : 0;
+  // fp32 with the local basis: dx is contracted inside the input-side GEMM,
+  // which leaves [n, I, 3 or 2] partial sums instead of E [n, ld]
+  p.fused_dx = need_x && std::is_same<T, float>::value && g_basis_impl.load() == 1 &&
+               fused_dx_enabled() && gemm_dx_supported(n, p.kaug, O, I, (int)G, (int)k, has_base);
+  p.e_elems = !need_x ? 0 : p.fused_dx ? (size_t)(n * I * (has_base ? 3 : 2)) : (size_t)(n * p.ld);
   p.part_elems = need_params ? (size_t)p.splits * (size_t)(O * p.ld) : 0;
   return p;
 }
@@ -204,6 +220,15 @@ int backward_impl(const void* D, const void* x, const void* grid, const void* bw
   if (need_x) {
     KAN_TRY(launch_build_waug_t<T>(static_cast<const T*>(sw), static_cast<const T*>(scaler),
                                    static_cast<const T*>(bw), waug, p.kaug, O, I, p.R, st));
+    if constexpr (std::is_same<T, float>::value) {
+      if (p.fused_dx) {
+        KAN_TRY(launch_gemm_dx(n, p.kaug, O, tD, O, waug, O, static_cast<const float*>(x),
+                               static_cast<const float*>(grid), I, (int)G, (int)k, has_base, E,
+                               static_cast<float*>(gx), st));
+      }
+    }
+  }
+  if (need_x && !p.fused_dx) {
     // E[n, k'] = sum_o D[n, o] Waug[o, k'] = sum_o D[n, o] WaugT[k', o]  (both K-contiguous)
     KAN_TRY(launch_gemm<T>(kLayoutNT, n, p.kaug, O, tD, O, waug, O, E, p.ld, 1, 0, st));
     KAN_TRY(launch_basis_grad<T>(static_cast<const T*>(x), static_cast<const T*>(grid), E, p.ld,

@@ -138,6 +138,16 @@ int launch_gemm(int layout, int64_t M, int64_t N, int64_t K, const T* A, int64_t
                 const T* B, int64_t ldb, T* C, int64_t ldc, int splits, int64_t split_stride,
                 hipStream_t st);
 
+// fp32 input-side product E = D Waug (NT against Waug^T [N, K]) contracted in
+// the GEMM epilogue with dB/dx and silu'(x) into dx [M, I]; part is a
+// [M, I, 3 or 2] scratch of partial sums (kan_gemm.hip).
+int launch_gemm_dx(int64_t M, int64_t N, int64_t K, const float* A, int64_t lda, const float* B,
+                   int64_t ldb, const float* x, const float* grid, int64_t I, int G, int k,
+                   bool has_base, float* part, float* gx, hipStream_t st);
+// Whether launch_gemm_dx takes this shape (the tile configuration it would
+// pick leaves room for every block's knots and samples).
+bool gemm_dx_supported(int64_t M, int64_t N, int64_t K, int64_t I, int G, int k, bool has_base);
+
 // Split count the GEMM scheduler would choose for a problem (1 = no split).
 template <typename T>
 int gemm_pick_splits(int64_t M, int64_t N, int64_t K);

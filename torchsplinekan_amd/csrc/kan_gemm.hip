@@ -46,6 +46,7 @@
 #include <type_traits>
 
 #include "kan_common.h"
+#include "kan_spline.h"
 
 namespace kan {
 namespace {
@@ -384,8 +385,178 @@ struct SchedSeq<KMF, KMF, R, W, L> {
   static __device__ __forceinline__ void run() {}
 };
 
-template <class C, bool AK, bool BKC>
-__global__ __launch_bounds__(C::kThreads, C::MINB) void gemm_pipe_kernel(GemmParams<float> p) {
+// ---- fused input-gradient epilogue --------------------------------------
+// For the input-side product E[n, c] = sum_o D[n, o] Waug[o, c] (columns
+// c = i*R + r of the spline block, then I*R + i of the base block), the
+// input gradient needs only
+//   dx[n, i] = sum_r E[n, i*R + r] dB_r/dx(x[n, i]) + E[n, I*R + i] silu'(x[n, i]),
+// so E is contracted in the GEMM epilogue instead of being written out.
+// Each wave stages its accumulator block in LDS, one 32-row MFMA tile row at
+// a time, and evaluates for every (sample, feature) whose columns meet the
+// block the derivative window of span m (the k+1 columns m-k..m) and, for
+// base columns, silu'.  Partial sums go to part[n, i, slot]:
+//   slot 0  spline columns of feature i in the block holding column i*R,
+//   slot 1  spline columns in the next block (0 if the feature fits in one),
+//   slot 2  the base column (when the layer has a base branch).
+// dx_finalize_kernel adds them in that fixed order.  A feature that fits in
+// one block sums its window in the same order as basis_grad_kernel.
+struct DxParams {
+  const float* x;     // [M, I] samples (the rows of the product)
+  const float* grid;  // [I, nk] knot rows
+  float* part;        // [M, I, nslot] partial input gradients
+  int64_t I;
+  int64_t ksp;        // I * R: first base column
+  int R, nk, nslot;
+};
+
+__device__ __forceinline__ void wave_sync_lds() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Column range of one wave block and the (sample, feature) items it owns.
+struct DxBlock {
+  int64_t c0, c_end, sp_end, fs, b0;
+  int nfs, nbase;
+  __device__ __host__ DxBlock(int64_t c0_, int64_t N, int64_t ksp, int R, int TN, bool base)
+      : c0(c0_) {
+    c_end = c0 + TN < N ? c0 + TN : N;
+    sp_end = c_end < ksp ? c_end : ksp;
+    fs = 0;
+    nfs = 0;
+    if (c0 < sp_end) {
+      fs = c0 / R;
+      nfs = (int)((sp_end - 1) / R - fs + 1);
+    }
+    b0 = c0 > ksp ? c0 : ksp;
+    nbase = (base && b0 < c_end) ? (int)(c_end - b0) : 0;
+  }
+};
+
+// LDS floats one wave's side buffer needs for a block: the knot rows of its
+// spline features, then x for nb MFMA tile rows (32 samples each) of items.
+__host__ __device__ inline int64_t dx_side_floats(const DxBlock& b, int nk, int nb) {
+  return (((int64_t)b.nfs * nk + 3) & ~(int64_t)3) + (int64_t)32 * nb * (b.nfs + b.nbase);
+}
+
+// v / p for 0 <= v < 2^13 and 1 <= p <= 2^8, with rcp = 1.0f / p: the
+// fraction of (v + 0.5) / p stays at least 0.5 / p from an integer, far above
+// the float product's error, so the truncation is exact.
+__device__ __forceinline__ int div_small(int v, float rcp) {
+  return (int)(((float)v + 0.5f) * rcp);
+}
+
+template <class C, int K>
+__device__ __forceinline__ void dx_epilogue(const GemmParams<float>& p, const DxParams& e,
+                                            const TileCoords& tc,
+                                            const f32x16 (&acc)[C::FM][C::FN], float* lds_stage,
+                                            float* lds_side, int side_floats, int wave, int wm,
+                                            int wn, int lane) {
+  typedef Mfma<float, 32> M;
+  constexpr int TN = C::TN, SW = C::TN + 1;  // staged row stride (odd: conflict-free columns)
+  float* stage = lds_stage + wave * 32 * SW;
+  const DxBlock blk(tc.n0 + (int64_t)wn * TN, p.N, e.ksp, e.R, TN, e.nslot == 3);
+  const int per_row = blk.nfs + blk.nbase;
+  if (per_row == 0) return;  // block lies past the last column
+  // side buffer: knots of features fs.., then x[row, item] for nb tile rows
+  float* kn = lds_side + wave * side_floats;
+  const int nkn = blk.nfs * e.nk;
+  float* xs = kn + ((nkn + 3) & ~3);
+  static_assert(C::FM == 1 || C::FM == 2 || C::FM == 4, "tile rows per wave: 1, 2 or 4");
+  int nb = C::FM;
+  while (nb > 1 && dx_side_floats(blk, e.nk, nb) > side_floats) nb >>= 1;
+  const float* gsrc = e.grid + blk.fs * e.nk;  // the block's knot rows are contiguous
+  for (int b = lane; b < nkn; b += 64 * 4) {
+    float v[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int idx = b + u * 64;
+      v[u] = gsrc[idx < nkn ? idx : 0];
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      if (b + u * 64 < nkn) kn[b + u * 64] = v[u];
+  }
+  const int64_t fbase = blk.b0 - e.ksp - blk.nfs;  // feature of base item idx: fbase + idx
+  const int total = 32 * nb * per_row;  // x values per batch of nb tile rows
+  const float rcp = 1.0f / (float)per_row;
+  // tile rows are unrolled so the accumulator indices stay compile-time
+#pragma unroll
+  for (int iq = 0; iq < C::FM; ++iq) {
+    const int q0 = iq & ~(nb - 1);
+    const int64_t rbase = tc.m0 + (int64_t)wm * C::TM + q0 * 32;
+    if (iq == q0) {
+      // x for tile rows q0 .. q0+nb-1, sample-major: xs[rq * per_row + idx]
+      // (consecutive lanes read consecutive features of one sample)
+      for (int b = lane; b < total; b += 64 * 8) {
+        float v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          const int el = b + u * 64;
+          const int rq = div_small(el, rcp), idx = el - rq * per_row;
+          const int64_t f = idx < blk.nfs ? blk.fs + idx : fbase + idx;
+          const int64_t n = rbase + rq;
+          const bool ok = el < total && n < p.M;
+          v[u] = e.x[ok ? n * e.I + f : 0];
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+          if (b + u * 64 < total) xs[b + u * 64] = v[u];
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < C::FN; ++j)
+#pragma unroll
+      for (int v = 0; v < M::kNAcc; ++v)
+        stage[M::out_row(lane, v) * SW + j * 32 + M::out_col(lane)] = acc[iq][j][v];
+    wave_sync_lds();
+    const float* xq = xs + (iq - q0) * 32 * per_row;
+    // items (sample row, idx) of this tile row, idx fastest across lanes
+    for (int it = lane; it < 32 * per_row; it += 64) {
+      const int row = div_small(it, rcp), idx = it - row * per_row;
+      const int64_t n = rbase + (iq - q0) * 32 + row;
+      const float* srow = stage + row * SW;
+      const float xv = xq[it];
+      if (idx < blk.nfs) {
+        const int64_t f = blk.fs + idx;
+        const float* t = kn + idx * e.nk;
+        const int64_t fc = f * e.R;
+        float sum = 0.0f;
+        const int m = knot_span(t, e.nk, xv);
+        if (m >= 0) {
+          float d[K + 1];
+          span_derivs<K, float>(t, e.nk, m, xv, d);
+#pragma unroll
+          for (int jj = 0; jj <= K; ++jj) {
+            const int r = m - K + jj;
+            const int64_t col = fc + r;
+            if (r >= 0 && r < e.R && col >= blk.c0 && col < blk.sp_end)
+              sum += srow[col - blk.c0] * d[jj];
+          }
+        }
+        if (n < p.M) {
+          float* dst = e.part + (n * e.I + f) * e.nslot;
+          if (fc >= blk.c0) {
+            dst[0] = sum;
+            if (fc + e.R <= blk.c0 + TN) dst[1] = 0.0f;
+          } else {
+            dst[1] = sum;
+          }
+        }
+      } else {
+        const int64_t col = blk.b0 + (idx - blk.nfs);
+        const float g = srow[col - blk.c0] * silu_grad_of<float>(xv);
+        if (n < p.M) e.part[(n * e.I + (col - e.ksp)) * e.nslot + 2] = g;
+      }
+    }
+    wave_sync_lds();
+  }
+}
+
+template <class C, bool AK, bool BKC, int EPIK>
+__global__ __launch_bounds__(C::kThreads, C::MINB) void gemm_pipe_kernel(GemmParams<float> p,
+                                                                         DxParams e) {
   typedef float T;
   typedef Mfma<float, C::MF> M;
   constexpr int BM = C::BM, BN = C::BN, BK = C::BK, NT = C::kThreads;
@@ -494,7 +665,29 @@ __global__ __launch_bounds__(C::kThreads, C::MINB) void gemm_pipe_kernel(GemmPar
     if (full) run(IC<1>());
     else run(IC<0>());
   }
-  store_tile<C>(p, tc, acc, wm, wn, lane);
+  if constexpr (EPIK == 0) {
+    (void)e;
+    store_tile<C>(p, tc, acc, wm, wn, lane);
+  } else {
+    static_assert(C::WM * C::WN * 32 * (C::TN + 1) <= 2 * SA::kElems,
+                  "dx staging must fit in the A slab buffers");
+    constexpr int kSide = 2 * SB::kElems / (C::WM * C::WN);
+    static_assert(kSide + 512 <= 8192, "div_small covers the side buffer's indices");
+    __syncthreads();  // every wave is done with the slab buffers
+    dx_epilogue<C, EPIK>(p, e, tc, acc, &lds_a[0][0], &lds_b[0][0], kSide, wave, wm, wn, lane);
+  }
+}
+
+// dx[n, i] = (part[n, i, 0] + part[n, i, 1]) (+ part[n, i, 2])
+__global__ void dx_finalize_kernel(const float* __restrict__ part, float* __restrict__ gx,
+                                   int64_t count, int nslot) {
+  for (int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; e < count;
+       e += (int64_t)gridDim.x * blockDim.x) {
+    const float* q = part + e * nslot;
+    float v = q[0] + q[1];
+    if (nslot == 3) v += q[2];
+    gx[e] = v;
+  }
 }
 
 template <typename T>
@@ -553,8 +746,8 @@ int pick_cfg_f32(int64_t M, int64_t N, int64_t K, int splits) {
   return t1 < t0 ? 1 : 0;
 }
 
-template <class C, bool AK, bool BKC>
-int launch_cfg(GemmParams<typename C::T> p, int splits, hipStream_t st) {
+template <class C, bool AK, bool BKC, int EPIK = 0>
+int launch_cfg(GemmParams<typename C::T> p, int splits, hipStream_t st, const DxParams* dx = nullptr) {
   if (splits < 1) splits = 1;
   p.k_per_split = round_up(ceil_div(p.K > 0 ? p.K : 1, splits), C::BK);
   const int64_t tm = ceil_div(p.M, C::BM), tn = ceil_div(p.N, C::BN);
@@ -564,12 +757,16 @@ int launch_cfg(GemmParams<typename C::T> p, int splits, hipStream_t st) {
   p.tiles_m = (int)tm;
   p.tiles_n = (int)tn;
   p.splits = splits;
-  if constexpr (std::is_same<typename C::T, float>::value)
-    hipLaunchKernelGGL((gemm_pipe_kernel<C, AK, BKC>), dim3((unsigned)blocks), dim3(C::kThreads), 0,
-                       st, p);
-  else
+  if constexpr (std::is_same<typename C::T, float>::value) {
+    DxParams e{};
+    if (dx != nullptr) e = *dx;
+    hipLaunchKernelGGL((gemm_pipe_kernel<C, AK, BKC, EPIK>), dim3((unsigned)blocks),
+                       dim3(C::kThreads), 0, st, p, e);
+  } else {
+    (void)dx;
     hipLaunchKernelGGL((gemm_kernel<C, AK, BKC>), dim3((unsigned)blocks), dim3(C::kThreads), 0,
                        st, p);
+  }
   return KAN_OK;
 }
 
@@ -581,6 +778,26 @@ int launch_layout(int layout, const GemmParams<typename C::T>& p, int splits, hi
     case kLayoutNN: return launch_cfg<C, true, false>(p, splits, st);
     default: return set_error(KAN_ERR_INVALID, "gemm: unknown layout %d", layout);
   }
+}
+
+// Every wave block's side buffer (knots + x of one tile row) fits in its
+// share of the B slab buffers; exact, by walking the blocks of the row.
+template <class C>
+bool dx_cfg_fits(int64_t N, int64_t I, int R, int nk, bool has_base) {
+  typedef Slab<C::BN, C::BK, true> SB;
+  constexpr int64_t kSide = 2 * SB::kElems / (C::WM * C::WN);
+  if (R > C::TN) return false;  // a feature's columns meet at most two blocks
+  const int64_t ksp = I * R;
+  for (int64_t c0 = 0; c0 < N; c0 += C::TN)
+    if (dx_side_floats(DxBlock(c0, N, ksp, R, C::TN, has_base), nk, 1) > kSide) return false;
+  return true;
+}
+
+template <class C>
+int launch_dx_cfg(const GemmParams<float>& p, const DxParams& e, int k, hipStream_t st) {
+  if (k == 1) return launch_cfg<C, true, true, 1>(p, 1, st, &e);
+  if (k == 2) return launch_cfg<C, true, true, 2>(p, 1, st, &e);
+  return launch_cfg<C, true, true, 3>(p, 1, st, &e);
 }
 
 }  // namespace
@@ -638,6 +855,61 @@ int launch_gemm(int layout, int64_t M, int64_t N, int64_t K, const T* A, int64_t
   }
   if (rc != KAN_OK) return rc;
   return check_launch("gemm");
+}
+
+bool gemm_dx_supported(int64_t M, int64_t N, int64_t K, int64_t I, int G, int k, bool has_base) {
+  if (k < 1 || k > 3) return false;
+  const int R = G + k, nk = G + 2 * k + 1;
+  if (pick_cfg_f32(M, N, K, 1) == 0) return dx_cfg_fits<CfgF32Big>(N, I, R, nk, has_base);
+  return dx_cfg_fits<CfgF32Small>(N, I, R, nk, has_base);
+}
+
+// Input-side product fused with the input-gradient contraction (NT layout:
+// A = D [M, K] row-major, B = Waug^T [N, K]): writes part [M, I, nslot]
+// through dx_epilogue, then dx [M, I] = the fixed-order sum of the partials.
+int launch_gemm_dx(int64_t M, int64_t N, int64_t K, const float* A, int64_t lda, const float* B,
+                   int64_t ldb, const float* x, const float* grid, int64_t I, int G, int k,
+                   bool has_base, float* part, float* gx, hipStream_t st) {
+  if (M <= 0 || I <= 0) return KAN_OK;
+  if (!gemm_dx_supported(M, N, K, I, G, k, has_base))
+    return set_error(KAN_ERR_LIMIT, "gemm_dx: layer shape not supported by the fused epilogue");
+  GemmParams<float> p;
+  p.A = A;
+  p.B = B;
+  p.C = nullptr;
+  p.M = M;
+  p.N = N;
+  p.K = K;
+  p.lda = lda;
+  p.ldb = ldb;
+  p.ldc = 0;
+  p.split_stride = 0;
+  p.vec = vec_ok(A, lda) && vec_ok(B, ldb);
+  DxParams e;
+  e.x = x;
+  e.grid = grid;
+  e.part = part;
+  e.I = I;
+  e.R = G + k;
+  e.ksp = I * e.R;
+  e.nk = G + 2 * k + 1;
+  e.nslot = has_base ? 3 : 2;
+  int rc;
+  {
+    TimedLaunch timed(kClassContraction, st, 2.0 * (double)M * (double)N * (double)K);
+    if (pick_cfg_f32(M, N, K, 1) == 0) rc = launch_dx_cfg<CfgF32Big>(p, e, k, st);
+    else rc = launch_dx_cfg<CfgF32Small>(p, e, k, st);
+    if (rc != KAN_OK) return rc;
+    rc = check_launch("gemm_dx");
+    if (rc != KAN_OK) return rc;
+  }
+  const int64_t count = M * I;
+  int64_t blocks = ceil_div(count, 256);
+  if (blocks > 65536) blocks = 65536;
+  TimedLaunch timed(kClassOther, st, 0.0);
+  hipLaunchKernelGGL(dx_finalize_kernel, dim3((unsigned)blocks), dim3(256), 0, st, part, gx,
+                     count, e.nslot);
+  return check_launch("dx_finalize");
 }
 
 template int launch_gemm<float>(int, int64_t, int64_t, int64_t, const float*, int64_t,
