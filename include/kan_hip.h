@@ -69,6 +69,28 @@ int kan_hip_basis_grad(int dtype, const void* x, const void* grid, const void* g
                        void* grad_x, int64_t n, int64_t in_features, int64_t grid_size,
                        int64_t spline_order, void* stream);
 
+/* out[n, i, r] = d^order B_r / dx^order at x[n, i] (order >= 0; order 0 is the
+ * basis itself, order > spline_order gives zeros), with the span, boundary
+ * and zero-denominator conventions of kan_hip_basis.  Replaces the
+ * differentiable basis derivatives that the reference builds from ATen ops
+ * when the backward is recorded (create_graph=True):
+ * compute_basis_derivative (spline_kan/reference_backend.py:99-125) and
+ * autograd through compute_basis (reference_backend.py:69-94), as used by
+ * kan_backward_composite (csrc/kan_cpu.cpp:301-345) and NativeBasis
+ * (spline_kan/fused.py:57-60). */
+int kan_hip_basis_deriv(int dtype, const void* x, const void* grid, void* out, int64_t n,
+                        int64_t in_features, int64_t grid_size, int64_t spline_order,
+                        int64_t order, void* stream);
+
+/* grad_x[n, i] = sum_r grad_basis[n, i, r] * d^order B_r/dx^order(x[n, i])
+ * (order 1 is kan_hip_basis_grad).  The contraction behind the higher-order
+ * derivatives of the same reference call sites, without forming the
+ * derivative tensor. */
+int kan_hip_basis_deriv_contract(int dtype, const void* x, const void* grid,
+                                 const void* grad_basis, void* grad_x, int64_t n,
+                                 int64_t in_features, int64_t grid_size, int64_t spline_order,
+                                 int64_t order, void* stream);
+
 /* Row width (elements) of the augmented basis and augmented weight buffers.
  * Returns -1 for invalid sizes.  No reference counterpart: the reference keeps
  * basis [n, I, R] and runs the SiLU branch as a second GEMM

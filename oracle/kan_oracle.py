@@ -26,6 +26,18 @@ How each function is pinned (tests/test_oracle.py):
                     points on every knot and out of range.
   basis_derivative  central finite differences of basis_dense in float64
                     away from knots; exact cubic reproduction (x^3 - x).
+  basis_derivative_n
+                    q = 0, 1 identical to basis_dense / basis_derivative;
+                    central finite differences of order q - 1 away from
+                    knots; exact reproduction of polynomial derivatives
+                    (6x and 6 for x^3, 2 for x^2 at k = 2); derivative rows
+                    sum to zero inside the knot span (partition of unity);
+                    zeros for q > k (tests/test_oracle_derivs.py).
+  silu_derivative   q = 0, 1 identical to silu / silu_grad; central finite
+                    differences of order q - 1.
+  kan_edge_derivative
+                    q = 0 summed over inputs equals kan_forward; central
+                    finite differences of order q - 1 (all edges).
   kan_forward       brute-force per-(n,o) loop over the definition; config-1
                     golden vectors of the reference (tests/test_golden.py).
   kan_backward      finite differences of kan_forward (all four gradients);
@@ -58,7 +70,10 @@ __all__ = [
     "basis_dense",
     "basis_local",
     "basis_derivative",
+    "basis_derivative_n",
     "silu",
+    "silu_derivative",
+    "kan_edge_derivative",
     "silu_grad",
     "kan_forward",
     "kan_backward",
@@ -228,6 +243,72 @@ def basis_derivative(x, grid, k, chunk=1 << 14):
     term1 = _guarded_div(lower[:, :, :R], np.broadcast_to(d1, shp))
     term2 = _guarded_div(lower[:, :, 1:R + 1], np.broadcast_to(d2, shp))
     return dt.type(k) * (term1 - term2)
+
+
+def basis_derivative_n(x, grid, k, q, chunk=1 << 14):
+    """q-th derivative D^q B_{r,k}(x) [N, I, G+k] (q >= 0).
+
+    q = 0 is basis_dense and q = 1 is basis_derivative, operation for
+    operation.  For q >= 1: the degree k-q basis, then q steps of the
+    derivative recurrence for p = k-q+1 .. k,
+        D^j B_{r,p} = p (D^(j-1) B_{r,p-1}/(t_{r+p}-t_r) - D^(j-1) B_{r+1,p-1}/(t_{r+p+1}-t_{r+1})),
+    zero-denominator terms dropped.  q > k gives zeros (a degree-k piecewise
+    polynomial).  This is the derivative autograd takes through the
+    differentiable recurrences of compute_basis / compute_basis_derivative
+    (spline_kan/reference_backend.py:69-125) when the reference records its
+    backward (kan_backward_composite, csrc/kan_cpu.cpp:301-345; create_graph
+    uses in tests/test_math_correctness.py:232-260)."""
+    x = np.asarray(x)
+    dt = x.dtype
+    grid = np.asarray(grid).astype(dt)
+    nk = grid.shape[1]
+    R = nk - k - 1
+    if q == 0:
+        return basis_dense(x, grid, k, chunk=chunk)
+    if q > k:
+        return np.zeros((x.shape[0], x.shape[1], R), dtype=dt)
+    cur = basis_dense(x, grid, k - q, chunk=chunk)
+    t = grid[None]
+    for p in range(k - q + 1, k + 1):
+        n = nk - p - 1
+        d1 = t[:, :, p:p + n] - t[:, :, :n]
+        d2 = t[:, :, p + 1:p + 1 + n] - t[:, :, 1:1 + n]
+        shp = (x.shape[0],) + d1.shape[1:]
+        term1 = _guarded_div(cur[:, :, :n], np.broadcast_to(d1, shp))
+        term2 = _guarded_div(cur[:, :, 1:n + 1], np.broadcast_to(d2, shp))
+        cur = dt.type(p) * (term1 - term2)
+    return cur
+
+
+def silu_derivative(x, q):
+    """q-th derivative of silu(x) = x sigmoid(x), q = 0..3, with s = sigmoid(x):
+    q=1  s (1 + x (1 - s))              (silu_grad; csrc/kan_cpu.cpp:279-281)
+    q=2  s (1 - s) (2 + x (1 - 2s))
+    q=3  s (1 - s) (3 (1 - 2s) + x (1 - 6s + 6s^2))
+    (from s' = s (1 - s))."""
+    x = np.asarray(x)
+    if q == 0:
+        return silu(x)
+    if q == 1:
+        return silu_grad(x)
+    s = 1.0 / (1.0 + np.exp(-x))
+    if q == 2:
+        return s * (1 - s) * (2 + x * (1 - 2 * s))
+    if q == 3:
+        return s * (1 - s) * (3 * (1 - 2 * s) + x * (1 - 6 * s + 6 * s * s))
+    raise ValueError("silu_derivative: q must be 0..3")
+
+
+def kan_edge_derivative(x, grid, base_weight, spline_weight, spline_scaler, k, q):
+    """phi^(q)[n, o, i] = bw[o,i] silu^(q)(x[n,i]) + sum_r Weff[o,i,r] D^q B_r(x[n,i]):
+    the q-th x-derivative of every edge function of the layer (the terms whose
+    sum over i is kan_forward for q = 0).  Dense [N, O, I]; small sizes only."""
+    W = _eff_weight(np.asarray(spline_weight), spline_scaler)
+    Hq = basis_derivative_n(x, grid, k, q)
+    phi = np.einsum("oir,nir->noi", W, Hq)
+    if base_weight is not None:
+        phi = phi + np.asarray(base_weight)[None] * silu_derivative(x, q)[:, None, :]
+    return phi
 
 
 def basis_fraction(xv, knots, k):

@@ -1,0 +1,185 @@
+"""GPU parity of the native higher-order path: kan_hip_basis_deriv /
+kan_hip_basis_deriv_contract and the recorded (create_graph=True) backward
+built on them (BasisDeriv, DerivContract, kan_backward_composite_device),
+against the oracle's basis_derivative_n / kan_edge_derivative
+(oracle/kan_oracle.py), which tests/test_oracle_derivs.py pins.
+
+Tolerances (normwise, max|u - v| / max|v|): fp64 1e-12 for derivative
+values and contractions, 1e-10 for PINN quantities built on two or three
+chained derivatives; fp32 2e-5 for derivative values of order <= 1 and 1e-4
+for orders 2 and 3 (each derivative step divides by knot spacings, which
+amplifies the float32 rounding of the lower-order values), against the fp64
+oracle evaluated on the same fp32 operands.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import kan_oracle as ko
+from tests._util import make_grid, normwise, np64
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def C():
+    from torchsplinekan_amd import _C
+    assert torch.cuda.is_available(), "GPU tests need a ROCm device"
+    return _C
+
+
+def _tol(dtype, q):
+    if dtype == torch.float64:
+        return 1e-12
+    return 2e-5 if q <= 1 else 1e-4
+
+
+@pytest.mark.parametrize("dtype", [torch.float64, torch.float32])
+@pytest.mark.parametrize("k,G,kind", [(1, 6, "uniform"), (2, 7, "nonuniform"),
+                                      (3, 10, "uniform"), (3, 5, "repeated")])
+def test_basis_derivatives_match_oracle(C, dtype, k, G, kind):
+    print(f"basis_deriv k={k} G={G} {kind} {dtype}", flush=True)
+    I, N = 37, 301
+    grid = make_grid(I, G, k, kind, seed=G).to(dtype)
+    g = torch.Generator().manual_seed(k)
+    x = (torch.rand(N, I, generator=g, dtype=torch.float64) * 2.4 - 1.2).to(dtype)
+    x[0, :5] = grid[:5, 0]                   # on the first knot
+    x[1, :5] = grid[:5, -1]                  # on the last knot
+    x[2, :5] = grid[:5, k + 2]               # on an interior knot
+    gH = torch.randn(N, I, G + k, generator=g, dtype=torch.float64).to(dtype)
+    xd, gd = x.cuda(), grid.cuda()
+    for q in range(0, k + 2):
+        ref = ko.basis_derivative_n(np64(x), np64(grid), k, q)
+        got = np64(C.basis_deriv(xd, gd, k, q))
+        if q > k:
+            assert not got.any()
+            continue
+        assert normwise(got, ref) < _tol(dtype, q), q
+        gx = np64(C.basis_deriv_contract(xd, gd, k, gH.cuda(), q))
+        rgx = np.einsum("nir,nir->ni", np64(gH), ref)
+        assert normwise(gx, rgx) < _tol(dtype, q), q
+    # order 1 of the contraction is the first-order basis_grad, bit for bit
+    assert torch.equal(C.basis_deriv_contract(xd, gd, k, gH.cuda(), 1),
+                       C.basis_grad(xd, gd, k, gH.cuda()))
+    assert torch.equal(C.basis_deriv(xd, gd, k, 0), C.basis(xd, gd, k))
+
+
+def test_deriv_entry_points_reject_bad_orders(C):
+    x = torch.rand(4, 3, device="cuda")
+    grid = make_grid(3, 5, 3, "uniform").float().cuda()
+    with pytest.raises(RuntimeError):
+        C.basis_deriv(x, grid, 3, -1)
+    with pytest.raises(RuntimeError):
+        C.basis_deriv_contract(x, grid, 3, torch.zeros(4, 3, 8, device="cuda"), -2)
+
+
+def _layer(I, O, G, k, dtype, seed=0):
+    from torchsplinekan_amd import KANLinear
+    torch.manual_seed(seed)
+    L = KANLinear(I, O, grid_size=G, spline_order=k, backend="cuda").to("cuda", dtype)
+    with torch.no_grad():
+        L.spline_weight.normal_(0, 0.2)
+        L.spline_scaler.uniform_(0.5, 1.5)
+    return L
+
+
+@pytest.mark.parametrize("dtype,tol", [(torch.float64, 1e-10), (torch.float32, 1e-4)])
+def test_pinn_derivatives_of_one_layer_match_oracle(C, dtype, tol):
+    """u_x, u_xx and the parameter/input gradients of a loss on u_xx, through
+    the native recorded backward, against closed forms of the oracle."""
+    I, O, G, k, N = 5, 4, 8, 3, 257
+    L = _layer(I, O, G, k, dtype)
+    x = (torch.rand(N, I, device="cuda", dtype=dtype) * 1.8 - 0.9).requires_grad_()
+    u = L(x)
+    ux = torch.autograd.grad(u.sum(), x, create_graph=True)[0]
+    uxx = torch.autograd.grad(ux.sum(), x, create_graph=True)[0]
+    tgt = torch.randn(N, I, device="cuda", dtype=dtype)
+    loss = ((uxx - tgt) ** 2).mean()
+    loss.backward()
+    a = lambda t: np64(t.detach())
+    args = (a(x), a(L.grid), a(L.base_weight), a(L.spline_weight), a(L.spline_scaler), k)
+    assert normwise(a(ux), ko.kan_edge_derivative(*args, 1).sum(1)) < tol
+    r_uxx = ko.kan_edge_derivative(*args, 2).sum(1)
+    assert normwise(a(uxx), r_uxx) < tol
+    # d loss / d(.) with g = 2 (u_xx - tgt) / (N I): u_xx[n, i] = sum_o phi''_oi(x[n, i])
+    gl = 2.0 * (r_uxx - a(tgt)) / (N * I)
+    B2 = ko.basis_derivative_n(args[0], args[1], k, 2)
+    r_gx = gl * ko.kan_edge_derivative(*args, 3).sum(1)
+    r_gbw = np.einsum("ni,ni->i", gl, ko.silu_derivative(args[0], 2))[None].repeat(O, 0)
+    dWeff = np.einsum("ni,nir->ir", gl, B2)[None].repeat(O, 0)
+    r_gsw = args[4][:, :, None] * dWeff
+    r_gsc = (args[3] * dWeff).sum(2)
+    for got, ref in [(x.grad, r_gx), (L.base_weight.grad, r_gbw),
+                     (L.spline_weight.grad, r_gsw), (L.spline_scaler.grad, r_gsc)]:
+        assert normwise(a(got), ref) < tol
+
+
+def test_recorded_backward_runs_native_kernels(C, monkeypatch):
+    """The device create_graph path never evaluates the dense ATen basis."""
+    from torchsplinekan_amd import _lib, composite, reference_backend
+
+    def boom(*args, **kwargs):
+        raise AssertionError("dense basis evaluated on the device create_graph path")
+
+    for mod in (composite, reference_backend):
+        monkeypatch.setattr(mod, "compute_basis", boom)
+        monkeypatch.setattr(mod, "compute_basis_derivative", boom)
+    L = _layer(6, 3, 5, 3, torch.float64, seed=1)
+    x = (torch.rand(64, 6, device="cuda", dtype=torch.float64) * 1.6 - 0.8).requires_grad_()
+    _lib.timing_enable(True)
+    try:
+        ux = torch.autograd.grad(L(x).sum(), x, create_graph=True)[0]
+        uxx = torch.autograd.grad(ux.sum(), x, create_graph=True)[0]
+        uxx.square().sum().backward()
+        torch.cuda.synchronize()
+        _, n_basis, _ = _lib.timing_read("basis")
+        _, n_contract, _ = _lib.timing_read("basis_grad")
+    finally:
+        _lib.timing_enable(False)
+    assert n_basis >= 1 and n_contract >= 3
+    assert torch.isfinite(x.grad).all()
+
+
+def test_gradgradcheck_native_layer(C):
+    """Second derivatives with respect to x and every parameter, through the
+    device recorded backward (float64)."""
+    L = _layer(3, 2, 6, 3, torch.float64, seed=2)
+    x = (torch.rand(20, 3, device="cuda", dtype=torch.float64) * 1.6 - 0.8).requires_grad_()
+    assert torch.autograd.gradcheck(lambda t: L(t), (x,), eps=1e-6, atol=1e-6)
+    assert torch.autograd.gradgradcheck(lambda t: L(t), (x,), eps=1e-6, atol=1e-5)
+    sw = L.spline_weight.detach().clone().requires_grad_()
+    bw = L.base_weight.detach().clone().requires_grad_()
+    sc = L.spline_scaler.detach().clone().requires_grad_()
+    f = lambda t, w, b, s: C.kan_apply(t, L.grid, b, w, s, 3, True)
+    assert torch.autograd.gradgradcheck(f, (x, sw, bw, sc), eps=1e-6, atol=1e-5)
+
+
+def test_pinn_two_layer_matches_reference_backend(C):
+    """README's PDE example shape (KAN [1, 16, 1]): u_xx and the loss
+    gradients on the device against the reference backend on the CPU
+    (autograd through the dense recurrences), float64."""
+    from torchsplinekan_amd import KAN
+    torch.manual_seed(3)
+    net = KAN([1, 16, 1], grid_size=5, backend="cuda").double()
+    ref = KAN([1, 16, 1], grid_size=5, backend="reference").double()
+    ref.load_state_dict(net.state_dict())
+    net = net.cuda()
+    xs = torch.linspace(-1, 1, 50, dtype=torch.float64).unsqueeze(1)
+    tgt = torch.sin(3 * xs)
+
+    def pde(model, x, t):
+        x = x.clone().requires_grad_()
+        u = model(x)
+        ux = torch.autograd.grad(u.sum(), x, create_graph=True)[0]
+        uxx = torch.autograd.grad(ux.sum(), x, create_graph=True)[0]
+        loss = ((uxx - t) ** 2).mean()
+        loss.backward()
+        return uxx.detach(), x.grad
+
+    uxx_d, gx_d = pde(net, xs.cuda(), tgt.cuda())
+    uxx_r, gx_r = pde(ref, xs, tgt)
+    assert normwise(np64(uxx_d), np64(uxx_r)) < 1e-10
+    assert normwise(np64(gx_d), np64(gx_r)) < 1e-10
+    for (n, p), (_, q) in zip(net.named_parameters(), ref.named_parameters()):
+        assert normwise(np64(p.grad), np64(q.grad)) < 1e-10, n

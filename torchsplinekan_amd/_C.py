@@ -190,9 +190,10 @@ class KANFunction(torch.autograd.Function):
 
     Forward saves the augmented basis produced by the kernels.  Backward
     computes only what autograd asks for (needs_input_grad); when the
-    backward itself is being recorded (create_graph=True) it switches to the
-    differentiable ATen formulation so that higher-order derivatives are
-    exact.
+    backward itself is being recorded (create_graph=True) it switches to a
+    differentiable formulation so that higher-order derivatives are exact:
+    on the device, kan_backward_composite_device (native basis derivatives
+    of any order); on the CPU, the ATen composite.
     """
 
     @staticmethod
@@ -216,7 +217,12 @@ class KANFunction(torch.autograd.Function):
         x, grid, bw, sw, sc, saved = ctx.saved_tensors
         k, has_scaler = ctx.spline_order, ctx.has_scaler
         if torch.is_grad_enabled():
-            gx, gbw, gsw, gsc = _cmp.kan_backward_composite(D, x, grid, bw, sw, sc, k, has_scaler)
+            if x.is_cuda:
+                gx, gbw, gsw, gsc = kan_backward_composite_device(D, x, grid, bw, sw, sc, k,
+                                                                  has_scaler)
+            else:
+                gx, gbw, gsw, gsc = _cmp.kan_backward_composite(D, x, grid, bw, sw, sc, k,
+                                                                has_scaler)
         elif x.is_cuda:
             nig = ctx.needs_input_grad
             need_spline = bool(nig[3] or (has_scaler and nig[4]))
@@ -303,6 +309,116 @@ def basis_grad(x, grid, spline_order: int, grad_basis) -> torch.Tensor:
         check(LIB.kan_hip_basis_grad(dtype_code(x.dtype), ptr(x), ptr(grid), ptr(gH), ptr(gx),
                                      B, I, G, spline_order, stream_of(x.device)))
     return gx
+
+
+def basis_deriv(x, grid, spline_order: int, order: int) -> torch.Tensor:
+    """d^order B / dx^order [B, I, R] (device; order 0 = basis, order > k = 0)."""
+    G = _check_basis_args(x, grid, spline_order)
+    _req(order >= 0, "kan_basis_deriv: order must be >= 0")
+    x, grid = x.contiguous(), grid.contiguous()
+    B, I = x.shape
+    out = torch.empty(B, I, G + spline_order, dtype=x.dtype, device=x.device)
+    if B == 0:
+        return out
+    with torch.cuda.device(x.device):
+        check(LIB.kan_hip_basis_deriv(dtype_code(x.dtype), ptr(x), ptr(grid), ptr(out), B, I, G,
+                                      spline_order, int(order), stream_of(x.device)))
+    return out
+
+
+def basis_deriv_contract(x, grid, spline_order: int, grad_basis, order: int) -> torch.Tensor:
+    """gx[b, i] = sum_r grad_basis[b, i, r] d^order B_r/dx^order (device)."""
+    G = _check_basis_args(x, grid, spline_order)
+    _req(order >= 0, "kan_basis_deriv_contract: order must be >= 0")
+    B, I = x.shape
+    R = G + spline_order
+    _req(grad_basis.dim() == 3 and tuple(grad_basis.shape) == (B, I, R),
+         "kan_basis_deriv_contract: gH must be [B, I, G+k]")
+    x, grid = x.contiguous(), grid.contiguous()
+    gH = grad_basis.contiguous().to(x.dtype)
+    gx = torch.empty(B, I, dtype=x.dtype, device=x.device)
+    if B == 0:
+        return gx
+    with torch.cuda.device(x.device):
+        check(LIB.kan_hip_basis_deriv_contract(dtype_code(x.dtype), ptr(x), ptr(grid), ptr(gH),
+                                               ptr(gx), B, I, G, spline_order, int(order),
+                                               stream_of(x.device)))
+    return gx
+
+
+class BasisDeriv(torch.autograd.Function):
+    """D^q B(x) [B, I, R] on the device kernels, differentiable to any order:
+    its x-gradient is DerivContract of order q + 1.  Together with
+    DerivContract it replaces the differentiable ATen recurrences the
+    reference records under create_graph=True (compute_basis and
+    compute_basis_derivative, spline_kan/reference_backend.py:69-125)."""
+
+    @staticmethod
+    def forward(ctx, x, grid, k: int, order: int):
+        ctx.k, ctx.order = k, order
+        ctx.save_for_backward(x, grid)
+        return basis_deriv(x, grid, k, order)
+
+    @staticmethod
+    def backward(ctx, gH):
+        x, grid = ctx.saved_tensors
+        if not ctx.needs_input_grad[0]:
+            return None, None, None, None
+        return DerivContract.apply(x, grid, gH, ctx.k, ctx.order + 1), None, None, None
+
+
+class DerivContract(torch.autograd.Function):
+    """gx[b, i] = sum_r G[b, i, r] D^q B_r(x[b, i]) on the device kernels; the
+    derivative tensor is never formed.  Gradients: w.r.t. G, g * D^q B(x)
+    (BasisDeriv); w.r.t. x, g * DerivContract of order q + 1.  Past q = k the
+    spline is constant between knots and every term is zero."""
+
+    @staticmethod
+    def forward(ctx, x, grid, G, k: int, order: int):
+        ctx.k, ctx.order = k, order
+        ctx.save_for_backward(x, grid, G)
+        return basis_deriv_contract(x, grid, k, G, order)
+
+    @staticmethod
+    def backward(ctx, g):
+        x, grid, G = ctx.saved_tensors
+        need_x, _, need_G = ctx.needs_input_grad[:3]
+        gx = gG = None
+        if need_x:
+            gx = g * DerivContract.apply(x, grid, G, ctx.k, ctx.order + 1)
+        if need_G:
+            gG = g.unsqueeze(-1) * BasisDeriv.apply(x, grid, ctx.k, ctx.order)
+        return gx, None, gG, None, None
+
+
+def kan_backward_composite_device(D, x, grid, base_weight, spline_weight, spline_scaler,
+                                  spline_order: int, has_scaler: bool):
+    """Differentiable first-order backward on the device (create_graph=True).
+
+    Same maths as kan_backward_composite (csrc/kan_cpu.cpp:301-345): the
+    basis is a function of x again, so the recorded graph carries the exact
+    spline curvature.  Here the basis and its derivative come from the native
+    kernels through BasisDeriv / DerivContract (dB/dx is contracted in
+    registers, never stored), and the products are plain GEMMs.
+    """
+    B, I = x.shape
+    O, _, R = spline_weight.shape
+    hb = _cmp.has_base(base_weight)
+    H = BasisDeriv.apply(x, grid, spline_order, 0)
+    DtH = (D.t() @ H.reshape(B, I * R)).reshape(O, I, R)
+    if has_scaler:
+        gsw = spline_scaler.unsqueeze(2) * DtH
+        gsc = (spline_weight * DtH).sum(2)
+    else:
+        gsw, gsc = DtH, None
+    W = _cmp._eff_weight(spline_weight, spline_scaler, has_scaler)
+    DW = (D @ W.reshape(O, I * R)).reshape(B, I, R)
+    gx = DerivContract.apply(x, grid, DW, spline_order, 1)
+    gbw = None
+    if hb:
+        gbw = D.t() @ torch.nn.functional.silu(x)
+        gx = gx + (D @ base_weight) * _cmp._silu_grad(x)
+    return gx, gbw, gsw, gsc
 
 
 def _check_edge_inputs(s, H, bw, W, hb):

@@ -149,7 +149,8 @@ constexpr int kMaxIters = 8;
 // the output, item rows of R values back to back) and writes each segment
 // out with coalesced 16-byte stores.  Only the knot staging needs a block
 // barrier; the stages are private to their waves.
-template <int K, typename T, int IMPL>
+// DER > 0 (impl 1 only) writes the order-DER derivatives instead of values.
+template <int K, typename T, int IMPL, int DER = 0>
 __global__ __launch_bounds__(kBasisThreads) void basis_kernel(
     const T* __restrict__ x, const T* __restrict__ grid, T* __restrict__ out, int64_t ld,
     T* __restrict__ silu_out, BasisShape sh) {
@@ -186,7 +187,7 @@ __global__ __launch_bounds__(kBasisThreads) void basis_kernel(
       const int m = ok ? knot_span(t, nk, xv) : -1;
       if (m >= 0) {
         T v[K + 1];
-        span_values<K, T>(t, nk, m, xv, v);
+        span_window<K, DER, T>(t, nk, m, xv, v);
 #pragma unroll
         for (int j = 0; j <= K; ++j) {
           const int r = m - K + j;
@@ -216,7 +217,8 @@ __global__ __launch_bounds__(kBasisThreads) void basis_kernel(
 // The gradient segments are staged into LDS with coalesced 16-byte loads;
 // each lane then reads the k+1 values of its span window (impl 1) or its
 // whole row (impl 0).
-template <int K, typename T, int IMPL>
+// DER selects the derivative order contracted by impl 1 (0 = values).
+template <int K, typename T, int IMPL, int DER = 1>
 __global__ __launch_bounds__(kBasisThreads) void basis_grad_kernel(
     const T* __restrict__ x, const T* __restrict__ grid, const T* __restrict__ g, int64_t ld,
     const T* __restrict__ gbase, T* __restrict__ gx, BasisShape sh) {
@@ -255,7 +257,7 @@ __global__ __launch_bounds__(kBasisThreads) void basis_grad_kernel(
         const int m = knot_span(t, nk, xv);
         if (m >= 0) {
           T d[K + 1];
-          span_derivs<K, T>(t, nk, m, xv, d);
+          span_window<K, DER, T>(t, nk, m, xv, d);
 #pragma unroll
           for (int j = 0; j <= K; ++j) {
             const int r = m - K + j;
@@ -492,6 +494,96 @@ int launch_basis_grad(const T* x, const T* grid, const T* gH, int64_t ld_g, cons
 #undef KAN_BGRAD_LAUNCH
   return check_launch("basis_grad");
 }
+
+namespace {
+template <typename T>
+__global__ void zero_fill_kernel(T* __restrict__ out, int64_t count) {
+  for (int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; e < count;
+       e += (int64_t)gridDim.x * blockDim.x)
+    out[e] = T(0);
+}
+}  // namespace
+
+template <typename T>
+int launch_basis_deriv(const T* x, const T* grid, T* out, int64_t n, int64_t I, int G, int k,
+                       int order, hipStream_t st) {
+  if (n == 0 || I == 0) return KAN_OK;
+  const int R = G + k, nk = G + 2 * k + 1;
+  if (order > k) {  // a degree-k piecewise polynomial: zero almost everywhere
+    hipLaunchKernelGGL(zero_fill_kernel<T>, dim3(gs_blocks(n * I * R)), dim3(256), 0, st, out,
+                       n * I * R);
+    return check_launch("basis_deriv (zero)");
+  }
+  int64_t by = 0;
+  BasisShape sh = make_shape(n, I, G, R, sizeof(T), I * R, out, &by);
+  if (by > 2147483647LL) return set_error(KAN_ERR_LIMIT, "basis_deriv: too many samples");
+  dim3 grid_dim((unsigned)ceil_div(I, sh.fb), (unsigned)by);
+  const size_t smem = basis_smem<T>(sh, nk, R);
+  TimedLaunch timed(kClassBasis, st, (double)sizeof(T) * (double)n * (double)I * (1.0 + R));
+#define KAN_BDER_LAUNCH(KK, DD)                                                              \
+  hipLaunchKernelGGL((basis_kernel<KK, T, 1, DD>), grid_dim, dim3(64 * sh.waves), smem, st, x, \
+                     grid, out, (int64_t)I * R, (T*)nullptr, sh)
+  if (k == 1) {
+    if (order == 0) KAN_BDER_LAUNCH(1, 0);
+    else KAN_BDER_LAUNCH(1, 1);
+  } else if (k == 2) {
+    if (order == 0) KAN_BDER_LAUNCH(2, 0);
+    else if (order == 1) KAN_BDER_LAUNCH(2, 1);
+    else KAN_BDER_LAUNCH(2, 2);
+  } else {
+    if (order == 0) KAN_BDER_LAUNCH(3, 0);
+    else if (order == 1) KAN_BDER_LAUNCH(3, 1);
+    else if (order == 2) KAN_BDER_LAUNCH(3, 2);
+    else KAN_BDER_LAUNCH(3, 3);
+  }
+#undef KAN_BDER_LAUNCH
+  return check_launch("basis_deriv");
+}
+
+template <typename T>
+int launch_basis_deriv_contract(const T* x, const T* grid, const T* gH, T* gx, int64_t n,
+                                int64_t I, int G, int k, int order, hipStream_t st) {
+  if (n == 0 || I == 0) return KAN_OK;
+  const int R = G + k, nk = G + 2 * k + 1;
+  if (order > k) {
+    hipLaunchKernelGGL(zero_fill_kernel<T>, dim3(gs_blocks(n * I)), dim3(256), 0, st, gx, n * I);
+    return check_launch("basis_deriv_contract (zero)");
+  }
+  int64_t by = 0;
+  BasisShape sh = make_shape(n, I, G, R, sizeof(T), I * R, gH, &by);
+  if (by > 2147483647LL) return set_error(KAN_ERR_LIMIT, "basis_deriv_contract: too many samples");
+  dim3 grid_dim((unsigned)ceil_div(I, sh.fb), (unsigned)by);
+  const size_t smem = basis_smem<T>(sh, nk, R);
+  TimedLaunch timed(kClassBasisGrad, st, (double)sizeof(T) * (double)n * (double)I * (2.0 + R));
+#define KAN_BDC_LAUNCH(KK, DD)                                                                  \
+  hipLaunchKernelGGL((basis_grad_kernel<KK, T, 1, DD>), grid_dim, dim3(64 * sh.waves), smem, st, \
+                     x, grid, gH, (int64_t)I * R, (const T*)nullptr, gx, sh)
+  if (k == 1) {
+    if (order == 0) KAN_BDC_LAUNCH(1, 0);
+    else KAN_BDC_LAUNCH(1, 1);
+  } else if (k == 2) {
+    if (order == 0) KAN_BDC_LAUNCH(2, 0);
+    else if (order == 1) KAN_BDC_LAUNCH(2, 1);
+    else KAN_BDC_LAUNCH(2, 2);
+  } else {
+    if (order == 0) KAN_BDC_LAUNCH(3, 0);
+    else if (order == 1) KAN_BDC_LAUNCH(3, 1);
+    else if (order == 2) KAN_BDC_LAUNCH(3, 2);
+    else KAN_BDC_LAUNCH(3, 3);
+  }
+#undef KAN_BDC_LAUNCH
+  return check_launch("basis_deriv_contract");
+}
+
+template int launch_basis_deriv<float>(const float*, const float*, float*, int64_t, int64_t, int,
+                                       int, int, hipStream_t);
+template int launch_basis_deriv<double>(const double*, const double*, double*, int64_t, int64_t,
+                                        int, int, int, hipStream_t);
+template int launch_basis_deriv_contract<float>(const float*, const float*, const float*, float*,
+                                                int64_t, int64_t, int, int, int, hipStream_t);
+template int launch_basis_deriv_contract<double>(const double*, const double*, const double*,
+                                                 double*, int64_t, int64_t, int, int, int,
+                                                 hipStream_t);
 
 template <typename T>
 int launch_pack_basis(const T* basis, const T* x, T* aug, int64_t ld_aug, int64_t n, int64_t I,

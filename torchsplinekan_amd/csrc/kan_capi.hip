@@ -340,6 +340,53 @@ int kan_hip_basis(int dtype, const void* x, const void* grid, void* basis, int64
                               g_basis_impl.load(), st);
 }
 
+int kan_hip_basis_deriv(int dtype, const void* x, const void* grid, void* out, int64_t n,
+                        int64_t I, int64_t G, int64_t k, int64_t order, void* stream) {
+  KAN_TRY(check_dtype(dtype, "kan_basis_deriv"));
+  KAN_TRY(check_layer("kan_basis_deriv", n, I, 0, G, k));
+  if (order < 0 || order > 64)
+    return set_error(KAN_ERR_INVALID, "kan_basis_deriv: order must lie in 0..64, got %lld",
+                     (long long)order);
+  if (n == 0 || I == 0) return KAN_OK;
+  KAN_TRY(need_ptr(x, "kan_basis_deriv", "x"));
+  KAN_TRY(need_ptr(grid, "kan_basis_deriv", "grid"));
+  KAN_TRY(need_ptr(out, "kan_basis_deriv", "out"));
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (dtype == KAN_DTYPE_F32)
+    return launch_basis_deriv<float>(static_cast<const float*>(x), static_cast<const float*>(grid),
+                                     static_cast<float*>(out), n, I, (int)G, (int)k, (int)order,
+                                     st);
+  return launch_basis_deriv<double>(static_cast<const double*>(x),
+                                    static_cast<const double*>(grid), static_cast<double*>(out),
+                                    n, I, (int)G, (int)k, (int)order, st);
+}
+
+int kan_hip_basis_deriv_contract(int dtype, const void* x, const void* grid, const void* gH,
+                                 void* gx, int64_t n, int64_t I, int64_t G, int64_t k,
+                                 int64_t order, void* stream) {
+  KAN_TRY(check_dtype(dtype, "kan_basis_deriv_contract"));
+  KAN_TRY(check_layer("kan_basis_deriv_contract", n, I, 0, G, k));
+  if (order < 0 || order > 64)
+    return set_error(KAN_ERR_INVALID,
+                     "kan_basis_deriv_contract: order must lie in 0..64, got %lld",
+                     (long long)order);
+  if (n == 0 || I == 0) return KAN_OK;
+  KAN_TRY(need_ptr(x, "kan_basis_deriv_contract", "x"));
+  KAN_TRY(need_ptr(grid, "kan_basis_deriv_contract", "grid"));
+  KAN_TRY(need_ptr(gH, "kan_basis_deriv_contract", "grad_basis"));
+  KAN_TRY(need_ptr(gx, "kan_basis_deriv_contract", "grad_x"));
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (dtype == KAN_DTYPE_F32)
+    return launch_basis_deriv_contract<float>(
+        static_cast<const float*>(x), static_cast<const float*>(grid),
+        static_cast<const float*>(gH), static_cast<float*>(gx), n, I, (int)G, (int)k,
+        (int)order, st);
+  return launch_basis_deriv_contract<double>(
+      static_cast<const double*>(x), static_cast<const double*>(grid),
+      static_cast<const double*>(gH), static_cast<double*>(gx), n, I, (int)G, (int)k, (int)order,
+      st);
+}
+
 int kan_hip_basis_grad(int dtype, const void* x, const void* grid, const void* gH, void* gx,
                        int64_t n, int64_t I, int64_t G, int64_t k, void* stream) {
   KAN_TRY(check_dtype(dtype, "kan_basis_grad"));

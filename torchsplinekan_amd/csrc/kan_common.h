@@ -101,6 +101,16 @@ template <typename T>
 int launch_basis_grad(const T* x, const T* grid, const T* gH, int64_t ld_g, const T* gbase,
                       T* gx, int64_t n, int64_t I, int G, int k, int impl, hipStream_t st);
 
+// Order-`order` derivatives of the basis, [n, I, R] (order 0 = values; order
+// > k gives zeros), and their contraction gx = sum_r gH * D^order B_r.
+template <typename T>
+int launch_basis_deriv(const T* x, const T* grid, T* out, int64_t n, int64_t I, int G, int k,
+                       int order, hipStream_t st);
+
+template <typename T>
+int launch_basis_deriv_contract(const T* x, const T* grid, const T* gH, T* gx, int64_t n,
+                                int64_t I, int G, int k, int order, hipStream_t st);
+
 template <typename T>
 int launch_pack_basis(const T* basis, const T* x, T* aug, int64_t ld_aug, int64_t n, int64_t I,
                       int64_t R, bool has_base, hipStream_t st);

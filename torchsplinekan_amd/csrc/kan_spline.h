@@ -89,4 +89,57 @@ __device__ __forceinline__ void span_derivs(const T* __restrict__ t, int nk, int
   }
 }
 
+// Order-Q derivatives (1 <= Q <= K) of the K+1 degree-K functions active on
+// span m, d[j] = D^Q B_{m-K+j, K}(x): the degree K-Q values on span m, then Q
+// steps of the derivative recurrence (p = K-Q+1 .. K)
+//   D^q B_{r,p} = p * ( D^(q-1) B_{r,p-1} / (t_{r+p} - t_r)
+//                     - D^(q-1) B_{r+1,p-1} / (t_{r+p+1} - t_{r+1}) ),
+// each term zero where its knot difference is zero.  This is the exact
+// derivative of the piecewise polynomial that autograd finds through the
+// differentiable recurrence of spline_kan/reference_backend.py:69-125
+// (The NURBS Book, eq. 2.9 and A2.3).  Q = 1 is span_derivs, operation for
+// operation.
+template <int K, int Q, typename T>
+__device__ __forceinline__ void span_derivs_n(const T* __restrict__ t, int nk, int m, T x,
+                                              T (&d)[K + 1]) {
+  static_assert(Q >= 1 && Q <= K, "derivative order must lie in 1..K");
+  T cur[K + 1];
+  {
+    T low[K - Q + 1];
+    span_values<K - Q, T>(t, nk, m, x, low);
+#pragma unroll
+    for (int j = 0; j <= K - Q; ++j) cur[j] = low[j];
+  }
+#pragma unroll
+  for (int p = K - Q + 1; p <= K; ++p) {
+    T nxt[K + 1];
+#pragma unroll
+    for (int j = 0; j <= p; ++j) {
+      const int r = m - p + j;
+      T a = T(0), b = T(0);
+      if (j >= 1) {
+        const T den = knot_at(t, nk, r + p) - knot_at(t, nk, r);
+        if (den != T(0)) a = cur[j - 1] / den;
+      }
+      if (j <= p - 1) {
+        const T den = knot_at(t, nk, r + p + 1) - knot_at(t, nk, r + 1);
+        if (den != T(0)) b = cur[j] / den;
+      }
+      nxt[j] = T(p) * (a - b);
+    }
+#pragma unroll
+    for (int j = 0; j <= p; ++j) cur[j] = nxt[j];
+  }
+#pragma unroll
+  for (int j = 0; j <= K; ++j) d[j] = cur[j];
+}
+
+// Values (Q = 0) or order-Q derivatives of the window on span m.
+template <int K, int Q, typename T>
+__device__ __forceinline__ void span_window(const T* __restrict__ t, int nk, int m, T x,
+                                            T (&d)[K + 1]) {
+  if constexpr (Q == 0) span_values<K, T>(t, nk, m, x, d);
+  else span_derivs_n<K, Q, T>(t, nk, m, x, d);
+}
+
 }  // namespace kan

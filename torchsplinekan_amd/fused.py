@@ -10,15 +10,17 @@ spline weight.  ``EdgeAbsMean`` evaluates it on the gfx950 kernels without
 storing the [N, O, I] edge tensor; its backward recomputes phi to get
 sign(phi).  ``NativeBasis`` evaluates H on the device; its backward contracts
 the incoming gradient with dB/dx in registers.  When the backward itself is
-recorded (create_graph=True) both switch to differentiable PyTorch formulas,
-so higher-order derivatives stay exact (fused.py:43-102 of the reference).
+recorded (create_graph=True), NativeBasis's backward is the native
+DerivContract (differentiable to any order on the device kernels), and
+EdgeAbsMean's switches to differentiable PyTorch formulas, so higher-order
+derivatives stay exact (fused.py:43-102 of the reference).
 """
 
 from typing import Optional
 
 import torch
 
-from .reference_backend import compute_basis, compute_basis_derivative, edge_abs_mean_dense
+from .reference_backend import compute_basis, edge_abs_mean_dense
 
 try:
     from . import _C
@@ -43,7 +45,8 @@ class NativeBasis(torch.autograd.Function):
         if not ctx.needs_input_grad[0]:
             return None, None, None
         if torch.is_grad_enabled():
-            return (gH * compute_basis_derivative(x, grid, ctx.k)).sum(-1), None, None
+            # recorded backward: the native contraction, itself differentiable
+            return _C.DerivContract.apply(x, grid, gH, ctx.k, 1), None, None
         return _C.basis_grad(x.contiguous(), grid, ctx.k, gH.contiguous()), None, None
 
 
