@@ -40,11 +40,14 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", default="c3", choices=["c3", "c3-nodx", "c4", "refit"],
+    ap.add_argument("--workload", default="c3",
+                    choices=["c3", "c3-nodx", "c4", "refit", "pinn"],
                     help="c3 (the metric's config, default), c3-nodx (x without grad, the "
                          "reference benchmark's semantics), c4 (KAN([256,512,512,64]) with "
-                         "forward_with_regularization) or refit (update_grid of c4's 512->512 "
-                         "layer); c4 and refit are reported separately, not the metric")
+                         "forward_with_regularization), refit (update_grid of c4's 512->512 "
+                         "layer) or pinn (Laplacian loss of KAN([2,128,128,1]) through "
+                         "create_graph); c4, refit and pinn are reported separately, not the "
+                         "metric")
     ap.add_argument("--n", type=int, default=65536, help="samples per step (default: config's 65536)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
@@ -248,6 +251,98 @@ def bench_refit(args):
     print(json.dumps(line), flush=True)
 
 
+def bench_pinn(args):
+    """Physics-informed step (README's higher-order use, in 2-D): KAN([2, 128,
+    128, 1], G=8, k=3) in fp64 on N=16384 collocation points; one step is
+    u = net(x), grad u and the Laplacian u_xx + u_yy through create_graph,
+    loss = mean((lap - f)^2), loss.backward().  The native recorded backward
+    (basis derivatives of any order on the device kernels) is timed, then the
+    reference's recorded-backward formulation (kan_backward_composite with the
+    dense differentiable recurrences, csrc/kan_cpu.cpp:301-345) on the same
+    GPU, then the reference backend on the CPU for a bounded sample."""
+    import torch
+    from torchsplinekan_amd import KAN, _C, _lib
+    from torchsplinekan_amd import composite as cmp
+    dev = torch.device("cuda", 0)
+    N = args.n if args.n != 65536 else 16384
+    widths, G, k = [2, 128, 128, 1], 8, 3
+    g = torch.Generator().manual_seed(0)
+    x = torch.rand(N, 2, generator=g, dtype=torch.float64) * 1.8 - 0.9
+    f = torch.sin(3 * x[:, :1]) * torch.cos(2 * x[:, 1:])
+    torch.manual_seed(0)
+    net = KAN(widths, grid_size=G, spline_order=k, backend="cuda").double()
+    with torch.no_grad():
+        for layer in net.layers:
+            layer.spline_weight.normal_(0.0, 0.1, generator=g)
+    ref_state = {n_: t.clone() for n_, t in net.state_dict().items()}
+    net = net.to(dev)
+    xd, fd = x.to(dev), f.to(dev)
+
+    def step(model, xx, ff):
+        for p in model.parameters():
+            p.grad = None
+        xg = xx.clone().requires_grad_()
+        u = model(xg)
+        gu = torch.autograd.grad(u.sum(), xg, create_graph=True)[0]
+        lap = (torch.autograd.grad(gu[:, 0].sum(), xg, create_graph=True)[0][:, 0]
+               + torch.autograd.grad(gu[:, 1].sum(), xg, create_graph=True)[0][:, 1])
+        loss = ((lap.unsqueeze(1) - ff) ** 2).mean()
+        loss.backward()
+        return loss
+
+    def timed(n_steps):
+        for _ in range(args.warmup):
+            step(net, xd, fd)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(n_steps):
+            step(net, xd, fd)
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) / n_steps
+
+    _lib.timing_enable(True)
+    native_s = timed(args.steps)
+    kern = {c: _lib.timing_read(c) for c in ("basis", "basis_grad", "contraction", "other")}
+    _lib.timing_enable(False)
+    # the reference's recorded backward (dense differentiable recurrences) on the same GPU
+    native_fn = _C.kan_backward_composite_device
+    _C.kan_backward_composite_device = cmp.kan_backward_composite
+    try:
+        dense_s = timed(max(2, args.steps // 2))
+    finally:
+        _C.kan_backward_composite_device = native_fn
+    cpu = None
+    if not args.no_cpu_baseline:
+        ref = KAN(widths, grid_size=G, spline_order=k, backend="reference").double()
+        ref.load_state_dict(ref_state)
+        n_cpu = 1024
+        t0 = time.perf_counter()
+        step(ref, x[:n_cpu], f[:n_cpu])
+        cpu_s = time.perf_counter() - t0
+        cpu = {"value": n_cpu / cpu_s, "unit": "samples/s", "cores": torch.get_num_threads(),
+               "kind": "port", "sample": f"one step of the reference backend (backend="
+               f"'reference', dense recurrences, torch CPU) on the first {n_cpu} of {N} points, "
+               f"{cpu_s:.2f} s"}
+    line = {
+        "metric": "PINN step samples/s, KAN([2,128,128,1]) G8 k3 fp64 N=16K, Laplacian loss",
+        "value": N / native_s, "unit": "samples/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": native_s * 1e3, "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "f64",
+        "data": "synthetic (x ~ U(-0.9, 0.9)^2 seeded, f = sin(3x) cos(2y))",
+        "config": {"workload": "pinn: KAN([2,128,128,1], G=8, k=3) fp64, N=%d, u -> grad u -> "
+                               "Laplacian (create_graph) -> MSE -> backward" % N},
+        "reference_formulation_same_gpu": {"ms_per_step": dense_s * 1e3,
+                                           "speedup": dense_s / native_s,
+                                           "what": "kan_backward_composite with the dense "
+                                                   "differentiable recurrences (the reference's "
+                                                   "create_graph path) on this GPU"},
+        "kernels": {k_: {"ms_per_step": v[0] / args.steps, "launches_per_step": v[1] / args.steps}
+                    for k_, v in kern.items()},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -271,6 +366,9 @@ def main():
     torch.cuda.set_device(dev)
     if args.workload == "c4":
         bench_c4(args)
+        return
+    if args.workload == "pinn":
+        bench_pinn(args)
         return
     if args.workload == "refit":
         bench_refit(args)

@@ -91,6 +91,22 @@ int kan_hip_basis_deriv_contract(int dtype, const void* x, const void* grid,
                                  int64_t in_features, int64_t grid_size, int64_t spline_order,
                                  int64_t order, void* stream);
 
+/* C[M, N] = op(A) op(B) on the MFMA contraction engine, for the products
+ * of the recorded (create_graph=True) backward.  op(A) is A [M, K] with row
+ * stride lda (trans_a = 0) or the transpose of A stored [K, M] (trans_a = 1);
+ * op(B) is B [K, N] (trans_b = 0) or the transpose of B stored [N, K]
+ * (trans_b = 1); C is [M, N] with row stride ldc.  Products with a long K
+ * and few output tiles (sample reductions such as D^T H) are split over K
+ * into partial slices in ws and summed in a fixed order, so results are
+ * deterministic.  Replaces the torch::mm calls of kan_backward_composite
+ * (csrc/kan_cpu.cpp:322-343) and the matmuls autograd records through them.
+ * kan_hip_matmul_workspace gives the ws size in bytes (0 when no split). */
+int kan_hip_matmul_workspace(int dtype, int trans_a, int trans_b, int64_t M, int64_t N,
+                             int64_t K, size_t* bytes);
+int kan_hip_matmul(int dtype, int trans_a, int trans_b, int64_t M, int64_t N, int64_t K,
+                   const void* A, int64_t lda, const void* B, int64_t ldb, void* C, int64_t ldc,
+                   void* ws, size_t ws_bytes, void* stream);
+
 /* Row width (elements) of the augmented basis and augmented weight buffers.
  * Returns -1 for invalid sizes.  No reference counterpart: the reference keeps
  * basis [n, I, R] and runs the SiLU branch as a second GEMM

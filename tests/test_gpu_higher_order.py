@@ -183,3 +183,49 @@ def test_pinn_two_layer_matches_reference_backend(C):
     assert normwise(np64(gx_d), np64(gx_r)) < 1e-10
     for (n, p), (_, q) in zip(net.named_parameters(), ref.named_parameters()):
         assert normwise(np64(p.grad), np64(q.grad)) < 1e-10, n
+
+
+def _view(t, trans):
+    """t itself, or the same values as the transpose of a row-major buffer."""
+    return t.t().contiguous().t() if trans else t
+
+
+@pytest.mark.parametrize("dtype,tol", [(torch.float64, 1e-12), (torch.float32, 1e-5)])
+@pytest.mark.parametrize("M,K,N", [(5, 3, 7), (128, 16384, 1408), (300, 37, 19), (1, 10, 64),
+                                   (64, 10, 1), (7, 0, 5), (257, 4100, 33)])
+def test_native_matmul_matches_torch(C, dtype, tol, M, K, N):
+    """kan_hip_matmul on all four transposition pairs, long-K (split) and
+    degenerate shapes, against the float64 product of the same operands."""
+    print(f"matmul M={M} K={K} N={N} {dtype}", flush=True)
+    g = torch.Generator().manual_seed(M + K + N)
+    a = torch.randn(M, K, generator=g, dtype=torch.float64).to(dtype)
+    b = torch.randn(K, N, generator=g, dtype=torch.float64).to(dtype)
+    ref = np64(a) @ np64(b)
+    for ta in (False, True):
+        for tb in (False, True):
+            c = C.matmul(_view(a.cuda(), ta), _view(b.cuda(), tb))
+            if K == 0:
+                assert not np64(c).any()
+                continue
+            assert normwise(np64(c), ref) < tol, (ta, tb)
+            assert torch.equal(c, C.matmul(_view(a.cuda(), ta), _view(b.cuda(), tb)))
+
+
+def test_native_matmul_gradients_and_workspace_check(C):
+    from torchsplinekan_amd import _lib
+    a = torch.randn(9, 6, device="cuda", dtype=torch.float64, requires_grad=True)
+    b = torch.randn(6, 4, device="cuda", dtype=torch.float64, requires_grad=True)
+    assert torch.autograd.gradcheck(C.NativeMatmul.apply, (a, b))
+    assert torch.autograd.gradgradcheck(C.NativeMatmul.apply, (a, b))
+    # a split product refuses a short workspace before launching anything
+    M, N, K = 64, 64, 1 << 16
+    nbytes = _lib.ctypes.c_size_t(0)
+    _lib.check(_lib.LIB.kan_hip_matmul_workspace(_lib.dtype_code(torch.float32), 0, 0, M, N, K,
+                                                 _lib.ctypes.byref(nbytes)))
+    assert nbytes.value > 0
+    x = torch.zeros(M, K, device="cuda")
+    y = torch.zeros(K, N, device="cuda")
+    z = torch.empty(M, N, device="cuda")
+    rc = _lib.LIB.kan_hip_matmul(_lib.dtype_code(torch.float32), 0, 0, M, N, K, _lib.ptr(x), K,
+                                 _lib.ptr(y), N, _lib.ptr(z), N, None, 0, None)
+    assert rc != 0

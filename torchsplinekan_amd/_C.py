@@ -346,6 +346,63 @@ def basis_deriv_contract(x, grid, spline_order: int, grad_basis, order: int) -> 
     return gx
 
 
+def _mm_operand(t: torch.Tensor):
+    """(tensor, trans, ld) presenting a 2-D tensor [rows, cols] to kan_hip_matmul
+    without a copy when it is row-major or the transpose of a row-major
+    buffer; anything else is made contiguous."""
+    rows, cols = t.shape
+    if rows > 1 and cols > 1:
+        if t.stride(1) == 1 and t.stride(0) >= cols:
+            return t, 0, t.stride(0)
+        if t.stride(0) == 1 and t.stride(1) >= rows:
+            return t, 1, t.stride(1)
+    t = t.contiguous()
+    return t, 0, max(cols, 1)
+
+
+def matmul(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    """a [M, K] @ b [K, N] on the MFMA contraction engine (device, fp32/fp64),
+    transposed views taken as they lie; long-K products are split over K and
+    summed in a fixed order."""
+    _req(a.is_cuda and b.is_cuda, "kan_matmul: operands must be CUDA tensors")
+    _req(a.dim() == 2 and b.dim() == 2 and a.shape[1] == b.shape[0],
+         "kan_matmul: shapes ", tuple(a.shape), " and ", tuple(b.shape), " do not chain")
+    _req(a.dtype == b.dtype and a.dtype in _F, "kan_matmul: operands must share an FP32/FP64 dtype")
+    M, K = a.shape
+    N = b.shape[1]
+    a, ta, lda = _mm_operand(a)
+    b, tb, ldb = _mm_operand(b)
+    c = torch.empty(M, N, dtype=a.dtype, device=a.device)
+    if M * N == 0:
+        return c
+    code = dtype_code(a.dtype)
+    nbytes = _lib.ctypes.c_size_t(0)
+    check(LIB.kan_hip_matmul_workspace(code, ta, tb, M, N, K, _lib.ctypes.byref(nbytes)))
+    ws = torch.empty(nbytes.value, dtype=torch.uint8, device=a.device) if nbytes.value else None
+    with torch.cuda.device(a.device):
+        check(LIB.kan_hip_matmul(code, ta, tb, M, N, K, ptr(a), lda, ptr(b), ldb, ptr(c), N,
+                                 ptr(ws) if ws is not None else None, nbytes.value,
+                                 stream_of(a.device)))
+    return c
+
+
+class NativeMatmul(torch.autograd.Function):
+    """a @ b through kan_hip_matmul, differentiable to any order (its
+    gradients g b^T and a^T g are NativeMatmul products again)."""
+
+    @staticmethod
+    def forward(ctx, a, b):
+        ctx.save_for_backward(a, b)
+        return matmul(a, b)
+
+    @staticmethod
+    def backward(ctx, g):
+        a, b = ctx.saved_tensors
+        ga = NativeMatmul.apply(g, b.t()) if ctx.needs_input_grad[0] else None
+        gb = NativeMatmul.apply(a.t(), g) if ctx.needs_input_grad[1] else None
+        return ga, gb
+
+
 class BasisDeriv(torch.autograd.Function):
     """D^q B(x) [B, I, R] on the device kernels, differentiable to any order:
     its x-gradient is DerivContract of order q + 1.  Together with
@@ -399,25 +456,28 @@ def kan_backward_composite_device(D, x, grid, base_weight, spline_weight, spline
     basis is a function of x again, so the recorded graph carries the exact
     spline curvature.  Here the basis and its derivative come from the native
     kernels through BasisDeriv / DerivContract (dB/dx is contracted in
-    registers, never stored), and the products are plain GEMMs.
+    registers, never stored), and the products run on the MFMA contraction
+    engine through NativeMatmul (split over the sample axis where the output
+    is small), differentiable in turn.
     """
     B, I = x.shape
     O, _, R = spline_weight.shape
     hb = _cmp.has_base(base_weight)
+    mm = NativeMatmul.apply
     H = BasisDeriv.apply(x, grid, spline_order, 0)
-    DtH = (D.t() @ H.reshape(B, I * R)).reshape(O, I, R)
+    DtH = mm(D.t(), H.reshape(B, I * R)).reshape(O, I, R)
     if has_scaler:
         gsw = spline_scaler.unsqueeze(2) * DtH
         gsc = (spline_weight * DtH).sum(2)
     else:
         gsw, gsc = DtH, None
     W = _cmp._eff_weight(spline_weight, spline_scaler, has_scaler)
-    DW = (D @ W.reshape(O, I * R)).reshape(B, I, R)
+    DW = mm(D, W.reshape(O, I * R)).reshape(B, I, R)
     gx = DerivContract.apply(x, grid, DW, spline_order, 1)
     gbw = None
     if hb:
-        gbw = D.t() @ torch.nn.functional.silu(x)
-        gx = gx + (D @ base_weight) * _cmp._silu_grad(x)
+        gbw = mm(D.t(), torch.nn.functional.silu(x))
+        gx = gx + mm(D, base_weight) * _cmp._silu_grad(x)
     return gx, gbw, gsw, gsc
 
 

@@ -340,6 +340,67 @@ int kan_hip_basis(int dtype, const void* x, const void* grid, void* basis, int64
                               g_basis_impl.load(), st);
 }
 
+namespace {
+int matmul_layout(int trans_a, int trans_b) {
+  if (trans_a == 0 && trans_b == 0) return kLayoutNN;
+  if (trans_a == 0 && trans_b == 1) return kLayoutNT;
+  if (trans_a == 1 && trans_b == 0) return kLayoutTN;
+  if (trans_a == 1 && trans_b == 1) return kLayoutTT;
+  return -1;
+}
+
+int check_matmul(int dtype, int trans_a, int trans_b, int64_t M, int64_t N, int64_t K,
+                 int64_t lda, int64_t ldb, int64_t ldc) {
+  KAN_TRY(check_dtype(dtype, "kan_matmul"));
+  if (matmul_layout(trans_a, trans_b) < 0)
+    return set_error(KAN_ERR_INVALID, "kan_matmul: trans_a and trans_b must be 0 or 1");
+  if (M < 0 || N < 0 || K < 0) return set_error(KAN_ERR_INVALID, "kan_matmul: negative size");
+  // leading dimensions cover the rows they index
+  const int64_t a_row = trans_a ? M : K, b_row = trans_b ? K : N;
+  if ((M * K > 0 && lda < a_row) || (K * N > 0 && ldb < b_row) || (M * N > 0 && ldc < N))
+    return set_error(KAN_ERR_INVALID, "kan_matmul: leading dimension smaller than the row");
+  return KAN_OK;
+}
+}  // namespace
+
+int kan_hip_matmul_workspace(int dtype, int trans_a, int trans_b, int64_t M, int64_t N,
+                             int64_t K, size_t* bytes) {
+  KAN_TRY(need_ptr(bytes, "kan_matmul_workspace", "bytes"));
+  KAN_TRY(check_matmul(dtype, trans_a, trans_b, M, N, K, trans_a ? M : K, trans_b ? K : N, N));
+  const int layout = matmul_layout(trans_a, trans_b);
+  *bytes = dtype == KAN_DTYPE_F32 ? 4 * (size_t)matmul_ws_elems<float>(layout, M, N, K)
+                                  : 8 * (size_t)matmul_ws_elems<double>(layout, M, N, K);
+  return KAN_OK;
+}
+
+int kan_hip_matmul(int dtype, int trans_a, int trans_b, int64_t M, int64_t N, int64_t K,
+                   const void* A, int64_t lda, const void* B, int64_t ldb, void* C, int64_t ldc,
+                   void* ws, size_t ws_bytes, void* stream) {
+  KAN_TRY(check_matmul(dtype, trans_a, trans_b, M, N, K, lda, ldb, ldc));
+  if (M * N == 0) return KAN_OK;
+  KAN_TRY(need_ptr(C, "kan_matmul", "C"));
+  if (K > 0) {
+    KAN_TRY(need_ptr(A, "kan_matmul", "A"));
+    KAN_TRY(need_ptr(B, "kan_matmul", "B"));
+  }
+  const int layout = matmul_layout(trans_a, trans_b);
+  const size_t elem = dtype == KAN_DTYPE_F32 ? 4 : 8;
+  const size_t need = elem * (size_t)(dtype == KAN_DTYPE_F32
+                                          ? matmul_ws_elems<float>(layout, M, N, K)
+                                          : matmul_ws_elems<double>(layout, M, N, K));
+  if (ws_bytes < need || (need > 0 && ws == nullptr))
+    return set_error(KAN_ERR_WORKSPACE, "kan_matmul: workspace of %zu bytes is smaller than the %zu required",
+                     ws_bytes, need);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (dtype == KAN_DTYPE_F32)
+    return launch_matmul<float>(layout, M, N, K, static_cast<const float*>(A), lda,
+                                static_cast<const float*>(B), ldb, static_cast<float*>(C), ldc,
+                                static_cast<float*>(ws), st);
+  return launch_matmul<double>(layout, M, N, K, static_cast<const double*>(A), lda,
+                               static_cast<const double*>(B), ldb, static_cast<double*>(C), ldc,
+                               static_cast<double*>(ws), st);
+}
+
 int kan_hip_basis_deriv(int dtype, const void* x, const void* grid, void* out, int64_t n,
                         int64_t I, int64_t G, int64_t k, int64_t order, void* stream) {
   KAN_TRY(check_dtype(dtype, "kan_basis_deriv"));

@@ -140,6 +140,7 @@ enum GemmLayout {
   kLayoutNT = 0,  // C[m,n] = sum_k A[m*lda+k] * B[n*ldb+k]
   kLayoutTN = 1,  // C[m,n] = sum_k A[k*lda+m] * B[k*ldb+n]
   kLayoutNN = 2,  // C[m,n] = sum_k A[m*lda+k] * B[k*ldb+n]
+  kLayoutTT = 3,  // C[m,n] = sum_k A[k*lda+m] * B[n*ldb+k]
 };
 
 // C (+ split * split_stride) = partial product over the split's K range.
@@ -157,6 +158,15 @@ int launch_gemm_dx(int64_t M, int64_t N, int64_t K, const float* A, int64_t lda,
 // Whether launch_gemm_dx takes this shape (the tile configuration it would
 // pick leaves room for every block's knots and samples).
 bool gemm_dx_supported(int64_t M, int64_t N, int64_t K, int64_t I, int G, int k, bool has_base);
+
+// General product C = op(A) op(B) for any transposition pair: the split
+// count from gemm_pick_splits, partial slices in ws, then a fixed-order sum
+// into C (kan_gemm.hip).  ws must hold matmul_ws_elems(...) elements.
+template <typename T>
+int64_t matmul_ws_elems(int layout, int64_t M, int64_t N, int64_t K);
+template <typename T>
+int launch_matmul(int layout, int64_t M, int64_t N, int64_t K, const T* A, int64_t lda,
+                  const T* B, int64_t ldb, T* C, int64_t ldc, T* ws, hipStream_t st);
 
 // Split count the GEMM scheduler would choose for a problem (1 = no split).
 template <typename T>

@@ -776,6 +776,7 @@ int launch_layout(int layout, const GemmParams<typename C::T>& p, int splits, hi
     case kLayoutNT: return launch_cfg<C, true, true>(p, splits, st);
     case kLayoutTN: return launch_cfg<C, false, false>(p, splits, st);
     case kLayoutNN: return launch_cfg<C, true, false>(p, splits, st);
+    case kLayoutTT: return launch_cfg<C, false, true>(p, splits, st);
     default: return set_error(KAN_ERR_INVALID, "gemm: unknown layout %d", layout);
   }
 }
@@ -856,6 +857,71 @@ int launch_gemm(int layout, int64_t M, int64_t N, int64_t K, const T* A, int64_t
   if (rc != KAN_OK) return rc;
   return check_launch("gemm");
 }
+
+namespace {
+// C[m, n] = sum_s part[s][m, n], s in order (deterministic split-K result).
+template <typename T>
+__global__ void split_sum_kernel(const T* __restrict__ part, int splits, int64_t M, int64_t N,
+                                 T* __restrict__ C, int64_t ldc) {
+  const int64_t count = M * N, stride = M * N;
+  for (int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; e < count;
+       e += (int64_t)gridDim.x * blockDim.x) {
+    T v = part[e];
+    for (int s = 1; s < splits; ++s) v += part[s * stride + e];
+    const int64_t m = e / N, n = e - m * N;
+    C[m * ldc + n] = v;
+  }
+}
+
+template <typename T>
+__global__ void fill_rows_kernel(T* __restrict__ C, int64_t M, int64_t N, int64_t ldc) {
+  const int64_t count = M * N;
+  for (int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; e < count;
+       e += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t m = e / N, n = e - m * N;
+    C[m * ldc + n] = T(0);
+  }
+}
+
+inline unsigned flat_blocks(int64_t count) {
+  int64_t b = ceil_div(count, 256);
+  if (b > 65536) b = 65536;
+  return (unsigned)(b < 1 ? 1 : b);
+}
+}  // namespace
+
+template <typename T>
+int64_t matmul_ws_elems(int layout, int64_t M, int64_t N, int64_t K) {
+  (void)layout;
+  if (M <= 0 || N <= 0 || K <= 0) return 0;
+  const int s = gemm_pick_splits<T>(M, N, K);
+  return s > 1 ? (int64_t)s * M * N : 0;
+}
+
+template <typename T>
+int launch_matmul(int layout, int64_t M, int64_t N, int64_t K, const T* A, int64_t lda,
+                  const T* B, int64_t ldb, T* C, int64_t ldc, T* ws, hipStream_t st) {
+  if (M <= 0 || N <= 0) return KAN_OK;
+  if (K <= 0) {
+    hipLaunchKernelGGL(fill_rows_kernel<T>, dim3(flat_blocks(M * N)), dim3(256), 0, st, C, M, N,
+                       ldc);
+    return check_launch("matmul (K = 0)");
+  }
+  const int s = gemm_pick_splits<T>(M, N, K);
+  if (s <= 1) return launch_gemm<T>(layout, M, N, K, A, lda, B, ldb, C, ldc, 1, 0, st);
+  const int rc = launch_gemm<T>(layout, M, N, K, A, lda, B, ldb, ws, N, s, M * N, st);
+  if (rc != KAN_OK) return rc;
+  hipLaunchKernelGGL(split_sum_kernel<T>, dim3(flat_blocks(M * N)), dim3(256), 0, st, ws, s, M,
+                     N, C, ldc);
+  return check_launch("matmul split sum");
+}
+
+template int64_t matmul_ws_elems<float>(int, int64_t, int64_t, int64_t);
+template int64_t matmul_ws_elems<double>(int, int64_t, int64_t, int64_t);
+template int launch_matmul<float>(int, int64_t, int64_t, int64_t, const float*, int64_t,
+                                  const float*, int64_t, float*, int64_t, float*, hipStream_t);
+template int launch_matmul<double>(int, int64_t, int64_t, int64_t, const double*, int64_t,
+                                   const double*, int64_t, double*, int64_t, double*, hipStream_t);
 
 bool gemm_dx_supported(int64_t M, int64_t N, int64_t K, int64_t I, int G, int k, bool has_base) {
   if (k < 1 || k > 3) return false;
