@@ -177,6 +177,31 @@ int kan_hip_edge_abs_mean_backward(int dtype, const void* grad_a, const void* s,
                                    size_t workspace_bytes, int64_t n, int64_t in_features,
                                    int64_t out_features, int64_t num_basis, void* stream);
 
+/* Double backward of the edge statistic, used when the regulariser's
+ * backward is itself recorded (create_graph=True).  With the sign pattern
+ * S = sign(phi) of the forward operands held fixed (its derivative is zero
+ * almost everywhere), the first-order gradients ds, dH, dbw, dW of
+ * kan_hip_edge_abs_mean_backward are linear in ga and in the operands they
+ * contract; given incoming gradients u_ds [n, I], u_dH [n, I, R],
+ * u_dbw [O, I], u_dW [O, I, R] (any may be NULL = zero) this writes
+ *   g_ga[o,i]   = (1/n) sum_m S (u_ds bw + <u_dH, W> + s u_dbw + <H, u_dW>)
+ *   g_bw, g_W   = (1/n) sum_m S ga [u_ds, u_dH]          (over samples)
+ *   g_s, g_H    = (1/n) sum_o S ga [u_dbw, u_dW]         (over outputs)
+ * (any output may be NULL).  Replaces the dense differentiable formulas of
+ * EdgeAbsMean.backward under create_graph (spline_kan/fused.py:80-95),
+ * which build the [n, O, I] sign tensor.  Workspace: query with the
+ * _workspace call. */
+int kan_hip_edge_abs_mean_double_backward_workspace(int dtype, int64_t n, int64_t in_features,
+                                                    int64_t out_features, int64_t R,
+                                                    size_t* bytes);
+int kan_hip_edge_abs_mean_double_backward(int dtype, const void* grad_a, const void* s,
+                                          const void* H, const void* base_weight, const void* W,
+                                          const void* u_ds, const void* u_dH, const void* u_dbw,
+                                          const void* u_dW, void* g_ga, void* g_s, void* g_H,
+                                          void* g_bw, void* g_W, void* ws, size_t ws_bytes,
+                                          int64_t n, int64_t in_features, int64_t out_features,
+                                          int64_t R, void* stream);
+
 /* Gram matrices of the least-squares spline refit used by update_grid and
  * extend_grid, per input feature i, accumulated in float64:
  *   gram[i]  = sum_b bn(x[b,i]) bn(x[b,i])^T   [I, Rn, Rn]  (A^T A on the new grid)

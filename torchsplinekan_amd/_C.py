@@ -549,3 +549,112 @@ def edge_abs_mean_backward(grad_a, s, H, base_weight, W, need_s: bool, need_H: b
             code, ptr(ga), ptr(sc), ptr(H), ptr(bw), ptr(W), ptr(ds), ptr(dH), ptr(dbw), ptr(dW),
             ptr(ws), int(nbytes.value), N, I, O, R, stream_of(H.device)))
     return ds, dH, dbw, dW
+
+
+def edge_abs_mean_double_backward(grad_a, s, H, base_weight, W, u_ds, u_dH, u_dbw, u_dW,
+                                  need_ga: bool, need_s: bool, need_H: bool, need_bw: bool,
+                                  need_W: bool):
+    """Double backward of edge_abs_mean at a fixed sign pattern (device):
+    gradients of <u_ds, ds> + <u_dH, dH> + <u_dbw, dbw> + <u_dW, dW> with
+    respect to (ga, s, H, bw, W); any u may be None (zero).  Returns
+    (g_ga, g_s, g_H, g_bw, g_W), None where not requested."""
+    hb = _cmp.has_base(base_weight)
+    _check_edge_inputs(s, H, base_weight, W, hb)
+    N, I, R = H.shape
+    O = W.shape[0]
+    _req(tuple(grad_a.shape) == (O, I), "edge_abs_mean_double_backward: grad shape")
+    cont = lambda t: None if t is None else t.contiguous().to(H.dtype)
+    if not hb:
+        u_ds = u_dbw = None
+    H, W, ga = H.contiguous(), W.contiguous(), cont(grad_a)
+    sc, bw = (cont(s), cont(base_weight)) if hb else (None, None)
+    u_ds, u_dH, u_dbw, u_dW = cont(u_ds), cont(u_dH), cont(u_dbw), cont(u_dW)
+    for u, shape in ((u_ds, (N, I)), (u_dH, (N, I, R)), (u_dbw, (O, I)), (u_dW, (O, I, R))):
+        _req(u is None or tuple(u.shape) == shape, "edge_abs_mean_double_backward: gradient shape")
+    opts = dict(dtype=H.dtype, device=H.device)
+    outs = (torch.empty(O, I, **opts) if need_ga else None,
+            torch.empty(N, I, **opts) if (need_s and hb) else None,
+            torch.empty(N, I, R, **opts) if need_H else None,
+            torch.empty(O, I, **opts) if (need_bw and hb) else None,
+            torch.empty(O, I, R, **opts) if need_W else None)
+    if any(t is not None for t in outs):
+        g_ga, g_s, g_H, g_bw, g_W = outs
+        code = dtype_code(H.dtype)
+        nbytes = _lib.ctypes.c_size_t(0)
+        with torch.cuda.device(H.device):
+            check(LIB.kan_hip_edge_abs_mean_double_backward_workspace(
+                code, N, I, O, R, _lib.ctypes.byref(nbytes)))
+            ws = torch.empty(max(int(nbytes.value), 1), dtype=torch.uint8, device=H.device)
+            check(LIB.kan_hip_edge_abs_mean_double_backward(
+                code, ptr(ga), ptr(sc), ptr(H), ptr(bw), ptr(W), ptr(u_ds), ptr(u_dH),
+                ptr(u_dbw), ptr(u_dW), ptr(g_ga), ptr(g_s), ptr(g_H), ptr(g_bw), ptr(g_W),
+                ptr(ws), int(nbytes.value), N, I, O, R, stream_of(H.device)))
+    return outs
+
+
+def _edge_double_backward_dense(ga, s, H, bw, W, u_ds, u_dH, u_dbw, u_dW, needs):
+    """The same double backward as differentiable PyTorch formulas (used when
+    it is itself recorded, i.e. third order).  Builds the [n, O, I] signs."""
+    n = H.shape[0]
+    phi = torch.einsum("oir,nir->noi", W, H)
+    if bw is not None:
+        phi = s.unsqueeze(1) * bw.unsqueeze(0) + phi
+    S = phi.sign().detach()
+    g = S * ga.unsqueeze(0) / n
+    need_ga, need_s, need_H, need_bw, need_W = needs
+    g_ga = g_s = g_H = g_bw = g_W = None
+    if need_ga:
+        t = torch.zeros_like(phi)
+        if u_dH is not None:
+            t = t + torch.einsum("nir,oir->noi", u_dH, W)
+        if u_dW is not None:
+            t = t + torch.einsum("nir,oir->noi", H, u_dW)
+        if bw is not None and u_ds is not None:
+            t = t + u_ds.unsqueeze(1) * bw.unsqueeze(0)
+        if bw is not None and u_dbw is not None:
+            t = t + s.unsqueeze(1) * u_dbw.unsqueeze(0)
+        g_ga = (S * t).sum(0) / n
+    if need_bw and bw is not None and u_ds is not None:
+        g_bw = (g * u_ds.unsqueeze(1)).sum(0)
+    if need_W and u_dH is not None:
+        g_W = torch.einsum("noi,nir->oir", g, u_dH)
+    if need_s and bw is not None and u_dbw is not None:
+        g_s = (g * u_dbw.unsqueeze(0)).sum(1)
+    if need_H and u_dW is not None:
+        g_H = torch.einsum("noi,oir->nir", g, u_dW)
+    return g_ga, g_s, g_H, g_bw, g_W
+
+
+class EdgeAbsMeanBackward(torch.autograd.Function):
+    """(ds, dH, dbw, dW) of edge_abs_mean as a differentiable function of
+    (ga, s, H, bw, W): the recorded backward of EdgeAbsMean.  Forward is the
+    native first-order backward; backward is the native double backward
+    (kan_hip_edge_abs_mean_double_backward, sign pattern fixed), so second
+    derivatives of the regulariser, mixed input x weight terms included,
+    never form the [n, O, I] edge tensor.  A third order (this backward
+    recorded again) uses the dense formulas.  ds and dbw are empty tensors
+    for a layer without a base branch."""
+
+    @staticmethod
+    def forward(ctx, ga, s, H, bw, W):
+        hb = bw is not None
+        ctx.hb = hb
+        ctx.set_materialize_grads(False)
+        empty = H.new_empty(0)
+        ctx.save_for_backward(ga, s if hb else empty, H, bw if hb else empty, W)
+        ds, dH, dbw, dW = edge_abs_mean_backward(ga, s, H, bw, W, hb, True, hb, True)
+        if not hb:
+            ds, dbw = empty.clone(), empty.clone()
+            ctx.mark_non_differentiable(ds, dbw)
+        return ds, dH, dbw, dW
+
+    @staticmethod
+    def backward(ctx, u_ds, u_dH, u_dbw, u_dW):
+        ga, s, H, bw, W = ctx.saved_tensors
+        if not ctx.hb:
+            s = bw = None
+            u_ds = u_dbw = None
+        needs = tuple(bool(v) for v in ctx.needs_input_grad)
+        if torch.is_grad_enabled():
+            return _edge_double_backward_dense(ga, s, H, bw, W, u_ds, u_dH, u_dbw, u_dW, needs)
+        return edge_abs_mean_double_backward(ga, s, H, bw, W, u_ds, u_dH, u_dbw, u_dW, *needs)

@@ -616,6 +616,44 @@ int kan_hip_edge_abs_mean_backward(int dtype, const void* ga, const void* s, con
       static_cast<double*>(ws), splits, n, I, O, R, st);
 }
 
+int kan_hip_edge_abs_mean_double_backward_workspace(int dtype, int64_t n, int64_t I, int64_t O,
+                                                    int64_t R, size_t* bytes) {
+  KAN_TRY(check_dtype(dtype, "edge_abs_mean_double_backward_workspace"));
+  KAN_TRY(need_ptr(bytes, "edge_abs_mean_double_backward_workspace", "bytes"));
+  if (n < 0 || I < 0 || O < 0 || R < 1)
+    return set_error(KAN_ERR_INVALID, "edge_abs_mean_double_backward_workspace: bad sizes");
+  *bytes = (dtype == KAN_DTYPE_F32 ? 4 : 8) * edge_double_backward_ws_elems(n, I, O, R);
+  return KAN_OK;
+}
+
+int kan_hip_edge_abs_mean_double_backward(int dtype, const void* ga, const void* s,
+                                          const void* H, const void* bw, const void* W,
+                                          const void* u_ds, const void* u_dH, const void* u_dbw,
+                                          const void* u_dW, void* g_ga, void* g_s, void* g_H,
+                                          void* g_bw, void* g_W, void* ws, size_t ws_bytes,
+                                          int64_t n, int64_t I, int64_t O, int64_t R,
+                                          void* stream) {
+  KAN_TRY(check_edge("edge_abs_mean_double_backward", dtype, s, H, bw, W, n, I, O, R));
+  KAN_TRY(need_ptr(ga, "edge_abs_mean_double_backward", "grad_a"));
+  if (bw == nullptr && (u_ds != nullptr || u_dbw != nullptr || g_s != nullptr || g_bw != nullptr))
+    return set_error(KAN_ERR_INVALID,
+                     "edge_abs_mean_double_backward: base-branch operands without a base branch");
+  const size_t need = (dtype == KAN_DTYPE_F32 ? 4 : 8) * edge_double_backward_ws_elems(n, I, O, R);
+  if (ws_bytes < need || (need > 0 && ws == nullptr))
+    return set_error(KAN_ERR_WORKSPACE, "edge_abs_mean_double_backward: workspace of %zu bytes is smaller than the %zu required", ws_bytes, need);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+#define KAN_EDB_CALL(T)                                                                         \
+  launch_edge_double_backward<T>(                                                               \
+      static_cast<const T*>(ga), static_cast<const T*>(s), static_cast<const T*>(H),            \
+      static_cast<const T*>(bw), static_cast<const T*>(W), static_cast<const T*>(u_ds),         \
+      static_cast<const T*>(u_dH), static_cast<const T*>(u_dbw), static_cast<const T*>(u_dW),   \
+      static_cast<T*>(g_ga), static_cast<T*>(g_s), static_cast<T*>(g_H), static_cast<T*>(g_bw), \
+      static_cast<T*>(g_W), static_cast<T*>(ws), n, I, O, R, st)
+  if (dtype == KAN_DTYPE_F32) return KAN_EDB_CALL(float);
+  return KAN_EDB_CALL(double);
+#undef KAN_EDB_CALL
+}
+
 int kan_hip_refit_gram(int dtype, const void* x_t, const void* grid_old, const void* grid_new,
                        double* gram, double* cross, int64_t n, int64_t I, int64_t G_old,
                        int64_t G_new, int64_t k, void* stream) {

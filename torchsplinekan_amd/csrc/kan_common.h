@@ -181,6 +181,16 @@ int launch_edge_backward(const T* ga, const T* s, const T* H, const T* bw, const
                          T* dH, T* dbw, T* dW, T* part, int splits, int64_t n, int64_t I,
                          int64_t O, int64_t R, hipStream_t st);
 
+// Double backward of the edge statistic (VALU kernels, fp32 and fp64): the
+// gradients of <u_ds, ds> + <u_dH, dH> + <u_dbw, dbw> + <u_dW, dW> with
+// respect to ga, s, H, bw and W at a fixed sign pattern (kan_edge.hip).
+size_t edge_double_backward_ws_elems(int64_t n, int64_t I, int64_t O, int64_t R);
+template <typename T>
+int launch_edge_double_backward(const T* ga, const T* s, const T* H, const T* bw, const T* W,
+                                const T* u_ds, const T* u_dH, const T* u_dbw, const T* u_dW,
+                                T* g_ga, T* g_s, T* g_H, T* g_bw, T* g_W, T* part, int64_t n,
+                                int64_t I, int64_t O, int64_t R, hipStream_t st);
+
 // Sample splits of the edge statistic (dtype code selects the fp32 MFMA or
 // the fp64 VALU kernels, which partition differently).
 int edge_pick_splits(int dtype, int64_t n, int64_t I, int64_t O, int64_t R);

@@ -61,6 +61,27 @@ __device__ __forceinline__ T edge_phi(const T* __restrict__ h, const T (&w)[RP],
   return phi;
 }
 
+// stage_h for optional operands: a null s or H stages zeros.
+template <typename T, int RP>
+__device__ __forceinline__ void stage_h_opt(T (*hs)[RP], const T* __restrict__ s,
+                                           const T* __restrict__ H, int64_t m0, int tn, int I,
+                                           int i, int R) {
+  const int R1 = R + 1;
+  const float inv = 1.0f / (float)R1;
+  for (int e = threadIdx.x; e < tn * R1; e += blockDim.x) {
+    const int tt = small_div_e(e, inv);
+    const int c = e - tt * R1;
+    const int64_t m = m0 + tt;
+    T v = T(0);
+    if (c == 0) {
+      if (s != nullptr) v = s[m * I + i];
+    } else if (H != nullptr) {
+      v = H[(m * I + i) * R + (c - 1)];
+    }
+    hs[tt][c] = v;
+  }
+}
+
 template <typename T, int RP>
 __global__ __launch_bounds__(kEdgeThreads) void edge_forward_kernel(
     const T* __restrict__ s, const T* __restrict__ H, const T* __restrict__ bw,
@@ -110,12 +131,18 @@ __global__ void edge_forward_finalize(const T* __restrict__ part, T* __restrict_
 // Parameter gradients: thread (o, i), sum over samples of g * h.
 // final_out: write dbw/dW directly; otherwise write the split's partial
 // [R+1] vector per edge into part.
-template <typename T, int RP>
+// SUB: the contraction rows come from (s2, H2) (either may be null = zero)
+// while sign(phi) still comes from (s, H) and (bw, W): the double backward
+// of the statistic contracts the incoming gradients with the same sign
+// pattern.
+template <typename T, int RP, bool SUB = false>
 __global__ __launch_bounds__(kEdgeThreads) void edge_param_grad_kernel(
     const T* __restrict__ ga, const T* __restrict__ s, const T* __restrict__ H,
     const T* __restrict__ bw, const T* __restrict__ W, T* __restrict__ dbw, T* __restrict__ dW,
-    T* __restrict__ part, int64_t n, int I, int O, int R, int64_t per_split, bool final_out) {
+    T* __restrict__ part, int64_t n, int I, int O, int R, int64_t per_split, bool final_out,
+    const T* __restrict__ s2 = nullptr, const T* __restrict__ H2 = nullptr) {
   __shared__ __align__(16) T hs[kEdgeTile][RP];
+  __shared__ __align__(16) T hs2[SUB ? kEdgeTile : 1][RP];
   const int i = blockIdx.y;
   const int o = blockIdx.x * kEdgeThreads + threadIdx.x;
   const bool valid = o < O;
@@ -135,13 +162,15 @@ __global__ __launch_bounds__(kEdgeThreads) void edge_param_grad_kernel(
   for (int64_t m0 = mb; m0 < me; m0 += kEdgeTile) {
     const int tn = (int)min((int64_t)kEdgeTile, me - m0);
     stage_h<T, RP>(hs, s, H, m0, tn, I, i, R);
+    if (SUB) stage_h_opt<T, RP>(hs2, s2, H2, m0, tn, I, i, R);
     __syncthreads();
     if (valid) {
       for (int tt = 0; tt < tn; ++tt) {
         const T g = gav * sign_of(edge_phi<T, RP>(hs[tt], w, R1));
+        const T* hc = SUB ? hs2[tt] : hs[tt];
 #pragma unroll
         for (int c = 0; c < RP; ++c)
-          if (c < R1) dw[c] = fma(g, hs[tt][c], dw[c]);
+          if (c < R1) dw[c] = fma(g, hc[c], dw[c]);
       }
     }
     __syncthreads();
@@ -182,12 +211,15 @@ __global__ void edge_param_finalize(const T* __restrict__ part, T* __restrict__ 
 }
 
 // Input gradients: thread (m, i), sum over outputs of g * w.
-template <typename T, int RP>
+// SUB: contraction rows from (bw2, W2) (null = zero), sign from (bw, W).
+template <typename T, int RP, bool SUB = false>
 __global__ __launch_bounds__(kEdgeThreads) void edge_input_grad_kernel(
     const T* __restrict__ ga, const T* __restrict__ s, const T* __restrict__ H,
     const T* __restrict__ bw, const T* __restrict__ W, T* __restrict__ ds, T* __restrict__ dH,
-    int64_t n, int I, int O, int R) {
+    int64_t n, int I, int O, int R, const T* __restrict__ bw2 = nullptr,
+    const T* __restrict__ W2 = nullptr) {
   __shared__ __align__(16) T ws[kEdgeTile][RP];
+  __shared__ __align__(16) T ws2[SUB ? kEdgeTile : 1][RP];
   __shared__ T gs[kEdgeTile];
   const int i = blockIdx.y;
   const int64_t m = (int64_t)blockIdx.x * kEdgeThreads + threadIdx.x;
@@ -210,6 +242,15 @@ __global__ __launch_bounds__(kEdgeThreads) void edge_input_grad_kernel(
       const int c = x - tt * R1;
       const int64_t e = (int64_t)(o0 + tt) * I + i;
       ws[tt][c] = (c == 0) ? (bw != nullptr ? bw[e] : T(0)) : W[e * R + (c - 1)];
+      if (SUB) {
+        T v = T(0);
+        if (c == 0) {
+          if (bw2 != nullptr) v = bw2[e];
+        } else if (W2 != nullptr) {
+          v = W2[e * R + (c - 1)];
+        }
+        ws2[tt][c] = v;
+      }
     }
     for (int x = threadIdx.x; x < to; x += blockDim.x)
       gs[x] = ga[(int64_t)(o0 + x) * I + i] / (T)n;
@@ -222,9 +263,10 @@ __global__ __launch_bounds__(kEdgeThreads) void edge_input_grad_kernel(
         for (int c = 0; c < RP; ++c)
           if (c < R1) phi = fma(h[c], wr[c], phi);
         const T g = gs[tt] * sign_of(phi);
+        const T* wc = SUB ? ws2[tt] : wr;
 #pragma unroll
         for (int c = 0; c < RP; ++c)
-          if (c < R1) dh[c] = fma(g, wr[c], dh[c]);
+          if (c < R1) dh[c] = fma(g, wc[c], dh[c]);
       }
     }
     __syncthreads();
@@ -236,6 +278,67 @@ __global__ __launch_bounds__(kEdgeThreads) void edge_input_grad_kernel(
     for (int c = 1; c < RP; ++c)
       if (c < R1) dH[f * R + (c - 1)] = dh[c];
   }
+}
+
+// d/dga of the double backward: thread (o, i),
+//   out[o, i] = sum_m sign(h.w) (h1.w + h.w2)   (h1 = [s1, H1], w2 = [bw2, W2]),
+// divided by n in the finalize (or here when the sum is not split).
+template <typename T, int RP>
+__global__ __launch_bounds__(kEdgeThreads) void edge_ga_grad_kernel(
+    const T* __restrict__ s, const T* __restrict__ H, const T* __restrict__ bw,
+    const T* __restrict__ W, const T* __restrict__ s1, const T* __restrict__ H1,
+    const T* __restrict__ bw2, const T* __restrict__ W2, T* __restrict__ out, int64_t n, int I,
+    int O, int R, int64_t per_split, bool final_out) {
+  __shared__ __align__(16) T hs[kEdgeTile][RP];
+  __shared__ __align__(16) T hs1[kEdgeTile][RP];
+  const int i = blockIdx.y;
+  const int o = blockIdx.x * kEdgeThreads + threadIdx.x;
+  const bool valid = o < O;
+  const int R1 = R + 1;
+  const int64_t e = (int64_t)o * I + i;
+  T w[RP], w2[RP];
+#pragma unroll
+  for (int c = 0; c < RP; ++c) {
+    T v = T(0), v2 = T(0);
+    if (valid && c < R1) {
+      if (c == 0) {
+        v = bw != nullptr ? bw[e] : T(0);
+        v2 = bw2 != nullptr ? bw2[e] : T(0);
+      } else {
+        v = W[e * R + (c - 1)];
+        v2 = W2 != nullptr ? W2[e * R + (c - 1)] : T(0);
+      }
+    }
+    w[c] = v;
+    w2[c] = v2;
+  }
+  const int64_t mb = (int64_t)blockIdx.z * per_split;
+  const int64_t me = min(n, mb + per_split);
+  T acc = T(0);
+  for (int64_t m0 = mb; m0 < me; m0 += kEdgeTile) {
+    const int tn = (int)min((int64_t)kEdgeTile, me - m0);
+    stage_h<T, RP>(hs, s, H, m0, tn, I, i, R);
+    stage_h_opt<T, RP>(hs1, s1, H1, m0, tn, I, i, R);
+    __syncthreads();
+    if (valid) {
+      for (int tt = 0; tt < tn; ++tt) {
+        const T sg = sign_of(edge_phi<T, RP>(hs[tt], w, R1));
+        const T psi = edge_phi<T, RP>(hs1[tt], w, R1) + edge_phi<T, RP>(hs[tt], w2, R1);
+        acc = fma(sg, psi, acc);
+      }
+    }
+    __syncthreads();
+  }
+  if (!valid) return;
+  if (final_out) out[e] = acc / (T)n;
+  else out[(int64_t)blockIdx.z * ((int64_t)O * I) + e] = acc;
+}
+
+template <typename T>
+__global__ void edge_zero_kernel(T* __restrict__ out, int64_t count) {
+  for (int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; e < count;
+       e += (int64_t)gridDim.x * blockDim.x)
+    out[e] = T(0);
 }
 
 inline int fin_blocks(int64_t total) {
@@ -337,6 +440,112 @@ int launch_edge_backward(const T* ga, const T* s, const T* H, const T* bw, const
   }
   return KAN_OK;
 }
+
+// Splits over samples for the VALU edge kernels (the sample sums).
+int edge_valu_splits(int64_t n, int64_t I, int64_t O) {
+  const int64_t blocks = ceil_div(O, kEdgeThreads) * I;
+  const int64_t target = 4LL * device_cu_count();
+  int64_t s = ceil_div(target, blocks > 0 ? blocks : 1);
+  const int64_t cap = ceil_div(n, 4 * kEdgeTile);
+  if (s > cap) s = cap;
+  if (s > 64) s = 64;
+  if (s < 1) s = 1;
+  return (int)s;
+}
+
+size_t edge_double_backward_ws_elems(int64_t n, int64_t I, int64_t O, int64_t R) {
+  const int splits = edge_valu_splits(n, I, O);
+  if (splits <= 1) return 0;
+  return (size_t)splits * (size_t)(O * I) * (size_t)(R + 1);  // covers the [s, O, I] slices too
+}
+
+template <typename T>
+int launch_edge_double_backward(const T* ga, const T* s, const T* H, const T* bw, const T* W,
+                                const T* u_ds, const T* u_dH, const T* u_dbw, const T* u_dW,
+                                T* g_ga, T* g_s, T* g_H, T* g_bw, T* g_W, T* part, int64_t n,
+                                int64_t I, int64_t O, int64_t R, hipStream_t st) {
+  const int R1 = (int)R + 1;
+  const int splits = edge_valu_splits(n, I, O);
+  if (splits > 1 && part == nullptr)
+    return set_error(KAN_ERR_WORKSPACE, "edge_abs_mean_double_backward: missing workspace");
+  const int64_t per_split = round_up(ceil_div(n, splits), kEdgeTile);
+  const bool fin = splits == 1;
+  const bool u_rows = u_ds != nullptr || u_dH != nullptr;   // sample-side incoming gradients
+  const bool u_cols = u_dbw != nullptr || u_dW != nullptr;  // weight-side incoming gradients
+  if (g_ga != nullptr && O > 0 && I > 0) {
+    dim3 grid((unsigned)ceil_div(O, kEdgeThreads), (unsigned)I, (unsigned)splits);
+    TimedLaunch timed(kClassEdgeGrad, st, 6.0 * (double)n * (double)O * (double)I * (double)R1);
+    KAN_EDGE_DISPATCH(R1, hipLaunchKernelGGL((edge_ga_grad_kernel<T, RP>), grid,
+                                             dim3(kEdgeThreads), 0, st, s, H, bw, W, u_ds, u_dH,
+                                             u_dbw, u_dW, fin ? g_ga : part, n, (int)I, (int)O,
+                                             (int)R, per_split, fin));
+    int rc = check_launch("edge_abs_mean_double_backward(ga)");
+    if (rc != KAN_OK) return rc;
+    if (!fin) {
+      hipLaunchKernelGGL((edge_forward_finalize<T>), dim3(fin_blocks(O * I)), dim3(256), 0, st,
+                         part, g_ga, splits, O * I, n);
+      rc = check_launch("edge_abs_mean_double_backward(ga finalize)");
+      if (rc != KAN_OK) return rc;
+    }
+  }
+  if ((g_bw != nullptr || g_W != nullptr) && O > 0 && I > 0) {
+    if (!u_rows) {
+      // no sample-side incoming gradient: these are zero
+      if (g_bw != nullptr)
+        hipLaunchKernelGGL((edge_zero_kernel<T>), dim3(fin_blocks(O * I)), dim3(256), 0, st,
+                           g_bw, O * I);
+      if (g_W != nullptr)
+        hipLaunchKernelGGL((edge_zero_kernel<T>), dim3(fin_blocks(O * I * R)), dim3(256), 0, st,
+                           g_W, O * I * R);
+    } else {
+      dim3 grid((unsigned)ceil_div(O, kEdgeThreads), (unsigned)I, (unsigned)splits);
+      TimedLaunch timed(kClassEdgeGrad, st, 4.0 * (double)n * (double)O * (double)I * (double)R1);
+      KAN_EDGE_DISPATCH(R1, hipLaunchKernelGGL((edge_param_grad_kernel<T, RP, true>), grid,
+                                               dim3(kEdgeThreads), 0, st, ga, s, H, bw, W, g_bw,
+                                               g_W, part, n, (int)I, (int)O, (int)R, per_split,
+                                               fin, u_ds, u_dH));
+      int rc = check_launch("edge_abs_mean_double_backward(params)");
+      if (rc != KAN_OK) return rc;
+      if (!fin) {
+        hipLaunchKernelGGL((edge_param_finalize<T>), dim3(fin_blocks(O * I * R1)), dim3(256), 0,
+                           st, part, g_bw, g_W, splits, O * I, (int)R);
+        rc = check_launch("edge_abs_mean_double_backward(params finalize)");
+        if (rc != KAN_OK) return rc;
+      }
+    }
+  }
+  if ((g_s != nullptr || g_H != nullptr) && n > 0 && I > 0) {
+    if (!u_cols) {
+      if (g_s != nullptr)
+        hipLaunchKernelGGL((edge_zero_kernel<T>), dim3(fin_blocks(n * I)), dim3(256), 0, st, g_s,
+                           n * I);
+      if (g_H != nullptr)
+        hipLaunchKernelGGL((edge_zero_kernel<T>), dim3(fin_blocks(n * I * R)), dim3(256), 0, st,
+                           g_H, n * I * R);
+    } else {
+      dim3 grid((unsigned)ceil_div(n, kEdgeThreads), (unsigned)I);
+      TimedLaunch timed(kClassEdgeGrad, st, 4.0 * (double)n * (double)O * (double)I * (double)R1);
+      KAN_EDGE_DISPATCH(R1, hipLaunchKernelGGL((edge_input_grad_kernel<T, RP, true>), grid,
+                                               dim3(kEdgeThreads), 0, st, ga, s, H, bw, W, g_s,
+                                               g_H, n, (int)I, (int)O, (int)R, u_dbw, u_dW));
+    }
+    int rc = check_launch("edge_abs_mean_double_backward(inputs)");
+    if (rc != KAN_OK) return rc;
+  }
+  return check_launch("edge_abs_mean_double_backward");
+}
+
+template int launch_edge_double_backward<float>(const float*, const float*, const float*,
+                                                const float*, const float*, const float*,
+                                                const float*, const float*, const float*, float*,
+                                                float*, float*, float*, float*, float*, int64_t,
+                                                int64_t, int64_t, int64_t, hipStream_t);
+template int launch_edge_double_backward<double>(const double*, const double*, const double*,
+                                                 const double*, const double*, const double*,
+                                                 const double*, const double*, const double*,
+                                                 double*, double*, double*, double*, double*,
+                                                 double*, int64_t, int64_t, int64_t, int64_t,
+                                                 hipStream_t);
 
 template <>
 int launch_edge_forward<float>(const float* s, const float* H, const float* bw, const float* W,

@@ -11,9 +11,11 @@ storing the [N, O, I] edge tensor; its backward recomputes phi to get
 sign(phi).  ``NativeBasis`` evaluates H on the device; its backward contracts
 the incoming gradient with dB/dx in registers.  When the backward itself is
 recorded (create_graph=True), NativeBasis's backward is the native
-DerivContract (differentiable to any order on the device kernels), and
-EdgeAbsMean's switches to differentiable PyTorch formulas, so higher-order
-derivatives stay exact (fused.py:43-102 of the reference).
+DerivContract (differentiable to any order on the device kernels) and
+EdgeAbsMean's is the native EdgeAbsMeanBackward, whose own backward runs the
+double-backward kernels at the fixed sign pattern; higher-order derivatives
+stay exact without the dense [N, O, I] tensors of the reference's recorded
+path (fused.py:43-102 of the reference).
 """
 
 from typing import Optional
@@ -66,6 +68,14 @@ class EdgeAbsMean(torch.autograd.Function):
         s, H, bw, W = ctx.saved_tensors
         has_base = ctx.has_base
         need_s, need_H, need_bw, need_W = ctx.needs_input_grad
+        if torch.is_grad_enabled() and H.is_cuda:
+            # Recorded backward: a differentiable native function of the
+            # saved tensors themselves (mixed input x weight terms kept),
+            # whose own backward runs the native double-backward kernels.
+            ds, dH, dbw, dW = _C.EdgeAbsMeanBackward.apply(
+                ga, s if has_base else None, H, bw if has_base else None, W)
+            return (ds if need_s and has_base else None, dH if need_H else None,
+                    dbw if need_bw and has_base else None, dW if need_W else None)
         if torch.is_grad_enabled():
             # Partial derivatives written in the saved tensors themselves, so
             # that double backward keeps the mixed (input x weight) terms;
