@@ -41,13 +41,14 @@ def parse():
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workload", default="c3",
-                    choices=["c3", "c3-nodx", "c4", "refit", "pinn"],
+                    choices=["c3", "c3-nodx", "c4", "refit", "pinn", "infer"],
                     help="c3 (the metric's config, default), c3-nodx (x without grad, the "
                          "reference benchmark's semantics), c4 (KAN([256,512,512,64]) with "
                          "forward_with_regularization), refit (update_grid of c4's 512->512 "
-                         "layer) or pinn (Laplacian loss of KAN([2,128,128,1]) through "
-                         "create_graph); c4, refit and pinn are reported separately, not the "
-                         "metric")
+                         "layer), pinn (Laplacian loss of KAN([2,128,128,1]) through "
+                         "create_graph) or infer (c3's layer, exported, inference forward: "
+                         "throughput at N=65536 and latency at small batches); these are "
+                         "reported separately, not the metric")
     ap.add_argument("--n", type=int, default=65536, help="samples per step (default: config's 65536)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
@@ -343,6 +344,84 @@ def bench_pinn(args):
     print(json.dumps(line), flush=True)
 
 
+def bench_infer(args):
+    """Inference forward of c3's layer (KANLinear(1024->1024, G=10, k=3) fp32,
+    exported: scaler folded, frozen, eval): throughput at N=65536 and latency
+    at small batches, through kan_hip_infer with the packed weight kept,
+    against the training-path forward op (kan_hip_forward: packs the weight
+    and runs the product unsplit on every call)."""
+    import torch
+    from torchsplinekan_amd import KANLinear, _C, _lib
+    dev = torch.device("cuda", 0)
+    I = O = 1024
+    G, k = 10, 3
+    g = torch.Generator().manual_seed(0)
+    L = KANLinear(I, O, grid_size=G, spline_order=k, backend="cuda")
+    with torch.no_grad():
+        L.spline_weight.normal_(0.0, 0.1, generator=g)
+        L.spline_scaler.uniform_(0.5, 1.5, generator=g)
+    E = L.export_inference().to(dev)
+    empty = torch.empty(0, device=dev)
+
+    def ev_median(fn, reps):
+        times = []
+        for _ in range(reps):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            fn()
+            b.record()
+            b.synchronize()
+            times.append(a.elapsed_time(b))
+        return statistics.median(times)
+
+    lat = {}
+    with torch.no_grad():
+        for n in (1, 16, 256, 4096):
+            x = (torch.rand(n, I, generator=g) * 2 - 1).to(dev)
+            f_inf = lambda: E(x)
+            f_fwd = lambda: _C.kan_forward(x, E.grid, E.base_weight, E.spline_weight, empty, k,
+                                           False)
+            for _ in range(3):
+                f_inf()
+                f_fwd()
+            lat[str(n)] = {"infer_ms": ev_median(f_inf, 30), "training_forward_op_ms":
+                           ev_median(f_fwd, 30)}
+        N = 65536
+        x = (torch.rand(N, I, generator=g) * 2 - 1).to(dev)
+        for _ in range(args.warmup):
+            E(x)
+        torch.cuda.synchronize()
+        _lib.timing_enable(True)
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            E(x)
+        torch.cuda.synchronize()
+        wall = (time.perf_counter() - t0) / args.steps
+        c_ms, c_cnt, c_work = _lib.timing_read("contraction")
+        b_ms, b_cnt, _ = _lib.timing_read("basis")
+        _lib.timing_enable(False)
+        fwd_ms = ev_median(lambda: _C.kan_forward(x, E.grid, E.base_weight, E.spline_weight,
+                                                   empty, k, False), max(args.steps, 3))
+    ach = c_work / (c_ms * 1e-3) / 1e12 if c_cnt else 0.0
+    line = {
+        "metric": "inference samples/s, KANLinear 1024->1024 G10 k3 fp32 (exported), N=64K",
+        "value": N / wall, "unit": "samples/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": wall * 1e3, "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic (x ~ U(-1, 1) seeded; coef ~ N(0, 0.1), scaler ~ U(0.5, 1.5) folded)",
+        "config": {"workload": "infer: c3 layer exported, no autograd; latency at n = 1, 16, "
+                               "256, 4096"},
+        "roofline": {"bound": "mfma", "kernel": "gemm_pipe_kernel (NT, packed weight)",
+                     "achieved": ach, "peak": PEAK_FP32_MFMA_TFLOPS, "unit": "TFLOP/s",
+                     "frac": ach / PEAK_FP32_MFMA_TFLOPS, "traffic": None,
+                     "avg_launch_ms": c_ms / max(c_cnt, 1), "launches": c_cnt},
+        "basis_ms": b_ms / max(b_cnt, 1),
+        "training_forward_op_ms_at_64K": fwd_ms,
+        "latency_ms": lat,
+    }
+    print(json.dumps(line), flush=True)
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -366,6 +445,9 @@ def main():
     torch.cuda.set_device(dev)
     if args.workload == "c4":
         bench_c4(args)
+        return
+    if args.workload == "infer":
+        bench_infer(args)
         return
     if args.workload == "pinn":
         bench_pinn(args)

@@ -107,6 +107,25 @@ int kan_hip_matmul(int dtype, int trans_a, int trans_b, int64_t M, int64_t N, in
                    const void* A, int64_t lda, const void* B, int64_t ldb, void* C, int64_t ldc,
                    void* ws, size_t ws_bytes, void* stream);
 
+/* Inference path (no saved basis).  kan_hip_pack_weight writes the packed
+ * weight waug [O, ld] = [spline_weight * spline_scaler | base_weight] once;
+ * an inference caller keeps it while the parameters do not change (the
+ * folding that export_inference performs, spline_kan/kan_linear.py:471-496).
+ * kan_hip_infer then computes output [n, O] from x with that weight: the
+ * augmented basis lives only in the caller's workspace, and products with
+ * few output tiles (small batches) are split over K and summed in a fixed
+ * order.  Same output as kan_hip_forward (csrc/kan_cuda.cu:469-532) up to
+ * the summation order of split products.  kan_hip_infer_workspace sizes ws. */
+int kan_hip_pack_weight(int dtype, const void* base_weight, const void* spline_weight,
+                        const void* spline_scaler, void* weight_aug, int64_t in_features,
+                        int64_t out_features, int64_t grid_size, int64_t spline_order,
+                        void* stream);
+int kan_hip_infer_workspace(int dtype, int64_t n, int64_t in_features, int64_t out_features,
+                            int64_t grid_size, int64_t spline_order, int has_base, size_t* bytes);
+int kan_hip_infer(int dtype, const void* x, const void* grid, const void* weight_aug, void* output,
+                  void* ws, size_t ws_bytes, int64_t n, int64_t in_features, int64_t out_features,
+                  int64_t grid_size, int64_t spline_order, int has_base, void* stream);
+
 /* Row width (elements) of the augmented basis and augmented weight buffers.
  * Returns -1 for invalid sizes.  No reference counterpart: the reference keeps
  * basis [n, I, R] and runs the SiLU branch as a second GEMM

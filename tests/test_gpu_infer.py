@@ -1,0 +1,108 @@
+"""GPU parity of the inference path (kan_hip_pack_weight + kan_hip_infer and
+KANLinear's no-autograd forward): the packed weight is built once for a
+frozen eval-mode layer (export_inference), the basis is never kept, and
+small batches split the product over K.
+
+Checked against the oracle's kan_forward (oracle/kan_oracle.py, after
+csrc/kan_cpu.cpp:136-173) at the forward tolerances: fp64 1e-12 and fp32
+1e-5 normwise."""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import kan_oracle as ko
+from tests._util import make_grid, normwise, np64
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def C():
+    from torchsplinekan_amd import _C
+    assert torch.cuda.is_available(), "GPU tests need a ROCm device"
+    return _C
+
+
+@pytest.mark.parametrize("dtype,tol", [(torch.float64, 1e-12), (torch.float32, 1e-5)])
+@pytest.mark.parametrize("N,I,O,G,k,base,scaler", [
+    (1, 1024, 1024, 10, 3, True, True),      # single sample: the product splits over K
+    (3, 200, 96, 7, 2, True, False),
+    (64, 512, 512, 8, 3, False, True),
+    (700, 33, 19, 5, 1, True, True),
+])
+def test_infer_matches_oracle(C, dtype, tol, N, I, O, G, k, base, scaler):
+    print(f"infer N={N} I={I} O={O} G={G} k={k} base={base} scaler={scaler} {dtype}", flush=True)
+    g = torch.Generator().manual_seed(N + I)
+    grid = make_grid(I, G, k, "nonuniform", seed=G).to(dtype)
+    x = ((torch.rand(N, I, generator=g, dtype=torch.float64) * 2.2 - 1.1)).to(dtype)
+    sw = (torch.randn(O, I, G + k, generator=g, dtype=torch.float64) * 0.1).to(dtype)
+    bw = ((torch.rand(O, I, generator=g, dtype=torch.float64) * 2 - 1) / np.sqrt(I)).to(dtype)
+    sc = (torch.rand(O, I, generator=g, dtype=torch.float64) + 0.5).to(dtype)
+    d = lambda t: t.cuda() if t is not None else None
+    waug = C.pack_weight(d(bw) if base else None, d(sw), d(sc) if scaler else None, k, scaler)
+    y = C.kan_infer(d(x), d(grid), waug, k, base)
+    ry, _ = ko.kan_forward(np64(x), np64(grid), np64(bw) if base else None, np64(sw),
+                           np64(sc) if scaler else None, k)
+    assert normwise(np64(y), ry) < tol
+    # same output as the training forward up to the summation order of split products
+    yf, _ = C.kan_forward(d(x), d(grid), d(bw) if base else torch.empty(0, device="cuda"),
+                          d(sw), d(sc) if scaler else torch.empty(0, device="cuda"), k, scaler)
+    assert normwise(np64(y), np64(yf)) < tol
+
+
+def test_frozen_eval_layer_keeps_packed_weight(C):
+    from torchsplinekan_amd import KANLinear
+    torch.manual_seed(0)
+    L = KANLinear(64, 32, grid_size=6, backend="cuda").cuda()
+    with torch.no_grad():
+        L.spline_weight.normal_(0, 0.1)
+    x = torch.rand(50, 64, device="cuda") * 2 - 1
+    y_train = L(x)                                   # autograd path (parameters require grad)
+    E = L.export_inference()
+    assert not E.training and not any(p.requires_grad for p in E.parameters())
+    with torch.no_grad():
+        y1 = E(x)
+        kept = E._waug_cache[1]
+        y2 = E(x)
+        assert E._waug_cache[1] is kept              # reused, not rebuilt
+    assert normwise(np64(y1), np64(y_train.detach())) < 1e-5
+    assert torch.equal(y1, y2)
+    # an in-place update (version counter) rebuilds it
+    with torch.no_grad():
+        E.spline_weight.mul_(2.0)
+        y3 = E(x)
+    assert E._waug_cache[1] is not kept
+    a = lambda t: np64(t.detach())
+    ry, _ = ko.kan_forward(a(x), a(E.grid), a(E.base_weight), a(E.spline_weight), None, 3)
+    assert normwise(np64(y3), ry) < 1e-5
+    E.release_packed_weight()
+    assert E._waug_cache is None
+
+
+def test_training_layer_under_no_grad_keeps_nothing(C):
+    from torchsplinekan_amd import KAN
+    torch.manual_seed(1)
+    net = KAN([16, 12, 4], grid_size=5, backend="cuda").cuda()
+    x = torch.rand(33, 16, device="cuda") * 2 - 1
+    y_grad = net(x)
+    with torch.no_grad():
+        y_ng = net(x)
+    assert all(getattr(l, "_waug_cache", None) is None for l in net.layers)
+    assert normwise(np64(y_ng), np64(y_grad.detach())) < 1e-5
+    net.eval()
+    with torch.no_grad():
+        net(x)
+    assert all(getattr(l, "_waug_cache", None) is None for l in net.layers)  # not frozen
+
+
+def test_infer_rejects_short_workspace(C):
+    from torchsplinekan_amd import _lib
+    x = torch.zeros(4, 8, device="cuda")
+    grid = make_grid(8, 5, 3, "uniform").float().cuda()
+    waug = C.pack_weight(torch.zeros(6, 8, device="cuda"), torch.zeros(6, 8, 8, device="cuda"),
+                         None, 3, False)
+    y = torch.empty(4, 6, device="cuda")
+    rc = _lib.LIB.kan_hip_infer(_lib.dtype_code(torch.float32), _lib.ptr(x), _lib.ptr(grid),
+                                _lib.ptr(waug), _lib.ptr(y), None, 0, 4, 8, 6, 5, 3, 1, None)
+    assert rc != 0

@@ -102,6 +102,51 @@ def _forward_device(x, grid, base_weight, spline_weight, spline_scaler, k, has_s
     return y, aug
 
 
+def pack_weight(base_weight, spline_weight, spline_scaler, spline_order: int,
+                has_scaler: bool) -> torch.Tensor:
+    """Packed inference weight [O, ld] = [spline_weight * scaler | base_weight]
+    (device); the operand kan_infer reads."""
+    hb = _cmp.has_base(base_weight)
+    sw = spline_weight.contiguous()
+    O, I, R = sw.shape
+    G = R - spline_order
+    bw = base_weight.contiguous().to(sw.dtype) if hb else None
+    sc = spline_scaler.contiguous().to(sw.dtype) if has_scaler else None
+    ld = int(LIB.kan_hip_aug_width(I, G, spline_order, int(hb)))
+    waug = torch.empty(O, ld, dtype=sw.dtype, device=sw.device)
+    with torch.cuda.device(sw.device):
+        check(LIB.kan_hip_pack_weight(dtype_code(sw.dtype), ptr(bw), ptr(sw), ptr(sc), ptr(waug),
+                                      I, O, G, spline_order, stream_of(sw.device)))
+    return waug
+
+
+def kan_infer(x, grid, waug, spline_order: int, has_base: bool) -> torch.Tensor:
+    """Inference forward y [B, O] from a packed weight (pack_weight): no
+    autograd, no saved basis; small batches split the product over K."""
+    _req(x.is_cuda and grid.is_cuda and waug.is_cuda, "kan_infer: tensors must be on the device")
+    _req(x.dim() == 2 and waug.dim() == 2 and grid.dim() == 2, "kan_infer: x [B, I], waug [O, ld]")
+    _req(x.dtype == grid.dtype == waug.dtype and x.dtype in _F, "kan_infer: dtype mismatch")
+    B, I = x.shape
+    G = grid.shape[1] - 2 * spline_order - 1
+    O = waug.shape[0]
+    ld = int(LIB.kan_hip_aug_width(I, G, spline_order, int(has_base)))
+    _req(tuple(waug.shape) == (O, ld) and grid.shape[0] == I, "kan_infer: packed weight shape")
+    x, grid, waug = x.contiguous(), grid.contiguous(), waug.contiguous()
+    y = torch.empty(B, O, dtype=x.dtype, device=x.device)
+    if B * O == 0:
+        return y
+    code = dtype_code(x.dtype)
+    nbytes = _lib.ctypes.c_size_t(0)
+    check(LIB.kan_hip_infer_workspace(code, B, I, O, G, spline_order, int(has_base),
+                                      _lib.ctypes.byref(nbytes)))
+    ws = torch.empty(max(int(nbytes.value), 1), dtype=torch.uint8, device=x.device)
+    with torch.cuda.device(x.device):
+        check(LIB.kan_hip_infer(code, ptr(x), ptr(grid), ptr(waug), ptr(y), ptr(ws),
+                                int(nbytes.value), B, I, O, G, spline_order, int(has_base),
+                                stream_of(x.device)))
+    return y
+
+
 def _basis_view(aug: torch.Tensor, I: int, R: int) -> torch.Tensor:
     """basis [B, I, R] as a view of the augmented rows (no copy)."""
     return aug[:, :I * R].reshape(aug.shape[0], I, R)

@@ -38,6 +38,11 @@ SIGNATURES = {
                                                                 ctypes.POINTER(_sz)]),
     "kan_hip_edge_abs_mean_double_backward": (_int, [_int] + [_vp] * 15 + [_sz, _i64, _i64, _i64,
                                                                            _i64, _vp]),
+    "kan_hip_pack_weight": (_int, [_int, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp]),
+    "kan_hip_infer_workspace": (_int, [_int, _i64, _i64, _i64, _i64, _i64, _int,
+                                       ctypes.POINTER(_sz)]),
+    "kan_hip_infer": (_int, [_int, _vp, _vp, _vp, _vp, _vp, _sz, _i64, _i64, _i64, _i64, _i64,
+                             _int, _vp]),
     "kan_hip_matmul_workspace": (_int, [_int, _int, _int, _i64, _i64, _i64, ctypes.POINTER(_sz)]),
     "kan_hip_matmul": (_int, [_int, _int, _int, _i64, _i64, _i64, _vp, _i64, _vp, _i64, _vp, _i64,
                               _vp, _sz, _vp]),

@@ -157,6 +157,17 @@ struct BackwardPlan {
   size_t waug_elems, e_elems, part_elems;
 };
 
+// Inference workspace: the augmented basis [n, ld], then the split-K
+// partial slices of the product (elements).
+template <typename T>
+void infer_plan(int64_t n, int64_t I, int64_t O, int64_t R, bool has_base, int64_t* ld,
+                int64_t* kaug, int64_t* aug_elems, int64_t* part_elems) {
+  *ld = aug_width(I, R, has_base);
+  *kaug = I * R + (has_base ? I : 0);
+  *aug_elems = round_up(n * *ld, 64);
+  *part_elems = matmul_ws_elems<T>(kLayoutNT, n, O, *kaug);
+}
+
 template <typename T>
 BackwardPlan plan_backward(int64_t n, int64_t I, int64_t O, int64_t G, int64_t k, bool has_base,
                            bool need_x, bool need_params) {
@@ -495,6 +506,77 @@ int kan_hip_forward(int dtype, const void* x, const void* grid, const void* bw, 
   if (dtype == KAN_DTYPE_F32)
     return forward_impl<float>(x, grid, bw, sw, scaler, out, aug, waug, n, I, O, G, k, st);
   return forward_impl<double>(x, grid, bw, sw, scaler, out, aug, waug, n, I, O, G, k, st);
+}
+
+int kan_hip_pack_weight(int dtype, const void* bw, const void* sw, const void* scaler, void* waug,
+                        int64_t I, int64_t O, int64_t G, int64_t k, void* stream) {
+  KAN_TRY(check_dtype(dtype, "kan_pack_weight"));
+  KAN_TRY(check_layer("kan_pack_weight", 0, I, O, G, k));
+  const int64_t R = G + k;
+  const int64_t ld = aug_width(I, R, bw != nullptr);
+  if (O * ld == 0) return KAN_OK;
+  KAN_TRY(need_ptr(sw, "kan_pack_weight", "spline_weight"));
+  KAN_TRY(need_ptr(waug, "kan_pack_weight", "weight_aug"));
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (dtype == KAN_DTYPE_F32)
+    return launch_build_waug<float>(static_cast<const float*>(sw), static_cast<const float*>(scaler),
+                                    static_cast<const float*>(bw), static_cast<float*>(waug), ld, O,
+                                    I, R, st);
+  return launch_build_waug<double>(static_cast<const double*>(sw),
+                                   static_cast<const double*>(scaler),
+                                   static_cast<const double*>(bw), static_cast<double*>(waug), ld,
+                                   O, I, R, st);
+}
+
+
+int kan_hip_infer_workspace(int dtype, int64_t n, int64_t I, int64_t O, int64_t G, int64_t k,
+                            int has_base, size_t* bytes) {
+  KAN_TRY(check_dtype(dtype, "kan_infer_workspace"));
+  KAN_TRY(check_layer("kan_infer_workspace", n, I, O, G, k));
+  KAN_TRY(need_ptr(bytes, "kan_infer_workspace", "bytes"));
+  int64_t ld, kaug, a, pe;
+  if (dtype == KAN_DTYPE_F32) infer_plan<float>(n, I, O, G + k, has_base != 0, &ld, &kaug, &a, &pe);
+  else infer_plan<double>(n, I, O, G + k, has_base != 0, &ld, &kaug, &a, &pe);
+  *bytes = (dtype == KAN_DTYPE_F32 ? 4 : 8) * (size_t)(a + pe);
+  return KAN_OK;
+}
+
+int kan_hip_infer(int dtype, const void* x, const void* grid, const void* waug, void* out,
+                  void* ws, size_t ws_bytes, int64_t n, int64_t I, int64_t O, int64_t G, int64_t k,
+                  int has_base, void* stream) {
+  KAN_TRY(check_dtype(dtype, "kan_infer"));
+  KAN_TRY(check_layer("kan_infer", n, I, O, G, k));
+  if (n * O == 0) return KAN_OK;
+  KAN_TRY(need_ptr(out, "kan_infer", "output"));
+  KAN_TRY(need_ptr(waug, "kan_infer", "weight_aug"));
+  if (n * I > 0) {
+    KAN_TRY(need_ptr(x, "kan_infer", "x"));
+    KAN_TRY(need_ptr(grid, "kan_infer", "grid"));
+  }
+  const int64_t R = G + k;
+  int64_t ld, kaug, aug_elems, part_elems;
+  const size_t elem = dtype == KAN_DTYPE_F32 ? 4 : 8;
+  if (dtype == KAN_DTYPE_F32)
+    infer_plan<float>(n, I, O, R, has_base != 0, &ld, &kaug, &aug_elems, &part_elems);
+  else
+    infer_plan<double>(n, I, O, R, has_base != 0, &ld, &kaug, &aug_elems, &part_elems);
+  const size_t need = elem * (size_t)(aug_elems + part_elems);
+  if (ws_bytes < need || ws == nullptr)
+    return set_error(KAN_ERR_WORKSPACE, "kan_infer: workspace of %zu bytes is smaller than the %zu required",
+                     ws_bytes, need);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+#define KAN_INFER_CALL(T)                                                                        \
+  do {                                                                                           \
+    T* aug = static_cast<T*>(ws);                                                                \
+    KAN_TRY(launch_basis<T>(static_cast<const T*>(x), static_cast<const T*>(grid), aug, ld,      \
+                            has_base ? aug + I * R : nullptr, n, I, (int)G, (int)k,              \
+                            g_basis_impl.load(), st));                                           \
+    return launch_matmul<T>(kLayoutNT, n, O, kaug, aug, ld, static_cast<const T*>(waug), ld,     \
+                            static_cast<T*>(out), O, aug + aug_elems, st);                       \
+  } while (0)
+  if (dtype == KAN_DTYPE_F32) KAN_INFER_CALL(float);
+  KAN_INFER_CALL(double);
+#undef KAN_INFER_CALL
 }
 
 int kan_hip_pack_basis(int dtype, const void* basis, const void* x, void* aug, int64_t n,

@@ -803,14 +803,15 @@ int launch_dx_cfg(const GemmParams<float>& p, const DxParams& e, int k, hipStrea
 
 }  // namespace
 
-// Split-K factor for a TN (parameter-gradient) product: the split count in
-// {1, 2, 4, 8, 16} with the smallest estimated time (whole waves of resident
-// blocks plus partial-sum traffic), keeping at least 8 slabs per split.
+// Split-K factor: the split count in {1, 2, 4, ..., 64} with the smallest
+// estimated time (whole waves of resident blocks plus partial-sum traffic),
+// keeping at least 8 slabs per split.  Long-K products with few output tiles
+// (the parameter product, sample reductions, small-batch inference) split.
 template <typename T>
 int gemm_pick_splits(int64_t M, int64_t N, int64_t K) {
   int best = 1;
   double best_t = 0.0;
-  for (int s = 1; s <= 16; s *= 2) {
+  for (int s = 1; s <= 64; s *= 2) {
     double t;
     if (std::is_same<T, float>::value) {
       if (s > 1 && K / s < 8 * kModelF32[0].bk) break;

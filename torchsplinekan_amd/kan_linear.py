@@ -154,12 +154,50 @@ class KANLinear(nn.Module):
         has_scaler = self.enable_standalone_scale_spline
         empty = xf.new_empty(0)
         fuse_base = self._native_fuses_base
-        out = _C.kan_apply(xf, self.grid, self.base_weight if fuse_base else empty,
-                           self.spline_weight, self.spline_scaler if has_scaler else empty,
-                           self.spline_order, has_scaler)
+        if self._needs_autograd(xf):
+            out = _C.kan_apply(xf, self.grid, self.base_weight if fuse_base else empty,
+                               self.spline_weight, self.spline_scaler if has_scaler else empty,
+                               self.spline_order, has_scaler)
+        else:
+            # inference: packed weight (cached in eval mode), no saved basis
+            _C._check_inputs(xf, self.grid, self.base_weight if fuse_base else empty,
+                             self.spline_weight, self.spline_scaler if has_scaler else empty,
+                             self.spline_order, has_scaler)
+            out = _C.kan_infer(xf, self.grid, self._packed_weight(fuse_base, has_scaler),
+                               self.spline_order, fuse_base)
         if not fuse_base:
             out = out + F.linear(self._ref.base_activation(xf), self.base_weight)
         return out.reshape(lead + (self.out_features,))
+
+    def _needs_autograd(self, xf: torch.Tensor) -> bool:
+        if not torch.is_grad_enabled():
+            return False
+        return xf.requires_grad or any(p.requires_grad for p in self.parameters())
+
+    def _packed_weight(self, fuse_base: bool, has_scaler: bool) -> torch.Tensor:
+        """[spline_weight * scaler | base_weight] for kan_infer.
+
+        A frozen layer in eval mode (what export_inference returns) keeps it
+        between calls, keyed on each parameter's storage and version counter,
+        so repeated inference skips the packing.  Writes through ``.data``
+        bypass the version counter: call release_packed_weight() after them.
+        Any other layer packs per call and keeps nothing."""
+        params = [self.spline_weight] + ([self.spline_scaler] if has_scaler else []) + \
+                 ([self.base_weight] if fuse_base else [])
+        key = (fuse_base, has_scaler) + tuple((p.data_ptr(), p._version, p.dtype) for p in params)
+        cache = getattr(self, "_waug_cache", None)
+        if cache is not None and cache[0] == key:
+            return cache[1]
+        waug = _C.pack_weight(self.base_weight if fuse_base else None, self.spline_weight,
+                              self.spline_scaler if has_scaler else None, self.spline_order,
+                              has_scaler)
+        frozen = not self.training and not any(p.requires_grad for p in self.parameters())
+        self._waug_cache = (key, waug) if frozen else None
+        return waug
+
+    def release_packed_weight(self) -> None:
+        """Drops the kept inference weight (rebuilt on the next inference call)."""
+        self._waug_cache = None
 
     # ------------------------------------------------------------------ grid update
 
