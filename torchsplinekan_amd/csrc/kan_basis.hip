@@ -396,6 +396,98 @@ __global__ __launch_bounds__(kPairs) void param_grads_kernel(
   }
 }
 
+
+// basis_grad_kernel for one sample per wave step (subs == 1) with 16-byte
+// rows: the next step's gradient segment (and x, gbase) is loaded into
+// registers while the current step is computed, and the stage hand-off uses
+// wave-scope syncs only, so every wave keeps a segment load in flight.
+// PV = 16-byte vectors per lane (the segment of fbv * R values is at most
+// 64 * PV vectors).  Same arithmetic, in the same order, as basis_grad_kernel
+// with impl 1.
+template <int K, typename T, int DER, int PV>
+__global__ __launch_bounds__(kBasisThreads) void basis_grad_pf_kernel(
+    const T* __restrict__ x, const T* __restrict__ grid, const T* __restrict__ g, int64_t ld,
+    const T* __restrict__ gbase, T* __restrict__ gx, BasisShape sh) {
+  typedef typename V16<T>::type VT;
+  constexpr int kV = V16<T>::kN;
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int nk = sh.G + 2 * K + 1, R = sh.G + K;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int i0 = blockIdx.x * sh.fb;
+  const int fbv = min(sh.fb, sh.I - i0);
+  T* knots = stage_knots<T>(smem, grid, i0, fbv, nk);
+  T* stage = knots + round_up((int64_t)sh.fb * nk, 4) + wave * 64 * R;
+  // the segment is segv whole vectors plus rem (< kV) trailing elements,
+  // which a ragged last feature block can leave
+  const int seg = fbv * R;
+  const int segv = seg / kV, rem = seg - segv * kV;
+  const bool lane_ok = lane < fbv;
+  const int fi = lane_ok ? lane : 0;
+  const T* t = knots + fi * nk;
+  const int64_t step = sh.waves;
+  int64_t nn = (int64_t)blockIdx.y * sh.iters * step + wave;
+  const T* row = stage + lane * R;
+  VT pf[PV];
+  T tail = T(0), xn = T(0), gbn = T(0);
+  // loads of sample ns (clamped into the operand; rows past n are never used)
+  auto issue = [&](int64_t ns) {
+    const int64_t nc = ns < sh.n ? ns : sh.n - 1;
+    const T* base = g + nc * ld + (int64_t)i0 * R;
+    const VT* src = reinterpret_cast<const VT*>(base);
+    if (segv > 0) {
+#pragma unroll
+      for (int j = 0; j < PV; ++j) {
+        const int c = lane + 64 * j;
+        pf[j] = src[c < segv ? c : segv - 1];
+      }
+    }
+    if (rem > 0) tail = base[segv * kV + (lane < rem ? lane : 0)];
+    xn = x[nc * sh.I + i0 + fi];
+    gbn = gbase != nullptr ? gbase[nc * ld + i0 + fi] : T(0);
+  };
+  issue(nn);
+  __syncthreads();  // knot rows staged
+  for (int it = 0; it < sh.iters; ++it, nn += step) {
+    wave_sync();  // the previous step's reads of the stage are done
+#pragma unroll
+    for (int j = 0; j < PV; ++j) {
+      const int c = lane + 64 * j;
+      if (c < segv) reinterpret_cast<VT*>(stage)[c] = pf[j];
+    }
+    if (lane < rem) stage[segv * kV + lane] = tail;
+    const T xv = xn, gb = gbn;
+    wave_sync();
+    if (it + 1 < sh.iters && nn + step < sh.n) issue(nn + step);
+    if (lane_ok && nn < sh.n) {
+      T acc = T(0);
+      const int m = knot_span(t, nk, xv);
+      if (m >= 0) {
+        T d[K + 1];
+        span_window<K, DER, T>(t, nk, m, xv, d);
+#pragma unroll
+        for (int j = 0; j <= K; ++j) {
+          const int r = m - K + j;
+          if (r >= 0 && r < R) acc += row[r] * d[j];
+        }
+      }
+      if (gbase != nullptr) acc += gb * silu_grad_of<T>(xv);
+      gx[nn * sh.I + i0 + lane] = acc;
+    }
+  }
+}
+
+// Register vectors per lane the prefetching kernel needs (0 = not eligible).
+template <typename T>
+int grad_pf_vectors(const BasisShape& sh, int R) {
+  if (sh.subs != 1 || !sh.vec) return 0;
+  constexpr int kV = 16 / (int)sizeof(T);
+  const int per_lane = (int)ceil_div((int64_t)sh.fb * R / kV, 64);
+  if (per_lane <= 4) return 4;
+  if (per_lane <= 8) return 8;
+  if (per_lane <= 18) return 18;
+  return 0;
+}
+
 BasisShape make_shape(int64_t n, int64_t I, int G, int R, size_t elem, int64_t ld,
                       const void* rows_ptr, int64_t* blocks_y) {
   BasisShape sh;
@@ -466,19 +558,63 @@ int launch_basis(const T* x, const T* grid, T* out, int64_t ld_out, T* silu_out,
   return check_launch("basis");
 }
 
+// Prefetching contraction (impl 1, order DER) when the shape allows it; returns
+// false (nothing launched) otherwise.
+template <typename T, int DER>
+bool launch_grad_pf(const T* x, const T* grid, const T* gH, int64_t ld_g, const T* gbase, T* gx,
+                    int64_t n, int64_t I, int G, int k, hipStream_t st, int* rc) {
+  if (k < DER) return false;
+  const int R = G + k, nk = G + 2 * k + 1;
+  int64_t by = 0;
+  BasisShape sh = make_shape(n, I, G, R, sizeof(T), ld_g, gH, &by);
+  const int pv = grad_pf_vectors<T>(sh, R);
+  if (pv == 0) return false;
+  // two steps per block: more blocks in flight, each still overlapping one load
+  const int64_t steps = ceil_div(n, (int64_t)sh.waves);
+  sh.iters = 2;
+  by = ceil_div(steps, (int64_t)sh.iters);
+  if (by > 2147483647LL) {
+    *rc = set_error(KAN_ERR_LIMIT, "basis_grad: too many samples");
+    return true;
+  }
+  dim3 grid_dim((unsigned)ceil_div(I, sh.fb), (unsigned)by);
+  const size_t smem = basis_smem<T>(sh, nk, R);
+#define KAN_BGPF(KK, PVV)                                                                         \
+  hipLaunchKernelGGL((basis_grad_pf_kernel<KK, T, DER, PVV>), grid_dim, dim3(64 * sh.waves), smem, \
+                     st, x, grid, gH, ld_g, gbase, gx, sh)
+#define KAN_BGPF_K(KK)                \
+  if (pv == 4) KAN_BGPF(KK, 4);       \
+  else if (pv == 8) KAN_BGPF(KK, 8);  \
+  else KAN_BGPF(KK, 18)
+  if (k == 1) {
+    if constexpr (DER <= 1) KAN_BGPF_K(1);
+  } else if (k == 2) {
+    if constexpr (DER <= 2) KAN_BGPF_K(2);
+  } else {
+    KAN_BGPF_K(3);
+  }
+#undef KAN_BGPF_K
+#undef KAN_BGPF
+  *rc = check_launch("basis_grad");
+  return true;
+}
+
 template <typename T>
 int launch_basis_grad(const T* x, const T* grid, const T* gH, int64_t ld_g, const T* gbase,
                       T* gx, int64_t n, int64_t I, int G, int k, int impl, hipStream_t st) {
   if (n == 0 || I == 0) return KAN_OK;
   const int R = G + k, nk = G + 2 * k + 1;
+  // algorithmic bytes: read x and the R gradient values (+ base), write gx
+  TimedLaunch timed(kClassBasisGrad, st,
+                    (double)sizeof(T) * (double)n * (double)I * (2.0 + R + (gbase ? 1 : 0)));
+  int rc = KAN_OK;
+  if (impl == 1 && launch_grad_pf<T, 1>(x, grid, gH, ld_g, gbase, gx, n, I, G, k, st, &rc))
+    return rc;
   int64_t by = 0;
   BasisShape sh = make_shape(n, I, G, R, sizeof(T), ld_g, gH, &by);
   if (by > 2147483647LL) return set_error(KAN_ERR_LIMIT, "basis_grad: too many samples");
   dim3 grid_dim((unsigned)ceil_div(I, sh.fb), (unsigned)by);
   const size_t smem = basis_smem<T>(sh, nk, R);
-  // algorithmic bytes: read x and the R gradient values (+ base), write gx
-  TimedLaunch timed(kClassBasisGrad, st,
-                    (double)sizeof(T) * (double)n * (double)I * (2.0 + R + (gbase ? 1 : 0)));
 #define KAN_BGRAD_LAUNCH(KK, IM)                                                             \
   hipLaunchKernelGGL((basis_grad_kernel<KK, T, IM>), grid_dim, dim3(64 * sh.waves), smem, st, \
                      x, grid, gH, ld_g, gbase, gx, sh)
@@ -549,12 +685,19 @@ int launch_basis_deriv_contract(const T* x, const T* grid, const T* gH, T* gx, i
     hipLaunchKernelGGL(zero_fill_kernel<T>, dim3(gs_blocks(n * I)), dim3(256), 0, st, gx, n * I);
     return check_launch("basis_deriv_contract (zero)");
   }
+  TimedLaunch timed(kClassBasisGrad, st, (double)sizeof(T) * (double)n * (double)I * (2.0 + R));
+  int rc = KAN_OK;
+  const T* none = nullptr;
+  if ((order == 0 && launch_grad_pf<T, 0>(x, grid, gH, I * R, none, gx, n, I, G, k, st, &rc)) ||
+      (order == 1 && launch_grad_pf<T, 1>(x, grid, gH, I * R, none, gx, n, I, G, k, st, &rc)) ||
+      (order == 2 && launch_grad_pf<T, 2>(x, grid, gH, I * R, none, gx, n, I, G, k, st, &rc)) ||
+      (order == 3 && launch_grad_pf<T, 3>(x, grid, gH, I * R, none, gx, n, I, G, k, st, &rc)))
+    return rc;
   int64_t by = 0;
   BasisShape sh = make_shape(n, I, G, R, sizeof(T), I * R, gH, &by);
   if (by > 2147483647LL) return set_error(KAN_ERR_LIMIT, "basis_deriv_contract: too many samples");
   dim3 grid_dim((unsigned)ceil_div(I, sh.fb), (unsigned)by);
   const size_t smem = basis_smem<T>(sh, nk, R);
-  TimedLaunch timed(kClassBasisGrad, st, (double)sizeof(T) * (double)n * (double)I * (2.0 + R));
 #define KAN_BDC_LAUNCH(KK, DD)                                                                  \
   hipLaunchKernelGGL((basis_grad_kernel<KK, T, 1, DD>), grid_dim, dim3(64 * sh.waves), smem, st, \
                      x, grid, gH, (int64_t)I * R, (const T*)nullptr, gx, sh)
