@@ -34,9 +34,14 @@ def _edge_inputs(N, I, O, R, dtype, seed):
 # (N, I, O, R): every k-step class of the fp32 MFMA kernels (R+1 = 2, 5, 9, 12, 14, 21,
 # 30, 45, 69), outputs beyond one 512-wide block and beyond one staged 1024-row
 # chunk, ragged sample counts and a sample count that is split across blocks.
+# Output widths cover every (tiles per wave, sample-sharing waves) tiling of the
+# forward and parameter kernels (O = 3..33 -> 2x4, 64/70 -> 4x4, 200 -> 4x2,
+# 300 -> 4x1, >= 512 -> 8x1); (8192, 260, 20, 7) runs the input kernel with
+# several sample blocks per workgroup on weights staged once.
 SHAPES = [(37, 5, 3, 4), (300, 16, 40, 8), (1000, 9, 70, 13), (64, 3, 300, 68),
           (5000, 4, 6, 11), (77, 3, 5, 1), (513, 2, 33, 20), (129, 3, 17, 29), (70, 2, 9, 44),
-          (200, 2, 1300, 11), (3000, 3, 600, 7)]
+          (200, 2, 1300, 11), (3000, 3, 600, 7), (2000, 3, 200, 11), (4097, 5, 64, 11),
+          (8192, 260, 20, 7)]
 
 
 @pytest.mark.parametrize("shape", SHAPES)

@@ -28,8 +28,17 @@ namespace {
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kEdgeMfThreads = 256;  // 4 waves
-constexpr int kOT = 8;               // 16-wide output tiles per wave (128 outputs)
-constexpr int kBlockOut = 4 * kOT * 16;
+// Output layout of the forward and parameter kernels: each wave owns OT
+// 16-wide output tiles; WS waves split a block's samples between them (their
+// partial sums meet in LDS, in wave order), and WO = 4 / WS waves cover
+// different outputs, so a block covers WO * OT * 16 outputs.  Narrow layers
+// (small O) use WS > 1 instead of leaving waves idle.
+template <int OT, int WS>
+struct EdgeTiling {
+  static constexpr int kWO = 4 / WS;
+  static constexpr int kBlockOut = kWO * OT * 16;
+  static_assert(kWO * WS == 4, "4 waves per block");
+};
 
 __device__ __forceinline__ f32x4 mfma16(float a, float b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
@@ -77,19 +86,23 @@ struct EdgeGeom {
 // KS = ceil((R+1)/4) k-steps.  The A fragments of the next P sample tiles are
 // in flight while the current tile runs (P = 4 for KS <= 4, fewer for wider
 // K to bound registers).
-template <int KS>
+template <int KS, int OT, int WS>
 __global__ __launch_bounds__(kEdgeMfThreads) void edge_fwd_mfma_kernel(
     const float* __restrict__ s, const float* __restrict__ H, const float* __restrict__ bw,
     const float* __restrict__ W, float* __restrict__ out, EdgeGeom g, int final_out) {
+  typedef EdgeTiling<OT, WS> Tl;
+  constexpr int kOT = OT;
   constexpr int P = KS <= 4 ? 4 : (KS <= 8 ? 2 : 1);
+  __shared__ float red[WS > 1 ? WS * Tl::kBlockOut : 1];
   const int64_t bid = blockIdx.x;
   const int i = (int)(bid % g.I);
   const int oc = (int)((bid / g.I) % g.ochunks);
   const int split = (int)(bid / ((int64_t)g.I * g.ochunks));
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int wo = wave % Tl::kWO, wsi = wave / Tl::kWO;
   const int q = lane >> 4, r = lane & 15;
-  const int obase = oc * kBlockOut + wave * kOT * 16;
-  if (obase >= g.O) return;
+  const int obase = oc * Tl::kBlockOut + wo * kOT * 16;
+  if (WS == 1 && obase >= g.O) return;  // (with WS > 1 every wave reaches the barrier)
   const int R1 = g.R + 1;
 
   float w[kOT][KS];
@@ -106,8 +119,13 @@ __global__ __launch_bounds__(kEdgeMfThreads) void edge_fwd_mfma_kernel(
 #pragma unroll
   for (int t = 0; t < kOT; ++t) tot[t] = 0.0f;
 
-  const int64_t nb = (int64_t)split * g.per_split;
-  const int64_t ne = min(g.n, nb + g.per_split);
+  int64_t nb = (int64_t)split * g.per_split;
+  int64_t ne = min(g.n, nb + g.per_split);
+  if (WS > 1) {  // this wave's share of the split's samples
+    const int64_t per_wave = round_up(ceil_div(g.per_split, (int64_t)WS), 16);
+    nb += wsi * per_wave;
+    ne = min(ne, nb + per_wave);
+  }
   float an[P][KS];
   auto load_a = [&](int64_t n0, float (&dst)[KS]) {
     const int64_t nn = n0 + r;
@@ -138,15 +156,33 @@ __global__ __launch_bounds__(kEdgeMfThreads) void edge_fwd_mfma_kernel(
     }
   }
   // combine the four row groups of each column in a fixed order
+  float colsum[kOT];
 #pragma unroll
   for (int t = 0; t < kOT; ++t) {
     const float s1 = tot[t] + __shfl_xor(tot[t], 16);
-    const float s2 = s1 + __shfl_xor(s1, 32);
+    colsum[t] = s1 + __shfl_xor(s1, 32);
+  }
+  if (WS > 1) {  // then the sample shares of the WS waves, in wave order
+#pragma unroll
+    for (int t = 0; t < kOT; ++t)
+      if (q == 0) red[wsi * Tl::kBlockOut + wo * kOT * 16 + t * 16 + r] = colsum[t];
+    __syncthreads();
+    if (wsi != 0 || obase >= g.O) return;
+#pragma unroll
+    for (int t = 0; t < kOT; ++t) {
+      const int c = wo * kOT * 16 + t * 16 + r;
+      float v = red[c];
+      for (int w = 1; w < WS; ++w) v += red[w * Tl::kBlockOut + c];
+      colsum[t] = v;
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < kOT; ++t) {
     const int o = obase + t * 16 + r;
     if (q == 0 && o < g.O) {
       const int64_t e = (int64_t)o * g.I + i;
-      if (final_out) out[e] = s2 / (float)g.n;
-      else out[(int64_t)split * g.O * g.I + e] = s2;
+      if (final_out) out[e] = colsum[t] / (float)g.n;
+      else out[(int64_t)split * g.O * g.I + e] = colsum[t];
     }
   }
 }
@@ -154,19 +190,24 @@ __global__ __launch_bounds__(kEdgeMfThreads) void edge_fwd_mfma_kernel(
 // Parameter gradients: block (i, output chunk, split).  Per 16-sample tile:
 // phi (rows n, columns o) -> g in registers -> dWc[o, c] += sum_n g Hc with
 // the accumulator entries as the A operand.  CT column tiles of 16 cover c.
-template <int KS, int CT>
+template <int KS, int CT, int OT, int WS>
 __global__ __launch_bounds__(kEdgeMfThreads) void edge_param_mfma_kernel(
     const float* __restrict__ ga, const float* __restrict__ s, const float* __restrict__ H,
     const float* __restrict__ bw, const float* __restrict__ W, float* __restrict__ dbw,
     float* __restrict__ dW, float* __restrict__ part, EdgeGeom g, int final_out) {
+  typedef EdgeTiling<OT, WS> Tl;
+  constexpr int kOT = OT;
+  // partial dWc of the WS sample shares: [WS][block outputs][CT * 16]
+  __shared__ float red[WS > 1 ? WS * Tl::kBlockOut * CT * 16 : 1];
   const int64_t bid = blockIdx.x;
   const int i = (int)(bid % g.I);
   const int oc = (int)((bid / g.I) % g.ochunks);
   const int split = (int)(bid / ((int64_t)g.I * g.ochunks));
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int wo = wave % Tl::kWO, wsi = wave / Tl::kWO;
   const int q = lane >> 4, r = lane & 15;
-  const int obase = oc * kBlockOut + wave * kOT * 16;
-  if (obase >= g.O) return;
+  const int obase = oc * Tl::kBlockOut + wo * kOT * 16;
+  if (WS == 1 && obase >= g.O) return;
   const int R1 = g.R + 1;
   const float inv_n = 1.0f / (float)g.n;
 
@@ -187,8 +228,13 @@ __global__ __launch_bounds__(kEdgeMfThreads) void edge_param_mfma_kernel(
 #pragma unroll
     for (int ct = 0; ct < CT; ++ct) dacc[t][ct] = zero4();
 
-  const int64_t nb = (int64_t)split * g.per_split;
-  const int64_t ne = min(g.n, nb + g.per_split);
+  int64_t nb = (int64_t)split * g.per_split;
+  int64_t ne = min(g.n, nb + g.per_split);
+  if (WS > 1) {
+    const int64_t per_wave = round_up(ceil_div(g.per_split, (int64_t)WS), 16);
+    nb += wsi * per_wave;
+    ne = min(ne, nb + per_wave);
+  }
   // operands of the next sample tile are loaded while the current one runs:
   // A of phi (Hc[n0 + r, 4k + q]) and B of the second product
   // (Hc[n0 + 4q + v, 16ct + r])
@@ -234,6 +280,30 @@ __global__ __launch_bounds__(kEdgeMfThreads) void edge_param_mfma_kernel(
         for (int v = 0; v < 4; ++v) dacc[t][ct] = mfma16(gv[v], hb[ct][v], dacc[t][ct]);
     }
   }
+  if (WS > 1) {  // add the WS sample shares in wave order
+    constexpr int kCols = CT * 16;
+#pragma unroll
+    for (int t = 0; t < kOT; ++t)
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+        for (int v = 0; v < 4; ++v)
+          red[(wsi * Tl::kBlockOut + wo * kOT * 16 + t * 16 + 4 * q + v) * kCols + ct * 16 + r] =
+              dacc[t][ct][v];
+    __syncthreads();
+    if (wsi != 0 || obase >= g.O) return;
+#pragma unroll
+    for (int t = 0; t < kOT; ++t)
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const int row = wo * kOT * 16 + t * 16 + 4 * q + v;
+          float acc = red[row * kCols + ct * 16 + r];
+          for (int w = 1; w < WS; ++w) acc += red[(w * Tl::kBlockOut + row) * kCols + ct * 16 + r];
+          dacc[t][ct][v] = acc;
+        }
+  }
   // dacc[t][ct]: lane (q, r) holds column c = 16ct + r, rows o = obase + 16t + 4q + v
 #pragma unroll
   for (int t = 0; t < kOT; ++t) {
@@ -273,37 +343,20 @@ template <int KS, int CT, int NTW>
 __global__ __launch_bounds__(kEdgeMfThreads) void edge_input_mfma_kernel(
     const float* __restrict__ ga, const float* __restrict__ s, const float* __restrict__ H,
     const float* __restrict__ bw, const float* __restrict__ W, float* __restrict__ ds,
-    float* __restrict__ dH, EdgeGeom g, int oc_rows) {
+    float* __restrict__ dH, EdgeGeom g, int oc_rows, int nsb) {
   __shared__ float wl[kInChunkFloats];
   __shared__ float gl[kInMaxRows];
+  const int64_t nblk = ceil_div(g.n, (int64_t)(64 * NTW));
   const int i = (int)(blockIdx.x % g.I);
-  const int64_t nbk = blockIdx.x / g.I;
+  const int64_t sb0 = (blockIdx.x / g.I) * (int64_t)nsb;  // first sample block of this group
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int q = lane >> 4, r = lane & 15;
   const int R1 = g.R + 1;
   const int stride = R1 | 1;  // odd row stride of the staged weights
   const float inv_n = 1.0f / (float)g.n;
+  const bool one_chunk = g.O <= oc_rows;  // weights staged once for all sample blocks
 
-  // this wave's sample tiles: n0 = nbase + (j*4 + wave)*16
-  const int64_t nbase = nbk * (int64_t)(64 * NTW);
-  float a[NTW][KS];
-#pragma unroll
-  for (int j = 0; j < NTW; ++j) {
-    const int64_t nn = nbase + (int64_t)(j * 4 + wave) * 16 + r;
-#pragma unroll
-    for (int k = 0; k < KS; ++k) {
-      const int c = 4 * k + q;
-      a[j][k] = (nn < g.n && c < R1) ? hc_val(s, H, nn, g.I, i, g.R, c) : 0.0f;
-    }
-  }
-  f32x4 dacc[NTW][CT];
-#pragma unroll
-  for (int j = 0; j < NTW; ++j)
-#pragma unroll
-    for (int ct = 0; ct < CT; ++ct) dacc[j][ct] = zero4();
-
-  for (int o0 = 0; o0 < g.O; o0 += oc_rows) {
-    const int orows = min(oc_rows, g.O - o0);
+  auto stage = [&](int o0, int orows) {
     __syncthreads();
     for (int e = threadIdx.x; e < oc_rows * R1; e += kEdgeMfThreads) {
       const int oo = e / R1, c = e - oo * R1;
@@ -312,58 +365,85 @@ __global__ __launch_bounds__(kEdgeMfThreads) void edge_input_mfma_kernel(
     for (int e = threadIdx.x; e < oc_rows; e += kEdgeMfThreads)
       gl[e] = e < orows ? ga[(int64_t)(o0 + e) * g.I + i] * inv_n : 0.0f;
     __syncthreads();
-    for (int ot = 0; ot < orows; ot += 16) {
-      // A operand of phi^T: Wc[o = ot + r, c = 4k + q]
-      float wa[KS];
+  };
+  if (one_chunk) stage(0, g.O);
+
+  for (int64_t sb = sb0; sb < min(sb0 + nsb, nblk); ++sb) {
+    // this wave's sample tiles: n0 = nbase + (j*4 + wave)*16
+    const int64_t nbase = sb * (int64_t)(64 * NTW);
+    float a[NTW][KS];
+#pragma unroll
+    for (int j = 0; j < NTW; ++j) {
+      const int64_t nn = nbase + (int64_t)(j * 4 + wave) * 16 + r;
 #pragma unroll
       for (int k = 0; k < KS; ++k) {
         const int c = 4 * k + q;
-        wa[k] = c < R1 ? wl[(ot + r) * stride + c] : 0.0f;
-      }
-      // g scale of the accumulator rows o = ot + 4q + v
-      float gs[4];
-#pragma unroll
-      for (int v = 0; v < 4; ++v) gs[v] = gl[ot + 4 * q + v];
-      // A operand of the second product: Wc[o = ot + 4q + v, c = 16ct + r]
-      float wb[CT][4];
-#pragma unroll
-      for (int ct = 0; ct < CT; ++ct) {
-        const int c = ct * 16 + r;
-#pragma unroll
-        for (int v = 0; v < 4; ++v) wb[ct][v] = c < R1 ? wl[(ot + 4 * q + v) * stride + c] : 0.0f;
-      }
-#pragma unroll
-      for (int j = 0; j < NTW; ++j) {
-        f32x4 acc = zero4();
-#pragma unroll
-        for (int k = 0; k < KS; ++k) acc = mfma16(wa[k], a[j][k], acc);
-        float gv[4];
-#pragma unroll
-        for (int v = 0; v < 4; ++v) gv[v] = g_sign(gs[v], acc[v]);
-#pragma unroll
-        for (int ct = 0; ct < CT; ++ct)
-#pragma unroll
-          for (int v = 0; v < 4; ++v) dacc[j][ct] = mfma16(wb[ct][v], gv[v], dacc[j][ct]);
+        a[j][k] = (nn < g.n && c < R1) ? hc_val(s, H, nn, g.I, i, g.R, c) : 0.0f;
       }
     }
-  }
-  // dacc[j][ct]: lane (q, r) holds column n = tile + r, rows c = 16ct + 4q + v
+    f32x4 dacc[NTW][CT];
 #pragma unroll
-  for (int j = 0; j < NTW; ++j) {
-    const int64_t nn = nbase + (int64_t)(j * 4 + wave) * 16 + r;
-    if (nn >= g.n) continue;
-    const int64_t f = nn * g.I + i;
+    for (int j = 0; j < NTW; ++j)
 #pragma unroll
-    for (int ct = 0; ct < CT; ++ct) {
+      for (int ct = 0; ct < CT; ++ct) dacc[j][ct] = zero4();
+
+    for (int o0 = 0; o0 < g.O; o0 += oc_rows) {
+      const int orows = min(oc_rows, g.O - o0);
+      if (!one_chunk) stage(o0, orows);
+      for (int ot = 0; ot < orows; ot += 16) {
+        // A operand of phi^T: Wc[o = ot + r, c = 4k + q]
+        float wa[KS];
 #pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const int c = ct * 16 + 4 * q + v;
-        if (c >= R1) continue;
-        const float val = dacc[j][ct][v];
-        if (c == 0) {
-          if (ds != nullptr) ds[f] = val;
-        } else if (dH != nullptr) {
-          dH[f * g.R + (c - 1)] = val;
+        for (int k = 0; k < KS; ++k) {
+          const int c = 4 * k + q;
+          wa[k] = c < R1 ? wl[(ot + r) * stride + c] : 0.0f;
+        }
+        // g scale of the accumulator rows o = ot + 4q + v
+        float gs[4];
+#pragma unroll
+        for (int v = 0; v < 4; ++v) gs[v] = gl[ot + 4 * q + v];
+        // A operand of the second product: Wc[o = ot + 4q + v, c = 16ct + r]
+        float wb[CT][4];
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct) {
+          const int c = ct * 16 + r;
+#pragma unroll
+          for (int v = 0; v < 4; ++v)
+            wb[ct][v] = c < R1 ? wl[(ot + 4 * q + v) * stride + c] : 0.0f;
+        }
+#pragma unroll
+        for (int j = 0; j < NTW; ++j) {
+          f32x4 acc = zero4();
+#pragma unroll
+          for (int k = 0; k < KS; ++k) acc = mfma16(wa[k], a[j][k], acc);
+          float gv[4];
+#pragma unroll
+          for (int v = 0; v < 4; ++v) gv[v] = g_sign(gs[v], acc[v]);
+#pragma unroll
+          for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) dacc[j][ct] = mfma16(wb[ct][v], gv[v], dacc[j][ct]);
+        }
+      }
+    }
+    // dacc[j][ct]: lane (q, r) holds column n = tile + r, rows c = 16ct + 4q + v
+#pragma unroll
+    for (int j = 0; j < NTW; ++j) {
+      const int64_t nn = nbase + (int64_t)(j * 4 + wave) * 16 + r;
+      if (nn >= g.n) continue;
+      const int64_t f = nn * g.I + i;
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct) {
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const int c = ct * 16 + 4 * q + v;
+          if (c >= R1) continue;
+          const float val = dacc[j][ct][v];
+          if (c == 0) {
+            if (ds != nullptr) ds[f] = val;
+          } else if (dH != nullptr) {
+            dH[f * g.R + (c - 1)] = val;
+          }
         }
       }
     }
@@ -421,9 +501,22 @@ inline int fin_blocks_f32(int64_t total) {
 
 }  // namespace
 
+// (OT, WS) of the forward and parameter kernels for a layer width O; see
+// EdgeTiling.  Returns the block's output coverage.
+int edge_tiling(int64_t O, int* ot, int* ws) {
+  const int64_t tiles = ceil_div(O, 16);
+  if (tiles >= 32) { *ot = 8; *ws = 1; }
+  else if (tiles >= 16) { *ot = 4; *ws = 1; }
+  else if (tiles >= 8) { *ot = 4; *ws = 2; }
+  else if (tiles >= 4) { *ot = 4; *ws = 4; }
+  else { *ot = 2; *ws = 4; }
+  return (4 / *ws) * *ot * 16;
+}
+
 int edge_mfma_splits(int64_t n, int64_t I, int64_t O, int64_t R) {
   (void)R;
-  const int64_t ochunks = ceil_div(O, kBlockOut);
+  int ot, ws;
+  const int64_t ochunks = ceil_div(O, (int64_t)edge_tiling(O, &ot, &ws));
   const int64_t blocks = I * ochunks;
   const int64_t target = 8LL * device_cu_count();
   int64_t s = ceil_div(target, blocks > 0 ? blocks : 1);
@@ -448,15 +541,23 @@ int launch_edge_forward_mfma(const float* s, const float* H, const float* bw, co
   g.R = (int)R;
   g.splits = splits;
   g.per_split = round_up(ceil_div(n, splits), 16);
-  g.ochunks = (int)ceil_div(O, kBlockOut);
+  int ot, ws;
+  g.ochunks = (int)ceil_div(O, (int64_t)edge_tiling(O, &ot, &ws));
   const int64_t blocks = I * g.ochunks * (int64_t)splits;
   if (blocks > 2147483647LL) return set_error(KAN_ERR_LIMIT, "edge_abs_mean: too many blocks");
   const bool fin = splits == 1;
   TimedLaunch timed(kClassEdge, st, 2.0 * (double)n * (double)O * (double)I * (double)R1);
-  KAN_EDGE_MF_DISPATCH(R1, (void)CT; hipLaunchKernelGGL((edge_fwd_mfma_kernel<KS>),
-                                                          dim3((unsigned)blocks),
-                                                          dim3(kEdgeMfThreads), 0, st, s, H, bw,
-                                                          W, fin ? a : part, g, fin ? 1 : 0));
+#define KAN_EDGE_FWD(OTV, WSV)                                                                  \
+  KAN_EDGE_MF_DISPATCH(R1, (void)CT; hipLaunchKernelGGL((edge_fwd_mfma_kernel<KS, OTV, WSV>),   \
+                                                          dim3((unsigned)blocks),                \
+                                                          dim3(kEdgeMfThreads), 0, st, s, H, bw, \
+                                                          W, fin ? a : part, g, fin ? 1 : 0))
+  if (ot == 8) KAN_EDGE_FWD(8, 1);
+  else if (ws == 1) KAN_EDGE_FWD(4, 1);
+  else if (ws == 2) KAN_EDGE_FWD(4, 2);
+  else if (ot == 4) KAN_EDGE_FWD(4, 4);
+  else KAN_EDGE_FWD(2, 4);
+#undef KAN_EDGE_FWD
   int rc = check_launch("edge_abs_mean");
   if (rc != KAN_OK || fin) return rc;
   hipLaunchKernelGGL(edge_fwd_finalize_f32, dim3(fin_blocks_f32(O * I)), dim3(256), 0, st, part,
@@ -476,7 +577,8 @@ int launch_edge_backward_mfma(const float* ga, const float* s, const float* H, c
   g.R = (int)R;
   g.splits = splits;
   g.per_split = round_up(ceil_div(n, splits), 16);
-  g.ochunks = (int)ceil_div(O, kBlockOut);
+  int ot, ws;
+  g.ochunks = (int)ceil_div(O, (int64_t)edge_tiling(O, &ot, &ws));
   if ((dbw != nullptr || dW != nullptr) && O > 0 && I > 0) {
     if (splits > 1 && part == nullptr)
       return set_error(KAN_ERR_WORKSPACE, "edge_abs_mean_backward: missing workspace");
@@ -485,10 +587,17 @@ int launch_edge_backward_mfma(const float* ga, const float* s, const float* H, c
       return set_error(KAN_ERR_LIMIT, "edge_abs_mean_backward: too many blocks");
     const bool fin = splits == 1;
     TimedLaunch timed(kClassEdgeGrad, st, 4.0 * (double)n * (double)O * (double)I * (double)R1);
-    KAN_EDGE_MF_DISPATCH(R1, hipLaunchKernelGGL((edge_param_mfma_kernel<KS, CT>),
-                                                dim3((unsigned)blocks), dim3(kEdgeMfThreads), 0,
-                                                st, ga, s, H, bw, W, dbw, dW, part, g,
-                                                fin ? 1 : 0));
+#define KAN_EDGE_PAR(OTV, WSV)                                                              \
+  KAN_EDGE_MF_DISPATCH(R1, hipLaunchKernelGGL((edge_param_mfma_kernel<KS, CT, OTV, WSV>),   \
+                                              dim3((unsigned)blocks), dim3(kEdgeMfThreads), \
+                                              0, st, ga, s, H, bw, W, dbw, dW, part, g,     \
+                                              fin ? 1 : 0))
+    if (ot == 8) KAN_EDGE_PAR(8, 1);
+    else if (ws == 1) KAN_EDGE_PAR(4, 1);
+    else if (ws == 2) KAN_EDGE_PAR(4, 2);
+    else if (ot == 4) KAN_EDGE_PAR(4, 4);
+    else KAN_EDGE_PAR(2, 4);
+#undef KAN_EDGE_PAR
     int rc = check_launch("edge_abs_mean_backward(params)");
     if (rc != KAN_OK) return rc;
     if (!fin) {
@@ -501,17 +610,25 @@ int launch_edge_backward_mfma(const float* ga, const float* s, const float* H, c
   if ((ds != nullptr || dH != nullptr) && n > 0 && I > 0 && O > 0) {
     constexpr int NTW = 4;
     const int64_t nblk = ceil_div(n, 64 * NTW);
-    const int64_t blocks = I * nblk;
-    if (blocks > 2147483647LL)
-      return set_error(KAN_ERR_LIMIT, "edge_abs_mean_backward: too many blocks");
     // staged output rows per chunk: a multiple of 16 that fits the LDS stage
     int oc_rows = (int)(kInChunkFloats / (R1 | 1)) / 16 * 16;
     if (oc_rows > kInMaxRows) oc_rows = kInMaxRows;
     if ((int64_t)oc_rows > round_up(O, 16)) oc_rows = (int)round_up(O, 16);
+    // when the weights fit one stage, a workgroup runs several sample blocks
+    // on them (short layers would otherwise spend their time staging), while
+    // keeping about 8 workgroups per CU
+    int nsb = 1;
+    if (O <= oc_rows) {
+      const int64_t target = 8LL * device_cu_count();
+      while (nsb < 8 && I * ceil_div(nblk, (int64_t)(2 * nsb)) >= target) nsb *= 2;
+    }
+    const int64_t blocks = I * ceil_div(nblk, (int64_t)nsb);
+    if (blocks > 2147483647LL)
+      return set_error(KAN_ERR_LIMIT, "edge_abs_mean_backward: too many blocks");
     TimedLaunch timed(kClassEdgeGrad, st, 4.0 * (double)n * (double)O * (double)I * (double)R1);
     KAN_EDGE_MF_DISPATCH(R1, hipLaunchKernelGGL((edge_input_mfma_kernel<KS, CT, NTW>),
                                                 dim3((unsigned)blocks), dim3(kEdgeMfThreads), 0,
-                                                st, ga, s, H, bw, W, ds, dH, g, oc_rows));
+                                                st, ga, s, H, bw, W, ds, dH, g, oc_rows, nsb));
     int rc = check_launch("edge_abs_mean_backward(inputs)");
     if (rc != KAN_OK) return rc;
   }
