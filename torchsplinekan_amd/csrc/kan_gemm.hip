@@ -625,18 +625,21 @@ __global__ __launch_bounds__(C::kThreads, C::MINB) void gemm_pipe_kernel(GemmPar
     const int cur = kt & 1;
 #pragma unroll
     for (int g = 0; g < NG; ++g) {
+      // The next group's fragment reads come first in program order: the
+      // compiler cannot tell the two slab buffers apart (runtime index), so
+      // reads placed after the stores of group 0 would wait for all of them.
+      if (g + 1 < NG) {
+        fread(lds_a[cur], lds_b[cur], g + 1, (g + 1) & 1);
+      } else if (NEXT) {
+        __syncthreads();
+        fread(lds_a[cur ^ 1], lds_b[cur ^ 1], 0, 0);
+      }
       if (g == 0) {
         if (STORE) {
           la.store(lds_a[cur ^ 1]);
           lb.store(lds_b[cur ^ 1]);
         }
         if (LOAD) gload(kt + 2, full_c);
-      }
-      if (g + 1 < NG) {
-        fread(lds_a[cur], lds_b[cur], g + 1, (g + 1) & 1);
-      } else if (NEXT) {
-        __syncthreads();
-        fread(lds_a[cur ^ 1], lds_b[cur ^ 1], 0, 0);
       }
       mfmas(g & 1);
       if (g == 0 && STORE && LOAD) SchedSeq<0, kMF, kDSR, kDSW, kGLD>::run();
