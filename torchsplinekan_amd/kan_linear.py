@@ -90,6 +90,7 @@ class KANLinear(nn.Module):
         self._native_ok = native_ok
         self.backend = backend
         self.last_backend: Optional[str] = None
+        self._waug_cache = None  # (key, packed inference weight) of a frozen eval-mode layer
 
         self._ref = ReferenceKANLayer(
             in_features=in_features, out_features=out_features, grid_size=grid_size,
