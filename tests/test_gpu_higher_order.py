@@ -211,6 +211,26 @@ def test_native_matmul_matches_torch(C, dtype, tol, M, K, N):
             assert torch.equal(c, C.matmul(_view(a.cuda(), ta), _view(b.cuda(), tb)))
 
 
+@pytest.mark.parametrize("tile", ["256x64", "128", "256"])
+@pytest.mark.parametrize("M,K,N", [(600, 5632, 64), (513, 407, 61), (16384, 64, 64),
+                                   (333, 16384, 19), (64, 100, 3)])
+def test_matmul_tile_configs_match_torch(C, monkeypatch, tile, M, K, N):
+    """The fp32 tile configurations forced through KAN_HIP_GEMM_TILE on
+    narrow products (N <= 64, the narrow 256x64 tile's range): ragged rows,
+    K tails past the 32-deep slab, unaligned leading dimensions and split-K,
+    all four transposition pairs, against the float64 product."""
+    print(f"matmul tile={tile} M={M} K={K} N={N}", flush=True)
+    monkeypatch.setenv("KAN_HIP_GEMM_TILE", tile)
+    g = torch.Generator().manual_seed(M + 3 * K + N)
+    a = torch.randn(M, K, generator=g, dtype=torch.float64).float()
+    b = torch.randn(K, N, generator=g, dtype=torch.float64).float()
+    ref = np64(a) @ np64(b)
+    for ta in (False, True):
+        for tb in (False, True):
+            c = C.matmul(_view(a.cuda(), ta), _view(b.cuda(), tb))
+            assert normwise(np64(c), ref) < 1e-5, (ta, tb)
+
+
 def test_native_matmul_gradients_and_workspace_check(C):
     from torchsplinekan_amd import _lib
     a = torch.randn(9, 6, device="cuda", dtype=torch.float64, requires_grad=True)

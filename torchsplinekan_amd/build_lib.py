@@ -29,6 +29,13 @@ COMMON_FLAGS = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
 ]
 
+# Per-source additions.  The edge-statistic kernels read every MFMA result
+# with VALU instructions (abs-sums, sign tests); MFMAs that write VGPRs
+# instead of accumulation registers save a copy per value and registers.
+SOURCE_FLAGS = {
+    "kan_edge_mfma.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+}
+
 
 def _hipcc() -> str:
     for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
@@ -56,7 +63,8 @@ def build_library(verbose: bool = False) -> str:
     for src in SOURCES:
         obj = os.path.join(BUILD_DIR, os.path.splitext(src)[0] + ".o")
         objs.append(obj)
-        cmds.append([hipcc, *COMMON_FLAGS, "-c", os.path.join(CSRC, src), "-o", obj])
+        cmds.append([hipcc, *COMMON_FLAGS, *SOURCE_FLAGS.get(src, []), "-c",
+                     os.path.join(CSRC, src), "-o", obj])
     workers = max(1, min(len(cmds), int(os.environ.get("MAX_JOBS", "8"))))
     with ThreadPoolExecutor(max_workers=workers) as ex:
         for out in ex.map(_run, cmds):

@@ -582,10 +582,12 @@ bool launch_grad_pf(const T* x, const T* grid, const T* gH, int64_t ld_g, const 
 #define KAN_BGPF(KK, PVV)                                                                         \
   hipLaunchKernelGGL((basis_grad_pf_kernel<KK, T, DER, PVV>), grid_dim, dim3(64 * sh.waves), smem, \
                      st, x, grid, gH, ld_g, gbase, gx, sh)
-#define KAN_BGPF_K(KK)                \
-  if (pv == 4) KAN_BGPF(KK, 4);       \
-  else if (pv == 8) KAN_BGPF(KK, 8);  \
-  else KAN_BGPF(KK, 18)
+#define KAN_BGPF_K(KK)                    \
+  do {                                    \
+    if (pv == 4) KAN_BGPF(KK, 4);         \
+    else if (pv == 8) KAN_BGPF(KK, 8);    \
+    else KAN_BGPF(KK, 18);                \
+  } while (0)
   if (k == 1) {
     if constexpr (DER <= 1) KAN_BGPF_K(1);
   } else if (k == 2) {

@@ -7,6 +7,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstdlib>
+#include <map>
 #include <mutex>
 #include <type_traits>
 #include <vector>
@@ -20,6 +21,7 @@ thread_local std::string g_last_error;
 std::atomic<int> g_basis_impl{1};
 std::mutex g_cu_mutex;
 int g_cu_count[64] = {0};
+std::map<std::pair<int, const void*>, int> g_resident;  // (device, kernel) -> blocks per CU
 
 // KAN_HIP_FUSED_DX=1 contracts dx inside the input-side GEMM (no E buffer:
 // the workspace shrinks by n * (ld - 3 I) floats, at about 10% more time for
@@ -64,6 +66,26 @@ int device_cu_count() {
     g_cu_count[dev] = cus;
   }
   return g_cu_count[dev];
+}
+
+int resident_blocks_per_cu(const void* kernel, int threads) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) {
+    (void)hipGetLastError();
+    return 1;
+  }
+  std::lock_guard<std::mutex> lock(g_cu_mutex);
+  const auto key = std::make_pair(dev, kernel);
+  auto it = g_resident.find(key);
+  if (it != g_resident.end()) return it->second;
+  int blocks = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, kernel, threads, 0) != hipSuccess ||
+      blocks < 1) {
+    (void)hipGetLastError();
+    blocks = 1;
+  }
+  g_resident[key] = blocks;
+  return blocks;
 }
 
 // ---- HIP-event timing -------------------------------------------------------
@@ -272,7 +294,7 @@ int check_edge(const char* who, int dtype, const void* s, const void* H, const v
 }
 
 size_t edge_ws_bytes(int dtype, int64_t n, int64_t I, int64_t O, int64_t R, bool backward) {
-  const int splits = edge_pick_splits(dtype, n, I, O, R);
+  const int splits = edge_pick_splits(dtype, n, I, O, R, backward);
   if (splits <= 1) return 0;
   const size_t elem = dtype == KAN_DTYPE_F64 ? 8 : 4;
   return elem * (size_t)splits * (size_t)(O * I) * (size_t)(backward ? R + 1 : 1);
@@ -658,7 +680,7 @@ int kan_hip_edge_abs_mean(int dtype, const void* s, const void* H, const void* b
   const size_t need = edge_ws_bytes(dtype, n, I, O, R, false);
   if (ws_bytes < need || (need > 0 && ws == nullptr))
     return set_error(KAN_ERR_WORKSPACE, "edge_abs_mean: workspace of %zu bytes is smaller than the %zu required", ws_bytes, need);
-  const int splits = need > 0 ? edge_pick_splits(dtype, n, I, O, R) : 1;
+  const int splits = need > 0 ? edge_pick_splits(dtype, n, I, O, R, false) : 1;
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (dtype == KAN_DTYPE_F32)
     return launch_edge_forward<float>(static_cast<const float*>(s), static_cast<const float*>(H),
@@ -683,7 +705,7 @@ int kan_hip_edge_abs_mean_backward(int dtype, const void* ga, const void* s, con
   const size_t need = want_params ? edge_ws_bytes(dtype, n, I, O, R, true) : 0;
   if (ws_bytes < need || (need > 0 && ws == nullptr))
     return set_error(KAN_ERR_WORKSPACE, "edge_abs_mean_backward: workspace of %zu bytes is smaller than the %zu required", ws_bytes, need);
-  const int splits = need > 0 ? edge_pick_splits(dtype, n, I, O, R) : 1;
+  const int splits = need > 0 ? edge_pick_splits(dtype, n, I, O, R, true) : 1;
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (dtype == KAN_DTYPE_F32)
     return launch_edge_backward<float>(

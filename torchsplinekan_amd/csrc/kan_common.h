@@ -29,6 +29,9 @@ int set_error(int code, const char* fmt, ...);
 int check_launch(const char* what);
 // Number of compute units of the current device (cached per device).
 int device_cu_count();
+// Workgroups of `threads` threads of `kernel` that fit on one CU at once (its
+// register and LDS occupancy), cached per device and kernel; 1 if unknown.
+int resident_blocks_per_cu(const void* kernel, int threads);
 
 __host__ __device__ inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 __host__ __device__ inline int64_t round_up(int64_t a, int64_t b) { return ceil_div(a, b) * b; }
@@ -191,12 +194,13 @@ int launch_edge_double_backward(const T* ga, const T* s, const T* H, const T* bw
                                 T* g_ga, T* g_s, T* g_H, T* g_bw, T* g_W, T* part, int64_t n,
                                 int64_t I, int64_t O, int64_t R, hipStream_t st);
 
-// Sample splits of the edge statistic (dtype code selects the fp32 MFMA or
-// the fp64 VALU kernels, which partition differently).
-int edge_pick_splits(int dtype, int64_t n, int64_t I, int64_t O, int64_t R);
+// Sample splits of the edge statistic's forward or parameter-gradient pass
+// (dtype code selects the fp32 MFMA or the fp64 VALU kernels, which partition
+// differently).
+int edge_pick_splits(int dtype, int64_t n, int64_t I, int64_t O, int64_t R, bool backward);
 
 // fp32 MFMA kernels of the edge statistic (kan_edge_mfma.hip).
-int edge_mfma_splits(int64_t n, int64_t I, int64_t O, int64_t R);
+int edge_mfma_splits(int64_t n, int64_t I, int64_t O, int64_t R, bool backward);
 int launch_edge_forward_mfma(const float* s, const float* H, const float* bw, const float* W,
                              float* a, float* part, int splits, int64_t n, int64_t I, int64_t O,
                              int64_t R, hipStream_t st);

@@ -372,8 +372,8 @@ inline int fin_blocks(int64_t total) {
 
 }  // namespace
 
-int edge_pick_splits(int dtype, int64_t n, int64_t I, int64_t O, int64_t R) {
-  if (dtype == KAN_DTYPE_F32) return edge_mfma_splits(n, I, O, R);
+int edge_pick_splits(int dtype, int64_t n, int64_t I, int64_t O, int64_t R, bool backward) {
+  if (dtype == KAN_DTYPE_F32) return edge_mfma_splits(n, I, O, R, backward);
   const int64_t blocks = ceil_div(O, kEdgeThreads) * I;
   const int64_t target = 4LL * device_cu_count();
   int64_t s = ceil_div(target, blocks > 0 ? blocks : 1);

@@ -28,6 +28,11 @@ namespace {
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kEdgeMfThreads = 256;  // 4 waves
+// Sample ranges of splits and waves are whole groups of 4 tiles of 16, so
+// that the forward kernel's prefetch loop has no early exit (an exit would
+// make the compiler wait for every load in flight at the loop head); tiles
+// past the last sample are read as zeros.
+constexpr int64_t kEdgeRowQuant = 64;
 // Output layout of the forward and parameter kernels: each wave owns OT
 // 16-wide output tiles; WS waves split a block's samples between them (their
 // partial sums meet in LDS, in wave order), and WO = 4 / WS waves cover
@@ -66,6 +71,71 @@ __device__ __forceinline__ float hc_val(const float* __restrict__ s, const float
   return H[f * R + (c - 1)];
 }
 
+// Buffer-resource loads of the augmented sample values Hc[n, c] of feature
+// i, one tile of 16 rows at a time (n0 wave-uniform): H rows lie I*R floats
+// apart, s rows I floats apart.  A tile's resource covers only its rows below
+// ne, and a lane whose column lies past R (or in the other array) uses an
+// offset past every tile's range, so the hardware returns 0 for both: no
+// branch, select or clamp around a load.  The loads go through the buffer
+// intrinsic rather than plain pointer loads, which the compiler would move
+// from the prefetch point to the point of use (a phi of loads becomes a load
+// of a phi), leaving nothing in flight.
+constexpr uint32_t kBufOob = 0x80000000u;      // an offset outside every tile
+constexpr int kBufWord3 = 0x00020000;          // gfx9 raw buffer, 32-bit data
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(const float* base, int64_t rows,
+                                                            int64_t row_floats) {
+  rows = rows < 0 ? 0 : (rows > 16 ? 16 : rows);
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), (short)0,
+                                           (int)(rows * row_floats * 4), kBufWord3);
+}
+
+// (the builtin returns the 32 bits as an integer: reinterpret, not convert)
+__device__ __forceinline__ float buf_ld(__amdgpu_buffer_rsrc_t rs, uint32_t off) {
+  return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rs, (int)off, 0, 0));
+}
+
+// The two resources of the tile at n0 (s's covers nothing without s).
+struct HcTile {
+  __amdgpu_buffer_rsrc_t h, s;
+};
+
+struct HcRows {
+  const float* s;  // (H in place of a missing s, whose rows then count as 0)
+  const float* H;
+  int64_t I, R;
+  int i;
+  bool has_s;
+  __device__ HcRows(const float* s_, const float* H_, int64_t I_, int64_t R_, int i_)
+      : s(s_ != nullptr ? s_ : H_), H(H_), I(I_), R(R_), i(i_), has_s(s_ != nullptr) {}
+  __device__ __forceinline__ HcTile tile(int64_t n0, int64_t ne) const {
+    HcTile t;
+    t.h = tile_rsrc(H + (n0 * I + i) * R, ne - n0, I * R);
+    t.s = tile_rsrc(s + n0 * I + i, has_s ? ne - n0 : 0, I);
+    return t;
+  }
+  // byte offsets of row rr, column c within a tile, into H and into s
+  __device__ __forceinline__ uint32_t off_h(int rr, int c) const {
+    return (c >= 1 && c <= R) ? (uint32_t)(((int64_t)rr * I * R + (c - 1)) * 4) : kBufOob;
+  }
+  __device__ __forceinline__ uint32_t off_s(int rr, int c) const {
+    return c == 0 ? (uint32_t)((int64_t)rr * I * 4) : kBufOob;
+  }
+};
+
+// Where column 0 can occur a lane loads from both arrays; at most one of the
+// two is in range, so OR-ing their bits gives the value exactly.  The OR is
+// taken where the tile is used, as an opaque instruction: a plain OR of two
+// loop-carried values is folded back to the loads (an OR of phis becomes a
+// phi of ORs), which would then wait for them as soon as they are issued.
+// The compiler's hazard checks do not see inside the asm, so it carries the
+// wait states an MFMA reading a VALU result needs (2 on this ISA; 5 given).
+__device__ __forceinline__ float hc_or(float h, float sv) {
+  float v;
+  asm volatile("v_or_b32 %0, %1, %2\n\ts_nop 4" : "=v"(v) : "v"(h), "v"(sv));
+  return v;
+}
+
 // augmented weight value Wc[o, c]
 __device__ __forceinline__ float wc_val(const float* __restrict__ bw, const float* __restrict__ W,
                                         int64_t o, int I, int i, int R, int c) {
@@ -77,7 +147,7 @@ __device__ __forceinline__ float wc_val(const float* __restrict__ bw, const floa
 struct EdgeGeom {
   int64_t n;
   int I, O, R;
-  int64_t per_split;  // samples per split (multiple of 16)
+  int64_t per_split;  // samples per split (multiple of kEdgeRowQuant)
   int ochunks;        // output chunks of kBlockOut
   int splits;
 };
@@ -98,7 +168,9 @@ __global__ __launch_bounds__(kEdgeMfThreads) void edge_fwd_mfma_kernel(
   const int i = (int)(bid % g.I);
   const int oc = (int)((bid / g.I) % g.ochunks);
   const int split = (int)(bid / ((int64_t)g.I * g.ochunks));
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  // (wave index through readfirstlane: the compiler then keeps the sample
+  // range, and the buffer resources built from it, in scalar registers)
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int wo = wave % Tl::kWO, wsi = wave / Tl::kWO;
   const int q = lane >> 4, r = lane & 15;
   const int obase = oc * Tl::kBlockOut + wo * kOT * 16;
@@ -122,37 +194,60 @@ __global__ __launch_bounds__(kEdgeMfThreads) void edge_fwd_mfma_kernel(
   int64_t nb = (int64_t)split * g.per_split;
   int64_t ne = min(g.n, nb + g.per_split);
   if (WS > 1) {  // this wave's share of the split's samples
-    const int64_t per_wave = round_up(ceil_div(g.per_split, (int64_t)WS), 16);
+    const int64_t per_wave = round_up(ceil_div(g.per_split, (int64_t)WS), kEdgeRowQuant);
     nb += wsi * per_wave;
     ne = min(ne, nb + per_wave);
   }
-  float an[P][KS];
-  auto load_a = [&](int64_t n0, float (&dst)[KS]) {
-    const int64_t nn = n0 + r;
+  // S register slots of sample tiles, S - 1 tiles ahead: sub-tile p uses slot
+  // p and first refills the slot sub-tile p - 1 has just finished with, so
+  // no old and new value of a slot are live together (which would cost
+  // register copies that wait for the loads at the loop end).
+  constexpr int S = P < 2 ? 2 : P;
+  float an[S][KS], asn[S];  // asn: the s part of k = 0
+  const HcRows hr(s, H, g.I, g.R, i);
+  uint32_t oh[KS];
 #pragma unroll
-    for (int k = 0; k < KS; ++k) {
-      const int c = 4 * k + q;
-      dst[k] = (nn < ne && c < R1) ? hc_val(s, H, nn, g.I, i, g.R, c) : 0.0f;
-    }
+  for (int k = 0; k < KS; ++k) oh[k] = hr.off_h(r, 4 * k + q);
+  const uint32_t os = hr.off_s(r, q);  // column 0 only at k = 0
+  auto load_a = [&](int64_t n0, float (&dst)[KS], float& dsts) {
+    const HcTile t = hr.tile(n0, ne);
+#pragma unroll
+    for (int k = 0; k < KS; ++k) dst[k] = buf_ld(t.h, oh[k]);
+    dsts = buf_ld(t.s, os);
   };
+  // (slots issued in order, so that the wait for slot 0 at the loop head
+  // leaves the later slots in flight on the first pass as on the others)
 #pragma unroll
-  for (int p = 0; p < P; ++p) load_a(nb + 16 * p, an[p]);
-  for (int64_t n0 = nb; n0 < ne; n0 += 16 * P) {
+  for (int p = 0; p < S - 1; ++p) {
+    __builtin_amdgcn_sched_barrier(0);
+    load_a(nb + 16 * p, an[p], asn[p]);
+  }
+  for (int64_t n0 = nb; n0 < ne; n0 += 16 * S) {
 #pragma unroll
-    for (int p = 0; p < P; ++p) {
+    for (int p = 0; p < S; ++p) {
       const int64_t nt = n0 + 16 * p;
-      if (nt >= ne) break;
+      constexpr int kLag = S - 1;
+      const int fill = (p + kLag) % S;
+      // keep each sub-tile's instructions in place: the scheduler would
+      // otherwise take the column-0 ORs (and their waits) up to the loads
+      __builtin_amdgcn_sched_barrier(0);
+      load_a(nt + 16 * kLag, an[fill], asn[fill]);
+      __builtin_amdgcn_sched_barrier(0);  // the loads go out before this tile's wait
       float a[KS];
 #pragma unroll
-      for (int k = 0; k < KS; ++k) a[k] = an[p][k];
-      load_a(nt + 16 * P, an[p]);
+      for (int k = 0; k < KS; ++k) a[k] = k == 0 ? hc_or(an[p][0], asn[p]) : an[p][k];
+      // k outermost: the kOT accumulation chains are independent, so a wave
+      // issues MFMAs back to back instead of waiting on one chain at a time
+      f32x4 acc[kOT];
 #pragma unroll
-      for (int t = 0; t < kOT; ++t) {
-        f32x4 acc = zero4();
+      for (int t = 0; t < kOT; ++t) acc[t] = zero4();
 #pragma unroll
-        for (int k = 0; k < KS; ++k) acc = mfma16(a[k], w[t][k], acc);
-        tot[t] += (fabsf(acc[0]) + fabsf(acc[1])) + (fabsf(acc[2]) + fabsf(acc[3]));
-      }
+      for (int k = 0; k < KS; ++k)
+#pragma unroll
+        for (int t = 0; t < kOT; ++t) acc[t] = mfma16(a[k], w[t][k], acc[t]);
+#pragma unroll
+      for (int t = 0; t < kOT; ++t)
+        tot[t] += (fabsf(acc[t][0]) + fabsf(acc[t][1])) + (fabsf(acc[t][2]) + fabsf(acc[t][3]));
     }
   }
   // combine the four row groups of each column in a fixed order
@@ -203,7 +298,9 @@ __global__ __launch_bounds__(kEdgeMfThreads) void edge_param_mfma_kernel(
   const int i = (int)(bid % g.I);
   const int oc = (int)((bid / g.I) % g.ochunks);
   const int split = (int)(bid / ((int64_t)g.I * g.ochunks));
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  // (wave index through readfirstlane: the compiler then keeps the sample
+  // range, and the buffer resources built from it, in scalar registers)
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int wo = wave % Tl::kWO, wsi = wave / Tl::kWO;
   const int q = lane >> 4, r = lane & 15;
   const int obase = oc * Tl::kBlockOut + wo * kOT * 16;
@@ -231,53 +328,74 @@ __global__ __launch_bounds__(kEdgeMfThreads) void edge_param_mfma_kernel(
   int64_t nb = (int64_t)split * g.per_split;
   int64_t ne = min(g.n, nb + g.per_split);
   if (WS > 1) {
-    const int64_t per_wave = round_up(ceil_div(g.per_split, (int64_t)WS), 16);
+    const int64_t per_wave = round_up(ceil_div(g.per_split, (int64_t)WS), kEdgeRowQuant);
     nb += wsi * per_wave;
     ne = min(ne, nb + per_wave);
   }
-  // operands of the next sample tile are loaded while the current one runs:
+  // Operands of the next sample tile are loaded while the current one runs:
   // A of phi (Hc[n0 + r, 4k + q]) and B of the second product
-  // (Hc[n0 + 4q + v, 16ct + r])
-  float an[KS], hn[CT][4];
-  auto load_tile = [&](int64_t n0) {
-    const int64_t nn = n0 + r;
+  // (Hc[n0 + 4q + v, 16ct + r]), in two register slots used alternately
+  // (the slot rotation of the forward kernel with S = 2).
+  float an[2][KS], asn[2], hn[2][CT][4], hsn[2][4];  // asn, hsn: s parts (k = 0, ct = 0)
+  const HcRows hr(s, H, g.I, g.R, i);
+  uint32_t oa[KS], ob[CT][4], obs[4];
 #pragma unroll
-    for (int k = 0; k < KS; ++k) {
-      const int c = 4 * k + q;
-      an[k] = (nn < ne && c < R1) ? hc_val(s, H, nn, g.I, i, g.R, c) : 0.0f;
-    }
+  for (int k = 0; k < KS; ++k) oa[k] = hr.off_h(r, 4 * k + q);
+  const uint32_t oas = hr.off_s(r, q);  // column 0 only at k = 0
 #pragma unroll
-    for (int ct = 0; ct < CT; ++ct) {
-      const int c = ct * 16 + r;
+  for (int v = 0; v < 4; ++v) {
 #pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const int64_t nk = n0 + 4 * q + v;
-        hn[ct][v] = (nk < ne && c < R1) ? hc_val(s, H, nk, g.I, i, g.R, c) : 0.0f;
-      }
+    for (int ct = 0; ct < CT; ++ct) ob[ct][v] = hr.off_h(4 * q + v, ct * 16 + r);
+    obs[v] = hr.off_s(4 * q + v, r);  // column 0 only at ct = 0
+  }
+  auto load_tile = [&](int64_t n0, float (&da)[KS], float& das, float (&dh)[CT][4],
+                       float (&dhs)[4]) {
+    const HcTile t = hr.tile(n0, ne);
+#pragma unroll
+    for (int k = 0; k < KS; ++k) da[k] = buf_ld(t.h, oa[k]);
+    das = buf_ld(t.s, oas);
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct) dh[ct][v] = buf_ld(t.h, ob[ct][v]);
+      dhs[v] = buf_ld(t.s, obs[v]);
     }
   };
-  load_tile(nb);
-  for (int64_t n0 = nb; n0 < ne; n0 += 16) {
-    float a[KS], hb[CT][4];
+  load_tile(nb, an[0], asn[0], hn[0], hsn[0]);
+  for (int64_t n0 = nb; n0 < ne; n0 += 32) {
 #pragma unroll
-    for (int k = 0; k < KS; ++k) a[k] = an[k];
+    for (int p = 0; p < 2; ++p) {
+      // (instructions kept per sub-tile, as in the forward kernel)
+      __builtin_amdgcn_sched_barrier(0);
+      load_tile(n0 + 16 * p + 16, an[p ^ 1], asn[p ^ 1], hn[p ^ 1], hsn[p ^ 1]);
+      __builtin_amdgcn_sched_barrier(0);  // the loads go out before this tile's wait
+      float a[KS], hb[CT][4];
 #pragma unroll
-    for (int ct = 0; ct < CT; ++ct)
-#pragma unroll
-      for (int v = 0; v < 4; ++v) hb[ct][v] = hn[ct][v];
-    load_tile(n0 + 16);
-#pragma unroll
-    for (int t = 0; t < kOT; ++t) {
-      f32x4 acc = zero4();
-#pragma unroll
-      for (int k = 0; k < KS; ++k) acc = mfma16(a[k], w[t][k], acc);
-      float gv[4];
-#pragma unroll
-      for (int v = 0; v < 4; ++v) gv[v] = g_sign(gav[t], acc[v]);
+      for (int k = 0; k < KS; ++k) a[k] = k == 0 ? hc_or(an[p][0], asn[p]) : an[p][k];
 #pragma unroll
       for (int ct = 0; ct < CT; ++ct)
 #pragma unroll
-        for (int v = 0; v < 4; ++v) dacc[t][ct] = mfma16(gv[v], hb[ct][v], dacc[t][ct]);
+        for (int v = 0; v < 4; ++v)
+          hb[ct][v] = ct == 0 ? hc_or(hn[p][0][v], hsn[p][v]) : hn[p][ct][v];
+      // both products with the output tiles innermost (independent chains)
+      f32x4 acc[kOT];
+#pragma unroll
+      for (int t = 0; t < kOT; ++t) acc[t] = zero4();
+#pragma unroll
+      for (int k = 0; k < KS; ++k)
+#pragma unroll
+        for (int t = 0; t < kOT; ++t) acc[t] = mfma16(a[k], w[t][k], acc[t]);
+      float gv[kOT][4];
+#pragma unroll
+      for (int t = 0; t < kOT; ++t)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) gv[t][v] = g_sign(gav[t], acc[t][v]);
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+        for (int v = 0; v < 4; ++v)
+#pragma unroll
+          for (int t = 0; t < kOT; ++t) dacc[t][ct] = mfma16(gv[t][v], hb[ct][v], dacc[t][ct]);
     }
   }
   if (WS > 1) {  // add the WS sample shares in wave order
@@ -331,11 +449,15 @@ __global__ __launch_bounds__(kEdgeMfThreads) void edge_param_mfma_kernel(
   }
 }
 
-// Input gradients: block (i, sample block of 4 waves x NTW tiles of 16).
-// The feature's weights and ga/n are staged in LDS one output chunk at a
-// time; each wave computes phi^T tiles (rows o, columns n) for its samples,
-// g in registers, and dHc^T[c, n] += sum_o Wc[o, c] g[n, o] with the
-// accumulator entries as the B operand.
+// Input gradients.  The work items are (i, sample block of 4 waves x NTW
+// tiles of 16) in feature-major order; workgroup b of the grid takes the
+// contiguous items [b W / G, (b + 1) W / G), so the items are spread evenly
+// over a grid that the device holds at once, and a workgroup restages
+// weights only where its feature changes.  The feature's weights and ga/n
+// are staged in LDS one output chunk at a time; each wave computes phi^T
+// tiles (rows o, columns n) for its samples, g in registers, and
+// dHc^T[c, n] += sum_o Wc[o, c] g[n, o] with the accumulator entries as the
+// B operand.
 constexpr int kInChunkFloats = 8192;  // LDS floats for one staged weight chunk
 constexpr int kInMaxRows = 1024;
 
@@ -343,18 +465,22 @@ template <int KS, int CT, int NTW>
 __global__ __launch_bounds__(kEdgeMfThreads) void edge_input_mfma_kernel(
     const float* __restrict__ ga, const float* __restrict__ s, const float* __restrict__ H,
     const float* __restrict__ bw, const float* __restrict__ W, float* __restrict__ ds,
-    float* __restrict__ dH, EdgeGeom g, int oc_rows, int nsb) {
+    float* __restrict__ dH, EdgeGeom g, int oc_rows) {
   __shared__ float wl[kInChunkFloats];
   __shared__ float gl[kInMaxRows];
   const int64_t nblk = ceil_div(g.n, (int64_t)(64 * NTW));
-  const int i = (int)(blockIdx.x % g.I);
-  const int64_t sb0 = (blockIdx.x / g.I) * (int64_t)nsb;  // first sample block of this group
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int64_t items = nblk * g.I;
+  const int64_t item_lo = (int64_t)blockIdx.x * items / gridDim.x;
+  const int64_t item_hi = ((int64_t)blockIdx.x + 1) * items / gridDim.x;
+  int i = -1;  // feature of the current item (and of the staged weights)
+  // (wave index through readfirstlane: the compiler then keeps the sample
+  // range, and the buffer resources built from it, in scalar registers)
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int q = lane >> 4, r = lane & 15;
   const int R1 = g.R + 1;
   const int stride = R1 | 1;  // odd row stride of the staged weights
   const float inv_n = 1.0f / (float)g.n;
-  const bool one_chunk = g.O <= oc_rows;  // weights staged once for all sample blocks
+  const bool one_chunk = g.O <= oc_rows;  // weights staged once per feature
 
   auto stage = [&](int o0, int orows) {
     __syncthreads();
@@ -366,9 +492,13 @@ __global__ __launch_bounds__(kEdgeMfThreads) void edge_input_mfma_kernel(
       gl[e] = e < orows ? ga[(int64_t)(o0 + e) * g.I + i] * inv_n : 0.0f;
     __syncthreads();
   };
-  if (one_chunk) stage(0, g.O);
-
-  for (int64_t sb = sb0; sb < min(sb0 + nsb, nblk); ++sb) {
+  for (int64_t item = item_lo; item < item_hi; ++item) {
+    const int fi = (int)(item / nblk);
+    const int64_t sb = item - (int64_t)fi * nblk;
+    if (fi != i) {
+      i = fi;
+      if (one_chunk) stage(0, g.O);
+    }
     // this wave's sample tiles: n0 = nbase + (j*4 + wave)*16
     const int64_t nbase = sb * (int64_t)(64 * NTW);
     float a[NTW][KS];
@@ -411,19 +541,25 @@ __global__ __launch_bounds__(kEdgeMfThreads) void edge_input_mfma_kernel(
           for (int v = 0; v < 4; ++v)
             wb[ct][v] = c < R1 ? wl[(ot + 4 * q + v) * stride + c] : 0.0f;
         }
+        // both products with the sample tiles innermost (independent chains)
+        f32x4 acc[NTW];
 #pragma unroll
-        for (int j = 0; j < NTW; ++j) {
-          f32x4 acc = zero4();
+        for (int j = 0; j < NTW; ++j) acc[j] = zero4();
 #pragma unroll
-          for (int k = 0; k < KS; ++k) acc = mfma16(wa[k], a[j][k], acc);
-          float gv[4];
+        for (int k = 0; k < KS; ++k)
 #pragma unroll
-          for (int v = 0; v < 4; ++v) gv[v] = g_sign(gs[v], acc[v]);
+          for (int j = 0; j < NTW; ++j) acc[j] = mfma16(wa[k], a[j][k], acc[j]);
+        float gv[NTW][4];
 #pragma unroll
-          for (int ct = 0; ct < CT; ++ct)
+        for (int j = 0; j < NTW; ++j)
 #pragma unroll
-            for (int v = 0; v < 4; ++v) dacc[j][ct] = mfma16(wb[ct][v], gv[v], dacc[j][ct]);
-        }
+          for (int v = 0; v < 4; ++v) gv[j][v] = g_sign(gs[v], acc[j][v]);
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+          for (int v = 0; v < 4; ++v)
+#pragma unroll
+            for (int j = 0; j < NTW; ++j) dacc[j][ct] = mfma16(wb[ct][v], gv[j][v], dacc[j][ct]);
       }
     }
     // dacc[j][ct]: lane (q, r) holds column n = tile + r, rows c = 16ct + 4q + v
@@ -513,14 +649,20 @@ int edge_tiling(int64_t O, int* ot, int* ws) {
   return (4 / *ws) * *ot * 16;
 }
 
-int edge_mfma_splits(int64_t n, int64_t I, int64_t O, int64_t R) {
+// Sample splits: about 8 workgroups per CU (measured at c4's layers, where
+// longer workgroups in fewer whole rounds ran slower than many short ones the
+// hardware balances by itself).  The forward pass of a narrow layer, whose
+// waves already split each workgroup's samples (WS > 1), takes 4 times as
+// many: its partial sums are only O x I per split.  At least 256 samples per
+// split, at most 64 splits.
+int edge_mfma_splits(int64_t n, int64_t I, int64_t O, int64_t R, bool backward) {
   (void)R;
   int ot, ws;
   const int64_t ochunks = ceil_div(O, (int64_t)edge_tiling(O, &ot, &ws));
   const int64_t blocks = I * ochunks;
-  const int64_t target = 8LL * device_cu_count();
+  const int64_t target = (!backward && ws > 1 ? 32LL : 8LL) * device_cu_count();
   int64_t s = ceil_div(target, blocks > 0 ? blocks : 1);
-  const int64_t cap = ceil_div(n, 256);  // at least 16 sample tiles per split
+  const int64_t cap = ceil_div(n, 256);
   if (s > cap) s = cap;
   if (s > 64) s = 64;
   if (s < 1) s = 1;
@@ -540,7 +682,7 @@ int launch_edge_forward_mfma(const float* s, const float* H, const float* bw, co
   g.O = (int)O;
   g.R = (int)R;
   g.splits = splits;
-  g.per_split = round_up(ceil_div(n, splits), 16);
+  g.per_split = round_up(ceil_div(n, splits), kEdgeRowQuant);
   int ot, ws;
   g.ochunks = (int)ceil_div(O, (int64_t)edge_tiling(O, &ot, &ws));
   const int64_t blocks = I * g.ochunks * (int64_t)splits;
@@ -576,7 +718,7 @@ int launch_edge_backward_mfma(const float* ga, const float* s, const float* H, c
   g.O = (int)O;
   g.R = (int)R;
   g.splits = splits;
-  g.per_split = round_up(ceil_div(n, splits), 16);
+  g.per_split = round_up(ceil_div(n, splits), kEdgeRowQuant);
   int ot, ws;
   g.ochunks = (int)ceil_div(O, (int64_t)edge_tiling(O, &ot, &ws));
   if ((dbw != nullptr || dW != nullptr) && O > 0 && I > 0) {
@@ -614,21 +756,18 @@ int launch_edge_backward_mfma(const float* ga, const float* s, const float* H, c
     int oc_rows = (int)(kInChunkFloats / (R1 | 1)) / 16 * 16;
     if (oc_rows > kInMaxRows) oc_rows = kInMaxRows;
     if ((int64_t)oc_rows > round_up(O, 16)) oc_rows = (int)round_up(O, 16);
-    // when the weights fit one stage, a workgroup runs several sample blocks
-    // on them (short layers would otherwise spend their time staging), while
-    // keeping about 8 workgroups per CU
-    int nsb = 1;
-    if (O <= oc_rows) {
-      const int64_t target = 8LL * device_cu_count();
-      while (nsb < 8 && I * ceil_div(nblk, (int64_t)(2 * nsb)) >= target) nsb *= 2;
-    }
-    const int64_t blocks = I * ceil_div(nblk, (int64_t)nsb);
-    if (blocks > 2147483647LL)
-      return set_error(KAN_ERR_LIMIT, "edge_abs_mean_backward: too many blocks");
+    // the items are shared by 4 rounds of resident workgroups (measured best
+    // at c4's layers between one round and one item per workgroup)
+    const int64_t items = I * nblk;
+    const void* fn = nullptr;
+    KAN_EDGE_MF_DISPATCH(R1, fn = reinterpret_cast<const void*>(
+                                 &edge_input_mfma_kernel<KS, CT, NTW>));
+    int64_t blocks = 4LL * device_cu_count() * resident_blocks_per_cu(fn, kEdgeMfThreads);
+    if (blocks > items) blocks = items;
     TimedLaunch timed(kClassEdgeGrad, st, 4.0 * (double)n * (double)O * (double)I * (double)R1);
     KAN_EDGE_MF_DISPATCH(R1, hipLaunchKernelGGL((edge_input_mfma_kernel<KS, CT, NTW>),
                                                 dim3((unsigned)blocks), dim3(kEdgeMfThreads), 0,
-                                                st, ga, s, H, bw, W, ds, dH, g, oc_rows, nsb));
+                                                st, ga, s, H, bw, W, ds, dH, g, oc_rows));
     int rc = check_launch("edge_abs_mean_backward(inputs)");
     if (rc != KAN_OK) return rc;
   }

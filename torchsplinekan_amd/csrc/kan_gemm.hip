@@ -113,6 +113,9 @@ struct Cfg {
 
 using CfgF32Big = Cfg<float, 256, 256, 32, 2, 2, 32, 1>;
 using CfgF32Small = Cfg<float, 128, 128, 32, 2, 2, 32, 2>;
+// Narrow outputs (N <= 64, e.g. a 64-wide layer): 4 waves stacked along M,
+// 64 x 64 each, so no wave computes padding columns.
+using CfgF32Narrow = Cfg<float, 256, 64, 32, 4, 1, 32, 1>;
 using CfgF64 = Cfg<double, 128, 128, 16, 2, 2, 16, 1>;
 
 template <typename T>
@@ -707,46 +710,64 @@ struct CfgModel {
   int bm, bn, bk, blocks_per_cu;
   double eff;
 };
-constexpr CfgModel kModelF32[2] = {{256, 256, 32, 1, 0.89}, {128, 128, 32, 2, 0.85}};
+constexpr CfgModel kModelF32[3] = {
+    {256, 256, 32, 1, 0.89}, {128, 128, 32, 2, 0.85}, {256, 64, 32, 1, 0.75}};
 constexpr CfgModel kModelF64 = {128, 128, 16, 1, 0.80};
 constexpr double kPeakPerCuF32 = 157.3e12 / 256.0;  // FP32 MFMA flop/s per CU
 constexpr double kPeakPerCuF64 = 78.6e12 / 256.0;
 constexpr double kStreamBytesPerS = 5.0e12;          // split-K partial-sum traffic
+// Per-block start-up and write-out, as the k-extent that would take as long:
+// a block that runs a short k range (a split of a moderate K) is charged for
+// it (measured at c4's layers: a 256 x 256 tile split twice over K = 5632
+// ran 10 % slower than 128 x 128 tiles over the whole K).
+constexpr double kKOverhead = 256.0;
 
 // Estimated seconds for M x N x K with `splits` K-slices: whole waves of
-// resident blocks times the duration of one block, plus the split-K partial
-// traffic (written once, read once by the caller's reduction).
+// resident blocks times the duration of one block (its k range plus
+// kKOverhead), plus the split-K partial traffic (written once, read once by
+// the caller's reduction).
 double est_seconds(const CfgModel& c, double peak_per_cu, int64_t M, int64_t N, int64_t K,
                    int splits, size_t elem) {
   const int64_t cus = device_cu_count();
   const int64_t tiles = ceil_div(M, c.bm) * ceil_div(N, c.bn) * splits;
   const int64_t waves = ceil_div(tiles, cus * c.blocks_per_cu);
   const int64_t kper = round_up(ceil_div(K > 0 ? K : 1, splits), c.bk);
-  const double block_s = 2.0 * c.bm * c.bn * (double)kper * c.blocks_per_cu / (peak_per_cu * c.eff);
+  const double block_s = 2.0 * c.bm * c.bn * ((double)kper + kKOverhead) * c.blocks_per_cu /
+                         (peak_per_cu * c.eff);
   double t = (double)waves * block_s;
   if (splits > 1) t += 2.0 * (double)splits * (double)(M * N) * (double)elem / kStreamBytesPerS;
   return t;
 }
 
-// Test override of the fp32 tile configuration: KAN_HIP_GEMM_TILE=256 or
-// 128 forces the big or the small configuration (read at every launch, so a
-// test can switch it between calls); unset or any other value leaves the
-// choice to the cost model.
+// Test override of the fp32 tile configuration: KAN_HIP_GEMM_TILE=256, 128
+// or 256x64 forces the big, the small or the narrow configuration (read at
+// every launch, so a test can switch it between calls); unset or any other
+// value leaves the choice to the cost model.
 int forced_cfg_f32() {
   const char* v = std::getenv("KAN_HIP_GEMM_TILE");
   if (v == nullptr) return -1;
   if (std::strcmp(v, "256") == 0) return 0;
   if (std::strcmp(v, "128") == 0) return 1;
+  if (std::strcmp(v, "256x64") == 0) return 2;
   return -1;
 }
 
-// fp32 configuration (0 = big, 1 = small) for a given split count.
+// fp32 configuration (0 = big, 1 = small, 2 = narrow) for a given split
+// count; the narrow one only where N fits its 64 columns.
 int pick_cfg_f32(int64_t M, int64_t N, int64_t K, int splits) {
   const int forced = forced_cfg_f32();
   if (forced >= 0) return forced;
-  const double t0 = est_seconds(kModelF32[0], kPeakPerCuF32, M, N, K, splits, 4);
-  const double t1 = est_seconds(kModelF32[1], kPeakPerCuF32, M, N, K, splits, 4);
-  return t1 < t0 ? 1 : 0;
+  const int last = N <= 64 ? 2 : 1;
+  int best = 0;
+  double best_t = est_seconds(kModelF32[0], kPeakPerCuF32, M, N, K, splits, 4);
+  for (int c = 1; c <= last; ++c) {
+    const double t = est_seconds(kModelF32[c], kPeakPerCuF32, M, N, K, splits, 4);
+    if (t < best_t) {
+      best = c;
+      best_t = t;
+    }
+  }
+  return best;
 }
 
 template <class C, bool AK, bool BKC, int EPIK = 0>
@@ -851,10 +872,10 @@ int launch_gemm(int layout, int64_t M, int64_t N, int64_t K, const T* A, int64_t
   TimedLaunch timed(kClassContraction, st, 2.0 * (double)M * (double)N * (double)K);
   int rc;
   if constexpr (std::is_same<T, float>::value) {
-    if (pick_cfg_f32(M, N, K, splits < 1 ? 1 : splits) == 0)
-      rc = launch_layout<CfgF32Big>(layout, p, splits, st);
-    else
-      rc = launch_layout<CfgF32Small>(layout, p, splits, st);
+    const int cfg = pick_cfg_f32(M, N, K, splits < 1 ? 1 : splits);
+    if (cfg == 0) rc = launch_layout<CfgF32Big>(layout, p, splits, st);
+    else if (cfg == 2) rc = launch_layout<CfgF32Narrow>(layout, p, splits, st);
+    else rc = launch_layout<CfgF32Small>(layout, p, splits, st);
   } else {
     rc = launch_layout<CfgF64>(layout, p, splits, st);
   }

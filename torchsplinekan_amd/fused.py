@@ -105,6 +105,17 @@ def edge_abs_mean(s: Optional[torch.Tensor], H: torch.Tensor, bw: Optional[torch
     return EdgeAbsMean.apply(s, H, bw, W)
 
 
+def native_linear(s: torch.Tensor, bw: torch.Tensor, H2: torch.Tensor,
+                  W2: torch.Tensor) -> torch.Tensor:
+    """Layer output s bw^T + H2 W2^T of the fused regularisation path, the two
+    products the reference takes with F.linear (spline_kan/kan_linear.py:
+    360-362), on the MFMA contraction engine (NativeMatmul: gradients are
+    engine products as well, the long sample reductions split over K and
+    summed in a fixed order)."""
+    y = _C.NativeMatmul.apply(s, bw.t())
+    return y + _C.NativeMatmul.apply(H2, W2.t())
+
+
 def edge_abs_mean_chunked(s: Optional[torch.Tensor], x: torch.Tensor, grid: torch.Tensor, k: int,
                           bw: Optional[torch.Tensor], W: torch.Tensor,
                           chunk_size: int) -> torch.Tensor:
