@@ -123,6 +123,11 @@ struct HcRows {
   }
 };
 
+// byte offset of row rr of s within a tile where the lane's column c is 0
+__device__ __forceinline__ uint32_t c0_off_s(int rr, int c, int64_t I) {
+  return c == 0 ? (uint32_t)((int64_t)rr * I * 4) : kBufOob;
+}
+
 // Where column 0 can occur a lane loads from both arrays; at most one of the
 // two is in range, so OR-ing their bits gives the value exactly.  The OR is
 // taken where the tile is used, as an opaque instruction: a plain OR of two
@@ -461,7 +466,7 @@ __global__ __launch_bounds__(kEdgeMfThreads) void edge_param_mfma_kernel(
 constexpr int kInChunkFloats = 8192;  // LDS floats for one staged weight chunk
 constexpr int kInMaxRows = 1024;
 
-template <int KS, int CT, int NTW>
+template <int KS, int CT, int NTW, bool PF>
 __global__ __launch_bounds__(kEdgeMfThreads) void edge_input_mfma_kernel(
     const float* __restrict__ ga, const float* __restrict__ s, const float* __restrict__ H,
     const float* __restrict__ bw, const float* __restrict__ W, float* __restrict__ ds,
@@ -492,7 +497,34 @@ __global__ __launch_bounds__(kEdgeMfThreads) void edge_input_mfma_kernel(
       gl[e] = e < orows ? ga[(int64_t)(o0 + e) * g.I + i] * inv_n : 0.0f;
     __syncthreads();
   };
-  for (int64_t item = item_lo; item < item_hi; ++item) {
+  // Sample rows through buffer resources of the item's feature (see HcRows);
+  // rows past n and items past item_hi read as zeros.  With PF the next
+  // item's rows are loaded while the current item runs, in two register
+  // slots used alternately (narrow layers, where an item's few output tiles
+  // cannot hide the loads; wide layers keep one slot and a wave more per
+  // SIMD instead).
+  uint32_t oh[KS];
+  {
+    const HcRows hr0(s, H, g.I, g.R, 0);
+#pragma unroll
+    for (int k = 0; k < KS; ++k) oh[k] = hr0.off_h(r, 4 * k + q);
+  }
+  const uint32_t os = c0_off_s(r, q, g.I);  // column 0 only at k = 0
+  auto load_item = [&](int64_t item, float (&dh)[NTW][KS], float (&dsv)[NTW]) {
+    const bool live = item < item_hi;
+    const int fi = live ? (int)(item / nblk) : 0;
+    const int64_t nbase = (item - (int64_t)fi * nblk) * (int64_t)(64 * NTW);
+    const HcRows hr(s, H, g.I, g.R, fi);
+#pragma unroll
+    for (int j = 0; j < NTW; ++j) {
+      const HcTile t = hr.tile(nbase + (int64_t)(j * 4 + wave) * 16, live ? g.n : 0);
+#pragma unroll
+      for (int k = 0; k < KS; ++k) dh[j][k] = buf_ld(t.h, oh[k]);
+      dsv[j] = buf_ld(t.s, os);
+    }
+  };
+  float h0[NTW][KS], s0[NTW], h1[NTW][KS], s1[NTW];
+  auto process = [&](int64_t item, const float (&dh)[NTW][KS], const float (&dsv)[NTW]) {
     const int fi = (int)(item / nblk);
     const int64_t sb = item - (int64_t)fi * nblk;
     if (fi != i) {
@@ -503,14 +535,9 @@ __global__ __launch_bounds__(kEdgeMfThreads) void edge_input_mfma_kernel(
     const int64_t nbase = sb * (int64_t)(64 * NTW);
     float a[NTW][KS];
 #pragma unroll
-    for (int j = 0; j < NTW; ++j) {
-      const int64_t nn = nbase + (int64_t)(j * 4 + wave) * 16 + r;
+    for (int j = 0; j < NTW; ++j)
 #pragma unroll
-      for (int k = 0; k < KS; ++k) {
-        const int c = 4 * k + q;
-        a[j][k] = (nn < g.n && c < R1) ? hc_val(s, H, nn, g.I, i, g.R, c) : 0.0f;
-      }
-    }
+      for (int k = 0; k < KS; ++k) a[j][k] = k == 0 ? hc_or(dh[j][0], dsv[j]) : dh[j][k];
     f32x4 dacc[NTW][CT];
 #pragma unroll
     for (int j = 0; j < NTW; ++j)
@@ -581,6 +608,28 @@ __global__ __launch_bounds__(kEdgeMfThreads) void edge_input_mfma_kernel(
             dH[f * g.R + (c - 1)] = val;
           }
         }
+      }
+    }
+  };
+  if constexpr (!PF) {
+    (void)h1;
+    (void)s1;
+    for (int64_t item = item_lo; item < item_hi; ++item) {
+      load_item(item, h0, s0);
+      process(item, h0, s0);
+    }
+  } else {
+    load_item(item_lo, h0, s0);
+    for (int64_t item = item_lo; item < item_hi; item += 2) {
+      __builtin_amdgcn_sched_barrier(0);
+      load_item(item + 1, h1, s1);
+      __builtin_amdgcn_sched_barrier(0);  // the loads go out before this item's wait
+      process(item, h0, s0);
+      if (item + 1 < item_hi) {
+        __builtin_amdgcn_sched_barrier(0);
+        load_item(item + 2, h0, s0);
+        __builtin_amdgcn_sched_barrier(0);
+        process(item + 1, h1, s1);
       }
     }
   }
@@ -759,15 +808,24 @@ int launch_edge_backward_mfma(const float* ga, const float* s, const float* H, c
     // the items are shared by 4 rounds of resident workgroups (measured best
     // at c4's layers between one round and one item per workgroup)
     const int64_t items = I * nblk;
+    // next-item prefetch for layers of at most 256 outputs (measured: 590 ->
+    // 553 us at c4's 64-wide layer, 2 % slower at its 512-wide one)
+    const bool pf = O <= 256;
     const void* fn = nullptr;
-    KAN_EDGE_MF_DISPATCH(R1, fn = reinterpret_cast<const void*>(
-                                 &edge_input_mfma_kernel<KS, CT, NTW>));
+    KAN_EDGE_MF_DISPATCH(R1, fn = pf ? reinterpret_cast<const void*>(
+                                           &edge_input_mfma_kernel<KS, CT, NTW, true>)
+                                     : reinterpret_cast<const void*>(
+                                           &edge_input_mfma_kernel<KS, CT, NTW, false>));
     int64_t blocks = 4LL * device_cu_count() * resident_blocks_per_cu(fn, kEdgeMfThreads);
     if (blocks > items) blocks = items;
     TimedLaunch timed(kClassEdgeGrad, st, 4.0 * (double)n * (double)O * (double)I * (double)R1);
-    KAN_EDGE_MF_DISPATCH(R1, hipLaunchKernelGGL((edge_input_mfma_kernel<KS, CT, NTW>),
-                                                dim3((unsigned)blocks), dim3(kEdgeMfThreads), 0,
-                                                st, ga, s, H, bw, W, ds, dH, g, oc_rows));
+#define KAN_EDGE_INP(PFV)                                                                   \
+  KAN_EDGE_MF_DISPATCH(R1, hipLaunchKernelGGL((edge_input_mfma_kernel<KS, CT, NTW, PFV>),   \
+                                              dim3((unsigned)blocks), dim3(kEdgeMfThreads), \
+                                              0, st, ga, s, H, bw, W, ds, dH, g, oc_rows))
+    if (pf) KAN_EDGE_INP(true);
+    else KAN_EDGE_INP(false);
+#undef KAN_EDGE_INP
     int rc = check_launch("edge_abs_mean_backward(inputs)");
     if (rc != KAN_OK) return rc;
   }
