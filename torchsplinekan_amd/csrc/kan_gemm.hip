@@ -129,6 +129,7 @@ struct GemmParams {
   int64_t split_stride;
   int tiles_m, tiles_n, splits;
   int vec;  // operands 16-byte aligned with leading dimensions % 4 == 0
+  int buf;  // a whole slab's byte offsets fit 31 bits (buffer-resource loads)
 };
 
 // LDS footprint of one operand slab.
@@ -201,6 +202,35 @@ struct SlabLoader {
       int64_t r, kk;
       coords(threadIdx.x + p * NT, row0, k0, r, kk);
       reg[p] = *reinterpret_cast<const Vec4<T>*>(KCONT ? src + r * ld + kk : src + kk * ld + r);
+    }
+  }
+
+  // Whole slab through a buffer resource (fp32).  A lane's byte offset
+  // within a slab is the same for every slab, and its chunks p lie a
+  // wave-uniform stride apart, so a load takes no per-lane address
+  // arithmetic: base (scalar, per slab) + voff (lane, set once) + p * stride
+  // (scalar soffset).  Needs NT to be a multiple of the chunks per row.
+  uint32_t voff;
+  static constexpr int64_t kStep = KCONT ? NT / (BK / 4) : NT / (ROWS / 4);  // rows (k) per p
+  __device__ __forceinline__ void init_buf(int64_t ld) {
+    static_assert(KCONT ? NT % (BK / 4) == 0 : NT % (ROWS / 4) == 0, "uniform chunk stride");
+    int64_t r, kk;
+    coords(threadIdx.x, 0, 0, r, kk);
+    voff = (uint32_t)((KCONT ? r * ld + kk : kk * ld + r) * (int64_t)sizeof(T));
+  }
+  __device__ __forceinline__ void load_buf(const T* __restrict__ src, int64_t ld, int64_t row0,
+                                           int64_t k0) {
+    static_assert(sizeof(T) == 4, "128-bit buffer loads of 4 fp32 values");
+    const T* base = KCONT ? src + row0 * ld + k0 : src + k0 * ld + row0;
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<T*>(base), (short)0, -1, 0x00020000 /* gfx9 raw buffer, 32-bit data */);
+#pragma unroll
+    for (int p = 0; p < kPer; ++p) {
+      typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+      const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(
+          rs, (int)voff, (int)((int64_t)p * kStep * ld * (int64_t)sizeof(T)), 0);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) reg[p].v[j] = __uint_as_float(v[j]);
     }
   }
 
@@ -609,11 +639,13 @@ __global__ __launch_bounds__(C::kThreads, C::MINB) void gemm_pipe_kernel(GemmPar
 #pragma unroll
         for (int j = 0; j < FN; ++j) acc[i][j] = M::mma(fa[slot][i][s], fb[slot][j][s], acc[i][j]);
   };
+  // full_c: 1 = whole slabs through buffer resources, 0 = edge slabs
+  // (guarded; also whole slabs whose offsets do not fit a buffer resource)
   auto gload = [&](int slab, auto full_c) {
     const int64_t k0 = tc.kbeg + (int64_t)slab * BK;
-    if (decltype(full_c)::value) {
-      la.load_full(p.A, p.lda, tc.m0, k0);
-      lb.load_full(p.B, p.ldb, tc.n0, k0);
+    if constexpr (decltype(full_c)::value == 1) {
+      la.load_buf(p.A, p.lda, tc.m0, k0);
+      lb.load_buf(p.B, p.ldb, tc.n0, k0);
     } else {
       la.load_guarded(p.A, p.lda, tc.m0, p.M, k0, tc.kend);
       lb.load_guarded(p.B, p.ldb, tc.n0, p.N, k0, tc.kend);
@@ -621,11 +653,14 @@ __global__ __launch_bounds__(C::kThreads, C::MINB) void gemm_pipe_kernel(GemmPar
   };
   // One slab.  STORE: registers of slab kt+1 -> the other LDS buffer;
   // LOAD: global loads of slab kt+2; NEXT: barrier + first fragments of kt+1.
-  auto slab = [&](int kt, auto store_c, auto load_c, auto next_c, auto full_c) {
+  // par_c = kt & 1 as a constant (static LDS addresses) in the main loop;
+  // IC<-1> takes it at run time (the last two slabs).
+  auto slab = [&](int kt, auto store_c, auto load_c, auto next_c, auto full_c, auto par_c) {
     constexpr bool STORE = decltype(store_c)::value != 0;
     constexpr bool LOAD = decltype(load_c)::value != 0;
     constexpr bool NEXT = decltype(next_c)::value != 0;
-    const int cur = kt & 1;
+    constexpr int kPar = decltype(par_c)::value;
+    const int cur = kPar >= 0 ? kPar : (kt & 1);
 #pragma unroll
     for (int g = 0; g < NG; ++g) {
       // The next group's fragment reads come first in program order: the
@@ -651,6 +686,10 @@ __global__ __launch_bounds__(C::kThreads, C::MINB) void gemm_pipe_kernel(GemmPar
     }
   };
   auto run = [&](auto full_c) {
+    if constexpr (decltype(full_c)::value == 1) {
+      la.init_buf(p.lda);
+      lb.init_buf(p.ldb);
+    }
     gload(0, full_c);
     la.store(lds_a[0]);
     lb.store(lds_b[0]);
@@ -658,15 +697,15 @@ __global__ __launch_bounds__(C::kThreads, C::MINB) void gemm_pipe_kernel(GemmPar
     __syncthreads();
     fread(lds_a[0], lds_b[0], 0, 0);
     int kt = 0;
-    for (; kt + 2 < tc.nkt; ++kt) slab(kt, IC<1>(), IC<1>(), IC<1>(), full_c);
+    for (; kt + 2 < tc.nkt; ++kt) slab(kt, IC<1>(), IC<1>(), IC<1>(), full_c, IC<-1>());
     if (kt + 1 < tc.nkt) {
-      slab(kt, IC<1>(), IC<0>(), IC<1>(), full_c);
+      slab(kt, IC<1>(), IC<0>(), IC<1>(), full_c, IC<-1>());
       ++kt;
     }
-    slab(kt, IC<0>(), IC<0>(), IC<0>(), full_c);
+    slab(kt, IC<0>(), IC<0>(), IC<0>(), full_c, IC<-1>());
   };
   if (tc.nkt > 0) {
-    const bool full = p.vec && (tc.m0 + BM <= p.M) && (tc.n0 + BN <= p.N) &&
+    const bool full = p.vec && p.buf && (tc.m0 + BM <= p.M) && (tc.n0 + BN <= p.N) &&
                       ((tc.kend - tc.kbeg) % BK == 0);
     if (full) run(IC<1>());
     else run(IC<0>());
@@ -781,6 +820,12 @@ int launch_cfg(GemmParams<typename C::T> p, int splits, hipStream_t st, const Dx
   p.tiles_m = (int)tm;
   p.tiles_n = (int)tn;
   p.splits = splits;
+  // whole-slab byte offsets (rows or k spanned by a slab times ld) in 31 bits
+  auto span_ok = [](bool kcont, int rows, int64_t ld) {
+    const int64_t span = kcont ? (int64_t)rows * ld + C::BK : (int64_t)C::BK * ld + rows;
+    return span * (int64_t)sizeof(typename C::T) < (int64_t)1 << 31;
+  };
+  p.buf = span_ok(AK, C::BM, p.lda) && span_ok(BKC, C::BN, p.ldb);
   if constexpr (std::is_same<typename C::T, float>::value) {
     DxParams e{};
     if (dx != nullptr) e = *dx;
