@@ -231,6 +231,28 @@ def test_matmul_tile_configs_match_torch(C, monkeypatch, tile, M, K, N):
             assert normwise(np64(c), ref) < 1e-5, (ta, tb)
 
 
+def test_matmul_whole_tiles_with_wide_leading_dimension(C):
+    """Whole tiles whose slab span exceeds 31-bit byte offsets (row stride
+    2^21 + 64 floats: 256 rows span 2 GiB) take the guarded loads instead of
+    the buffer-resource ones; both transposition routes of A, against the
+    float64 product (2.1 GB operand buffer)."""
+    ld = (1 << 21) + 64
+    M, K, N = 256, 96, 64
+    print(f"matmul wide ld={ld}", flush=True)
+    buf = torch.empty(M, ld, device="cuda")
+    a = buf[:, :K]
+    g = torch.Generator().manual_seed(7)
+    a.copy_(torch.randn(M, K, generator=g))
+    b = torch.randn(K, N, generator=g).cuda()
+    ref = np64(a.cpu()) @ np64(b.cpu())
+    assert normwise(np64(C.matmul(a, b)), ref) < 1e-5
+    bt = torch.empty(N, ld, device="cuda")[:, :K]
+    bt.copy_(b.t())
+    assert normwise(np64(C.matmul(a, bt.t())), ref) < 1e-5
+    del buf, bt
+    torch.cuda.empty_cache()
+
+
 def test_native_matmul_gradients_and_workspace_check(C):
     from torchsplinekan_amd import _lib
     a = torch.randn(9, 6, device="cuda", dtype=torch.float64, requires_grad=True)
