@@ -34,6 +34,17 @@ int device_cu_count();
 int resident_blocks_per_cu(const void* kernel, int threads);
 
 __host__ __device__ inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// Workgroups are dealt to the 8 XCDs (each with its own L2) round-robin by
+// id.  This bijective remap of the dispatch order gives each XCD a
+// contiguous range of logical ids, so that neighbouring work items (tiles
+// sharing operand slabs, features sharing cache lines) meet in one L2.
+constexpr int kNumXcd = 8;
+__device__ __forceinline__ int xcd_remap(int pid, int total) {
+  const int per = total / kNumXcd, rem = total % kNumXcd;
+  const int xcd = pid % kNumXcd, idx = pid / kNumXcd;
+  return xcd * per + min(xcd, rem) + idx;
+}
 __host__ __device__ inline int64_t round_up(int64_t a, int64_t b) { return ceil_div(a, b) * b; }
 
 // Width of one augmented basis row [H(n, 0..I*R-1) | silu(x(n, 0..I-1))],

@@ -169,7 +169,9 @@ __global__ __launch_bounds__(kEdgeMfThreads) void edge_fwd_mfma_kernel(
   constexpr int kOT = OT;
   constexpr int P = KS <= 4 ? 4 : (KS <= 8 ? 2 : 1);
   __shared__ float red[WS > 1 ? WS * Tl::kBlockOut : 1];
-  const int64_t bid = blockIdx.x;
+  // (features in XCD-contiguous ranges: the H rows of neighbouring features
+  // share cache lines)
+  const int64_t bid = xcd_remap((int)blockIdx.x, (int)gridDim.x);
   const int i = (int)(bid % g.I);
   const int oc = (int)((bid / g.I) % g.ochunks);
   const int split = (int)(bid / ((int64_t)g.I * g.ochunks));
@@ -299,7 +301,9 @@ __global__ __launch_bounds__(kEdgeMfThreads) void edge_param_mfma_kernel(
   constexpr int kOT = OT;
   // partial dWc of the WS sample shares: [WS][block outputs][CT * 16]
   __shared__ float red[WS > 1 ? WS * Tl::kBlockOut * CT * 16 : 1];
-  const int64_t bid = blockIdx.x;
+  // (features in XCD-contiguous ranges: the H rows of neighbouring features
+  // share cache lines)
+  const int64_t bid = xcd_remap((int)blockIdx.x, (int)gridDim.x);
   const int i = (int)(bid % g.I);
   const int oc = (int)((bid / g.I) % g.ochunks);
   const int split = (int)(bid / ((int64_t)g.I * g.ochunks));

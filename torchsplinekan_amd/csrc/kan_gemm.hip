@@ -53,7 +53,6 @@ namespace {
 
 constexpr int kPadK = 4;
 constexpr int kPadMN = 4;
-constexpr int kNumXcd = 8;
 constexpr int kGroupM = 8;
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -138,14 +137,6 @@ struct Slab {
   static constexpr int kStride = KCONT ? (BK + kPadK) : (ROWS + kPadMN);
   static constexpr int kElems = KCONT ? ROWS * (BK + kPadK) : BK * (ROWS + kPadMN);
 };
-
-// Bijective remap of the dispatch order so that each XCD receives a
-// contiguous range of logical tile ids.
-__device__ __forceinline__ int xcd_remap(int pid, int total) {
-  const int per = total / kNumXcd, rem = total % kNumXcd;
-  const int xcd = pid % kNumXcd, idx = pid / kNumXcd;
-  return xcd * per + min(xcd, rem) + idx;
-}
 
 // Tile owned by this block: output origin, split and K range.
 struct TileCoords {
