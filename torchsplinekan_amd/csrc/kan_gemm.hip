@@ -863,15 +863,16 @@ int launch_dx_cfg(const GemmParams<float>& p, const DxParams& e, int k, hipStrea
 
 }  // namespace
 
-// Split-K factor: the split count in {1, 2, 4, ..., 64} with the smallest
-// estimated time (whole waves of resident blocks plus partial-sum traffic),
-// keeping at least 8 slabs per split.  Long-K products with few output tiles
+// Split-K factor: the split count in 1..64 with the smallest estimated time
+// (whole waves of resident blocks plus partial-sum traffic), keeping at least
+// 8 slabs per split; any count, not only powers of two, so that the tiles of
+// all splits fill their last wave of resident blocks.  Long-K products with few output tiles
 // (the parameter product, sample reductions, small-batch inference) split.
 template <typename T>
 int gemm_pick_splits(int64_t M, int64_t N, int64_t K) {
   int best = 1;
   double best_t = 0.0;
-  for (int s = 1; s <= 64; s *= 2) {
+  for (int s = 1; s <= 64; ++s) {
     double t;
     if (std::is_same<T, float>::value) {
       if (s > 1 && K / s < 8 * kModelF32[0].bk) break;
@@ -880,7 +881,7 @@ int gemm_pick_splits(int64_t M, int64_t N, int64_t K) {
       if (s > 1 && K / s < 8 * kModelF64.bk) break;
       t = est_seconds(kModelF64, kPeakPerCuF64, M, N, K, s, sizeof(T));
     }
-    if (s == 1 || t < best_t) {
+    if (s == 1 || t < best_t * (1.0 - 1e-9)) {
       best = s;
       best_t = t;
     }
