@@ -432,8 +432,8 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
-              "(the sample axis would shard over GPUs with one all-reduce of the parameter "
-              "gradients; see DESIGN.md)", file=sys.stderr)
+              "(the sample axis would shard over GPUs, with one all-reduce of the parameter "
+              "gradients per step)", file=sys.stderr)
         sys.exit(2)
 
     if args.copy_calibration:

@@ -171,7 +171,9 @@ int kan_hip_backward(int dtype, const void* grad_output, const void* x, const vo
                      int64_t out_features, int64_t grid_size, int64_t spline_order,
                      void* stream);
 
-/* Workspace bytes for the edge statistic (backward != 0: backward pass). */
+/* Workspace bytes for the edge statistic (backward != 0: backward pass).  The
+ * two passes split the samples differently, so each call needs the size
+ * queried for its own pass. */
 int kan_hip_edge_workspace(int dtype, int64_t n, int64_t in_features, int64_t out_features,
                            int64_t num_basis, int backward, size_t* bytes);
 
