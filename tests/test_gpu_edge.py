@@ -76,6 +76,25 @@ def test_edge_abs_mean_and_backward_match_oracle(C, shape, dtype, base):
         assert ds is None and dbw is None
 
 
+def test_edge_at_the_in_features_limit(C):
+    """in_features = 65535 and R = 72 (the widest augmented rows, k-steps 19 and
+    5 column tiles): the fp32 kernels' per-tile buffer offsets reach 15 rows x
+    I x R x 4 bytes = 283 MB, and the last feature's rows end at the end of H.
+    Forward and backward against the oracle."""
+    N, I, O, R = 23, 65535, 2, 72
+    print(f"edge at the limit {(N, I, O, R)}", flush=True)
+    s, H, bw, W, ga = _edge_inputs(N, I, O, R, torch.float32, seed=11)
+    a = C.edge_abs_mean(s.cuda(), H.cuda(), bw.cuda(), W.cuda())
+    ra = ko.edge_abs_mean(np64(s), np64(H), np64(bw), np64(W))
+    assert normwise(np64(a), ra) < 1e-5
+    ds, dH, dbw, dW = C.edge_abs_mean_backward(ga.cuda(), s.cuda(), H.cuda(), bw.cuda(),
+                                               W.cuda(), True, True, True, True)
+    rds, rdH, rdbw, rdW = ko.edge_abs_mean_backward(np64(ga), np64(s), np64(H), np64(bw),
+                                                    np64(W))
+    for got, ref in ((ds, rds), (dH, rdH), (dbw, rdbw), (dW, rdW)):
+        assert normwise(np64(got), ref) < 1e-4
+
+
 def test_edge_backward_partial_requests(C):
     s, H, bw, W, ga = _edge_inputs(100, 6, 10, 8, torch.float64, seed=3)
     d = [t.cuda() for t in (s, H, bw, W, ga)]
