@@ -1,6 +1,7 @@
-"""GPU parity of the fp32 contraction engine in both tile configurations
-(256x256 with 128x128 per wave, and 128x128 with 64x64 per wave), each
-forced through KAN_HIP_GEMM_TILE, on layer shapes chosen so that the
+"""GPU parity of the fp32 contraction engine in its tile configurations
+(256x256 over 8 waves of 128x64, 256x256 over 4 waves of 128x128, and
+128x128 with 64x64 per wave), each forced through KAN_HIP_GEMM_TILE, on
+layer shapes chosen so that the
 forward (NT), input-gradient (NT against the transposed weight; both the
 two-pass route and, with KAN_HIP_FUSED_DX=1, dx contracted in the GEMM
 epilogue, where the spline columns of one feature straddle two wave blocks
@@ -57,7 +58,7 @@ def tile_env():
 
 
 @pytest.mark.parametrize("fused_dx", ["0", "1"])
-@pytest.mark.parametrize("tile", ["256", "128"])
+@pytest.mark.parametrize("tile", ["256", "256w4", "128"])
 @pytest.mark.parametrize("shape", SHAPES)
 def test_contraction_configs_match_oracle(C, tile_env, tile, shape, fused_dx):
     N, I, O, G, k, kind = shape

@@ -211,7 +211,7 @@ def test_native_matmul_matches_torch(C, dtype, tol, M, K, N):
             assert torch.equal(c, C.matmul(_view(a.cuda(), ta), _view(b.cuda(), tb)))
 
 
-@pytest.mark.parametrize("tile", ["256x64", "128", "256"])
+@pytest.mark.parametrize("tile", ["256x64", "128", "256", "256w4"])
 @pytest.mark.parametrize("M,K,N", [(600, 5632, 64), (513, 407, 61), (16384, 64, 64),
                                    (333, 16384, 19), (64, 100, 3)])
 def test_matmul_tile_configs_match_torch(C, monkeypatch, tile, M, K, N):

@@ -9,12 +9,16 @@
 // They replace the cuBLAS calls of csrc/kan_cuda.cu:521-529, 579-604.
 //
 // fp32 runs on gemm_pipe_kernel, a software-pipelined v_mfma_f32_32x32x2f32
-// main loop, in one of two tile configurations picked per problem by a cost
-// model (pick_cfg_f32):
-//   big    256x256 block tile, 4 waves of 128x128 (256 accumulator registers
-//          per lane), one block per CU;
+// main loop, in one of three tile configurations picked per problem by a
+// cost model (pick_cfg_f32):
+//   big    256x256 block tile, 8 waves of 128x64 (two waves per SIMD), one
+//          block per CU;
 //   small  128x128 block tile, 4 waves of 64x64, two blocks per CU (for
-//          problems with too few big tiles to fill the chip).
+//          problems with too few big tiles to fill the chip);
+//   narrow 256x64 block tile, 4 waves of 64x64, for outputs of at most 64
+//          columns.
+// A 256x256 tile over 4 waves of 128x128 (one wave per SIMD) serves the
+// fused input-gradient epilogue.
 // fp64 runs on gemm_kernel: 128x128 tile, 2x2 waves, v_mfma_f64_16x16x4f64.
 //
 // Operand slabs (BK deep) are staged through LDS with double buffering.  Each
@@ -110,7 +114,12 @@ struct Cfg {
   static_assert(BK % Mfma<T, MF>::kKG == 0, "slab must be whole k-groups");
 };
 
-using CfgF32Big = Cfg<float, 256, 256, 32, 2, 2, 32, 1>;
+// 256 x 256 block tiles: 8 waves of 128 x 64 (two per SIMD: while one wave
+// of a SIMD waits at the slab barrier or on its fragment reads, the other
+// issues MFMAs), or 4 waves of 128 x 128 (one per SIMD; the fused
+// input-gradient epilogue needs its wave blocks and LDS budget).
+using CfgF32Big = Cfg<float, 256, 256, 32, 2, 4, 32, 1>;
+using CfgF32Big4 = Cfg<float, 256, 256, 32, 2, 2, 32, 1>;
 using CfgF32Small = Cfg<float, 128, 128, 32, 2, 2, 32, 2>;
 // Narrow outputs (N <= 64, e.g. a 64-wide layer): 4 waves stacked along M,
 // 64 x 64 each, so no wave computes padding columns.
@@ -740,8 +749,9 @@ struct CfgModel {
   int bm, bn, bk, blocks_per_cu;
   double eff;
 };
-constexpr CfgModel kModelF32[3] = {
-    {256, 256, 32, 1, 0.89}, {128, 128, 32, 2, 0.85}, {256, 64, 32, 1, 0.75}};
+constexpr CfgModel kModelF32[4] = {
+    {256, 256, 32, 1, 0.89}, {128, 128, 32, 2, 0.85}, {256, 64, 32, 1, 0.75},
+    {256, 256, 32, 1, 0.89}};
 constexpr CfgModel kModelF64 = {128, 128, 16, 1, 0.80};
 constexpr double kPeakPerCuF32 = 157.3e12 / 256.0;  // FP32 MFMA flop/s per CU
 constexpr double kPeakPerCuF64 = 78.6e12 / 256.0;
@@ -769,21 +779,24 @@ double est_seconds(const CfgModel& c, double peak_per_cu, int64_t M, int64_t N, 
   return t;
 }
 
-// Test override of the fp32 tile configuration: KAN_HIP_GEMM_TILE=256, 128
-// or 256x64 forces the big, the small or the narrow configuration (read at
-// every launch, so a test can switch it between calls); unset or any other
-// value leaves the choice to the cost model.
+// Test override of the fp32 tile configuration: KAN_HIP_GEMM_TILE=256, 128,
+// 256x64 or 256w4 forces the big, the small, the narrow or the 4-wave
+// 256x256 configuration (read at every launch, so a test can switch it
+// between calls); unset or any other value leaves the choice to the cost
+// model.
 int forced_cfg_f32() {
   const char* v = std::getenv("KAN_HIP_GEMM_TILE");
   if (v == nullptr) return -1;
   if (std::strcmp(v, "256") == 0) return 0;
   if (std::strcmp(v, "128") == 0) return 1;
   if (std::strcmp(v, "256x64") == 0) return 2;
+  if (std::strcmp(v, "256w4") == 0) return 3;
   return -1;
 }
 
-// fp32 configuration (0 = big, 1 = small, 2 = narrow) for a given split
-// count; the narrow one only where N fits its 64 columns.
+// fp32 configuration (0 = big, 1 = small, 2 = narrow, 3 = 4-wave big, only
+// when forced) for a given split count; the narrow one only where N fits its
+// 64 columns.
 int pick_cfg_f32(int64_t M, int64_t N, int64_t K, int splits) {
   const int forced = forced_cfg_f32();
   if (forced >= 0) return forced;
@@ -911,6 +924,7 @@ int launch_gemm(int layout, int64_t M, int64_t N, int64_t K, const T* A, int64_t
   if constexpr (std::is_same<T, float>::value) {
     const int cfg = pick_cfg_f32(M, N, K, splits < 1 ? 1 : splits);
     if (cfg == 0) rc = launch_layout<CfgF32Big>(layout, p, splits, st);
+    else if (cfg == 3) rc = launch_layout<CfgF32Big4>(layout, p, splits, st);
     else if (cfg == 2) rc = launch_layout<CfgF32Narrow>(layout, p, splits, st);
     else rc = launch_layout<CfgF32Small>(layout, p, splits, st);
   } else {
@@ -988,7 +1002,8 @@ template int launch_matmul<double>(int, int64_t, int64_t, int64_t, const double*
 bool gemm_dx_supported(int64_t M, int64_t N, int64_t K, int64_t I, int G, int k, bool has_base) {
   if (k < 1 || k > 3) return false;
   const int R = G + k, nk = G + 2 * k + 1;
-  if (pick_cfg_f32(M, N, K, 1) == 0) return dx_cfg_fits<CfgF32Big>(N, I, R, nk, has_base);
+  const int cfg = pick_cfg_f32(M, N, K, 1);
+  if (cfg == 0 || cfg == 3) return dx_cfg_fits<CfgF32Big4>(N, I, R, nk, has_base);
   return dx_cfg_fits<CfgF32Small>(N, I, R, nk, has_base);
 }
 
@@ -1025,7 +1040,8 @@ int launch_gemm_dx(int64_t M, int64_t N, int64_t K, const float* A, int64_t lda,
   int rc;
   {
     TimedLaunch timed(kClassContraction, st, 2.0 * (double)M * (double)N * (double)K);
-    if (pick_cfg_f32(M, N, K, 1) == 0) rc = launch_dx_cfg<CfgF32Big>(p, e, k, st);
+    const int cfg = pick_cfg_f32(M, N, K, 1);
+    if (cfg == 0 || cfg == 3) rc = launch_dx_cfg<CfgF32Big4>(p, e, k, st);
     else rc = launch_dx_cfg<CfgF32Small>(p, e, k, st);
     if (rc != KAN_OK) return rc;
     rc = check_launch("gemm_dx");
