@@ -37,19 +37,29 @@ def _edge_inputs(N, I, O, R, dtype, seed):
 # Output widths cover every (tiles per wave, sample-sharing waves) tiling of the
 # forward and parameter kernels (O = 3..33 -> 2x4, 64/70 -> 4x4, 200 -> 4x2,
 # 300 -> 4x1, >= 512 -> 8x1); (8192, 260, 20, 7) runs the input kernel with
-# several sample blocks per workgroup on weights staged once.
+# several sample blocks per workgroup on weights staged once.  The fused
+# backward's tilings (one chunk covering O): O <= 32 -> 2x4, 33..64 -> 4x4,
+# 65..128 -> 4x2 (100; output partials of 2 waves added per group of 2 tiles),
+# 129..256 -> 4x1 (200), 257..512 -> 8x1 (300, 512).
 SHAPES = [(37, 5, 3, 4), (300, 16, 40, 8), (1000, 9, 70, 13), (64, 3, 300, 68),
           (5000, 4, 6, 11), (77, 3, 5, 1), (513, 2, 33, 20), (129, 3, 17, 29), (70, 2, 9, 44),
           (200, 2, 1300, 11), (3000, 3, 600, 7), (2000, 3, 200, 11), (4097, 5, 64, 11),
-          (8192, 260, 20, 7)]
+          (8192, 260, 20, 7), (2100, 3, 512, 11), (700, 2, 300, 8), (1200, 3, 100, 3)]
 
 
 @pytest.mark.parametrize("shape", SHAPES)
 @pytest.mark.parametrize("dtype", [torch.float64, torch.float32])
 @pytest.mark.parametrize("base", [True, False])
-def test_edge_abs_mean_and_backward_match_oracle(C, shape, dtype, base):
+@pytest.mark.parametrize("route", ["auto", "separate"])
+def test_edge_abs_mean_and_backward_match_oracle(C, monkeypatch, shape, dtype, base, route):
+    """route "auto": fp32 layers with O <= 512 and R + 1 <= 16 take the fused
+    backward kernel (both gradient sides from one phi); "separate" forces the
+    parameter and input kernels (KAN_HIP_EDGE_FUSED=0)."""
     N, I, O, R = shape
-    print(f"edge {shape} {dtype} base={base}", flush=True)
+    if route == "separate" and dtype == torch.float64:
+        pytest.skip("the route applies to the fp32 MFMA kernels only")
+    monkeypatch.setenv("KAN_HIP_EDGE_FUSED", "0" if route == "separate" else "1")
+    print(f"edge {shape} {dtype} base={base} route={route}", flush=True)
     s, H, bw, W, ga = _edge_inputs(N, I, O, R, dtype, seed=N + O)
     empty = torch.empty(0, dtype=dtype, device="cuda")
     sd = s.cuda() if base else empty

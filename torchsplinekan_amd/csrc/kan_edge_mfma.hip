@@ -20,6 +20,9 @@
 // workgroups; each split writes its own partial slice, added in a fixed order
 // by the finalize kernels, so results are deterministic.
 
+#include <cstdlib>
+#include <cstring>
+
 #include "kan_common.h"
 
 namespace kan {
@@ -639,6 +642,262 @@ __global__ __launch_bounds__(kEdgeMfThreads) void edge_input_mfma_kernel(
   }
 }
 
+// Fused backward (both gradient sides of one layer): block (i, split), with
+// a tiling whose one output chunk covers every output (O <= 512), so that a
+// block owns whole samples.  Per 16-sample tile each wave computes phi (rows n, columns o) for
+// its kOT output tiles once and uses g = ga sign(phi) / n twice:
+//   params  dWc[o, c] += sum_n g[n, o] Hc[n, c]   (accumulator entries as the
+//           A operand, as in edge_param_mfma_kernel);
+//   inputs  dHc^T[c, n] += sum_o Wc[o, c] g[n, o] (g transposed through a
+//           per-wave LDS tile, then the B operand, as in
+//           edge_input_mfma_kernel).
+// 11 MFMAs per 16 x 16 (n, o) tile instead of the 14 of the two kernels (phi
+// is not recomputed), and the sample rows are read once.  Waves that split
+// the outputs (WO > 1) add their dHc partials through LDS in wave order once
+// per group of GP sample tiles; waves that split the samples (WS > 1) add
+// their dWc partials at the end, as in the parameter kernel.  Every wave runs
+// the same number of groups (tiles past a wave's range read as zeros and
+// contribute nothing), so the group barriers are reached by all.
+template <int OT, int WS>
+struct EdgeBwdLds {
+  typedef EdgeTiling<OT, WS> Tl;
+  static constexpr int kWO = Tl::kWO;
+  static constexpr int kGP = kWO > 1 ? 4 / WS : 2;  // sample tiles per group
+  static constexpr int kTS = 20;                    // transposed tile row stride
+  static constexpr int kTrans = 4 * OT * 16 * kTS;  // one tile per (wave, t)
+  static constexpr int kRedIn = kWO > 1 ? WS * kWO * kGP * 256 : 0;
+};
+
+__device__ __forceinline__ void edge_wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+template <int KS, int OT, int WS>
+__global__ __launch_bounds__(kEdgeMfThreads) void edge_bwd_mfma_kernel(
+    const float* __restrict__ ga, const float* __restrict__ s, const float* __restrict__ H,
+    const float* __restrict__ bw, const float* __restrict__ W, float* __restrict__ ds,
+    float* __restrict__ dH, float* __restrict__ dbw, float* __restrict__ dW,
+    float* __restrict__ part, EdgeGeom g, int final_out) {
+  static_assert(KS <= 4, "one column tile of 16 covers c");
+  typedef EdgeTiling<OT, WS> Tl;
+  typedef EdgeBwdLds<OT, WS> L;
+  constexpr int kOT = OT, kWO = Tl::kWO, GP = L::kGP, TS = L::kTS;
+  __shared__ __align__(16) float trans[L::kTrans];
+  __shared__ __align__(16) float red_in[L::kRedIn > 0 ? L::kRedIn : 4];
+  __shared__ float red[WS > 1 ? WS * Tl::kBlockOut * 16 : 1];
+  const int64_t bid = xcd_remap((int)blockIdx.x, (int)gridDim.x);
+  const int i = (int)(bid % g.I);
+  const int split = (int)(bid / g.I);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int wo = wave % kWO, wsi = wave / kWO;
+  const int q = lane >> 4, r = lane & 15;
+  const int obase = wo * kOT * 16;  // (waves past O keep zero weights and g)
+  const int R1 = g.R + 1;
+  const float inv_n = 1.0f / (float)g.n;
+
+  // phi's B operand Wc[o = obase + 16t + r, c = 4k + q]; the input product's
+  // A operand Wc[o = obase + 16t + 4q + v, c = r]; ga / n of columns o.
+  float w[kOT][KS], wb[kOT][4], gav[kOT];
+#pragma unroll
+  for (int t = 0; t < kOT; ++t) {
+    const int o = obase + t * 16 + r;
+    gav[t] = o < g.O ? ga[(int64_t)o * g.I + i] * inv_n : 0.0f;
+#pragma unroll
+    for (int k = 0; k < KS; ++k) {
+      const int c = 4 * k + q;
+      w[t][k] = (o < g.O && c < R1) ? wc_val(bw, W, o, g.I, i, g.R, c) : 0.0f;
+    }
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int ov = obase + t * 16 + 4 * q + v;
+      wb[t][v] = (ov < g.O && r < R1) ? wc_val(bw, W, ov, g.I, i, g.R, r) : 0.0f;
+    }
+  }
+  f32x4 dacc[kOT];
+#pragma unroll
+  for (int t = 0; t < kOT; ++t) dacc[t] = zero4();
+
+  const int64_t bnb = (int64_t)split * g.per_split;
+  const int64_t bne = min(g.n, bnb + g.per_split);
+  const int64_t per_wave =
+      WS > 1 ? round_up(ceil_div(g.per_split, (int64_t)WS), kEdgeRowQuant) : g.per_split;
+  const int64_t nb = bnb + (WS > 1 ? wsi * per_wave : 0);
+  const int64_t ne = min(bne, nb + per_wave);
+  // groups of GP tiles: the same count for every wave (that of wave 0)
+  const int64_t span0 = min(per_wave, bne - bnb);
+  const int64_t groups = span0 > 0 ? ceil_div(span0, (int64_t)(16 * GP)) : 0;
+
+  float an[2][KS], asn[2], hn[2][4], hsn[2][4];
+  const HcRows hr(s, H, g.I, g.R, i);
+  uint32_t oa[KS], ob[4], obs[4];
+#pragma unroll
+  for (int k = 0; k < KS; ++k) oa[k] = hr.off_h(r, 4 * k + q);
+  const uint32_t oas = hr.off_s(r, q);
+#pragma unroll
+  for (int v = 0; v < 4; ++v) {
+    ob[v] = hr.off_h(4 * q + v, r);
+    obs[v] = hr.off_s(4 * q + v, r);
+  }
+  auto load_tile = [&](int64_t n0, float (&da)[KS], float& das, float (&dh)[4], float (&dhs)[4]) {
+    const HcTile t = hr.tile(n0, ne);
+#pragma unroll
+    for (int k = 0; k < KS; ++k) da[k] = buf_ld(t.h, oa[k]);
+    das = buf_ld(t.s, oas);
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      dh[v] = buf_ld(t.h, ob[v]);
+      dhs[v] = buf_ld(t.s, obs[v]);
+    }
+  };
+  // dHc^T of one sample tile: lane (q, r) holds c = 4q + v, n = n0 + r;
+  // rows at or past lim (the end of the tile owner's sample range) are not
+  // written (they belong to another wave's range or lie past n)
+  auto write_din = [&](const f32x4& d, int64_t n0, int64_t lim) {
+    const int64_t nn = n0 + r;
+    if (nn >= lim) return;
+    const int64_t f = nn * g.I + i;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int c = 4 * q + v;
+      if (c >= R1) continue;
+      if (c == 0) {
+        if (ds != nullptr) ds[f] = d[v];
+      } else if (dH != nullptr) {
+        dH[f * g.R + (c - 1)] = d[v];
+      }
+    }
+  };
+  float* tb = trans + wave * (kOT * 16 * TS);
+
+  load_tile(nb, an[0], asn[0], hn[0], hsn[0]);
+  for (int64_t gi = 0; gi < groups; ++gi) {
+    const int64_t g0 = nb + gi * (16 * GP);
+    f32x4 din[GP];
+#pragma unroll
+    for (int j = 0; j < GP; ++j) {
+      const int p = j & 1;
+      __builtin_amdgcn_sched_barrier(0);
+      load_tile(g0 + 16 * j + 16, an[p ^ 1], asn[p ^ 1], hn[p ^ 1], hsn[p ^ 1]);
+      __builtin_amdgcn_sched_barrier(0);  // the loads go out before this tile's wait
+      float a[KS], hb[4];
+#pragma unroll
+      for (int k = 0; k < KS; ++k) a[k] = k == 0 ? hc_or(an[p][0], asn[p]) : an[p][k];
+#pragma unroll
+      for (int v = 0; v < 4; ++v) hb[v] = hc_or(hn[p][v], hsn[p][v]);
+      f32x4 acc[kOT];
+#pragma unroll
+      for (int t = 0; t < kOT; ++t) acc[t] = zero4();
+#pragma unroll
+      for (int k = 0; k < KS; ++k)
+#pragma unroll
+        for (int t = 0; t < kOT; ++t) acc[t] = mfma16(a[k], w[t][k], acc[t]);
+      float gv[kOT][4];
+#pragma unroll
+      for (int t = 0; t < kOT; ++t)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) gv[t][v] = g_sign(gav[t], acc[t][v]);
+      // g[n = 4q + v, o = 16t + r] -> tile t at [o][n] (one 16-byte store per lane)
+#pragma unroll
+      for (int t = 0; t < kOT; ++t) {
+        f32x4 gq;
+        gq[0] = gv[t][0];
+        gq[1] = gv[t][1];
+        gq[2] = gv[t][2];
+        gq[3] = gv[t][3];
+        *reinterpret_cast<f32x4*>(tb + t * 16 * TS + r * TS + 4 * q) = gq;
+      }
+#pragma unroll
+      for (int v = 0; v < 4; ++v)
+#pragma unroll
+        for (int t = 0; t < kOT; ++t) dacc[t] = mfma16(gv[t][v], hb[v], dacc[t]);
+      edge_wave_sync();
+      // g[n = r, o = 16t + 4q + v]
+      float gt[kOT][4];
+#pragma unroll
+      for (int t = 0; t < kOT; ++t)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) gt[t][v] = tb[t * 16 * TS + (4 * q + v) * TS + r];
+      edge_wave_sync();  // (the next tile's stores come after these reads)
+      f32x4 d0 = zero4(), d1 = zero4();
+#pragma unroll
+      for (int v = 0; v < 4; ++v)
+#pragma unroll
+        for (int t = 0; t < kOT; t += 2) {
+          d0 = mfma16(wb[t][v], gt[t][v], d0);
+          if (t + 1 < kOT) d1 = mfma16(wb[t + 1][v], gt[t + 1][v], d1);
+        }
+#pragma unroll
+      for (int v = 0; v < 4; ++v) din[j][v] = d0[v] + d1[v];
+    }
+    if constexpr (kWO == 1) {
+#pragma unroll
+      for (int j = 0; j < GP; ++j) write_din(din[j], g0 + 16 * j, ne);
+    } else {
+      // partials of the kWO output ranges, added in wave order: task
+      // wave -> (sample share ws2, tile j2); WS * GP = 4 tasks
+#pragma unroll
+      for (int j = 0; j < GP; ++j)
+        *reinterpret_cast<f32x4*>(red_in + (((wsi * kWO + wo) * GP + j) * 64 + lane) * 4) = din[j];
+      __syncthreads();
+      const int ws2 = wave / GP, j2 = wave % GP;
+      f32x4 d = *reinterpret_cast<const f32x4*>(red_in + (((ws2 * kWO) * GP + j2) * 64 + lane) * 4);
+#pragma unroll
+      for (int w2 = 1; w2 < kWO; ++w2) {
+        const f32x4 e =
+            *reinterpret_cast<const f32x4*>(red_in + (((ws2 * kWO + w2) * GP + j2) * 64 + lane) * 4);
+#pragma unroll
+        for (int v = 0; v < 4; ++v) d[v] += e[v];
+      }
+      const int64_t nb2 = bnb + (WS > 1 ? ws2 * per_wave : 0);
+      const int64_t ne2 = min(bne, nb2 + per_wave);
+      const int64_t n2 = nb2 + gi * (16 * GP) + 16 * j2;
+      write_din(d, n2, ne2);
+      __syncthreads();
+    }
+  }
+  if (WS > 1) {  // add the WS sample shares of dWc in wave order
+#pragma unroll
+    for (int t = 0; t < kOT; ++t)
+#pragma unroll
+      for (int v = 0; v < 4; ++v)
+        red[(wsi * Tl::kBlockOut + wo * kOT * 16 + t * 16 + 4 * q + v) * 16 + r] = dacc[t][v];
+    __syncthreads();
+    if (wsi != 0) return;
+#pragma unroll
+    for (int t = 0; t < kOT; ++t)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int row = wo * kOT * 16 + t * 16 + 4 * q + v;
+        float acc = red[row * 16 + r];
+        for (int w2 = 1; w2 < WS; ++w2) acc += red[(w2 * Tl::kBlockOut + row) * 16 + r];
+        dacc[t][v] = acc;
+      }
+  }
+  // dacc[t]: lane (q, r) holds column c = r, rows o = obase + 16t + 4q + v
+  if (r >= R1) return;
+#pragma unroll
+  for (int t = 0; t < kOT; ++t) {
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int o = obase + t * 16 + 4 * q + v;
+      if (o >= g.O) continue;
+      const int64_t e = (int64_t)o * g.I + i;
+      const float val = dacc[t][v];
+      if (final_out) {
+        if (r == 0) {
+          if (dbw != nullptr) dbw[e] = val;
+        } else if (dW != nullptr) {
+          dW[e * g.R + (r - 1)] = val;
+        }
+      } else {
+        part[((int64_t)split * g.O * g.I + e) * R1 + r] = val;
+      }
+    }
+  }
+}
+
 __global__ void edge_fwd_finalize_f32(const float* __restrict__ part, float* __restrict__ a,
                                       int splits, int64_t count, int64_t n) {
   for (int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; e < count;
@@ -688,7 +947,25 @@ inline int fin_blocks_f32(int64_t total) {
     else { constexpr int KS = 19, CT = 5; __VA_ARGS__; }        \
   } while (0)
 
+// k-steps KS = ceil((R+1)/4) for R + 1 <= 16 (one column tile of 16).
+#define KAN_EDGE_MF_DISPATCH4(R1, ...)                                  \
+  do {                                                                  \
+    const int ks_ = ((R1) + 3) / 4;                                     \
+    if (ks_ <= 1) { constexpr int KS = 1; __VA_ARGS__; }                \
+    else if (ks_ == 2) { constexpr int KS = 2; __VA_ARGS__; }           \
+    else if (ks_ == 3) { constexpr int KS = 3; __VA_ARGS__; }           \
+    else { constexpr int KS = 4; __VA_ARGS__; }                         \
+  } while (0)
+
 }  // namespace
+
+// Both gradient sides of a layer in one fused kernel where it applies (set
+// KAN_HIP_EDGE_FUSED=0 to take the separate parameter and input kernels; read
+// at every call, so a test can switch it between calls).
+bool edge_fused_enabled() {
+  const char* v = std::getenv("KAN_HIP_EDGE_FUSED");
+  return v == nullptr || std::strcmp(v, "0") != 0;
+}
 
 // (OT, WS) of the forward and parameter kernels for a layer width O; see
 // EdgeTiling.  Returns the block's output coverage.
@@ -774,7 +1051,44 @@ int launch_edge_backward_mfma(const float* ga, const float* s, const float* H, c
   g.per_split = round_up(ceil_div(n, splits), kEdgeRowQuant);
   int ot, ws;
   g.ochunks = (int)ceil_div(O, (int64_t)edge_tiling(O, &ot, &ws));
-  if ((dbw != nullptr || dW != nullptr) && O > 0 && I > 0) {
+  const bool need_p = (dbw != nullptr || dW != nullptr) && O > 0 && I > 0;
+  const bool need_x = (ds != nullptr || dH != nullptr) && n > 0 && I > 0 && O > 0;
+  if (need_p && need_x && O <= 512 && R1 <= 16 && edge_fused_enabled()) {
+    // the narrowest block tiling that covers every output (one chunk)
+    if (O <= 32) { ot = 2; ws = 4; }
+    else if (O <= 64) { ot = 4; ws = 4; }
+    else if (O <= 128) { ot = 4; ws = 2; }
+    else if (O <= 256) { ot = 4; ws = 1; }
+    else { ot = 8; ws = 1; }
+    g.ochunks = 1;
+    if (splits > 1 && part == nullptr)
+      return set_error(KAN_ERR_WORKSPACE, "edge_abs_mean_backward: missing workspace");
+    const int64_t blocks = I * (int64_t)splits;
+    if (blocks > 2147483647LL)
+      return set_error(KAN_ERR_LIMIT, "edge_abs_mean_backward: too many blocks");
+    const bool fin = splits == 1;
+    {
+      TimedLaunch timed(kClassEdgeGrad, st, 6.0 * (double)n * (double)O * (double)I * (double)R1);
+#define KAN_EDGE_BWD(OTV, WSV)                                                                  \
+  KAN_EDGE_MF_DISPATCH4(R1, hipLaunchKernelGGL((edge_bwd_mfma_kernel<KS, OTV, WSV>),            \
+                                                          dim3((unsigned)blocks),                \
+                                                          dim3(kEdgeMfThreads), 0, st, ga, s, H, \
+                                                          bw, W, ds, dH, dbw, dW, part, g,       \
+                                                          fin ? 1 : 0))
+      if (ot == 8) KAN_EDGE_BWD(8, 1);
+      else if (ws == 1) KAN_EDGE_BWD(4, 1);
+      else if (ws == 2) KAN_EDGE_BWD(4, 2);
+      else if (ot == 4) KAN_EDGE_BWD(4, 4);
+      else KAN_EDGE_BWD(2, 4);
+#undef KAN_EDGE_BWD
+      const int rc = check_launch("edge_abs_mean_backward(fused)");
+      if (rc != KAN_OK || fin) return rc;
+    }
+    hipLaunchKernelGGL(edge_param_finalize_f32, dim3(fin_blocks_f32(O * I * R1)), dim3(256), 0, st,
+                       part, dbw, dW, splits, O * I, (int)R);
+    return check_launch("edge_abs_mean_backward(finalize)");
+  }
+  if (need_p) {
     if (splits > 1 && part == nullptr)
       return set_error(KAN_ERR_WORKSPACE, "edge_abs_mean_backward: missing workspace");
     const int64_t blocks = I * g.ochunks * (int64_t)splits;
@@ -802,7 +1116,7 @@ int launch_edge_backward_mfma(const float* ga, const float* s, const float* H, c
       if (rc != KAN_OK) return rc;
     }
   }
-  if ((ds != nullptr || dH != nullptr) && n > 0 && I > 0 && O > 0) {
+  if (need_x) {
     constexpr int NTW = 4;
     const int64_t nblk = ceil_div(n, 64 * NTW);
     // staged output rows per chunk: a multiple of 16 that fits the LDS stage
