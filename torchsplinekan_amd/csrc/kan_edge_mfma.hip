@@ -662,7 +662,7 @@ template <int OT, int WS>
 struct EdgeBwdLds {
   typedef EdgeTiling<OT, WS> Tl;
   static constexpr int kWO = Tl::kWO;
-  static constexpr int kGP = kWO > 1 ? 4 / WS : 2;  // sample tiles per group
+  static constexpr int kGP = kWO > 1 ? 4 / WS : 4;  // sample tiles per group
   static constexpr int kTS = 20;                    // transposed tile row stride
   static constexpr int kTrans = 4 * OT * 16 * kTS;  // one tile per (wave, t)
   static constexpr int kRedIn = kWO > 1 ? WS * kWO * kGP * 256 : 0;
@@ -729,7 +729,11 @@ __global__ __launch_bounds__(kEdgeMfThreads) void edge_bwd_mfma_kernel(
   const int64_t span0 = min(per_wave, bne - bnb);
   const int64_t groups = span0 > 0 ? ceil_div(span0, (int64_t)(16 * GP)) : 0;
 
-  float an[2][KS], asn[2], hn[2][4], hsn[2][4];
+  // GP register slots of sample-tile operands, GP - 1 tiles ahead (the slot
+  // rotation of the forward kernel): tile j of a group uses slot j and first
+  // refills the slot tile j - 1 has just finished with.
+  constexpr int S = GP;
+  float an[S][KS], asn[S], hn[S][4], hsn[S][4];
   const HcRows hr(s, H, g.I, g.R, i);
   uint32_t oa[KS], ob[4], obs[4];
 #pragma unroll
@@ -771,15 +775,19 @@ __global__ __launch_bounds__(kEdgeMfThreads) void edge_bwd_mfma_kernel(
   };
   float* tb = trans + wave * (kOT * 16 * TS);
 
-  load_tile(nb, an[0], asn[0], hn[0], hsn[0]);
+#pragma unroll
+  for (int p = 0; p < S - 1; ++p) {
+    __builtin_amdgcn_sched_barrier(0);
+    load_tile(nb + 16 * p, an[p], asn[p], hn[p], hsn[p]);
+  }
   for (int64_t gi = 0; gi < groups; ++gi) {
     const int64_t g0 = nb + gi * (16 * GP);
     f32x4 din[GP];
 #pragma unroll
     for (int j = 0; j < GP; ++j) {
-      const int p = j & 1;
+      const int p = j, fill = (j + S - 1) % S;
       __builtin_amdgcn_sched_barrier(0);
-      load_tile(g0 + 16 * j + 16, an[p ^ 1], asn[p ^ 1], hn[p ^ 1], hsn[p ^ 1]);
+      load_tile(g0 + 16 * (j + S - 1), an[fill], asn[fill], hn[fill], hsn[fill]);
       __builtin_amdgcn_sched_barrier(0);  // the loads go out before this tile's wait
       float a[KS], hb[4];
 #pragma unroll
