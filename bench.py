@@ -184,10 +184,13 @@ def bench_c4(args):
         "data": "synthetic (Gaussian-mixture x, seeded; knots from update_grid)",
         "config": {"workload": "c4: KAN([256,512,512,64], G=8, k=3) fp32, N=%d, "
                                "forward_with_regularization(1e-2, 1e-2, 'auto') + MSE + backward" % N},
-        # dominant kernel class: the edge-statistic backward (parameter and
-        # input kernels, 4 n O I (R+1) flops each), on FP32 MFMA
+        # dominant kernel class: the edge-statistic backward on FP32 MFMA
+        # (fused kernel for layers that need both gradient sides: phi once
+        # plus two products, 6 n O I (R+1) flops; parameter kernel for the
+        # first layer, whose input needs no gradient: 4 n O I (R+1))
         "roofline": {"bound": "mfma",
-                     "kernel": "edge_param_mfma_kernel + edge_input_mfma_kernel (fused mean|phi| backward)",
+                     "kernel": "edge_bwd_mfma_kernel (both gradient sides) + edge_param_mfma_kernel "
+                               "(first layer): mean|phi| backward",
                      "achieved": ach_g, "peak": PEAK_FP32_MFMA_TFLOPS, "unit": "TFLOP/s",
                      "frac": ach_g / PEAK_FP32_MFMA_TFLOPS, "traffic": None,
                      "flop_per_launch": eg_work / max(eg_cnt, 1),
