@@ -198,6 +198,31 @@ int kan_hip_edge_abs_mean_backward(int dtype, const void* grad_a, const void* s,
                                    size_t workspace_bytes, int64_t n, int64_t in_features,
                                    int64_t out_features, int64_t num_basis, void* stream);
 
+/* Backward of one regularised layer's output and edge statistic together.
+ * The layer output y = s bw^T + H W^T (flattened over I and R) and the edge
+ * statistic a[o,i] = (1/n) sum_m |phi[m,o,i]| share their operands; with
+ * grad_y = dL/dy [n, O] and grad_a = dL/da [O, I] every gradient is one
+ * contraction of g'[m,o,i] = grad_a[o,i] sign(phi[m,o,i]) / n + grad_y[m,o]:
+ *   grad_s  = sum_o g' bw,   grad_H  = sum_o g' W      (any may be NULL)
+ *   grad_bw = sum_m g' s,    grad_W  = sum_m g' H.
+ * The reference takes these as the separate F.linear gradients plus
+ * EdgeAbsMean's backward, which autograd adds (spline_kan/kan_linear.py:
+ * 384-387, spline_kan/fused.py:73-102, csrc/kan_reg_cuda.cu:284-312); here
+ * they come from the fused edge kernel with grad_y added to g, with no
+ * separate products.  float32 only, for 0 < out_features <= 512 with
+ * out_features % 4 == 0, num_basis + 1 <= 16 and n > 0
+ * (kan_hip_edge_linear_supported returns 1 exactly then); grad_y 16-byte
+ * aligned.  Workspace: as kan_hip_edge_abs_mean_backward (kan_hip_edge_workspace
+ * with backward = 1). */
+int kan_hip_edge_linear_supported(int dtype, int64_t n, int64_t in_features,
+                                  int64_t out_features, int64_t num_basis);
+int kan_hip_edge_linear_backward(int dtype, const void* grad_a, const void* grad_y, const void* s,
+                                 const void* basis, const void* base_weight, const void* weight,
+                                 void* grad_s, void* grad_basis, void* grad_base_weight,
+                                 void* grad_weight, void* workspace, size_t workspace_bytes,
+                                 int64_t n, int64_t in_features, int64_t out_features,
+                                 int64_t num_basis, void* stream);
+
 /* Double backward of the edge statistic, used when the regulariser's
  * backward is itself recorded (create_graph=True).  With the sign pattern
  * S = sign(phi) of the forward operands held fixed (its derivative is zero

@@ -134,3 +134,108 @@ def test_forward_with_regularization_fused_matches_dense(C, dtype):
     for impl in ("dense", "checkpoint"):
         for a, b in zip(res["fused"], res[impl]):
             assert normwise(np64(a), np64(b)) < tol
+
+
+# (N, I, O, R): every tiling of the folded backward (O = 4 -> 2x4, 64 -> 4x4,
+# 100 -> 4x2, 200 -> 4x1, 300 and 512 -> 8x1), ragged sample counts, sample
+# splits across blocks (4097, 6000) and R + 1 at 5, 12 and 16.
+LINEAR_SHAPES = [(37, 5, 4, 4), (300, 7, 64, 11), (1000, 9, 100, 15), (513, 3, 200, 11),
+                 (700, 2, 300, 8), (4097, 5, 512, 11), (6000, 3, 64, 11)]
+
+
+@pytest.mark.parametrize("shape", LINEAR_SHAPES)
+def test_edge_linear_backward_matches_oracle(C, shape):
+    """kan_hip_edge_linear_backward: the gradients of a layer's output
+    y = s bw^T + H W^T and of its edge statistic together (grad_y folded into
+    the edge kernel's g) against the oracle's edge backward plus the linear
+    layer's products in float64."""
+    N, I, O, R = shape
+    print(f"edge linear {shape}", flush=True)
+    s, H, bw, W, ga = _edge_inputs(N, I, O, R, torch.float32, seed=N + 7 * O)
+    gy = torch.randn(N, O, generator=torch.Generator().manual_seed(O), dtype=torch.float64).float()
+    assert C.edge_linear_supported(H.cuda(), W.cuda())
+    ds, dH, dbw, dW = C.edge_linear_backward(ga.cuda(), gy.cuda(), s.cuda(), H.cuda(), bw.cuda(),
+                                             W.cuda(), True, True, True, True)
+    rds, rdH, rdbw, rdW = ko.edge_abs_mean_backward(np64(ga), np64(s), np64(H), np64(bw), np64(W))
+    D = np64(gy)
+    rds = rds + D @ np64(bw)
+    rdH = rdH + (D @ np64(W).reshape(O, I * R)).reshape(N, I, R)
+    rdbw = rdbw + D.T @ np64(s)
+    rdW = rdW + (D.T @ np64(H).reshape(N, I * R)).reshape(O, I, R)
+    for name, got, ref in (("ds", ds, rds), ("dH", dH, rdH), ("dbw", dbw, rdbw), ("dW", dW, rdW)):
+        assert normwise(np64(got), ref) < 1e-4, name
+    # a partial request leaves the other outputs unwritten and the rest equal
+    ds2, dH2, dbw2, dW2 = C.edge_linear_backward(ga.cuda(), gy.cuda(), s.cuda(), H.cuda(),
+                                                 bw.cuda(), W.cuda(), False, True, False, True)
+    assert ds2 is None and dbw2 is None
+    assert torch.equal(dH2, dH) and torch.equal(dW2, dW)
+
+
+def test_edge_linear_supported_range(C):
+    mk = lambda N, I, O, R, dt=torch.float32: (torch.empty(N, I, R, dtype=dt, device="cuda"),
+                                               torch.empty(O, I, R, dtype=dt, device="cuda"))
+    assert C.edge_linear_supported(*mk(10, 3, 512, 15))
+    assert not C.edge_linear_supported(*mk(10, 3, 516, 11))   # O > 512
+    assert not C.edge_linear_supported(*mk(10, 3, 70, 11))    # O % 4 != 0
+    assert not C.edge_linear_supported(*mk(10, 3, 64, 16))    # R + 1 > 16
+    assert not C.edge_linear_supported(*mk(10, 3, 64, 11, torch.float64))
+
+
+def _reg_grads(net, x, impl, create_graph=False):
+    for p in net.parameters():
+        p.grad = None
+    y, r = net.forward_with_regularization(x, 1e-2, 1e-2, reg_impl=impl, chunk_size=256)
+    loss = y.square().mean() + r
+    if not create_graph:
+        loss.backward()
+        return [y.detach(), r.detach()] + [p.grad for p in net.parameters()] + \
+               ([x.grad] if x.requires_grad else [])
+    params = list(net.parameters())
+    gs = torch.autograd.grad(loss, params, create_graph=True)
+    second = torch.autograd.grad(sum((g * g).sum() for g in gs), params)
+    return list(gs) + list(second)
+
+
+@pytest.mark.parametrize("x_grad", [True, False])
+def test_regularized_layers_folded_backward_match_dense(C, monkeypatch, x_grad):
+    """KAN([16, 64, 100, 12]) fp32: every layer's output and edge statistic go
+    through EdgeLinear (the 12-wide layer too: 12 % 4 == 0); with x requiring
+    grad the first layer takes the folded kernel as well, without it the
+    weight-only branch.
+    * Gradients against the unfolded native path (separate output products
+      and edge backward, summed by autograd): the same kernels form phi, so
+      the sign patterns agree and only summation order differs: 1e-5.
+    * Output and regulariser against the dense path: 1e-5.  (Gradients of
+      the native and the dense path differ by sign flips of phi at rounding
+      level, up to 4e-4 normwise on dbw at these sizes, with or without the
+      fold; their agreement at the reference's shapes and tolerance is
+      test_forward_with_regularization_fused_matches_dense.)"""
+    from torchsplinekan_amd import KAN
+    from torchsplinekan_amd import fused as fz
+    torch.manual_seed(1)
+    net = KAN([16, 64, 100, 12], grid_size=7, backend="cuda").to("cuda")
+    x = torch.rand(3000, 16, device="cuda") * 2.2 - 1.1
+    res = {}
+    for impl in ("fused", "dense"):
+        xx = x.clone().requires_grad_(x_grad)
+        res[impl] = _reg_grads(net, xx, impl)
+    monkeypatch.setattr(fz, "edge_linear_applies", lambda *a: False)
+    res["unfolded"] = _reg_grads(net, x.clone().requires_grad_(x_grad), "fused")
+    for a, b in zip(res["fused"], res["unfolded"]):
+        assert normwise(np64(a), np64(b)) < 1e-5
+    for a, b in zip(res["fused"][:2], res["dense"][:2]):
+        assert normwise(np64(a), np64(b)) < 1e-5
+
+
+def test_regularized_layers_folded_backward_recorded(C):
+    """create_graph through EdgeLinear (its recorded branch: the separate
+    differentiable pieces): first and second derivatives with respect to the
+    parameters against the dense path."""
+    from torchsplinekan_amd import KAN
+    torch.manual_seed(2)
+    net = KAN([6, 8, 4], grid_size=5, backend="cuda").to("cuda")
+    x = torch.rand(400, 6, device="cuda") * 2.2 - 1.1
+    f = _reg_grads(net, x.clone().requires_grad_(), "fused", create_graph=True)
+    d = _reg_grads(net, x.clone().requires_grad_(), "dense", create_graph=True)
+    for a, b in zip(f, d):
+        assert normwise(np64(a), np64(b)) < 1e-4

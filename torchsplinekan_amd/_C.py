@@ -596,6 +596,55 @@ def edge_abs_mean_backward(grad_a, s, H, base_weight, W, need_s: bool, need_H: b
     return ds, dH, dbw, dW
 
 
+def edge_linear_supported(H: torch.Tensor, W: torch.Tensor) -> bool:
+    """True where edge_linear_backward applies to these operands (float32,
+    0 < out_features <= 512 with out_features % 4 == 0, num_basis + 1 <= 16,
+    at least one sample)."""
+    if not (H.is_cuda and H.dim() == 3 and W.dim() == 3):
+        return False
+    N, I, R = H.shape
+    return bool(LIB.kan_hip_edge_linear_supported(dtype_code(H.dtype) if H.dtype in _F else -1,
+                                                  N, I, W.shape[0], R))
+
+
+def edge_linear_backward(grad_a, grad_y, s, H, base_weight, W, need_s: bool, need_H: bool,
+                         need_bw: bool, need_W: bool):
+    """Gradients of one regularised layer's output y = s bw^T + H W^T and its
+    edge statistic a together: with g' = grad_a sign(phi) / n + grad_y,
+    (ds, dH, dbw, dW) = (sum_o g' bw, sum_o g' W, sum_n g' s, sum_n g' H), each
+    None where not requested (device, float32; see edge_linear_supported)."""
+    hb = _cmp.has_base(base_weight)
+    _check_edge_inputs(s, H, base_weight, W, hb)
+    _req(edge_linear_supported(H, W), "edge_linear_backward: configuration not supported")
+    N, I, R = H.shape
+    O = W.shape[0]
+    _req(tuple(grad_a.shape) == (O, I), "edge_linear_backward: grad_a shape")
+    _req(tuple(grad_y.shape) == (N, O), "edge_linear_backward: grad_y shape")
+    H, W = H.contiguous(), W.contiguous()
+    ga = grad_a.contiguous().to(W.dtype)
+    gy = grad_y.contiguous().to(W.dtype)
+    if gy.data_ptr() % 16 != 0:
+        gy = gy.clone()
+    sc = s.contiguous() if hb else None
+    bw = base_weight.contiguous() if hb else None
+    opts = dict(dtype=H.dtype, device=H.device)
+    ds = torch.empty(N, I, **opts) if (need_s and hb) else None
+    dH = torch.empty(N, I, R, **opts) if need_H else None
+    dbw = torch.empty(O, I, **opts) if (need_bw and hb) else None
+    dW = torch.empty(O, I, R, **opts) if need_W else None
+    if ds is None and dH is None and dbw is None and dW is None:
+        return ds, dH, dbw, dW
+    code = dtype_code(H.dtype)
+    nbytes = _lib.ctypes.c_size_t(0)
+    with torch.cuda.device(H.device):
+        check(LIB.kan_hip_edge_workspace(code, N, I, O, R, 1, _lib.ctypes.byref(nbytes)))
+        ws = torch.empty(max(int(nbytes.value), 1), dtype=torch.uint8, device=H.device)
+        check(LIB.kan_hip_edge_linear_backward(
+            code, ptr(ga), ptr(gy), ptr(sc), ptr(H), ptr(bw), ptr(W), ptr(ds), ptr(dH), ptr(dbw),
+            ptr(dW), ptr(ws), int(nbytes.value), N, I, O, R, stream_of(H.device)))
+    return ds, dH, dbw, dW
+
+
 def edge_abs_mean_double_backward(grad_a, s, H, base_weight, W, u_ds, u_dH, u_dbw, u_dW,
                                   need_ga: bool, need_s: bool, need_H: bool, need_bw: bool,
                                   need_W: bool):

@@ -62,6 +62,9 @@ SIGNATURES = {
                                      _i64, _i64, _i64, _i64, _vp]),
     "kan_hip_edge_abs_mean_backward": (_int, [_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                                               _vp, _sz, _i64, _i64, _i64, _i64, _vp]),
+    "kan_hip_edge_linear_supported": (_int, [_int, _i64, _i64, _i64, _i64]),
+    "kan_hip_edge_linear_backward": (_int, [_int] + [_vp] * 11 + [_sz, _i64, _i64, _i64, _i64,
+                                                                _vp]),
     "kan_hip_refit_gram": (_int, [_int, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64,
                                   _vp]),
     "kan_hip_timing_enable": (_int, [_int]),

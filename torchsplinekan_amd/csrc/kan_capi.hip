@@ -720,6 +720,33 @@ int kan_hip_edge_abs_mean_backward(int dtype, const void* ga, const void* s, con
       static_cast<double*>(ws), splits, n, I, O, R, st);
 }
 
+int kan_hip_edge_linear_supported(int dtype, int64_t n, int64_t I, int64_t O, int64_t R) {
+  return dtype == KAN_DTYPE_F32 && edge_linear_fold_supported(n, I, O, R) ? 1 : 0;
+}
+
+int kan_hip_edge_linear_backward(int dtype, const void* ga, const void* gy, const void* s,
+                                 const void* H, const void* bw, const void* W, void* gs, void* gH,
+                                 void* gbw, void* gW, void* ws, size_t ws_bytes, int64_t n,
+                                 int64_t I, int64_t O, int64_t R, void* stream) {
+  KAN_TRY(check_edge("edge_linear_backward", dtype, s, H, bw, W, n, I, O, R));
+  KAN_TRY(need_ptr(ga, "edge_linear_backward", "grad_a"));
+  KAN_TRY(need_ptr(gy, "edge_linear_backward", "grad_y"));
+  if ((gs != nullptr || gbw != nullptr) && bw == nullptr)
+    return set_error(KAN_ERR_INVALID, "edge_linear_backward: base gradients requested without a base branch");
+  if (!kan_hip_edge_linear_supported(dtype, n, I, O, R))
+    return set_error(KAN_ERR_LIMIT, "edge_linear_backward: needs float32, n > 0, out_features <= 512 and a multiple of 4, num_basis + 1 <= 16");
+  const size_t need = edge_ws_bytes(dtype, n, I, O, R, true);
+  if (ws_bytes < need || (need > 0 && ws == nullptr))
+    return set_error(KAN_ERR_WORKSPACE, "edge_linear_backward: workspace of %zu bytes is smaller than the %zu required", ws_bytes, need);
+  const int splits = edge_pick_splits(dtype, n, I, O, R, true);
+  return launch_edge_linear_backward_mfma(
+      static_cast<const float*>(ga), static_cast<const float*>(gy), static_cast<const float*>(s),
+      static_cast<const float*>(H), static_cast<const float*>(bw), static_cast<const float*>(W),
+      static_cast<float*>(gs), static_cast<float*>(gH), static_cast<float*>(gbw),
+      static_cast<float*>(gW), static_cast<float*>(ws), splits, n, I, O, R,
+      static_cast<hipStream_t>(stream));
+}
+
 int kan_hip_edge_abs_mean_double_backward_workspace(int dtype, int64_t n, int64_t I, int64_t O,
                                                     int64_t R, size_t* bytes) {
   KAN_TRY(check_dtype(dtype, "edge_abs_mean_double_backward_workspace"));

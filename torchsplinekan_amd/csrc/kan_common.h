@@ -219,5 +219,12 @@ int launch_edge_backward_mfma(const float* ga, const float* s, const float* H, c
                               const float* W, float* ds, float* dH, float* dbw, float* dW,
                               float* part, int splits, int64_t n, int64_t I, int64_t O, int64_t R,
                               hipStream_t st);
+// Backward of a layer's output y = s bw^T + <H, W> and its edge statistic
+// together (D = dL/dy folded into g); see edge_linear_fold_supported.
+bool edge_linear_fold_supported(int64_t n, int64_t I, int64_t O, int64_t R);
+int launch_edge_linear_backward_mfma(const float* ga, const float* D, const float* s,
+                                     const float* H, const float* bw, const float* W, float* ds,
+                                     float* dH, float* dbw, float* dW, float* part, int splits,
+                                     int64_t n, int64_t I, int64_t O, int64_t R, hipStream_t st);
 
 }  // namespace kan

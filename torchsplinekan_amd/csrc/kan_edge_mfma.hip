@@ -674,12 +674,12 @@ __device__ __forceinline__ void edge_wave_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-template <int KS, int OT, int WS>
+template <int KS, int OT, int WS, bool HASD>
 __global__ __launch_bounds__(kEdgeMfThreads) void edge_bwd_mfma_kernel(
-    const float* __restrict__ ga, const float* __restrict__ s, const float* __restrict__ H,
-    const float* __restrict__ bw, const float* __restrict__ W, float* __restrict__ ds,
-    float* __restrict__ dH, float* __restrict__ dbw, float* __restrict__ dW,
-    float* __restrict__ part, EdgeGeom g, int final_out) {
+    const float* __restrict__ ga, const float* __restrict__ D, const float* __restrict__ s,
+    const float* __restrict__ H, const float* __restrict__ bw, const float* __restrict__ W,
+    float* __restrict__ ds, float* __restrict__ dH, float* __restrict__ dbw,
+    float* __restrict__ dW, float* __restrict__ part, EdgeGeom g, int final_out) {
   static_assert(KS <= 4, "one column tile of 16 covers c");
   typedef EdgeTiling<OT, WS> Tl;
   typedef EdgeBwdLds<OT, WS> L;
@@ -729,10 +729,12 @@ __global__ __launch_bounds__(kEdgeMfThreads) void edge_bwd_mfma_kernel(
   const int64_t span0 = min(per_wave, bne - bnb);
   const int64_t groups = span0 > 0 ? ceil_div(span0, (int64_t)(16 * GP)) : 0;
 
-  // GP register slots of sample-tile operands, GP - 1 tiles ahead (the slot
-  // rotation of the forward kernel): tile j of a group uses slot j and first
-  // refills the slot tile j - 1 has just finished with.
-  constexpr int S = GP;
+  // S register slots of sample-tile operands, S - 1 tiles ahead (the slot
+  // rotation of the forward kernel): tile j of a group uses slot j % S and
+  // first refills the slot tile j - 1 has just finished with.  With the
+  // layer-output gradient (HASD) two slots, to leave registers for its rows.
+  constexpr int S = HASD ? 2 : GP;
+  static_assert(GP % S == 0, "slots divide the group");
   float an[S][KS], asn[S], hn[S][4], hsn[S][4];
   const HcRows hr(s, H, g.I, g.R, i);
   uint32_t oa[KS], ob[4], obs[4];
@@ -785,7 +787,7 @@ __global__ __launch_bounds__(kEdgeMfThreads) void edge_bwd_mfma_kernel(
     f32x4 din[GP];
 #pragma unroll
     for (int j = 0; j < GP; ++j) {
-      const int p = j, fill = (j + S - 1) % S;
+      const int p = j % S, fill = (j + S - 1) % S;
       __builtin_amdgcn_sched_barrier(0);
       load_tile(g0 + 16 * (j + S - 1), an[fill], asn[fill], hn[fill], hsn[fill]);
       __builtin_amdgcn_sched_barrier(0);  // the loads go out before this tile's wait
@@ -794,6 +796,22 @@ __global__ __launch_bounds__(kEdgeMfThreads) void edge_bwd_mfma_kernel(
       for (int k = 0; k < KS; ++k) a[k] = k == 0 ? hc_or(an[p][0], asn[p]) : an[p][k];
 #pragma unroll
       for (int v = 0; v < 4; ++v) hb[v] = hc_or(hn[p][v], hsn[p][v]);
+      // layer-output gradient D[n0 + r, obase + 16t + 4q .. + 3] (rows past
+      // the range and columns past O read as zeros), issued before phi
+      f32x4 dq[HASD ? kOT : 1];
+      if constexpr (HASD) {
+        const int64_t nt = g0 + 16 * j;
+        const __amdgpu_buffer_rsrc_t rd = tile_rsrc(D + nt * g.O, ne - nt, g.O);
+#pragma unroll
+        for (int t = 0; t < kOT; ++t) {
+          const int oc = obase + t * 16 + 4 * q;
+          const uint32_t off = oc < g.O ? (uint32_t)((r * g.O + oc) * 4) : kBufOob;
+          typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+          const u32x4 u = __builtin_amdgcn_raw_buffer_load_b128(rd, (int)off, 0, 0);
+#pragma unroll
+          for (int v = 0; v < 4; ++v) dq[t][v] = __uint_as_float(u[v]);
+        }
+      }
       f32x4 acc[kOT];
 #pragma unroll
       for (int t = 0; t < kOT; ++t) acc[t] = zero4();
@@ -806,6 +824,20 @@ __global__ __launch_bounds__(kEdgeMfThreads) void edge_bwd_mfma_kernel(
       for (int t = 0; t < kOT; ++t)
 #pragma unroll
         for (int v = 0; v < 4; ++v) gv[t][v] = g_sign(gav[t], acc[t][v]);
+      if constexpr (HASD) {
+        // D rows [n][o] through the same LDS tiles, read back as
+        // D[n = 4q + v, o = 16t + r] (the accumulator layout of g), added to g:
+        // both products then carry the layer output's gradient as well
+#pragma unroll
+        for (int t = 0; t < kOT; ++t)
+          *reinterpret_cast<f32x4*>(tb + t * 16 * TS + r * TS + 4 * q) = dq[t];
+        edge_wave_sync();
+#pragma unroll
+        for (int t = 0; t < kOT; ++t)
+#pragma unroll
+          for (int v = 0; v < 4; ++v) gv[t][v] += tb[t * 16 * TS + (4 * q + v) * TS + r];
+        edge_wave_sync();  // (g's stores below come after these reads)
+      }
       // g[n = 4q + v, o = 16t + r] -> tile t at [o][n] (one 16-byte store per lane)
 #pragma unroll
       for (int t = 0; t < kOT; ++t) {
@@ -1045,6 +1077,79 @@ int launch_edge_forward_mfma(const float* s, const float* H, const float* bw, co
   return check_launch("edge_abs_mean_finalize");
 }
 
+// The fused backward (both gradient sides; with D also the layer output's
+// gradient) for O <= 512 and R + 1 <= 16.
+int launch_edge_fused(const float* ga, const float* D, const float* s, const float* H,
+                      const float* bw, const float* W, float* ds, float* dH, float* dbw,
+                      float* dW, float* part, int splits, int64_t n, int64_t I, int64_t O,
+                      int64_t R, hipStream_t st) {
+  const int R1 = (int)R + 1;
+  EdgeGeom g;
+  g.n = n;
+  g.I = (int)I;
+  g.O = (int)O;
+  g.R = (int)R;
+  g.splits = splits;
+  g.per_split = round_up(ceil_div(n, splits), kEdgeRowQuant);
+  g.ochunks = 1;
+  // the narrowest block tiling that covers every output (one chunk)
+  int ot, ws;
+  if (O <= 32) { ot = 2; ws = 4; }
+  else if (O <= 64) { ot = 4; ws = 4; }
+  else if (O <= 128) { ot = 4; ws = 2; }
+  else if (O <= 256) { ot = 4; ws = 1; }
+  else { ot = 8; ws = 1; }
+  if (splits > 1 && part == nullptr)
+    return set_error(KAN_ERR_WORKSPACE, "edge_abs_mean_backward: missing workspace");
+  const int64_t blocks = I * (int64_t)splits;
+  if (blocks > 2147483647LL)
+    return set_error(KAN_ERR_LIMIT, "edge_abs_mean_backward: too many blocks");
+  const bool fin = splits == 1;
+  {
+    TimedLaunch timed(kClassEdgeGrad, st, 6.0 * (double)n * (double)O * (double)I * (double)R1);
+#define KAN_EDGE_BWD(OTV, WSV, HD)                                                             \
+  KAN_EDGE_MF_DISPATCH4(R1, hipLaunchKernelGGL((edge_bwd_mfma_kernel<KS, OTV, WSV, HD>),       \
+                                               dim3((unsigned)blocks), dim3(kEdgeMfThreads), 0, \
+                                               st, ga, D, s, H, bw, W, ds, dH, dbw, dW, part, g, \
+                                               fin ? 1 : 0))
+#define KAN_EDGE_BWD_T(HD)                    \
+  if (ot == 8) KAN_EDGE_BWD(8, 1, HD);        \
+  else if (ws == 1) KAN_EDGE_BWD(4, 1, HD);   \
+  else if (ws == 2) KAN_EDGE_BWD(4, 2, HD);   \
+  else if (ot == 4) KAN_EDGE_BWD(4, 4, HD);   \
+  else KAN_EDGE_BWD(2, 4, HD)
+    if (D != nullptr) {
+      KAN_EDGE_BWD_T(true);
+    } else {
+      KAN_EDGE_BWD_T(false);
+    }
+#undef KAN_EDGE_BWD_T
+#undef KAN_EDGE_BWD
+    const int rc = check_launch("edge_abs_mean_backward(fused)");
+    if (rc != KAN_OK || fin) return rc;
+  }
+  hipLaunchKernelGGL(edge_param_finalize_f32, dim3(fin_blocks_f32(O * I * R1)), dim3(256), 0, st,
+                     part, dbw, dW, splits, O * I, (int)R);
+  return check_launch("edge_abs_mean_backward(finalize)");
+}
+
+bool edge_linear_fold_supported(int64_t n, int64_t I, int64_t O, int64_t R) {
+  return n > 0 && I > 0 && O > 0 && O <= 512 && O % 4 == 0 && R + 1 <= 16;
+}
+
+int launch_edge_linear_backward_mfma(const float* ga, const float* D, const float* s,
+                                     const float* H, const float* bw, const float* W, float* ds,
+                                     float* dH, float* dbw, float* dW, float* part, int splits,
+                                     int64_t n, int64_t I, int64_t O, int64_t R, hipStream_t st) {
+  if (!edge_linear_fold_supported(n, I, O, R))
+    return set_error(KAN_ERR_LIMIT,
+                     "edge_linear_backward: needs 0 < out_features <= 512, out_features %% 4 == 0, "
+                     "num_basis + 1 <= 16 and n > 0");
+  if ((reinterpret_cast<uintptr_t>(D) & 15) != 0)
+    return set_error(KAN_ERR_INVALID, "edge_linear_backward: grad_y must be 16-byte aligned");
+  return launch_edge_fused(ga, D, s, H, bw, W, ds, dH, dbw, dW, part, splits, n, I, O, R, st);
+}
+
 int launch_edge_backward_mfma(const float* ga, const float* s, const float* H, const float* bw,
                               const float* W, float* ds, float* dH, float* dbw, float* dW,
                               float* part, int splits, int64_t n, int64_t I, int64_t O, int64_t R,
@@ -1061,41 +1166,9 @@ int launch_edge_backward_mfma(const float* ga, const float* s, const float* H, c
   g.ochunks = (int)ceil_div(O, (int64_t)edge_tiling(O, &ot, &ws));
   const bool need_p = (dbw != nullptr || dW != nullptr) && O > 0 && I > 0;
   const bool need_x = (ds != nullptr || dH != nullptr) && n > 0 && I > 0 && O > 0;
-  if (need_p && need_x && O <= 512 && R1 <= 16 && edge_fused_enabled()) {
-    // the narrowest block tiling that covers every output (one chunk)
-    if (O <= 32) { ot = 2; ws = 4; }
-    else if (O <= 64) { ot = 4; ws = 4; }
-    else if (O <= 128) { ot = 4; ws = 2; }
-    else if (O <= 256) { ot = 4; ws = 1; }
-    else { ot = 8; ws = 1; }
-    g.ochunks = 1;
-    if (splits > 1 && part == nullptr)
-      return set_error(KAN_ERR_WORKSPACE, "edge_abs_mean_backward: missing workspace");
-    const int64_t blocks = I * (int64_t)splits;
-    if (blocks > 2147483647LL)
-      return set_error(KAN_ERR_LIMIT, "edge_abs_mean_backward: too many blocks");
-    const bool fin = splits == 1;
-    {
-      TimedLaunch timed(kClassEdgeGrad, st, 6.0 * (double)n * (double)O * (double)I * (double)R1);
-#define KAN_EDGE_BWD(OTV, WSV)                                                                  \
-  KAN_EDGE_MF_DISPATCH4(R1, hipLaunchKernelGGL((edge_bwd_mfma_kernel<KS, OTV, WSV>),            \
-                                                          dim3((unsigned)blocks),                \
-                                                          dim3(kEdgeMfThreads), 0, st, ga, s, H, \
-                                                          bw, W, ds, dH, dbw, dW, part, g,       \
-                                                          fin ? 1 : 0))
-      if (ot == 8) KAN_EDGE_BWD(8, 1);
-      else if (ws == 1) KAN_EDGE_BWD(4, 1);
-      else if (ws == 2) KAN_EDGE_BWD(4, 2);
-      else if (ot == 4) KAN_EDGE_BWD(4, 4);
-      else KAN_EDGE_BWD(2, 4);
-#undef KAN_EDGE_BWD
-      const int rc = check_launch("edge_abs_mean_backward(fused)");
-      if (rc != KAN_OK || fin) return rc;
-    }
-    hipLaunchKernelGGL(edge_param_finalize_f32, dim3(fin_blocks_f32(O * I * R1)), dim3(256), 0, st,
-                       part, dbw, dW, splits, O * I, (int)R);
-    return check_launch("edge_abs_mean_backward(finalize)");
-  }
+  if (need_p && need_x && O <= 512 && R1 <= 16 && edge_fused_enabled())
+    return launch_edge_fused(ga, nullptr, s, H, bw, W, ds, dH, dbw, dW, part, splits, n, I, O, R,
+                             st);
   if (need_p) {
     if (splits > 1 && part == nullptr)
       return set_error(KAN_ERR_WORKSPACE, "edge_abs_mean_backward: missing workspace");

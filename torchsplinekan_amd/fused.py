@@ -96,6 +96,75 @@ class EdgeAbsMean(torch.autograd.Function):
                 dbw if need_bw and has_base else None, dW if need_W else None)
 
 
+class EdgeLinear(torch.autograd.Function):
+    """(y, a) of one regularised layer from the same operands:
+    y = s bw^T + H W^T (flattened over I and R) and a = mean_n |phi|.
+    The reference builds them separately (two F.linear calls and EdgeAbsMean,
+    spline_kan/kan_linear.py:384-387), so autograd runs the linear layer's
+    gradient products, the edge statistic's backward and the sums of the two.
+    Every one of those gradients is a contraction of
+    g' = ga sign(phi) / n + dL/dy, so here a single native launch
+    (_C.edge_linear_backward: dL/dy added to g inside the fused edge kernel)
+    returns all four.  Recorded backwards (create_graph) use the separate
+    differentiable pieces; a backward that needs only the weight gradients
+    uses the parameter kernel plus two products."""
+
+    @staticmethod
+    def forward(ctx, s, H, bw, W):
+        B, I, R = H.shape
+        O = W.shape[0]
+        y = _C.matmul(s, bw.t()) + _C.matmul(H.reshape(B, I * R), W.reshape(O, I * R).t())
+        a = _C.edge_abs_mean(s, H, bw, W)
+        ctx.save_for_backward(s, H, bw, W)
+        return y, a
+
+    @staticmethod
+    def backward(ctx, gy, ga):
+        s, H, bw, W = ctx.saved_tensors
+        need_s, need_H, need_bw, need_W = ctx.needs_input_grad
+        B, I, R = H.shape
+        O = W.shape[0]
+        if gy is None:
+            gy = H.new_zeros(B, O)
+        if ga is None:
+            ga = H.new_zeros(O, I)
+        H2, W2 = H.reshape(B, I * R), W.reshape(O, I * R)
+        if torch.is_grad_enabled():
+            # recorded backward: differentiable native pieces (as the
+            # separate F.linear + EdgeAbsMean path records them)
+            mm = _C.NativeMatmul.apply
+            ds, dH, dbw, dW = _C.EdgeAbsMeanBackward.apply(ga, s, H, bw, W)
+            ds = ds + mm(gy, bw) if need_s else None
+            dH = dH + mm(gy, W2).reshape(B, I, R) if need_H else None
+            dbw = dbw + mm(gy.t(), s) if need_bw else None
+            dW = dW + mm(gy.t(), H2).reshape(O, I, R) if need_W else None
+            return ds, dH, dbw, dW
+        if not (need_s or need_H):
+            _, _, dbw, dW = _C.edge_abs_mean_backward(ga, s, H, bw, W, False, False,
+                                                       bool(need_bw), bool(need_W))
+            if need_bw:
+                dbw = dbw + _C.matmul(gy.t(), s)
+            if need_W:
+                dW = dW + _C.matmul(gy.t(), H2).reshape(O, I, R)
+            return None, None, dbw, dW
+        return _C.edge_linear_backward(ga, gy, s, H, bw, W, bool(need_s), bool(need_H),
+                                       bool(need_bw), bool(need_W))
+
+
+def edge_linear_applies(s: Optional[torch.Tensor], H: torch.Tensor, bw: Optional[torch.Tensor],
+                        W: torch.Tensor) -> bool:
+    """Whether edge_linear covers this layer: a base branch, and operands the
+    folded native backward supports (float32, O <= 512 with O % 4 == 0,
+    R + 1 <= 16; _C.edge_linear_supported)."""
+    return (s is not None and bw is not None and _C is not None and H.is_cuda
+            and _C.edge_linear_supported(H, W))
+
+
+def edge_linear(s: torch.Tensor, H: torch.Tensor, bw: torch.Tensor, W: torch.Tensor):
+    """(y [B, O], a [O, I]) of a regularised layer (see EdgeLinear)."""
+    return EdgeLinear.apply(s, H, bw, W)
+
+
 def native_basis(x: torch.Tensor, grid: torch.Tensor, k: int) -> torch.Tensor:
     return NativeBasis.apply(x, grid, k)
 

@@ -324,14 +324,20 @@ class KANLinear(nn.Module):
         H = self._basis(xf, impl)
         W = self._ref.effective_spline_weight()
         B, R = xf.shape[0], self.grid_size + self.spline_order
-        if impl == "fused" and B > 0:
+        a = None
+        if impl == "fused" and B > 0 and _fused.edge_linear_applies(s, H, self.base_weight, W):
+            # output and edge statistic as one function: its backward folds
+            # dL/dy into the edge kernel (one launch for all four gradients)
+            y, a = _fused.edge_linear(s, H, self.base_weight, W)
+        elif impl == "fused" and B > 0:
             y = _fused.native_linear(s, self.base_weight, H.reshape(B, self.in_features * R),
                                      W.reshape(self.out_features, -1))
         else:
             y = F.linear(s, self.base_weight) + F.linear(H.reshape(B, self.in_features * R),
                                                          W.reshape(self.out_features, -1))
         self.last_backend = "cuda" if impl == "fused" else "reference"
-        a = self._edge_abs_mean(xf, s, H, W, impl, chunk_size)
+        if a is None:
+            a = self._edge_abs_mean(xf, s, H, W, impl, chunk_size)
         reg = regularization_from_edge_means(a, reg_act, reg_entropy)
         return y.reshape(lead + (self.out_features,)), reg
 
