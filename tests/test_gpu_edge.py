@@ -136,11 +136,13 @@ def test_forward_with_regularization_fused_matches_dense(C, dtype):
             assert normwise(np64(a), np64(b)) < tol
 
 
-# (N, I, O, R): every tiling of the folded backward (O = 4 -> 2x4, 64 -> 4x4,
-# 100 -> 4x2, 200 -> 4x1, 300 and 512 -> 8x1), ragged sample counts, sample
-# splits across blocks (4097, 6000) and R + 1 at 5, 12 and 16.
-LINEAR_SHAPES = [(37, 5, 4, 4), (300, 7, 64, 11), (1000, 9, 100, 15), (513, 3, 200, 11),
-                 (700, 2, 300, 8), (4097, 5, 512, 11), (6000, 3, 64, 11)]
+# (N, I, O, R): every tiling of the folded backward (O = 4, 7 -> 2x4, 33, 64 ->
+# 4x4, 100 -> 4x2, 200 -> 4x1, 300 and 512 -> 8x1; odd widths leave partial
+# output tiles), ragged sample counts, sample splits across blocks (4097, 6000)
+# and R + 1 at 5, 12 and 16.
+LINEAR_SHAPES = [(37, 5, 4, 4), (90, 3, 7, 6), (300, 7, 64, 11), (250, 4, 33, 11),
+                 (1000, 9, 100, 15), (513, 3, 200, 11), (700, 2, 300, 8), (4097, 5, 512, 11),
+                 (6000, 3, 64, 11)]
 
 
 @pytest.mark.parametrize("shape", LINEAR_SHAPES)
@@ -176,7 +178,7 @@ def test_edge_linear_supported_range(C):
                                                torch.empty(O, I, R, dtype=dt, device="cuda"))
     assert C.edge_linear_supported(*mk(10, 3, 512, 15))
     assert not C.edge_linear_supported(*mk(10, 3, 516, 11))   # O > 512
-    assert not C.edge_linear_supported(*mk(10, 3, 70, 11))    # O % 4 != 0
+    assert C.edge_linear_supported(*mk(10, 3, 70, 11))
     assert not C.edge_linear_supported(*mk(10, 3, 64, 16))    # R + 1 > 16
     assert not C.edge_linear_supported(*mk(10, 3, 64, 11, torch.float64))
 
@@ -199,7 +201,7 @@ def _reg_grads(net, x, impl, create_graph=False):
 @pytest.mark.parametrize("x_grad", [True, False])
 def test_regularized_layers_folded_backward_match_dense(C, monkeypatch, x_grad):
     """KAN([16, 64, 100, 12]) fp32: every layer's output and edge statistic go
-    through EdgeLinear (the 12-wide layer too: 12 % 4 == 0); with x requiring
+    through EdgeLinear; with x requiring
     grad the first layer takes the folded kernel as well, without it the
     weight-only branch.
     * Gradients against the unfolded native path (separate output products

@@ -598,8 +598,7 @@ def edge_abs_mean_backward(grad_a, s, H, base_weight, W, need_s: bool, need_H: b
 
 def edge_linear_supported(H: torch.Tensor, W: torch.Tensor) -> bool:
     """True where edge_linear_backward applies to these operands (float32,
-    0 < out_features <= 512 with out_features % 4 == 0, num_basis + 1 <= 16,
-    at least one sample)."""
+    0 < out_features <= 512, num_basis + 1 <= 16, at least one sample)."""
     if not (H.is_cuda and H.dim() == 3 and W.dim() == 3):
         return False
     N, I, R = H.shape
@@ -623,8 +622,6 @@ def edge_linear_backward(grad_a, grad_y, s, H, base_weight, W, need_s: bool, nee
     H, W = H.contiguous(), W.contiguous()
     ga = grad_a.contiguous().to(W.dtype)
     gy = grad_y.contiguous().to(W.dtype)
-    if gy.data_ptr() % 16 != 0:
-        gy = gy.clone()
     sc = s.contiguous() if hb else None
     bw = base_weight.contiguous() if hb else None
     opts = dict(dtype=H.dtype, device=H.device)

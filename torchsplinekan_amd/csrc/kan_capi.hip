@@ -734,7 +734,7 @@ int kan_hip_edge_linear_backward(int dtype, const void* ga, const void* gy, cons
   if ((gs != nullptr || gbw != nullptr) && bw == nullptr)
     return set_error(KAN_ERR_INVALID, "edge_linear_backward: base gradients requested without a base branch");
   if (!kan_hip_edge_linear_supported(dtype, n, I, O, R))
-    return set_error(KAN_ERR_LIMIT, "edge_linear_backward: needs float32, n > 0, out_features <= 512 and a multiple of 4, num_basis + 1 <= 16");
+    return set_error(KAN_ERR_LIMIT, "edge_linear_backward: needs float32, n > 0, out_features <= 512, num_basis + 1 <= 16");
   const size_t need = edge_ws_bytes(dtype, n, I, O, R, true);
   if (ws_bytes < need || (need > 0 && ws == nullptr))
     return set_error(KAN_ERR_WORKSPACE, "edge_linear_backward: workspace of %zu bytes is smaller than the %zu required", ws_bytes, need);

@@ -796,20 +796,22 @@ __global__ __launch_bounds__(kEdgeMfThreads) void edge_bwd_mfma_kernel(
       for (int k = 0; k < KS; ++k) a[k] = k == 0 ? hc_or(an[p][0], asn[p]) : an[p][k];
 #pragma unroll
       for (int v = 0; v < 4; ++v) hb[v] = hc_or(hn[p][v], hsn[p][v]);
-      // layer-output gradient D[n0 + r, obase + 16t + 4q .. + 3] (rows past
-      // the range and columns past O read as zeros), issued before phi
-      f32x4 dq[HASD ? kOT : 1];
+      // layer-output gradient in the accumulator layout of g,
+      // D[n0 + 4q + v, obase + 16t + r] (16 consecutive columns of 4 rows per
+      // load; rows past the range and columns past O read as zeros), issued
+      // before phi so that its MFMAs cover the loads
+      float dq[HASD ? kOT : 1][4];
       if constexpr (HASD) {
         const int64_t nt = g0 + 16 * j;
         const __amdgpu_buffer_rsrc_t rd = tile_rsrc(D + nt * g.O, ne - nt, g.O);
 #pragma unroll
         for (int t = 0; t < kOT; ++t) {
-          const int oc = obase + t * 16 + 4 * q;
-          const uint32_t off = oc < g.O ? (uint32_t)((r * g.O + oc) * 4) : kBufOob;
-          typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
-          const u32x4 u = __builtin_amdgcn_raw_buffer_load_b128(rd, (int)off, 0, 0);
+          const int oc = obase + t * 16 + r;
 #pragma unroll
-          for (int v = 0; v < 4; ++v) dq[t][v] = __uint_as_float(u[v]);
+          for (int v = 0; v < 4; ++v) {
+            const uint32_t off = oc < g.O ? (uint32_t)(((4 * q + v) * g.O + oc) * 4) : kBufOob;
+            dq[t][v] = buf_ld(rd, off);
+          }
         }
       }
       f32x4 acc[kOT];
@@ -825,18 +827,11 @@ __global__ __launch_bounds__(kEdgeMfThreads) void edge_bwd_mfma_kernel(
 #pragma unroll
         for (int v = 0; v < 4; ++v) gv[t][v] = g_sign(gav[t], acc[t][v]);
       if constexpr (HASD) {
-        // D rows [n][o] through the same LDS tiles, read back as
-        // D[n = 4q + v, o = 16t + r] (the accumulator layout of g), added to g:
         // both products then carry the layer output's gradient as well
 #pragma unroll
         for (int t = 0; t < kOT; ++t)
-          *reinterpret_cast<f32x4*>(tb + t * 16 * TS + r * TS + 4 * q) = dq[t];
-        edge_wave_sync();
 #pragma unroll
-        for (int t = 0; t < kOT; ++t)
-#pragma unroll
-          for (int v = 0; v < 4; ++v) gv[t][v] += tb[t * 16 * TS + (4 * q + v) * TS + r];
-        edge_wave_sync();  // (g's stores below come after these reads)
+          for (int v = 0; v < 4; ++v) gv[t][v] += dq[t][v];
       }
       // g[n = 4q + v, o = 16t + r] -> tile t at [o][n] (one 16-byte store per lane)
 #pragma unroll
@@ -1134,7 +1129,7 @@ int launch_edge_fused(const float* ga, const float* D, const float* s, const flo
 }
 
 bool edge_linear_fold_supported(int64_t n, int64_t I, int64_t O, int64_t R) {
-  return n > 0 && I > 0 && O > 0 && O <= 512 && O % 4 == 0 && R + 1 <= 16;
+  return n > 0 && I > 0 && O > 0 && O <= 512 && R + 1 <= 16;
 }
 
 int launch_edge_linear_backward_mfma(const float* ga, const float* D, const float* s,
@@ -1143,10 +1138,8 @@ int launch_edge_linear_backward_mfma(const float* ga, const float* D, const floa
                                      int64_t n, int64_t I, int64_t O, int64_t R, hipStream_t st) {
   if (!edge_linear_fold_supported(n, I, O, R))
     return set_error(KAN_ERR_LIMIT,
-                     "edge_linear_backward: needs 0 < out_features <= 512, out_features %% 4 == 0, "
-                     "num_basis + 1 <= 16 and n > 0");
-  if ((reinterpret_cast<uintptr_t>(D) & 15) != 0)
-    return set_error(KAN_ERR_INVALID, "edge_linear_backward: grad_y must be 16-byte aligned");
+                     "edge_linear_backward: needs 0 < out_features <= 512, num_basis + 1 <= 16 "
+                     "and n > 0");
   return launch_edge_fused(ga, D, s, H, bw, W, ds, dH, dbw, dW, part, splits, n, I, O, R, st);
 }
 

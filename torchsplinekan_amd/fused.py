@@ -154,8 +154,8 @@ class EdgeLinear(torch.autograd.Function):
 def edge_linear_applies(s: Optional[torch.Tensor], H: torch.Tensor, bw: Optional[torch.Tensor],
                         W: torch.Tensor) -> bool:
     """Whether edge_linear covers this layer: a base branch, and operands the
-    folded native backward supports (float32, O <= 512 with O % 4 == 0,
-    R + 1 <= 16; _C.edge_linear_supported)."""
+    folded native backward supports (float32, O <= 512, R + 1 <= 16;
+    _C.edge_linear_supported)."""
     return (s is not None and bw is not None and _C is not None and H.is_cuda
             and _C.edge_linear_supported(H, W))
 
