@@ -209,7 +209,9 @@ int kan_hip_edge_abs_mean_backward(int dtype, const void* grad_a, const void* s,
  * EdgeAbsMean's backward, which autograd adds (spline_kan/kan_linear.py:
  * 384-387, spline_kan/fused.py:73-102, csrc/kan_reg_cuda.cu:284-312); here
  * they come from the fused edge kernel with grad_y added to g, with no
- * separate products.  float32 only, for 0 < out_features <= 512,
+ * separate products (with grad_s and grad_basis both NULL, from the
+ * parameter kernel with grad_y added alike).  float32 only, for
+ * 0 < out_features <= 512,
  * num_basis + 1 <= 16 and n > 0 (kan_hip_edge_linear_supported returns 1
  * exactly then).  Workspace: as kan_hip_edge_abs_mean_backward
  * (kan_hip_edge_workspace with backward = 1). */

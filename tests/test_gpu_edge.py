@@ -171,6 +171,11 @@ def test_edge_linear_backward_matches_oracle(C, shape):
                                                  bw.cuda(), W.cuda(), False, True, False, True)
     assert ds2 is None and dbw2 is None
     assert torch.equal(dH2, dH) and torch.equal(dW2, dW)
+    # weight gradients only: the parameter kernel with grad_y added
+    ds3, dH3, dbw3, dW3 = C.edge_linear_backward(ga.cuda(), gy.cuda(), s.cuda(), H.cuda(),
+                                                 bw.cuda(), W.cuda(), False, False, True, True)
+    assert ds3 is None and dH3 is None
+    assert normwise(np64(dbw3), rdbw) < 1e-4 and normwise(np64(dW3), rdW) < 1e-4
 
 
 def test_edge_linear_supported_range(C):

@@ -295,11 +295,14 @@ __global__ __launch_bounds__(kEdgeMfThreads) void edge_fwd_mfma_kernel(
 // Parameter gradients: block (i, output chunk, split).  Per 16-sample tile:
 // phi (rows n, columns o) -> g in registers -> dWc[o, c] += sum_n g Hc with
 // the accumulator entries as the A operand.  CT column tiles of 16 cover c.
-template <int KS, int CT, int OT, int WS>
+// With HASD the layer output's gradient D [n, O] is added to g (the weight
+// gradients of y = s bw^T + H W^T and of the statistic together).
+template <int KS, int CT, int OT, int WS, bool HASD>
 __global__ __launch_bounds__(kEdgeMfThreads) void edge_param_mfma_kernel(
-    const float* __restrict__ ga, const float* __restrict__ s, const float* __restrict__ H,
-    const float* __restrict__ bw, const float* __restrict__ W, float* __restrict__ dbw,
-    float* __restrict__ dW, float* __restrict__ part, EdgeGeom g, int final_out) {
+    const float* __restrict__ ga, const float* __restrict__ D, const float* __restrict__ s,
+    const float* __restrict__ H, const float* __restrict__ bw, const float* __restrict__ W,
+    float* __restrict__ dbw, float* __restrict__ dW, float* __restrict__ part, EdgeGeom g,
+    int final_out) {
   typedef EdgeTiling<OT, WS> Tl;
   constexpr int kOT = OT;
   // partial dWc of the WS sample shares: [WS][block outputs][CT * 16]
@@ -389,6 +392,22 @@ __global__ __launch_bounds__(kEdgeMfThreads) void edge_param_mfma_kernel(
 #pragma unroll
         for (int v = 0; v < 4; ++v)
           hb[ct][v] = ct == 0 ? hc_or(hn[p][0][v], hsn[p][v]) : hn[p][ct][v];
+      // D[n0 + 4q + v, obase + 16t + r] in the accumulator layout of g (rows
+      // past the range and columns past O read as zeros)
+      float dq[HASD ? kOT : 1][4];
+      if constexpr (HASD) {
+        const int64_t nt = n0 + 16 * p;
+        const __amdgpu_buffer_rsrc_t rd = tile_rsrc(D + nt * g.O, ne - nt, g.O);
+#pragma unroll
+        for (int t = 0; t < kOT; ++t) {
+          const int oc = obase + t * 16 + r;
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            const uint32_t off = oc < g.O ? (uint32_t)(((4 * q + v) * g.O + oc) * 4) : kBufOob;
+            dq[t][v] = buf_ld(rd, off);
+          }
+        }
+      }
       // both products with the output tiles innermost (independent chains)
       f32x4 acc[kOT];
 #pragma unroll
@@ -402,6 +421,12 @@ __global__ __launch_bounds__(kEdgeMfThreads) void edge_param_mfma_kernel(
       for (int t = 0; t < kOT; ++t)
 #pragma unroll
         for (int v = 0; v < 4; ++v) gv[t][v] = g_sign(gav[t], acc[t][v]);
+      if constexpr (HASD) {
+#pragma unroll
+        for (int t = 0; t < kOT; ++t)
+#pragma unroll
+          for (int v = 0; v < 4; ++v) gv[t][v] += dq[t][v];
+      }
 #pragma unroll
       for (int ct = 0; ct < CT; ++ct)
 #pragma unroll
@@ -1072,6 +1097,54 @@ int launch_edge_forward_mfma(const float* s, const float* H, const float* bw, co
   return check_launch("edge_abs_mean_finalize");
 }
 
+// Weight gradients of the statistic (with D also those of the layer output).
+int launch_edge_params(const float* ga, const float* D, const float* s, const float* H,
+                       const float* bw, const float* W, float* dbw, float* dW, float* part,
+                       int splits, int64_t n, int64_t I, int64_t O, int64_t R, hipStream_t st) {
+  const int R1 = (int)R + 1;
+  EdgeGeom g;
+  g.n = n;
+  g.I = (int)I;
+  g.O = (int)O;
+  g.R = (int)R;
+  g.splits = splits;
+  g.per_split = round_up(ceil_div(n, splits), kEdgeRowQuant);
+  int ot, ws;
+  g.ochunks = (int)ceil_div(O, (int64_t)edge_tiling(O, &ot, &ws));
+  if (splits > 1 && part == nullptr)
+    return set_error(KAN_ERR_WORKSPACE, "edge_abs_mean_backward: missing workspace");
+  const int64_t blocks = I * g.ochunks * (int64_t)splits;
+  if (blocks > 2147483647LL)
+    return set_error(KAN_ERR_LIMIT, "edge_abs_mean_backward: too many blocks");
+  const bool fin = splits == 1;
+  {
+    TimedLaunch timed(kClassEdgeGrad, st, 4.0 * (double)n * (double)O * (double)I * (double)R1);
+#define KAN_EDGE_PAR(OTV, WSV, HD)                                                              \
+  KAN_EDGE_MF_DISPATCH(R1, hipLaunchKernelGGL((edge_param_mfma_kernel<KS, CT, OTV, WSV, HD>),   \
+                                              dim3((unsigned)blocks), dim3(kEdgeMfThreads),     \
+                                              0, st, ga, D, s, H, bw, W, dbw, dW, part, g,      \
+                                              fin ? 1 : 0))
+#define KAN_EDGE_PAR_T(HD)                   \
+  if (ot == 8) KAN_EDGE_PAR(8, 1, HD);       \
+  else if (ws == 1) KAN_EDGE_PAR(4, 1, HD);  \
+  else if (ws == 2) KAN_EDGE_PAR(4, 2, HD);  \
+  else if (ot == 4) KAN_EDGE_PAR(4, 4, HD);  \
+  else KAN_EDGE_PAR(2, 4, HD)
+    if (D != nullptr) {
+      KAN_EDGE_PAR_T(true);
+    } else {
+      KAN_EDGE_PAR_T(false);
+    }
+#undef KAN_EDGE_PAR_T
+#undef KAN_EDGE_PAR
+    const int rc = check_launch("edge_abs_mean_backward(params)");
+    if (rc != KAN_OK || fin) return rc;
+  }
+  hipLaunchKernelGGL(edge_param_finalize_f32, dim3(fin_blocks_f32(O * I * R1)), dim3(256), 0, st,
+                     part, dbw, dW, splits, O * I, (int)R);
+  return check_launch("edge_abs_mean_backward(finalize)");
+}
+
 // The fused backward (both gradient sides; with D also the layer output's
 // gradient) for O <= 512 and R + 1 <= 16.
 int launch_edge_fused(const float* ga, const float* D, const float* s, const float* H,
@@ -1140,6 +1213,10 @@ int launch_edge_linear_backward_mfma(const float* ga, const float* D, const floa
     return set_error(KAN_ERR_LIMIT,
                      "edge_linear_backward: needs 0 < out_features <= 512, num_basis + 1 <= 16 "
                      "and n > 0");
+  if (ds == nullptr && dH == nullptr)  // weight gradients only: the parameter kernel
+    return dbw == nullptr && dW == nullptr
+               ? KAN_OK
+               : launch_edge_params(ga, D, s, H, bw, W, dbw, dW, part, splits, n, I, O, R, st);
   return launch_edge_fused(ga, D, s, H, bw, W, ds, dH, dbw, dW, part, splits, n, I, O, R, st);
 }
 
@@ -1163,32 +1240,9 @@ int launch_edge_backward_mfma(const float* ga, const float* s, const float* H, c
     return launch_edge_fused(ga, nullptr, s, H, bw, W, ds, dH, dbw, dW, part, splits, n, I, O, R,
                              st);
   if (need_p) {
-    if (splits > 1 && part == nullptr)
-      return set_error(KAN_ERR_WORKSPACE, "edge_abs_mean_backward: missing workspace");
-    const int64_t blocks = I * g.ochunks * (int64_t)splits;
-    if (blocks > 2147483647LL)
-      return set_error(KAN_ERR_LIMIT, "edge_abs_mean_backward: too many blocks");
-    const bool fin = splits == 1;
-    TimedLaunch timed(kClassEdgeGrad, st, 4.0 * (double)n * (double)O * (double)I * (double)R1);
-#define KAN_EDGE_PAR(OTV, WSV)                                                              \
-  KAN_EDGE_MF_DISPATCH(R1, hipLaunchKernelGGL((edge_param_mfma_kernel<KS, CT, OTV, WSV>),   \
-                                              dim3((unsigned)blocks), dim3(kEdgeMfThreads), \
-                                              0, st, ga, s, H, bw, W, dbw, dW, part, g,     \
-                                              fin ? 1 : 0))
-    if (ot == 8) KAN_EDGE_PAR(8, 1);
-    else if (ws == 1) KAN_EDGE_PAR(4, 1);
-    else if (ws == 2) KAN_EDGE_PAR(4, 2);
-    else if (ot == 4) KAN_EDGE_PAR(4, 4);
-    else KAN_EDGE_PAR(2, 4);
-#undef KAN_EDGE_PAR
-    int rc = check_launch("edge_abs_mean_backward(params)");
+    const int rc = launch_edge_params(ga, nullptr, s, H, bw, W, dbw, dW, part, splits, n, I, O, R,
+                                      st);
     if (rc != KAN_OK) return rc;
-    if (!fin) {
-      hipLaunchKernelGGL(edge_param_finalize_f32, dim3(fin_blocks_f32(O * I * R1)), dim3(256), 0,
-                         st, part, dbw, dW, splits, O * I, (int)R);
-      rc = check_launch("edge_abs_mean_backward(finalize)");
-      if (rc != KAN_OK) return rc;
-    }
   }
   if (need_x) {
     constexpr int NTW = 4;

@@ -105,9 +105,9 @@ class EdgeLinear(torch.autograd.Function):
     Every one of those gradients is a contraction of
     g' = ga sign(phi) / n + dL/dy, so here a single native launch
     (_C.edge_linear_backward: dL/dy added to g inside the fused edge kernel)
-    returns all four.  Recorded backwards (create_graph) use the separate
-    differentiable pieces; a backward that needs only the weight gradients
-    uses the parameter kernel plus two products."""
+    returns all four (only the weight gradients: the parameter kernel with
+    dL/dy added the same way).  Recorded backwards (create_graph) use the
+    separate differentiable pieces."""
 
     @staticmethod
     def forward(ctx, s, H, bw, W):
@@ -139,14 +139,6 @@ class EdgeLinear(torch.autograd.Function):
             dbw = dbw + mm(gy.t(), s) if need_bw else None
             dW = dW + mm(gy.t(), H2).reshape(O, I, R) if need_W else None
             return ds, dH, dbw, dW
-        if not (need_s or need_H):
-            _, _, dbw, dW = _C.edge_abs_mean_backward(ga, s, H, bw, W, False, False,
-                                                       bool(need_bw), bool(need_W))
-            if need_bw:
-                dbw = dbw + _C.matmul(gy.t(), s)
-            if need_W:
-                dW = dW + _C.matmul(gy.t(), H2).reshape(O, I, R)
-            return None, None, dbw, dW
         return _C.edge_linear_backward(ga, gy, s, H, bw, W, bool(need_s), bool(need_H),
                                        bool(need_bw), bool(need_W))
 
