@@ -170,7 +170,7 @@ def native_linear(s: torch.Tensor, bw: torch.Tensor, H2: torch.Tensor,
                   W2: torch.Tensor) -> torch.Tensor:
     """Layer output s bw^T + H2 W2^T of the fused regularisation path, the two
     products the reference takes with F.linear (spline_kan/kan_linear.py:
-    360-362), on the MFMA contraction engine (NativeMatmul: gradients are
+    384-385), on the MFMA contraction engine (NativeMatmul: gradients are
     engine products as well, the long sample reductions split over K and
     summed in a fixed order)."""
     y = _C.NativeMatmul.apply(s, bw.t())
