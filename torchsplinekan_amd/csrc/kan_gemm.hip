@@ -17,8 +17,8 @@
 //          problems with too few big tiles to fill the chip);
 //   narrow 256x64 block tile, 4 waves of 64x64, for outputs of at most 64
 //          columns.
-// A 256x256 tile over 4 waves of 128x128 (one wave per SIMD) serves the
-// fused input-gradient epilogue.
+// A 256x256 tile over 4 waves of 128x128 (one wave per SIMD) can be forced
+// for comparison.
 // fp64 runs on gemm_kernel: 128x128 tile, 2x2 waves, v_mfma_f64_16x16x4f64.
 //
 // Operand slabs (BK deep) are staged through LDS with double buffering.  Each
@@ -116,8 +116,7 @@ struct Cfg {
 
 // 256 x 256 block tiles: 8 waves of 128 x 64 (two per SIMD: while one wave
 // of a SIMD waits at the slab barrier or on its fragment reads, the other
-// issues MFMAs), or 4 waves of 128 x 128 (one per SIMD; the fused
-// input-gradient epilogue needs its wave blocks and LDS budget).
+// issues MFMAs), or 4 waves of 128 x 128 (one per SIMD; only when forced).
 using CfgF32Big = Cfg<float, 256, 256, 32, 2, 4, 32, 1>;
 using CfgF32Big4 = Cfg<float, 256, 256, 32, 2, 2, 32, 1>;
 using CfgF32Small = Cfg<float, 128, 128, 32, 2, 2, 32, 2>;
@@ -1003,7 +1002,8 @@ bool gemm_dx_supported(int64_t M, int64_t N, int64_t K, int64_t I, int G, int k,
   if (k < 1 || k > 3) return false;
   const int R = G + k, nk = G + 2 * k + 1;
   const int cfg = pick_cfg_f32(M, N, K, 1);
-  if (cfg == 0 || cfg == 3) return dx_cfg_fits<CfgF32Big4>(N, I, R, nk, has_base);
+  if (cfg == 0) return dx_cfg_fits<CfgF32Big>(N, I, R, nk, has_base);
+  if (cfg == 3) return dx_cfg_fits<CfgF32Big4>(N, I, R, nk, has_base);
   return dx_cfg_fits<CfgF32Small>(N, I, R, nk, has_base);
 }
 
@@ -1041,7 +1041,8 @@ int launch_gemm_dx(int64_t M, int64_t N, int64_t K, const float* A, int64_t lda,
   {
     TimedLaunch timed(kClassContraction, st, 2.0 * (double)M * (double)N * (double)K);
     const int cfg = pick_cfg_f32(M, N, K, 1);
-    if (cfg == 0 || cfg == 3) rc = launch_dx_cfg<CfgF32Big4>(p, e, k, st);
+    if (cfg == 0) rc = launch_dx_cfg<CfgF32Big>(p, e, k, st);
+    else if (cfg == 3) rc = launch_dx_cfg<CfgF32Big4>(p, e, k, st);
     else rc = launch_dx_cfg<CfgF32Small>(p, e, k, st);
     if (rc != KAN_OK) return rc;
     rc = check_launch("gemm_dx");
