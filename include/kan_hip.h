@@ -46,24 +46,29 @@ extern "C" {
 /* Message for the last non-zero status returned on this thread ("" if none). */
 const char* kan_hip_last_error(void);
 
+/* Hex digest of the sources and compiler flags the library was built from
+ * (no reference counterpart: the loader uses it to refuse a library that is
+ * older than the sources beside it). */
+const char* kan_hip_source_hash(void);
+
 /* Limits query.  Replaces the module attributes CUDA_MAX_DEG0_BASIS and
  * CUDA_MAX_IN_FEATURES (csrc/kan_ext.cpp:164-165, csrc/kan_ops.h:15-17). */
 int kan_hip_limits(int64_t* max_deg0_basis, int64_t* max_in_features);
 
 /* Basis implementation switch: 0 = dense Cox-de Boor recurrence, 1 = local
  * (default).  Replaces _C.set_basis_impl / _C.get_basis_impl
- * (csrc/kan_cuda.cu:274-279, csrc/kan_ext.cpp:373-375).  Any other value
+ * (csrc/kan_cuda.cu:274-279, csrc/kan_ext.cpp:193-195).  Any other value
  * returns KAN_ERR_INVALID. */
 int kan_hip_set_basis_impl(int64_t impl);
 int64_t kan_hip_get_basis_impl(void);
 
 /* basis[n, I, R] = B-spline basis of x.  Replaces _C.basis / kan_basis_cuda
- * (csrc/kan_ext.cpp:376-377, csrc/kan_cuda.cu:666-680). */
+ * (csrc/kan_ext.cpp:196-197, csrc/kan_cuda.cu:666-680). */
 int kan_hip_basis(int dtype, const void* x, const void* grid, void* basis, int64_t n,
                   int64_t in_features, int64_t grid_size, int64_t spline_order, void* stream);
 
 /* grad_x[n, i] = sum_r grad_basis[n, i, r] * dB_r/dx(x[n, i]).  Replaces
- * _C.basis_grad / kan_basis_grad_cuda (csrc/kan_ext.cpp:378-380,
+ * _C.basis_grad / kan_basis_grad_cuda (csrc/kan_ext.cpp:198-200,
  * csrc/kan_cuda.cu:682-699). */
 int kan_hip_basis_grad(int dtype, const void* x, const void* grid, const void* grad_basis,
                        void* grad_x, int64_t n, int64_t in_features, int64_t grid_size,
@@ -180,7 +185,7 @@ int kan_hip_edge_workspace(int dtype, int64_t n, int64_t in_features, int64_t ou
 /* a[o, i] = (1/n) sum_m | s[m,i] bw[o,i] + sum_r basis[m,i,r] weight[o,i,r] |
  * without materialising the [n, O, I] edge tensor.  s and base_weight may both
  * be NULL (no base branch).  Replaces _C.edge_abs_mean / edge_abs_mean_cuda
- * (csrc/kan_ext.cpp:381-383, csrc/kan_reg_cuda.cu:263-280). */
+ * (csrc/kan_ext.cpp:201-203, csrc/kan_reg_cuda.cu:263-280). */
 int kan_hip_edge_abs_mean(int dtype, const void* s, const void* basis, const void* base_weight,
                           const void* weight, void* a, void* workspace, size_t workspace_bytes,
                           int64_t n, int64_t in_features, int64_t out_features,
@@ -190,7 +195,7 @@ int kan_hip_edge_abs_mean(int dtype, const void* s, const void* basis, const voi
  * NULL when not needed: grad_s [n, I], grad_basis [n, I, R],
  * grad_base_weight [O, I], grad_weight [O, I, R].  Replaces
  * _C.edge_abs_mean_backward / edge_abs_mean_backward_cuda
- * (csrc/kan_ext.cpp:384-387, csrc/kan_reg_cuda.cu:284-312). */
+ * (csrc/kan_ext.cpp:204-207, csrc/kan_reg_cuda.cu:284-312). */
 int kan_hip_edge_abs_mean_backward(int dtype, const void* grad_a, const void* s,
                                    const void* basis, const void* base_weight,
                                    const void* weight, void* grad_s, void* grad_basis,

@@ -35,6 +35,27 @@ def test_library_exports_every_declared_symbol(lib):
     assert set(names) <= set(lib.SIGNATURES)
 
 
+def test_library_matches_its_sources(lib, tmp_path, monkeypatch):
+    """The library carries the digest of the sources it was built from; the
+    loader refuses one whose digest differs from the sources beside it."""
+    from torchsplinekan_amd import build_lib
+    built = lib.LIB.kan_hip_source_hash().decode()
+    assert built == build_lib.source_hash()
+    # a changed source changes the digest
+    csrc = tmp_path / "csrc"
+    csrc.mkdir()
+    for f in os.listdir(build_lib.CSRC):
+        if f.endswith((".hip", ".h")):
+            (csrc / f).write_bytes(open(os.path.join(build_lib.CSRC, f), "rb").read())
+    monkeypatch.setattr(build_lib, "CSRC", str(csrc))
+    assert build_lib.source_hash() == built
+    with open(csrc / "kan_capi.hip", "a") as f:
+        f.write("\n// edited\n")
+    assert build_lib.source_hash() != built
+    with pytest.raises(ImportError, match="stale"):
+        lib._load()
+
+
 def test_limits(lib):
     assert lib.limits() == (71, 65535)
     from torchsplinekan_amd import _C

@@ -80,6 +80,7 @@ def test_raw_forward_backward_match_oracle(C, case, dtype, variant):
                                        sc is not None)
     ry, rgx, rgbw, rgsw, rgsc = _oracle(x, grid, bw, sw, sc, D, k)
     assert H.shape == (N, I, G + k)
+    assert H.is_contiguous() and H.view(-1).numel() == N * I * (G + k)
     assert np.allclose(np64(H), ko.basis_dense(np64(x), np64(grid), k),
                        atol=1e-13 if dtype == torch.float64 else 2e-6, rtol=0)
     pairs = [(y, ry), (gx, rgx), (gsw, rgsw)]

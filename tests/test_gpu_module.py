@@ -1,7 +1,7 @@
 """Module-level GPU behaviour of the native backend, after the reference's own
 tests of the same API (tests/test_fused_regularization.py:58-219,
 tests/test_math_correctness.py:180-360, tests/test_cuda.py:88-95,
-tests/test_export.py:24-90, tests/test_grid_extension.py): every
+tests/test_export.py:24-86, tests/test_grid_extension.py): every
 regularisation implementation against the dense one across k, G and base
 activations, the cross-layer gradient, the zero layer, no graph state kept on
 modules, the fused path's memory bound, device movement, non-SiLU base

@@ -113,6 +113,27 @@ def test_backend_selection_on_cpu():
         KANLinear(4, 4, grid_size=-1)
 
 
+def test_auto_falls_back_with_warning_when_library_missing(monkeypatch):
+    """backend="auto" without the native library: device inputs go to the
+    reference backend as in spline_kan/kan_linear.py:147-148, with one
+    RuntimeWarning per process naming the missing library."""
+    import types
+    from torchsplinekan_amd import kan_linear as kl
+    monkeypatch.setattr(kl, "_CUDA_EXT_LOADED", False)
+    monkeypatch.setattr(kl, "_MISSING_WARNED", False)
+    L = KANLinear(4, 3, backend="auto")
+    assert L.selected_backend == "reference"
+    dev_like = types.SimpleNamespace(is_cuda=True)
+    with pytest.warns(RuntimeWarning, match="libkan_hip.so is not built"):
+        assert L.backend_for(dev_like) == "reference"
+    import warnings
+    with warnings.catch_warnings():
+        warnings.simplefilter("error")
+        assert L.backend_for(dev_like) == "reference"   # warned once only
+    with pytest.raises(RuntimeError, match="could not be loaded"):
+        KANLinear(4, 3, backend="cuda")
+
+
 def test_state_dict_keys_and_roundtrip():
     L = KANLinear(4, 3, grid_size=5, backend="auto")
     keys = set(L.state_dict().keys())

@@ -147,9 +147,11 @@ def kan_infer(x, grid, waug, spline_order: int, has_base: bool) -> torch.Tensor:
     return y
 
 
-def _basis_view(aug: torch.Tensor, I: int, R: int) -> torch.Tensor:
-    """basis [B, I, R] as a view of the augmented rows (no copy)."""
-    return aug[:, :I * R].reshape(aug.shape[0], I, R)
+def _basis_of(aug: torch.Tensor, I: int, R: int) -> torch.Tensor:
+    """basis [B, I, R] copied out of the augmented rows into its own
+    contiguous tensor, the layout kan_forward_cuda returns
+    (csrc/kan_cuda.cu:501), so callers may view or flatten it freely."""
+    return aug[:, :I * R].reshape(aug.shape[0], I, R).contiguous()
 
 
 def _backward_device(D, x, grid, base_weight, spline_weight, spline_scaler, aug, k, has_scaler,
@@ -206,7 +208,7 @@ def kan_forward(x, grid, base_weight, spline_weight, spline_scaler, spline_order
     if x.is_cuda:
         y, aug = _forward_device(x, grid, base_weight, spline_weight, spline_scaler,
                                  spline_order, has_scaler)
-        return y, _basis_view(aug, x.shape[1], spline_weight.shape[2])
+        return y, _basis_of(aug, x.shape[1], spline_weight.shape[2])
     return _cmp.kan_forward_cpu(x.contiguous(), grid.contiguous(), base_weight,
                                 spline_weight.contiguous(), spline_scaler, spline_order,
                                 has_scaler)
@@ -749,3 +751,62 @@ class EdgeAbsMeanBackward(torch.autograd.Function):
         if torch.is_grad_enabled():
             return _edge_double_backward_dense(ga, s, H, bw, W, u_ds, u_dH, u_dbw, u_dW, needs)
         return edge_abs_mean_double_backward(ga, s, H, bw, W, u_ds, u_dH, u_dbw, u_dW, *needs)
+
+
+# ---------------------------------------------------------------------------
+# op registry: torch.ops.spline_kan.kan_forward / kan_backward
+# (TORCH_LIBRARY(spline_kan) with CPU, CUDA and Meta kernels,
+# csrc/kan_ext.cpp:62-155)
+# ---------------------------------------------------------------------------
+
+_KAN_FORWARD_SCHEMA = (
+    "kan_forward(Tensor x, Tensor grid, Tensor base_weight, Tensor spline_weight, "
+    "Tensor spline_scaler, int spline_order, bool has_scaler) -> (Tensor output, Tensor basis)")
+_KAN_BACKWARD_SCHEMA = (
+    "kan_backward(Tensor grad_output, Tensor x, Tensor grid, Tensor base_weight, "
+    "Tensor spline_weight, Tensor spline_scaler, Tensor basis, int spline_order, "
+    "bool has_scaler) -> (Tensor grad_x, Tensor grad_base_weight, Tensor grad_spline_weight, "
+    "Tensor grad_spline_scaler)")
+
+
+def _kan_forward_meta(x, grid, base_weight, spline_weight, spline_scaler, spline_order,
+                      has_scaler):
+    """Shapes only: output [B, O], basis [B, I, R] with R = knots - k - 1."""
+    B, I = x.shape[0], x.shape[1]
+    O = spline_weight.shape[0]
+    R = grid.shape[1] - spline_order - 1
+    return x.new_empty((B, O)), x.new_empty((B, I, R))
+
+
+def _kan_backward_meta(grad_output, x, grid, base_weight, spline_weight, spline_scaler, basis,
+                       spline_order, has_scaler):
+    """Shapes only; an absent base branch or scaler gives an undefined
+    gradient (None in Python), as the CPU and device kernels return."""
+    gbw = base_weight.new_empty(base_weight.shape) if _cmp.has_base(base_weight) else None
+    gsc = spline_scaler.new_empty(spline_scaler.shape) if has_scaler else None
+    return (x.new_empty(x.shape), gbw, spline_weight.new_empty(spline_weight.shape), gsc)
+
+
+def _register_ops():
+    """Defines the spline_kan ops once per process.  The CPU and CUDA kernels
+    are kan_forward / kan_backward above (CPU: the ATen formulation; CUDA,
+    i.e. ROCm device tensors: libkan_hip.so); Meta gives shapes for tracing
+    and FakeTensor.  A second import of this module (a rebuilt package in
+    the same process) finds the ops defined and keeps them."""
+    try:
+        torch._C._dispatch_find_schema_or_throw("spline_kan::kan_forward", "")
+        return None
+    except RuntimeError:
+        pass
+    lib = torch.library.Library("spline_kan", "DEF")
+    lib.define(_KAN_FORWARD_SCHEMA)
+    lib.define(_KAN_BACKWARD_SCHEMA)
+    for key in ("CPU", "CUDA"):
+        lib.impl("kan_forward", kan_forward, key)
+        lib.impl("kan_backward", kan_backward, key)
+    lib.impl("kan_forward", _kan_forward_meta, "Meta")
+    lib.impl("kan_backward", _kan_backward_meta, "Meta")
+    return lib
+
+
+_OPS_LIBRARY = _register_ops()

@@ -3,13 +3,17 @@
 torch is imported before the library is opened so that the HIP runtime torch
 already loaded (same soname, libamdhip64.so.7) is the one the kernels use:
 streams and device pointers handed over from torch are then valid in the
-library.  Loading fails loudly (ImportError) when the library is missing.
+library.  Loading fails loudly (ImportError) when the library is missing, lacks
+an entry point, or was built from other sources than those in csrc/ (the
+library carries a digest of its sources and flags, see build_lib).
 """
 
 import ctypes
 import os
 
 import torch  # noqa: F401  (must precede the CDLL open, see module docstring)
+
+from . import build_lib as _build_lib
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libkan_hip.so")
 
@@ -29,6 +33,7 @@ _sz = ctypes.c_size_t
 # name -> (restype, argtypes)
 SIGNATURES = {
     "kan_hip_last_error": (ctypes.c_char_p, []),
+    "kan_hip_source_hash": (ctypes.c_char_p, []),
     "kan_hip_limits": (_int, [ctypes.POINTER(_i64), ctypes.POINTER(_i64)]),
     "kan_hip_set_basis_impl": (_int, [_i64]),
     "kan_hip_get_basis_impl": (_i64, []),
@@ -94,6 +99,12 @@ def _load():
             raise ImportError(f"{LIB_PATH} does not export {name}: rebuild it") from exc
         fn.restype = res
         fn.argtypes = args
+    if os.path.isdir(_build_lib.CSRC):
+        built = lib.kan_hip_source_hash().decode()
+        if built != _build_lib.source_hash():
+            raise ImportError(
+                f"{LIB_PATH} is stale: it was built from other sources than those in "
+                f"{_build_lib.CSRC}; rebuild it with `python -m torchsplinekan_amd.build_lib`")
     return lib
 
 

@@ -6,6 +6,7 @@ The library is compiled with hipcc for gfx950 only, from the sources in
 tree and is found by :mod:`torchsplinekan_amd._lib` without any install step.
 """
 
+import hashlib
 import os
 import shutil
 import subprocess
@@ -37,6 +38,25 @@ SOURCE_FLAGS = {
 }
 
 
+def source_hash() -> str:
+    """SHA-256 over every source, header and flag the library is built from
+    (csrc/*, include/kan_hip.h when present, the flag lists); compiled into
+    the library and checked by the loader."""
+    h = hashlib.sha256()
+    paths = sorted(os.path.join(CSRC, f) for f in os.listdir(CSRC)
+                   if f.endswith((".hip", ".h")))
+    header = os.path.join(os.path.dirname(PKG_DIR), "include", "kan_hip.h")
+    if os.path.exists(header):
+        paths.append(header)
+    for path in paths:
+        h.update(os.path.basename(path).encode() + b"\0")
+        with open(path, "rb") as f:
+            h.update(f.read())
+        h.update(b"\0")
+    h.update(repr((ARCH, COMMON_FLAGS, sorted(SOURCE_FLAGS.items()))).encode())
+    return h.hexdigest()
+
+
 def _hipcc() -> str:
     for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
         if cand and os.path.exists(cand):
@@ -60,10 +80,12 @@ def build_library(verbose: bool = False) -> str:
     os.makedirs(BUILD_DIR, exist_ok=True)
     objs = []
     cmds = []
+    digest = source_hash()
     for src in SOURCES:
         obj = os.path.join(BUILD_DIR, os.path.splitext(src)[0] + ".o")
         objs.append(obj)
-        cmds.append([hipcc, *COMMON_FLAGS, *SOURCE_FLAGS.get(src, []), "-c",
+        extra = [f'-DKAN_SOURCE_HASH="{digest}"'] if src == "kan_capi.hip" else []
+        cmds.append([hipcc, *COMMON_FLAGS, *SOURCE_FLAGS.get(src, []), *extra, "-c",
                      os.path.join(CSRC, src), "-o", obj])
     workers = max(1, min(len(cmds), int(os.environ.get("MAX_JOBS", "8"))))
     with ThreadPoolExecutor(max_workers=workers) as ex:

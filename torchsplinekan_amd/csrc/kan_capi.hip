@@ -305,9 +305,18 @@ size_t edge_ws_bytes(int dtype, int64_t n, int64_t I, int64_t O, int64_t R, bool
 
 using namespace kan;
 
+// Digest of the sources and flags this library was built from, passed by
+// the build script; the Python loader compares it with the sources beside
+// the library and refuses a library built from other sources.
+#ifndef KAN_SOURCE_HASH
+#define KAN_SOURCE_HASH "unset"
+#endif
+
 extern "C" {
 
 const char* kan_hip_last_error(void) { return g_last_error.c_str(); }
+
+const char* kan_hip_source_hash(void) { return KAN_SOURCE_HASH; }
 
 int kan_hip_limits(int64_t* max_deg0_basis, int64_t* max_in_features) {
   if (max_deg0_basis != nullptr) *max_deg0_basis = kMaxDeg0Basis;

@@ -9,12 +9,13 @@ Backend selection (kan_linear.py:127-150, 193-213 of the reference):
   "cuda"      native kernels; raises if the library is missing, the shape is
               unsupported or the input is on the CPU.
   "reference" the pure-PyTorch backend.
-One deliberate difference: with "auto", a device input on a supported shape
-raises RuntimeError when libkan_hip.so is not built, instead of silently
-running the pure-PyTorch path on the device.
+With "auto" and libkan_hip.so not built, device inputs run on the reference
+backend as in the reference; the first such forward emits a RuntimeWarning
+naming the missing library, so the fallback is never silent.
 """
 
 import copy
+import warnings
 from typing import Optional, Tuple
 
 import torch
@@ -37,6 +38,21 @@ REG_IMPLS = ("auto", "dense", "fused", "checkpoint")
 
 CUDA_MAX_DEG0_BASIS = int(getattr(_C, "CUDA_MAX_DEG0_BASIS", 71)) if _C is not None else 71
 CUDA_MAX_IN_FEATURES = int(getattr(_C, "CUDA_MAX_IN_FEATURES", 65535)) if _C is not None else 65535
+
+
+_MISSING_WARNED = False
+
+
+def _warn_missing_library() -> None:
+    """One RuntimeWarning per process when backend="auto" falls back to the
+    reference backend on a device tensor because libkan_hip.so is missing
+    (the reference falls back silently, spline_kan/kan_linear.py:147-148)."""
+    global _MISSING_WARNED
+    if not _MISSING_WARNED:
+        _MISSING_WARNED = True
+        warnings.warn("KANLinear(backend='auto'): libkan_hip.so is not built, so device inputs "
+                      "run on the pure-PyTorch reference backend; build it with "
+                      "`python -m torchsplinekan_amd.build_lib`", RuntimeWarning, stacklevel=3)
 
 
 def native_config_supported(in_features: int, grid_size: int, spline_order: int) -> Tuple[bool, str]:
@@ -122,10 +138,7 @@ class KANLinear(nn.Module):
         if not self._use_cuda:
             if (x.is_cuda and self.backend == "auto" and self._native_ok
                     and not _CUDA_EXT_LOADED):
-                raise RuntimeError(
-                    "KANLinear(backend='auto') received a device tensor but libkan_hip.so is "
-                    "not built; build it (python -m torchsplinekan_amd.build_lib) or choose "
-                    "backend='reference' explicitly.")
+                _warn_missing_library()
             return "reference"
         if self.backend == "cuda" or x.is_cuda:
             return "cuda"
