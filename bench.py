@@ -13,10 +13,14 @@ the device before timing starts.
 
 Prints one JSON line (the benchmark contract): whole-job samples/s, the
 roofline of the dominant kernel (the MFMA contraction, timed live with HIP
-events recorded by the library on the launch stream) and a CPU baseline
-(the numpy oracle on a bounded sample of the same workload, rank 0 only).
+events recorded by the library on the launch stream), a CPU baseline (the
+ATen/MKL formulation of the reference's CPU path, csrc/kan_cpu.cpp, on the
+host's cores, rank 0 only) and, under "other_configs", the same figures for
+BASELINE.json's other single-GPU configs (c2, c4, c5), reported beside the
+metric.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c3|c3-nodx]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
+                       [--workload c3|c3-nodx|c2|c4|c5|stream|refit|pinn|infer]
 """
 
 import argparse
@@ -33,6 +37,7 @@ if ROOT not in sys.path:
 METRIC = "fwd+bwd samples/s, KANLinear 1024→1024 G10 k3 N=64K; % MFMA/HBM roofline"
 PEAK_FP32_MFMA_TFLOPS = 157.3
 PEAK_HBM_GBS = 8000.0
+C3_TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "contraction_c3_traffic.json")
 
 
 def parse():
@@ -41,18 +46,23 @@ def parse():
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workload", default="c3",
-                    choices=["c3", "c3-nodx", "c4", "refit", "pinn", "infer"],
+                    choices=["c3", "c3-nodx", "c2", "c4", "c5", "stream", "refit", "pinn",
+                             "infer"],
                     help="c3 (the metric's config, default), c3-nodx (x without grad, the "
-                         "reference benchmark's semantics), c4 (KAN([256,512,512,64]) with "
-                         "forward_with_regularization), refit (update_grid of c4's 512->512 "
-                         "layer), pinn (Laplacian loss of KAN([2,128,128,1]) through "
-                         "create_graph) or infer (c3's layer, exported, inference forward: "
-                         "throughput at N=65536 and latency at small batches); these are "
-                         "reported separately, not the metric")
-    ap.add_argument("--n", type=int, default=65536, help="samples per step (default: config's 65536)")
+                         "reference benchmark's semantics), c2 (KAN([784,256,10])), c4 "
+                         "(KAN([256,512,512,64]) with forward_with_regularization), c5 "
+                         "(4096->256 G65, the kernel-limit layer), stream (HBM streaming "
+                         "ceiling over a buffer of c3's augmented-basis size), refit "
+                         "(update_grid of c4's 512->512 layer), pinn (Laplacian loss of "
+                         "KAN([2,128,128,1]) through create_graph) or infer (c3's layer, "
+                         "exported, inference forward); all but c3 are reported separately, "
+                         "not the metric")
+    ap.add_argument("--n", type=int, default=0, help="samples per step (default: the config's)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-other-configs", action="store_true",
+                    help="c3 only: skip the c2, c4 and c5 figures of the JSON line")
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
-                    help="target CPU time of the baseline sample")
+                    help="target CPU time of each baseline sample (3 timed repetitions)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a plain 1 GiB device-to-device copy (3 times); the HBM "
                          "counters of this known-size copy scale the counter readings of the "
@@ -71,8 +81,12 @@ def copy_calibration():
     print(json.dumps({"copy_bytes_read": 4 * n, "copy_bytes_written": 4 * n, "launches": 3}))
 
 
+# ---------------------------------------------------------------------------
+# workloads; the GPU parity tests build the same ones
+# ---------------------------------------------------------------------------
+
 def make_inputs(N, I, O, G, k, seed=0):
-    """Seeded CPU draws in a fixed order: x, coef, base_weight, scaler, target."""
+    """c3: seeded CPU draws in a fixed order: x, coef, base_weight, scaler, target."""
     import torch
     g = torch.Generator().manual_seed(seed)
     x = torch.rand(N, I, generator=g) * 2 - 1
@@ -83,59 +97,53 @@ def make_inputs(N, I, O, G, k, seed=0):
     return x, coef, bw, scaler, target
 
 
-def cpu_baseline(x, coef, bw, scaler, target, grid, k, need_dx, seconds):
-    """The numpy oracle (restatement of the reference CPU path: basis
-    recurrence, BLAS GEMMs, analytic backward) timed on this host on
-    consecutive 1024-row chunks of the same workload until `seconds` of work
-    are done; returns samples/s, BLAS threads and the sample description."""
-    import numpy as np
-    from oracle import kan_oracle as ko
-    try:
-        from threadpoolctl import threadpool_info
-        threads = max([p.get("num_threads", 1) for p in threadpool_info()
-                       if p.get("user_api") == "blas"] or [1])
-    except Exception:  # threadpoolctl missing: report the env setting
-        threads = int(os.environ.get("OMP_NUM_THREADS", "1"))
-    N, O = target.shape
-    gridn = grid.numpy()
-    sw, bwn, sc = coef.numpy(), bw.numpy(), scaler.numpy()
-    chunk = 1024
-    done, t_total = 0, 0.0
-    for n0 in range(0, N, chunk):
-        xs = x[n0:n0 + chunk].numpy()
-        ts = target[n0:n0 + chunk].numpy()
-        t0 = time.perf_counter()
-        y, H = ko.kan_forward(xs, gridn, bwn, sw, sc, k)
-        D = (np.float32(2.0) / np.float32(N * O)) * (y - ts)
-        if need_dx:
-            ko.kan_backward(D, xs, gridn, bwn, sw, sc, k, basis=H)
-        else:
-            ko.kan_backward_params(D, xs, bwn, sw, sc, H)
-        t_total += time.perf_counter() - t0
-        done += xs.shape[0]
-        if t_total >= seconds:
-            break
-    return {
-        "value": done / t_total,
-        "unit": "samples/s",
-        "cores": threads,
-        "kind": "port",
-        "sample": (f"numpy oracle (oracle/kan_oracle.py) fp32 fwd+MSE+bwd of the first {done} of "
-                   f"{N} rows in {chunk}-row chunks, {t_total:.1f} s; BLAS threads={threads}, "
-                   f"elementwise work single-threaded; host {os.cpu_count()} logical CPUs"),
-    }
-
-
-def bench_c4(args):
-    """KAN([256, 512, 512, 64], grid_size=8, spline_order=3) fp32, knots from
-    update_grid on x drawn from a 4-component Gaussian mixture (means +-0.5,
-    +-0.8, sd 0.1), N=16384; one step is forward_with_regularization(1e-2,
-    1e-2, reg_impl="auto") + MSE + backward (x without grad)."""
+def build_c3(dev, N=65536, need_dx=True):
+    """(layer on dev, x on dev with requires_grad=need_dx, target on dev,
+    CPU copies of (x, coef, bw, scaler, target, grid)) for c3."""
     import torch
-    import torch.nn.functional as F
-    from torchsplinekan_amd import KAN, _lib
-    dev = torch.device("cuda", 0)
-    N, widths = args.n if args.n != 65536 else 16384, [256, 512, 512, 64]
+    from torchsplinekan_amd import KANLinear
+    I = O = 1024
+    G, k = 10, 3
+    x, coef, bw, scaler, target = make_inputs(N, I, O, G, k, seed=0)
+    L = KANLinear(I, O, grid_size=G, spline_order=k, backend="cuda")
+    with torch.no_grad():
+        L.spline_weight.copy_(coef)
+        L.base_weight.copy_(bw)
+        L.spline_scaler.copy_(scaler)
+    grid_cpu = L.grid.detach().clone()
+    L = L.to(dev)
+    xd = x.to(dev).requires_grad_(need_dx)
+    return L, xd, target.to(dev), (x, coef, bw, scaler, target, grid_cpu)
+
+
+def build_c2(dev, N=4096):
+    """c2: KAN([784, 256, 10], G=5, k=3) fp32, uniform knots on [-1, 1];
+    x ~ U(-1, 1) [N, 784]; coef ~ N(0, 0.1); base_weight Kaiming-uniform
+    (the layer's default init, global seed 0); scaler = 1; target ~ N(0, 1).
+    Returns (net on dev, x, target) with x and target on the CPU."""
+    import torch
+    from torchsplinekan_amd import KAN
+    g = torch.Generator().manual_seed(2)
+    x = torch.rand(N, 784, generator=g) * 2 - 1
+    target = torch.randn(N, 10, generator=g)
+    torch.manual_seed(0)
+    net = KAN([784, 256, 10], grid_size=5, spline_order=3, backend="cuda")
+    with torch.no_grad():
+        for layer in net.layers:
+            layer.spline_weight.normal_(0.0, 0.1, generator=g)
+            layer.spline_scaler.fill_(1.0)
+    return net.to(dev), x, target
+
+
+def build_c4(dev, N=16384):
+    """c4: KAN([256, 512, 512, 64], G=8, k=3) fp32; x [N, 256] from a
+    4-component Gaussian mixture (means +-0.5, +-0.8, sd 0.1, equal weights);
+    coef ~ N(0, 0.1); knots and coefficients then set by the network's
+    update_grid on x (on the device: native Gram kernel + float64 device
+    solve).  Returns (net on dev, x on dev, target on dev)."""
+    import torch
+    from torchsplinekan_amd import KAN
+    widths = [256, 512, 512, 64]
     g = torch.Generator().manual_seed(0)
     means = torch.tensor([-0.8, -0.5, 0.5, 0.8])
     comp = torch.randint(0, 4, (N, widths[0]), generator=g)
@@ -147,8 +155,262 @@ def bench_c4(args):
         for layer in net.layers:
             layer.spline_weight.normal_(0.0, 0.1, generator=g)
     net = net.to(dev)
+    xd = x.to(dev)
+    net.update_grid(xd)
+    return net, xd, target.to(dev)
+
+
+def build_c5(dev, N=8192):
+    """c5: KANLinear(4096 -> 256, G=65, k=3) fp32 (72 knots, R = 68) on uniform
+    [-1, 1] knots; x ~ U(-1.1, 1.1) [N, 4096] (0.7 % of the inputs fall
+    outside [t_0, t_71] and take the zero-basis path); coef ~ N(0, 0.05);
+    base_weight and scaler from the layer's default init (global seed 0);
+    target ~ N(0, 1).  Returns (layer on dev, x on the CPU, target on the CPU)."""
+    import torch
+    from torchsplinekan_amd import KANLinear
+    g = torch.Generator().manual_seed(5)
+    x = (torch.rand(N, 4096, generator=g) * 2 - 1) * 1.1
+    target = torch.randn(N, 256, generator=g)
+    torch.manual_seed(0)
+    L = KANLinear(4096, 256, grid_size=65, spline_order=3, backend="cuda")
+    with torch.no_grad():
+        L.spline_weight.normal_(0.0, 0.05, generator=g)
+    return L.to(dev), x, target
+
+
+def contraction_flops(N, I, O, R):
+    """Dense-equivalent flops of one contraction: 2 N O I (R + 1)."""
+    return 2.0 * N * O * I * (R + 1)
+
+
+# ---------------------------------------------------------------------------
+# CPU baseline (the reference CPU path's formulation, csrc/kan_cpu.cpp)
+# ---------------------------------------------------------------------------
+
+def host_cpu():
+    """lscpu-style facts of this host: model name, physical cores, logical
+    CPUs, CPUs this process may run on, and the thread count the baseline
+    uses (physical cores, capped by the CPU share and OMP_NUM_THREADS)."""
+    model, cores = "unknown", set()
+    phys = core = None
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                key, _, val = line.partition(":")
+                key, val = key.strip(), val.strip()
+                if key == "model name" and model == "unknown":
+                    model = val
+                elif key == "physical id":
+                    phys = val
+                elif key == "core id":
+                    core = val
+                elif not key and phys is not None and core is not None:
+                    cores.add((phys, core))
+                    phys = core = None
+        if phys is not None and core is not None:
+            cores.add((phys, core))
+    except OSError:
+        pass
+    logical = os.cpu_count() or 1
+    try:
+        share = len(os.sched_getaffinity(0))
+    except AttributeError:
+        share = logical
+    physical = len(cores) or logical
+    threads = min(physical, share)
+    omp = os.environ.get("OMP_NUM_THREADS", "")
+    if omp.isdigit() and int(omp) > 0:
+        threads = min(threads, int(omp))
+    return {"model": model, "physical_cores": physical, "logical_cpus": logical,
+            "cpus_allowed": share, "threads": max(1, threads)}
+
+
+def _median_reps(run_rows, total_rows, chunk, seconds):
+    """Times run_rows(n0, n1) over the first rows of the workload: one
+    untimed chunk, then the number of chunks that makes one repetition
+    about seconds/3, three timed repetitions; -> (rows, median seconds,
+    all repetition times)."""
+    n1 = min(chunk, total_rows)
+    t0 = time.perf_counter()
+    run_rows(0, n1)
+    per_chunk = time.perf_counter() - t0
+    chunks = max(1, min(-(-total_rows // chunk), int(seconds / 3.0 / max(per_chunk, 1e-6))))
+    rows = min(total_rows, chunks * chunk)
+    reps = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        for a in range(0, rows, chunk):
+            run_rows(a, min(a + chunk, rows))
+        reps.append(time.perf_counter() - t0)
+    return rows, statistics.median(reps), reps
+
+
+def cpu_baseline_layers(layers, x, target, need_dx, seconds, chunk, label):
+    """Forward + MSE + backward of a stack of KAN layers on the host through
+    the ATen formulation of csrc/kan_cpu.cpp (the raw ops' CPU dispatch:
+    dense Cox-de Boor basis, MKL GEMMs, analytic backward), on consecutive
+    row chunks of the same inputs.  `layers` are (grid, bw, sw, scaler)
+    float32 CPU tensors; the loss scale is the full batch's, so every chunk
+    does the work it does inside the full step."""
+    import torch
+    from torchsplinekan_amd import _C
+    info = host_cpu()
+    prev = torch.get_num_threads()
+    torch.set_num_threads(info["threads"])
+    params = [(g, bw.clone().requires_grad_(), sw.clone().requires_grad_(),
+               sc.clone().requires_grad_()) for g, bw, sw, sc in layers]
+    scale = float(target.numel())
+
+    def run_rows(n0, n1):
+        h = x[n0:n1].clone().requires_grad_(need_dx)
+        out = h
+        for g, bw, sw, sc in params:
+            out = _C.kan_apply(out, g, bw, sw, sc, 3, True)
+        loss = ((out - target[n0:n1]) ** 2).sum() / scale
+        loss.backward()
+        for _, bw, sw, sc in params:
+            bw.grad = sw.grad = sc.grad = None
+
+    try:
+        rows, med, reps = _median_reps(run_rows, x.shape[0], chunk, seconds)
+    finally:
+        torch.set_num_threads(prev)
+    return {
+        "value": rows / med, "unit": "samples/s", "cores": info["threads"], "kind": "port",
+        "sample": (f"{label}: the ATen/MKL formulation of csrc/kan_cpu.cpp (raw-op CPU "
+                   f"dispatch, torchsplinekan_amd/composite.py) fp32 fwd + MSE + bwd "
+                   f"{'with' if need_dx else 'without'} dx on the first {rows} of "
+                   f"{x.shape[0]} rows in {chunk}-row chunks; median of 3 repetitions "
+                   f"({', '.join(f'{r:.2f}' for r in reps)} s)"),
+        "host": info, "torch_threads": info["threads"],
+    }
+
+
+def cpu_baseline_c4(net_cpu, x, target, seconds, chunk=512):
+    """c4 on the host through the reference backend (backend="reference" on
+    CPU tensors: forward_with_regularization resolves reg_impl "auto" to the
+    dense [n, O, I] edge tensor, spline_kan/kan_linear.py:398-422), on row
+    chunks; the edge means are per chunk."""
+    import torch
+    info = host_cpu()
+    prev = torch.get_num_threads()
+    torch.set_num_threads(info["threads"])
+    scale = float(target.numel())
+
+    def run_rows(n0, n1):
+        for p in net_cpu.parameters():
+            p.grad = None
+        y, reg = net_cpu.forward_with_regularization(x[n0:n1], 1e-2, 1e-2, reg_impl="auto")
+        (((y - target[n0:n1]) ** 2).sum() / scale + reg).backward()
+
+    try:
+        rows, med, reps = _median_reps(run_rows, x.shape[0], chunk, seconds)
+    finally:
+        torch.set_num_threads(prev)
+    return {
+        "value": rows / med, "unit": "samples/s", "cores": info["threads"], "kind": "port",
+        "sample": (f"c4 on the reference backend (torchsplinekan_amd/reference_backend.py, the "
+                   f"restated spline_kan reference path) fp32 forward_with_regularization "
+                   f"(reg_impl 'auto' -> dense on CPU) + MSE + backward on the first {rows} of "
+                   f"{x.shape[0]} rows in {chunk}-row chunks (edge means per chunk); median of "
+                   f"3 repetitions ({', '.join(f'{r:.2f}' for r in reps)} s)"),
+        "host": info, "torch_threads": info["threads"],
+    }
+
+
+def _layer_tensors(layer):
+    """(grid, base_weight, spline_weight, spline_scaler) as float32 CPU tensors."""
+    f = lambda t: t.detach().float().cpu().clone()
+    return f(layer.grid), f(layer.base_weight), f(layer.spline_weight), f(layer.spline_scaler)
+
+
+# ---------------------------------------------------------------------------
+# timed GPU steps
+# ---------------------------------------------------------------------------
+
+def timed_steps(step, steps, warmup, classes):
+    """warmup untimed steps, then `steps` timed ones between two device
+    synchronisations, with the library's per-launch HIP-event timing on:
+    -> (wall seconds, {class: (ms, launches, work)})."""
+    import torch
+    from torchsplinekan_amd import _lib
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    _lib.timing_enable(True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    kern = {c: _lib.timing_read(c) for c in classes}
+    _lib.timing_enable(False)
+    return wall, kern
+
+
+def _mfma_roofline(kern, cls, kernel_name, traffic=None, traffic_source=None):
+    ms, cnt, work = kern[cls]
+    ach = work / (ms * 1e-3) / 1e12 if cnt else 0.0
+    return {"bound": "mfma", "kernel": kernel_name, "achieved": ach,
+            "peak": PEAK_FP32_MFMA_TFLOPS, "unit": "TFLOP/s", "frac": ach / PEAK_FP32_MFMA_TFLOPS,
+            "traffic": traffic, "traffic_source": traffic_source,
+            "flop_per_launch": work / max(cnt, 1), "avg_launch_ms": ms / max(cnt, 1),
+            "launches": cnt}
+
+
+def _line(metric, N, steps, warmup, wall, workload, roofline, kern, **extra):
+    line = {
+        "metric": metric, "value": N * steps / wall, "unit": "samples/s", "n_gpus": 1,
+        "steps": steps, "warmup": warmup, "ms_per_step": wall * 1e3 / steps,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic (seeded torch.Generator draws, random-init weights of the config)",
+        "config": {"workload": workload}, "roofline": roofline,
+        "kernels": {c: {"ms_per_step": v[0] / steps, "launches_per_step": v[1] / steps}
+                    for c, v in kern.items()},
+    }
+    line.update(extra)
+    return line
+
+
+def run_c2(args, dev, steps, warmup):
+    """c2: KAN([784, 256, 10]) G5 k3 fp32, N = 4096, fwd + MSE + bwd (x
+    without grad, the network input of a classifier)."""
+    import torch
+    import torch.nn.functional as F
+    N = args.n or 4096
+    net, x, target = build_c2(dev, N)
     xd, td = x.to(dev), target.to(dev)
-    net.update_grid(xd)          # before timing (least squares on the host)
+
+    def step():
+        for p in net.parameters():
+            p.grad = None
+        F.mse_loss(net(xd), td).backward()
+
+    wall, kern = timed_steps(step, steps, warmup, ("contraction", "basis", "basis_grad", "other"))
+    if any(l.last_backend != "cuda" for l in net.layers):
+        raise RuntimeError("c2 did not run on the native backend")
+    line = _line("fwd+bwd samples/s, KAN([784,256,10]) G5 k3 N=4096", N, steps, warmup, wall,
+                 "c2: KAN([784,256,10], G=5, k=3) fp32, N=%d, fwd + MSE + bwd (x without "
+                 "grad)" % N,
+                 _mfma_roofline(kern, "contraction", "gemm_pipe_kernel (fp32 MFMA contraction; "
+                                "forward and parameter products of both layers, input product "
+                                "of the second)"), kern)
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = cpu_baseline_layers(
+            [_layer_tensors(l) for l in net.layers], x, target, False, args.cpu_seconds, 1024,
+            "c2")
+    return line
+
+
+def run_c4(args, dev, steps, warmup):
+    """c4: KAN([256, 512, 512, 64]) G8 k3 fp32 with update_grid knots, N =
+    16384; one step is forward_with_regularization(1e-2, 1e-2, "auto") + MSE
+    + backward (x without grad)."""
+    import torch
+    import torch.nn.functional as F
+    N = args.n or 16384
+    net, xd, td = build_c4(dev, N)
 
     def step():
         for p in net.parameters():
@@ -156,51 +418,63 @@ def bench_c4(args):
         y, reg = net.forward_with_regularization(xd, 1e-2, 1e-2, reg_impl="auto")
         (F.mse_loss(y, td) + reg).backward()
 
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-    _lib.timing_enable(True)
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        step()
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
+    wall, kern = timed_steps(step, steps, warmup, ("edge", "edge_grad", "basis", "basis_grad",
+                                                   "contraction", "other"))
     if any(l.last_backend != "cuda" for l in net.layers):
         raise RuntimeError("c4 did not run the fused native path")
-    kern = {c: _lib.timing_read(c) for c in ("edge", "edge_grad", "basis", "basis_grad",
-                                             "contraction", "other")}
-    _lib.timing_enable(False)
+    # dominant kernel class: the edge-statistic backward on FP32 MFMA (fused
+    # kernel for the layers that need both gradient sides: phi once plus two
+    # products, 6 n O I (R+1) flops; parameter kernel for the first layer,
+    # whose input needs no gradient: 4 n O I (R+1))
+    roof = _mfma_roofline(kern, "edge_grad", "edge_bwd_mfma_kernel (both gradient sides, "
+                          "dL/dy folded in) + edge_param_mfma_kernel (first layer): mean|phi| "
+                          "backward", traffic=None,
+                          traffic_source="profiles/edge_counters_c4.txt (rocprofv3 --pmc, per "
+                                         "kernel; not per class)")
     e_ms, e_cnt, e_work = kern["edge"]
-    eg_ms, eg_cnt, eg_work = kern["edge_grad"]
-    c_ms, c_cnt, c_work = kern["contraction"]
-    ach = e_work / (e_ms * 1e-3) / 1e12 if e_cnt else 0.0
-    ach_g = eg_work / (eg_ms * 1e-3) / 1e12 if eg_cnt else 0.0
-    ach_c = c_work / (c_ms * 1e-3) / 1e12 if c_cnt else 0.0
-    line = {
-        "metric": "fwd+bwd samples/s, KAN([256,512,512,64]) G8 k3 N=16K forward_with_regularization",
-        "value": N * args.steps / wall, "unit": "samples/s", "n_gpus": 1, "steps": args.steps,
-        "warmup": args.warmup, "ms_per_step": wall * 1e3 / args.steps, "higher_is_better": True,
-        "scaling": "weak", "vs_baseline": None, "dtype": "f32",
-        "data": "synthetic (Gaussian-mixture x, seeded; knots from update_grid)",
-        "config": {"workload": "c4: KAN([256,512,512,64], G=8, k=3) fp32, N=%d, "
-                               "forward_with_regularization(1e-2, 1e-2, 'auto') + MSE + backward" % N},
-        # dominant kernel class: the edge-statistic backward on FP32 MFMA
-        # (fused kernel for layers that need both gradient sides: phi once
-        # plus two products, 6 n O I (R+1) flops; parameter kernel for the
-        # first layer, whose input needs no gradient: 4 n O I (R+1))
-        "roofline": {"bound": "mfma",
-                     "kernel": "edge_bwd_mfma_kernel (both gradient sides) + edge_param_mfma_kernel "
-                               "(first layer): mean|phi| backward",
-                     "achieved": ach_g, "peak": PEAK_FP32_MFMA_TFLOPS, "unit": "TFLOP/s",
-                     "frac": ach_g / PEAK_FP32_MFMA_TFLOPS, "traffic": None,
-                     "flop_per_launch": eg_work / max(eg_cnt, 1),
-                     "avg_launch_ms": eg_ms / max(eg_cnt, 1), "launches": eg_cnt},
-        "kernels": {k_: {"ms_per_step": v[0] / args.steps, "launches_per_step": v[1] / args.steps}
-                    for k_, v in kern.items()},
-        "edge_forward_tflops": ach,
-        "contraction_tflops": ach_c,
-    }
-    print(json.dumps(line), flush=True)
+    line = _line("fwd+bwd samples/s, KAN([256,512,512,64]) G8 k3 N=16K forward_with_regularization",
+                 N, steps, warmup, wall,
+                 "c4: KAN([256,512,512,64], G=8, k=3) fp32, N=%d, update_grid knots, "
+                 "forward_with_regularization(1e-2, 1e-2, 'auto') + MSE + backward" % N, roof,
+                 kern, edge_forward_tflops=e_work / (e_ms * 1e-3) / 1e12 if e_cnt else 0.0)
+    if not args.no_cpu_baseline:
+        from torchsplinekan_amd import KAN
+        net_cpu = KAN([256, 512, 512, 64], grid_size=8, spline_order=3, backend="reference")
+        net_cpu.load_state_dict({k_: v.detach().cpu() for k_, v in net.state_dict().items()})
+        line["cpu_baseline"] = cpu_baseline_c4(net_cpu, xd.cpu(), td.cpu(), args.cpu_seconds)
+    return line
+
+
+def run_c5(args, dev, steps, warmup):
+    """c5: KANLinear(4096 -> 256, G=65, k=3) fp32, N = 8192, fwd + MSE + bwd
+    with dx (three contractions of K = 4096 x 69 = 282624)."""
+    import torch
+    import torch.nn.functional as F
+    N = args.n or 8192
+    L, x, target = build_c5(dev, N)
+    xd, td = x.to(dev).requires_grad_(), target.to(dev)
+
+    def step():
+        for p in L.parameters():
+            p.grad = None
+        xd.grad = None
+        F.mse_loss(L(xd), td).backward()
+
+    wall, kern = timed_steps(step, steps, warmup, ("contraction", "basis", "basis_grad", "other"))
+    if L.last_backend != "cuda":
+        raise RuntimeError("c5 did not run on the native backend")
+    line = _line("fwd+bwd samples/s, KANLinear 4096->256 G65 k3 N=8192", N, steps, warmup, wall,
+                 "c5: KANLinear(4096->256, G=65, k=3) fp32, N=%d, x ~ U(-1.1, 1.1), fwd + MSE "
+                 "+ bwd with dx (3 contractions)" % N,
+                 _mfma_roofline(kern, "contraction", "gemm_pipe_kernel (fp32 MFMA contraction; "
+                                "forward, parameter and input products)"), kern)
+    b_ms, b_cnt, b_work = kern["basis"]
+    if b_cnt:
+        line["basis_GBps"] = b_work / max(b_cnt, 1) / (b_ms / b_cnt * 1e-3) / 1e9
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = cpu_baseline_layers([_layer_tensors(L)], x, target, True,
+                                                   args.cpu_seconds, 256, "c5")
+    return line
 
 
 def bench_refit(args):
@@ -212,7 +486,7 @@ def bench_refit(args):
     import torch
     from torchsplinekan_amd import KANLinear
     from torchsplinekan_amd.reference_backend import ReferenceKANLayer
-    N, I, O, G, k = (args.n if args.n != 65536 else 16384), 512, 512, 8, 3
+    N, I, O, G, k = (args.n or 16384), 512, 512, 8, 3
     g = torch.Generator().manual_seed(0)
     means = torch.tensor([-0.8, -0.5, 0.5, 0.8])
     x = means[torch.randint(0, 4, (N, I), generator=g)] + 0.1 * torch.randn(N, I, generator=g)
@@ -274,7 +548,7 @@ def bench_pinn(args):
     from torchsplinekan_amd import KAN, _C, _lib
     from torchsplinekan_amd import composite as cmp
     dev = torch.device("cuda", 0)
-    N = args.n if args.n != 65536 else 16384
+    N = args.n or 16384
     widths, G, k = [2, 128, 128, 1], 8, 3
     g = torch.Generator().manual_seed(0)
     x = torch.rand(N, 2, generator=g, dtype=torch.float64) * 1.8 - 0.9
@@ -431,6 +705,42 @@ def bench_infer(args):
     print(json.dumps(line), flush=True)
 
 
+
+def bench_stream(args):
+    """HBM streaming ceiling of this GPU for buffers of c3's size: float4
+    write, read and copy kernels (kan_hip_stream_probe) over a buffer of the
+    c3 augmented basis' size (65536 x 14336 fp32 = 3.76 GB), each timed with
+    the library's HIP events; the basis kernels' GB/s are judged against
+    these."""
+    import torch
+    from torchsplinekan_amd import _C, _lib
+    dev = torch.device("cuda", 0)
+    nbytes = 65536 * 14336 * 4
+    a = torch.empty(nbytes // 4, dtype=torch.float32, device=dev)
+    b = torch.zeros(nbytes // 4, dtype=torch.float32, device=dev)
+    out = {}
+    for mode, name, moved in ((0, "write", nbytes), (1, "read", nbytes), (2, "copy", 2 * nbytes)):
+        for _ in range(args.warmup):
+            _C.stream_probe(mode, a, b)
+        torch.cuda.synchronize()
+        _lib.timing_enable(True)
+        for _ in range(args.steps):
+            _C.stream_probe(mode, a, b)
+        torch.cuda.synchronize()
+        ms, cnt, _ = _lib.timing_read("stream")
+        _lib.timing_enable(False)
+        avg = ms / max(cnt, 1)
+        out[name] = {"avg_ms": avg, "GB/s": moved / (avg * 1e-3) / 1e9,
+                     "frac_of_8TBps": moved / (avg * 1e-3) / 1e9 / PEAK_HBM_GBS,
+                     "bytes_per_launch": moved, "launches": cnt}
+    line = {"metric": "HBM streaming GB/s (float4 kernels, c3 augmented-basis-sized buffer)",
+            "value": out["write"]["GB/s"], "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+            "warmup": args.warmup, "higher_is_better": True, "dtype": "f32",
+            "data": "synthetic", "config": {"workload": "stream: %d-byte buffer" % nbytes},
+            "modes": out}
+    print(json.dumps(line), flush=True)
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -445,40 +755,26 @@ def main():
 
     import torch
     import torch.nn.functional as F
-    from torchsplinekan_amd import KANLinear, _lib
 
     if not torch.cuda.is_available():
         print("bench.py: no ROCm device visible", file=sys.stderr)
         sys.exit(1)
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
-    if args.workload == "c4":
-        bench_c4(args)
+    single = {"c2": run_c2, "c4": run_c4, "c5": run_c5}
+    if args.workload in single:
+        print(json.dumps(single[args.workload](args, dev, args.steps, args.warmup)), flush=True)
         return
-    if args.workload == "infer":
-        bench_infer(args)
-        return
-    if args.workload == "pinn":
-        bench_pinn(args)
-        return
-    if args.workload == "refit":
-        bench_refit(args)
+    other = {"stream": bench_stream, "infer": bench_infer, "pinn": bench_pinn,
+             "refit": bench_refit}
+    if args.workload in other:
+        other[args.workload](args)
         return
 
-    I = O = 1024
-    G, k = 10, 3
-    N = args.n
+    N = args.n or 65536
     need_dx = args.workload == "c3"
-    x, coef, bw, scaler, target = make_inputs(N, I, O, G, k, seed=0)
-    L = KANLinear(I, O, grid_size=G, spline_order=k, backend="cuda")
-    with torch.no_grad():
-        L.spline_weight.copy_(coef)
-        L.base_weight.copy_(bw)
-        L.spline_scaler.copy_(scaler)
-    grid_cpu = L.grid.detach().clone()
-    L = L.to(dev)
-    xd = x.to(dev).requires_grad_(need_dx)
-    td = target.to(dev)
+    L, xd, td, cpu_inputs = build_c3(dev, N, need_dx)
+    I, O, R = L.in_features, L.out_features, L.grid_size + L.spline_order
     torch.cuda.synchronize()
 
     def step():
@@ -493,6 +789,7 @@ def main():
         step()
     torch.cuda.synchronize()
 
+    from torchsplinekan_amd import _lib
     stream = torch.cuda.current_stream(dev)
     ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
           for _ in range(args.steps)]
@@ -508,35 +805,31 @@ def main():
     if L.last_backend != "cuda":
         raise RuntimeError("the timed steps did not run on the native backend")
     step_ms = [a.elapsed_time(b) for a, b in ev]
-    kernels = {}
-    for cls in ("contraction", "basis", "basis_grad", "other"):
-        ms, cnt, work = _lib.timing_read(cls)
-        kernels[cls] = (ms, cnt, work)
+    kernels = {cls: _lib.timing_read(cls) for cls in ("contraction", "basis", "basis_grad",
+                                                       "other")}
     _lib.timing_enable(False)
 
-    ms_per_step = wall * 1e3 / args.steps
-    value = N * args.steps / wall
-
     c_ms, c_cnt, c_work = kernels["contraction"]
-    c_avg_ms = c_ms / max(c_cnt, 1)
-    c_flop = c_work / max(c_cnt, 1)
-    achieved = c_flop / (c_avg_ms * 1e-3) / 1e12 if c_cnt else 0.0
     traffic = None
-    tpath = os.path.join(ROOT, "profiles", "contraction_c3_traffic.json")
-    if os.path.exists(tpath):
-        with open(tpath) as f:
+    if os.path.exists(C3_TRAFFIC_PROFILE):
+        with open(C3_TRAFFIC_PROFILE) as f:
             traffic = json.load(f).get("hbm_bytes_per_launch")
+    roof = _mfma_roofline(kernels, "contraction",
+                          "gemm_pipe_kernel (fp32 MFMA contraction; average over the forward, "
+                          "parameter and input launches)", traffic,
+                          "recorded: profiles/hbm_traffic_c3.txt (rocprofv3 --pmc FETCH_SIZE "
+                          "and WRITE_SIZE, calibrated on a 1 GiB copy), not measured in this run")
     b_ms, b_cnt, b_work = kernels["basis"]
     g_ms, g_cnt, g_work = kernels["basis_grad"]
-
+    gbps = lambda w, ms, n: (w / n) / (ms / n * 1e-3) / 1e9 if n else None
     line = {
         "metric": METRIC,
-        "value": value,
+        "value": N * args.steps / wall,
         "unit": "samples/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": ms_per_step,
+        "ms_per_step": wall * 1e3 / args.steps,
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -546,36 +839,34 @@ def main():
             "workload": ("c3: KANLinear(1024->1024, grid_size=10, spline_order=3) fp32, N=%d, "
                          "fwd + MSE + bwd %s" % (N, "with dx (3 contractions)" if need_dx
                                                  else "without dx (2 contractions)")),
-            "in_features": I, "out_features": O, "grid_size": G, "spline_order": k,
-            "samples_per_step": N, "x_requires_grad": need_dx,
+            "in_features": I, "out_features": O, "grid_size": L.grid_size,
+            "spline_order": L.spline_order, "samples_per_step": N, "x_requires_grad": need_dx,
         },
-        "roofline": {
-            "bound": "mfma",
-            "kernel": "gemm_pipe_kernel (fp32 MFMA contraction; average over the forward, parameter and input launches)",
-            "achieved": achieved,
-            "peak": PEAK_FP32_MFMA_TFLOPS,
-            "unit": "TFLOP/s",
-            "frac": achieved / PEAK_FP32_MFMA_TFLOPS,
-            "traffic": traffic,
-            "flop_per_launch": c_flop,
-            "avg_launch_ms": c_avg_ms,
-            "launches": c_cnt,
-        },
+        "roofline": roof,
         "step_ms_median_events": statistics.median(step_ms),
         "kernels": {
             "basis": {"avg_ms": b_ms / max(b_cnt, 1), "launches": b_cnt,
-                      "GB/s": (b_work / max(b_cnt, 1)) / (b_ms / max(b_cnt, 1) * 1e-3) / 1e9
-                      if b_cnt else None},
+                      "GB/s": gbps(b_work, b_ms, b_cnt)},
             "basis_grad": {"avg_ms": g_ms / max(g_cnt, 1), "launches": g_cnt,
-                           "GB/s": (g_work / max(g_cnt, 1)) / (g_ms / max(g_cnt, 1) * 1e-3) / 1e9
-                           if g_cnt else None},
+                           "GB/s": gbps(g_work, g_ms, g_cnt)},
             "contraction_ms_per_step": c_ms / args.steps,
             "other_ms_per_step": kernels["other"][0] / args.steps,
         },
     }
     if not args.no_cpu_baseline:
-        line["cpu_baseline"] = cpu_baseline(x, coef, bw, scaler, target, grid_cpu, k, need_dx,
-                                            args.cpu_seconds)
+        x, coef, bw, scaler, target, grid = cpu_inputs
+        line["cpu_baseline"] = cpu_baseline_layers([(grid, bw, coef, scaler)], x, target, need_dx,
+                                                   args.cpu_seconds, 2048, "c3")
+    if args.workload == "c3" and not args.no_other_configs and not args.n:
+        del L, xd, td, cpu_inputs
+        torch.cuda.empty_cache()
+        line["other_configs"] = {}
+        for name, fn in (("c2", run_c2), ("c4", run_c4), ("c5", run_c5)):
+            try:
+                line["other_configs"][name] = fn(args, dev, args.steps, args.warmup)
+            except Exception as exc:  # reported in the line; the metric stands on its own
+                line["other_configs"][name] = {"error": f"{type(exc).__name__}: {exc}"}
+            torch.cuda.empty_cache()
     print(json.dumps(line), flush=True)
 
 

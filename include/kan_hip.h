@@ -281,9 +281,17 @@ int kan_hip_refit_gram(int dtype, const void* x_t, const void* grid_old, const v
  * returns the summed duration (ms), the launch count and the summed work
  * (flops for class 0, bytes for classes 1-2, flops for classes 3-4).
  * Classes: 0 contraction GEMM, 1 basis, 2 basis_grad, 3 edge statistic,
- * 4 edge statistic backward, 5 packing/finalize. */
+ * 4 edge statistic backward, 5 packing/finalize, 6 streaming probe. */
 int kan_hip_timing_enable(int on);
 int kan_hip_timing_read(int kernel_class, double* total_ms, int64_t* launches, double* work);
+
+/* Streaming probe (measurement support, no reference counterpart): float4
+ * kernels that write a (mode 0), read a (mode 1; b receives nothing in
+ * practice but must be a valid 4-byte buffer) or copy a to b (mode 2), over
+ * `bytes` (a multiple of 16; 16-byte aligned buffers).  Timed as kernel
+ * class 6 with the bytes moved as work; the HBM ceiling the memory-bound
+ * kernels are compared with. */
+int kan_hip_stream_probe(int mode, void* a, void* b, int64_t bytes, void* stream);
 
 #ifdef __cplusplus
 }

@@ -43,6 +43,9 @@ How each function is pinned (tests/test_oracle.py):
   kan_backward      finite differences of kan_forward (all four gradients);
                     config-1 golden vectors.
   edge_abs_mean     brute-force per-(n,o,i) loop.
+  edge_abs_mean_by_feature
+                    agreement with edge_abs_mean to 1e-13 in float64 (with
+                    and without the base branch, on a feature subset).
   edge_abs_mean_backward
                     finite differences of edge_abs_mean away from phi = 0.
   regularization_from_edge_means (+ _grad)
@@ -79,6 +82,7 @@ __all__ = [
     "kan_backward",
     "kan_backward_params",
     "edge_abs_mean",
+    "edge_abs_mean_by_feature",
     "edge_abs_mean_backward",
     "regularization_from_edge_means",
     "regularization_grad",
@@ -432,6 +436,33 @@ def edge_abs_mean(s, H, bw, W, chunk=256):
         sc = s[n0:n0 + chunk] if s is not None else None
         acc += np.abs(_phi_chunk(sc, H[n0:n0 + chunk], bw, W)).sum(axis=0)
     return acc / H.dtype.type(N)
+
+
+def edge_abs_mean_by_feature(s, H, bw, W, features=None, workers=8):
+    """The statistic of edge_abs_mean, one input feature at a time: column i
+    of a is (1/N) sum_n |[s_i | H_i] [bw_i | W_i]^T|, a [N, R+1] x [R+1, O]
+    product per feature, the features spread over `workers` threads (numpy
+    releases the GIL in the products and reductions).  Same arithmetic as
+    edge_abs_mean (spline_kan/reference_backend.py:128-146) in a form whose
+    cost is a few seconds at a network layer of 16384 samples x 512 x 512
+    edges.  `features` selects columns (default all) -> a [O, len(features)]."""
+    from concurrent.futures import ThreadPoolExecutor
+    N, I, R = H.shape
+    feats = list(range(I)) if features is None else list(features)
+    dt = np.float64 if H.dtype == np.float64 else H.dtype
+
+    def column(i):
+        A = H[:, i, :]
+        B = W[:, i, :]
+        if bw is not None:
+            A = np.concatenate([s[:, i:i + 1], A], axis=1)
+            B = np.concatenate([bw[:, i:i + 1], B], axis=1)
+        return np.abs(A @ B.T).sum(axis=0, dtype=dt)
+
+    with ThreadPoolExecutor(max(1, workers)) as ex:
+        cols = list(ex.map(column, feats))
+    out = np.stack(cols, axis=1) if cols else np.zeros((W.shape[0], 0), dtype=dt)
+    return out / dt(N)
 
 
 def edge_abs_mean_backward(ga, s, H, bw, W, chunk=256):

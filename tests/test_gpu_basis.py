@@ -9,7 +9,7 @@ import pytest
 import torch
 
 from oracle import kan_oracle as ko
-from tests._util import make_grid, make_points, np64
+from tests._util import make_grid, make_points, normwise, np64
 
 pytestmark = pytest.mark.gpu
 
@@ -58,12 +58,47 @@ def test_basis_fp32_and_out_of_range_rows_exact(C, k, impl):
     assert out.any()
     assert (H[out] == 0).all()
     assert (ref[out] == 0).all()
-    # the zero pattern of in-range rows is bit-identical to the reference rounding
-    assert np.array_equal(H == 0, ref == 0) or np.abs(H - ref).max() < 1e-6
+    # the zero pattern is exact: zeros where the fp64 oracle evaluated on the
+    # same float32 inputs has them (outside the span, inactive functions, and
+    # on knots where the active ones vanish), nowhere else
+    assert np.array_equal(H == 0, ref64 == 0)
+    assert np.array_equal(ref == 0, ref64 == 0)
     assert np.abs(H - ref64).max() < 2e-6
     if impl == 0:
         # the dense recurrence reproduces the reference's fp32 rounding exactly
         assert np.array_equal(H, ref)
+
+
+@pytest.mark.parametrize("k", [1, 2, 3])
+@pytest.mark.parametrize("kind", ["uniform", "nonuniform", "repeated"])
+@pytest.mark.parametrize("dtype", [torch.float64, torch.float32])
+def test_legacy_impl_basis_grad_matches_oracle(C, k, kind, dtype):
+    """impl 0 (the dense derivative recurrence of basis_derivative_kernel,
+    csrc/kan_cuda.cu:104-186, contracted in registers) against the oracle's
+    derivative: fp64 1e-10, fp32 normwise 1e-5; and its basis values with
+    impl 0 against the oracle too (tests/test_local_basis.py:71-90 of the
+    reference require both impls to give the layer's results)."""
+    print(f"legacy basis_grad k={k} kind={kind} {dtype}", flush=True)
+    G = 9
+    grid = make_grid(37, G, k, kind, seed=7 + k, dtype=dtype)
+    x = make_points(grid, n=1500, seed=k)
+    gH = torch.randn(x.shape[0], 37, G + k, dtype=torch.float64,
+                     generator=torch.Generator().manual_seed(k)).to(dtype)
+    try:
+        C.set_basis_impl(0)
+        H = C.basis(x.cuda(), grid.cuda(), k).cpu()
+        gx = C.basis_grad(x.cuda(), grid.cuda(), k, gH.cuda()).cpu()
+    finally:
+        C.set_basis_impl(1)
+    x64, g64 = x.double().numpy(), grid.double().numpy()
+    gref = (gH.double().numpy() * ko.basis_derivative(x64, g64, k)).sum(-1)
+    Href = ko.basis_dense(x64, g64, k)
+    if dtype == torch.float64:
+        assert np.abs(H.numpy() - Href).max() < 1e-13
+        assert np.abs(gx.numpy() - gref).max() < 1e-10 * max(1.0, np.abs(gref).max())
+    else:
+        assert np.abs(H.double().numpy() - Href).max() < 2e-6
+        assert normwise(gx.double().numpy(), gref) < 1e-5
 
 
 @pytest.mark.parametrize("k", [1, 2, 3])

@@ -1,0 +1,252 @@
+"""GPU parity at BASELINE.json's workloads themselves, built by the same
+functions bench.py times (bench.build_c2 .. build_c5), against the fp64
+oracle at the north star's fp32 bar (normwise relative 1e-5):
+
+* c3: KANLinear 1024 -> 1024 G10 k3, N = 65536, x with grad: y and dx on 64
+  rows, dcoef / dscaler / dbase_w on 64 edges over all samples.
+* c5: KANLinear 4096 -> 256 G65 k3, N = 8192 (N I (G + 2k) = 2.38e9, past
+  the reference's 32-bit guard): the same checks, exact zero basis rows
+  outside the knot span, and the edge statistic on the c5 basis (2.28e9
+  elements) with its backward.
+* c4: KAN([256, 512, 512, 64]) G8 with update_grid knots on the Gaussian
+  mixture, forward_with_regularization(1e-2, 1e-2, "auto") + MSE + backward:
+  per layer, outputs on rows, the regulariser from the oracle's edge means
+  over all edges, parameter gradients on sampled edges and input gradients
+  on sampled rows, with sign flips of phi at fp32 rounding level bounded
+  term by term (tests/_slack.py); the network output on rows through the
+  full oracle chain; layer 0's knots against the oracle's grid_from_samples.
+* c2: KAN([784, 256, 10]) G5, N = 4096 + MSE: every output and gradient
+  against the full oracle chain.
+
+The matching reference tests hold the native backend to the reference
+backend (tests/test_math_correctness.py:284-306); here the bar is the fp64
+oracle.
+"""
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import kan_oracle as ko
+from tests import _netcheck, _slack
+from tests._util import normwise, np64
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-5
+
+
+@pytest.fixture(scope="module")
+def bench():
+    assert torch.cuda.is_available(), "GPU tests need a ROCm device"
+    import bench as b
+    return b
+
+
+def _say(*a):
+    print(*a, flush=True)
+
+
+_params = _netcheck.params
+basis_threaded = _netcheck.basis_threaded
+
+
+def _edge_param_oracle(D, x, grid, bw, sw, sc, k, edges):
+    """dbw, dcoef, dscaler of sampled edges over all samples, each edge as a
+    1 x 1 sub-layer of the oracle's kan_backward_params (an edge's gradients
+    depend only on its own input column and output column of D)."""
+    gbw, gsw, gsc = [], [], []
+    for o, i in edges:
+        Hi = ko.basis_dense(x[:, i:i + 1], grid[i:i + 1], k)
+        b, w, c = ko.kan_backward_params(D[:, o:o + 1], x[:, i:i + 1], bw[o:o + 1, i:i + 1],
+                                         sw[o:o + 1, i:i + 1], sc[o:o + 1, i:i + 1], Hi)
+        gbw.append(b[0, 0])
+        gsw.append(w[0, 0])
+        gsc.append(c[0, 0])
+    return np.array(gbw), np.array(gsw), np.array(gsc)
+
+
+_sample_edges = _netcheck.sample_edges
+
+
+def _check_single_layer(L, xd, td, x_cpu, k, n_rows, n_edges, tag):
+    """One training step of a single KANLinear (the bench's step) and its
+    outputs against the oracle on rows and sampled edges."""
+    for p in L.parameters():
+        p.grad = None
+    y = L(xd)
+    F.mse_loss(y, td).backward()
+    torch.cuda.synchronize()
+    assert L.last_backend == "cuda"
+    N, O = y.shape
+    I = xd.shape[1]
+    grid, bw, sw, sc = _params(L)
+    x = x_cpu.detach().double().numpy()
+    D = 2.0 * (np64(y) - np64(td)) / (N * O)
+    rows = np.unique(np.linspace(0, N - 1, n_rows).astype(int))
+    ry, H = ko.kan_forward(x[rows], grid, bw, sw, sc, k)
+    e = normwise(np64(y[rows]), ry)
+    _say(f"{tag}: y rows {e:.2e}")
+    assert e < TOL
+    rgx, _, _, _ = ko.kan_backward(D[rows], x[rows], grid, bw, sw, sc, k, basis=H)
+    e = normwise(np64(xd.grad[rows]), rgx)
+    _say(f"{tag}: dx rows {e:.2e}")
+    assert e < TOL
+    edges = _sample_edges(O, I, n_edges, seed=N)
+    gbw, gsw, gsc = _edge_param_oracle(D, x, grid, bw, sw, sc, k, edges)
+    oo, ii = map(list, zip(*edges))
+    for name, got, ref in (("dbase_w", L.base_weight.grad[oo, ii], gbw),
+                           ("dcoef", L.spline_weight.grad[oo, ii], gsw),
+                           ("dscaler", L.spline_scaler.grad[oo, ii], gsc)):
+        e = normwise(np64(got), ref)
+        _say(f"{tag}: {name} on {len(edges)} edges {e:.2e}")
+        assert e < TOL, name
+
+
+@pytest.mark.timeout(900)
+def test_c3_training_step_matches_oracle(bench):
+    dev = torch.device("cuda", 0)
+    L, xd, td, cpu = bench.build_c3(dev, 65536, need_dx=True)
+    _say("c3: KANLinear 1024->1024 G10 k3 N=65536 fwd+MSE+bwd with dx")
+    _check_single_layer(L, xd, td, cpu[0], 3, n_rows=64, n_edges=64, tag="c3")
+
+
+@pytest.mark.timeout(900)
+def test_c5_kernel_limit_layer_full_size(bench):
+    dev = torch.device("cuda", 0)
+    L, x, target = bench.build_c5(dev, 8192)
+    N, I = x.shape
+    k = 3
+    assert N * I * (L.grid_size + 2 * k) > 2 ** 31 - 1   # past the reference's guard
+    xd, td = x.to(dev).requires_grad_(), target.to(dev)
+    _say("c5: KANLinear 4096->256 G65 k3 N=8192 fwd+MSE+bwd with dx")
+    _check_single_layer(L, xd, td, x, k, n_rows=32, n_edges=48, tag="c5")
+    # basis past 2^31 elements: exact zero rows outside [t_0, t_71], values on rows
+    from torchsplinekan_amd import _C
+    with torch.no_grad():
+        Hg = _C.basis(xd.detach(), L.grid, k)
+        assert Hg.numel() > 2 ** 31
+        xg = xd.detach()
+        out = (xg < L.grid[:, 0][None]) | (xg > L.grid[:, -1][None])
+        frac = out.float().mean().item()
+        _say(f"c5: {frac:.4f} of inputs outside the knot span")
+        assert 0.004 < frac < 0.01
+        assert int((Hg[out] != 0).sum()) == 0
+        inside = ~out
+        assert bool(((Hg.sum(-1) - 1.0).abs()[inside & (xg.abs() <= 1.0)] < 1e-5).all())
+    rows = [0, 4095, N - 1]
+    rH = ko.basis_dense(x[rows].double().numpy(), np64(L.grid), k)
+    assert np.abs(np64(Hg[rows]) - rH).max() < 2e-6
+    # edge statistic on the c5 basis and its backward (separate route: R + 1 = 69)
+    s = torch.nn.functional.silu(xg)
+    W = (L.spline_weight * L.spline_scaler.unsqueeze(-1)).detach()
+    bw = L.base_weight.detach()
+    a = _C.edge_abs_mean(s, Hg, bw, W)
+    ga = torch.randn(a.shape, generator=torch.Generator().manual_seed(9)).to(dev)
+    ds, dH, dbw, dW = _C.edge_abs_mean_backward(ga, s, Hg, bw, W, True, True, True, True)
+    torch.cuda.synchronize()
+    del Hg
+    xs = x.detach().double().numpy()
+    grid = np64(L.grid)
+    feats = [0, 1234, 4095]
+    Hf = np.concatenate([ko.basis_dense(xs[:, i:i + 1], grid[i:i + 1], k) for i in feats], 1)
+    sf, Wn, bwn, gan = ko.silu(xs[:, feats]), np64(W), np64(bw), np64(ga)
+    ra = ko.edge_abs_mean_by_feature(sf, Hf, bwn[:, feats], Wn[:, feats])
+    e = normwise(np64(a[:, feats]), ra)
+    _say(f"c5 edge: mean|phi| on features {feats} {e:.2e}")
+    assert e < TOL
+    edges = [(o, i) for o in (0, 100, 255) for i in feats]
+    res, n_amb = _slack.edge_param_grads(None, gan[:, feats],
+                                         sf, Hf, bwn[:, feats], Wn[:, feats],
+                                         np.ones((Wn.shape[0], len(feats))),
+                                         [(o, feats.index(i)) for o, i in edges])
+    oo, ii = map(list, zip(*edges))
+    for name, got in (("dW", dW[oo, ii]), ("dbw", dbw[oo, ii])):
+        ref, slack = res["spline_weight" if name == "dW" else "base_weight"]
+        e = _slack.within(np64(got), ref, slack, TOL)
+        _say(f"c5 edge: {name} on {len(edges)} edges {e:.2e} ({n_amb} ambiguous terms)")
+        assert e < TOL
+    rows_e = [7, 5000]
+    sr = ko.silu(xs[rows_e])
+    Hr = ko.basis_dense(xs[rows_e], grid, k)
+    rds, sds, rdH, sdH, n_amb = _slack.edge_operand_grads(gan, sr, Hr, bwn, Wn, [0, 1],
+                                                          n_total=N)
+    for name, got, ref, slack in (("ds", ds[rows_e], rds, sds), ("dH", dH[rows_e], rdH, sdH)):
+        e = _slack.within(np64(got), ref, slack, TOL)
+        _say(f"c5 edge: {name} on rows {rows_e} {e:.2e} ({n_amb} ambiguous terms)")
+        assert e < TOL
+
+
+@pytest.mark.timeout(1200)
+def test_c4_regularised_network_matches_oracle(bench):
+    dev = torch.device("cuda", 0)
+    net, xd, td = bench.build_c4(dev, 16384)
+    N = xd.shape[0]
+    k = 3
+    mu = 1e-2
+    _say("c4: KAN([256,512,512,64]) G8 update_grid knots, forward_with_regularization")
+    # layer 0's knots against the oracle's grid_from_samples on the same samples
+    L0 = net.layers[0]
+    rg = ko.grid_from_samples(np64(xd), 8, k, L0._ref.grid_eps)
+    e = normwise(np64(L0.grid), rg)
+    _say(f"c4: layer-0 knots vs grid_from_samples {e:.2e}")
+    assert e < 1e-6
+    # one training step (the bench's), each layer's input, output and regulariser captured
+    with _netcheck.capture(net) as cap:
+        for p in net.parameters():
+            p.grad = None
+        y, reg = net.forward_with_regularization(xd, mu, mu, reg_impl="auto")
+        (F.mse_loss(y, td) + reg).backward()
+        torch.cuda.synchronize()
+    assert all(l.last_backend == "cuda" for l in net.layers) and len(cap) == 3
+    # network output on rows through the full fp64 oracle chain
+    rows = np.unique(np.linspace(0, N - 1, 32).astype(int))
+    h = np64(xd)[rows]
+    for layer in net.layers:
+        grid, bw, sw, sc = _netcheck.params(layer)
+        h, _ = ko.kan_forward(h, grid, bw, sw, sc, k)
+    e = normwise(np64(y[rows]), h)
+    _say(f"c4: network output rows {e:.2e}")
+    assert e < TOL
+    reg_total = _netcheck.check_layers(net, cap, mu, k, TOL, say=lambda m: _say("c4 " + m))
+    e = abs(reg.item() - reg_total) / abs(reg_total)
+    _say(f"c4: total regulariser {e:.2e}")
+    assert e < TOL
+
+
+@pytest.mark.timeout(900)
+def test_c2_network_matches_oracle(bench):
+    dev = torch.device("cuda", 0)
+    net, x, target = bench.build_c2(dev, 4096)
+    xd, td = x.to(dev).requires_grad_(), target.to(dev)
+    N = xd.shape[0]
+    k = 3
+    _say("c2: KAN([784,256,10]) G5 N=4096 fwd+MSE+bwd")
+    y = net(xd)
+    F.mse_loss(y, td).backward()
+    torch.cuda.synchronize()
+    assert all(l.last_backend == "cuda" for l in net.layers)
+    (g1, bw1, sw1, sc1), (g2, bw2, sw2, sc2) = [_params(l) for l in net.layers]
+    xs = x.detach().double().numpy()
+    H1 = basis_threaded(xs, g1, k)
+    y1, _ = ko.kan_forward(xs, g1, bw1, sw1, sc1, k, basis=H1)
+    y2, H2 = ko.kan_forward(y1, g2, bw2, sw2, sc2, k)
+    e = normwise(np64(y), y2)
+    _say(f"c2: output {e:.2e}")
+    assert e < TOL
+    D2 = 2.0 * (np64(y) - np64(td)) / y.numel()
+    gx2, gbw2, gsw2, gsc2 = ko.kan_backward(D2, y1, g2, bw2, sw2, sc2, k, basis=H2)
+    gx1, gbw1, gsw1, gsc1 = ko.kan_backward(gx2, xs, g1, bw1, sw1, sc1, k, basis=H1)
+    l1, l2 = net.layers
+    for name, got, ref in (("dx", xd.grad, gx1),
+                           ("layer 0 dbase_w", l1.base_weight.grad, gbw1),
+                           ("layer 0 dcoef", l1.spline_weight.grad, gsw1),
+                           ("layer 0 dscaler", l1.spline_scaler.grad, gsc1),
+                           ("layer 1 dbase_w", l2.base_weight.grad, gbw2),
+                           ("layer 1 dcoef", l2.spline_weight.grad, gsw2),
+                           ("layer 1 dscaler", l2.spline_scaler.grad, gsc2)):
+        e = normwise(np64(got), ref)
+        _say(f"c2: {name} {e:.2e}")
+        assert e < TOL, name
+

@@ -9,6 +9,7 @@ import pytest
 import torch
 
 from oracle import kan_oracle as ko
+from tests import _netcheck, _slack
 from tests._util import normwise, np64
 
 pytestmark = pytest.mark.gpu
@@ -71,19 +72,33 @@ def test_edge_abs_mean_and_backward_match_oracle(C, monkeypatch, shape, dtype, b
     assert normwise(np64(a), ra) < tol
     ds, dH, dbw, dW = C.edge_abs_mean_backward(ga.cuda(), sd, H.cuda(), bwd, W.cuda(),
                                                True, True, True, True)
-    rds, rdH, rdbw, rdW = ko.edge_abs_mean_backward(np64(ga), np64(s) if base else None,
-                                                    np64(H), np64(bw) if base else None,
-                                                    np64(W))
-    # fp32: sign(phi) may flip where |phi| is at rounding level; the normwise
-    # bound allows for a handful of such terms.
-    gtol = 1e-12 if dtype == torch.float64 else 1e-4
-    assert normwise(np64(dH), rdH) < gtol
-    assert normwise(np64(dW), rdW) < gtol
-    if base:
-        assert normwise(np64(ds), rds) < gtol
-        assert normwise(np64(dbw), rdbw) < gtol
-    else:
+    if not base:
         assert ds is None and dbw is None
+    _check_edge_grads((ds, dH, dbw, dW), ga, s if base else None, H, bw if base else None, W,
+                      dtype)
+
+
+def _check_edge_grads(got, ga, s, H, bw, W, dtype, D=None, which=(True, True, True, True)):
+    """Device edge gradients against the oracle: fp64 at 1e-12; fp32 at
+    1e-5 normwise, with the terms whose sign fp32 cannot decide (|phi|
+    within its rounding bound) counted and bounded term by term
+    (tests/_slack.py; operands shared exactly, so no extra allowance)."""
+    a = lambda t: None if t is None else np64(t)
+    refs, slacks, n_amb = _slack.edge_backward_full(a(ga), a(s), a(H), a(bw), a(W), D=a(D),
+                                                    extra=0)
+    N, O, I = H.shape[0], W.shape[0], W.shape[1]
+    names = ("ds", "dH", "dbw", "dW")
+    for name, want, g, ref, slack in zip(names, which, got, refs, slacks):
+        if not want or ref is None:
+            continue
+        if dtype == torch.float64:
+            assert normwise(np64(g), ref) < 1e-12, name
+        else:
+            e = _slack.within(np64(g), ref, slack, 1e-5)
+            assert e < 1e-5, (name, e, n_amb)
+    if dtype == torch.float32:
+        print(f"  {n_amb} of {N * O * I} terms within fp32 rounding of phi = 0", flush=True)
+        assert n_amb <= max(3, 1e-4 * N * O * I)
 
 
 def test_edge_at_the_in_features_limit(C):
@@ -99,10 +114,7 @@ def test_edge_at_the_in_features_limit(C):
     assert normwise(np64(a), ra) < 1e-5
     ds, dH, dbw, dW = C.edge_abs_mean_backward(ga.cuda(), s.cuda(), H.cuda(), bw.cuda(),
                                                W.cuda(), True, True, True, True)
-    rds, rdH, rdbw, rdW = ko.edge_abs_mean_backward(np64(ga), np64(s), np64(H), np64(bw),
-                                                    np64(W))
-    for got, ref in ((ds, rds), (dH, rdH), (dbw, rdbw), (dW, rdW)):
-        assert normwise(np64(got), ref) < 1e-4
+    _check_edge_grads((ds, dH, dbw, dW), ga, s, H, bw, W, torch.float32)
 
 
 def test_edge_backward_partial_requests(C):
@@ -158,14 +170,7 @@ def test_edge_linear_backward_matches_oracle(C, shape):
     assert C.edge_linear_supported(H.cuda(), W.cuda())
     ds, dH, dbw, dW = C.edge_linear_backward(ga.cuda(), gy.cuda(), s.cuda(), H.cuda(), bw.cuda(),
                                              W.cuda(), True, True, True, True)
-    rds, rdH, rdbw, rdW = ko.edge_abs_mean_backward(np64(ga), np64(s), np64(H), np64(bw), np64(W))
-    D = np64(gy)
-    rds = rds + D @ np64(bw)
-    rdH = rdH + (D @ np64(W).reshape(O, I * R)).reshape(N, I, R)
-    rdbw = rdbw + D.T @ np64(s)
-    rdW = rdW + (D.T @ np64(H).reshape(N, I * R)).reshape(O, I, R)
-    for name, got, ref in (("ds", ds, rds), ("dH", dH, rdH), ("dbw", dbw, rdbw), ("dW", dW, rdW)):
-        assert normwise(np64(got), ref) < 1e-4, name
+    _check_edge_grads((ds, dH, dbw, dW), ga, s, H, bw, W, torch.float32, D=gy)
     # a partial request leaves the other outputs unwritten and the rest equal
     ds2, dH2, dbw2, dW2 = C.edge_linear_backward(ga.cuda(), gy.cuda(), s.cuda(), H.cuda(),
                                                  bw.cuda(), W.cuda(), False, True, False, True)
@@ -175,7 +180,8 @@ def test_edge_linear_backward_matches_oracle(C, shape):
     ds3, dH3, dbw3, dW3 = C.edge_linear_backward(ga.cuda(), gy.cuda(), s.cuda(), H.cuda(),
                                                  bw.cuda(), W.cuda(), False, False, True, True)
     assert ds3 is None and dH3 is None
-    assert normwise(np64(dbw3), rdbw) < 1e-4 and normwise(np64(dW3), rdW) < 1e-4
+    _check_edge_grads((None, None, dbw3, dW3), ga, s, H, bw, W, torch.float32, D=gy,
+                      which=(False, False, True, True))
 
 
 def test_edge_linear_supported_range(C):
@@ -204,45 +210,55 @@ def _reg_grads(net, x, impl, create_graph=False):
 
 
 @pytest.mark.parametrize("x_grad", [True, False])
-def test_regularized_layers_folded_backward_match_dense(C, monkeypatch, x_grad):
-    """KAN([16, 64, 100, 12]) fp32: every layer's output and edge statistic go
-    through EdgeLinear; with x requiring
-    grad the first layer takes the folded kernel as well, without it the
-    weight-only branch.
-    * Gradients against the unfolded native path (separate output products
-      and edge backward, summed by autograd): the same kernels form phi, so
-      the sign patterns agree and only summation order differs: 1e-5.
-    * Output and regulariser against the dense path: 1e-5.  (Gradients of
-      the native and the dense path differ by sign flips of phi at rounding
-      level, up to 4e-4 normwise on dbw at these sizes, with or without the
-      fold; their agreement at the reference's shapes and tolerance is
-      test_forward_with_regularization_fused_matches_dense.)"""
+@pytest.mark.parametrize("route", ["folded", "unfolded", "dense"])
+def test_regularized_layers_match_oracle(C, monkeypatch, x_grad, route):
+    """KAN([16, 64, 100, 12]) fp32, forward_with_regularization + loss +
+    backward through each route, every layer held to the fp64 oracle
+    (tests/_netcheck.py: outputs, regulariser, parameter gradients on
+    sampled edges, input gradients on sampled rows) at 1e-5 with sign flips
+    of phi at fp32 rounding level counted and bounded term by term:
+    * "folded": output and edge statistic through EdgeLinear (one folded
+      native backward launch per layer; the weight-only branch for the first
+      layer when x needs no gradient);
+    * "unfolded": the separate native output products and edge backward,
+      summed by autograd;
+    * "dense": the PyTorch dense path (reg_impl="dense").
+    All three meeting the same oracle bar shows that their differences are
+    the counted flips."""
     from torchsplinekan_amd import KAN
     from torchsplinekan_amd import fused as fz
+    print(f"regularised KAN([16,64,100,12]) route={route} x_grad={x_grad}", flush=True)
     torch.manual_seed(1)
     net = KAN([16, 64, 100, 12], grid_size=7, backend="cuda").to("cuda")
-    x = torch.rand(3000, 16, device="cuda") * 2.2 - 1.1
-    res = {}
-    for impl in ("fused", "dense"):
-        xx = x.clone().requires_grad_(x_grad)
-        res[impl] = _reg_grads(net, xx, impl)
-    monkeypatch.setattr(fz, "edge_linear_applies", lambda *a: False)
-    res["unfolded"] = _reg_grads(net, x.clone().requires_grad_(x_grad), "fused")
-    for a, b in zip(res["fused"], res["unfolded"]):
-        assert normwise(np64(a), np64(b)) < 1e-5
-    for a, b in zip(res["fused"][:2], res["dense"][:2]):
-        assert normwise(np64(a), np64(b)) < 1e-5
+    x = (torch.rand(3000, 16, device="cuda") * 2.2 - 1.1).requires_grad_(x_grad)
+    if route == "unfolded":
+        monkeypatch.setattr(fz, "edge_linear_applies", lambda *a: False)
+    impl = "dense" if route == "dense" else "fused"
+    with _netcheck.capture(net) as cap:
+        y, r = net.forward_with_regularization(x, 1e-2, 1e-2, reg_impl=impl, chunk_size=256)
+        (y.square().mean() + r).backward()
+        torch.cuda.synchronize()
+    assert all(l.last_backend == ("reference" if route == "dense" else "cuda")
+               for l in net.layers)
+    reg = _netcheck.check_layers(net, cap, 1e-2, 3, 1e-5, n_rows=24, n_edges=40, n_xrows=8,
+                                 say=lambda m: print("  " + m, flush=True))
+    assert abs(r.item() - reg) < 1e-5 * abs(reg)
+    if x_grad:
+        assert x.grad is not None
 
 
 def test_regularized_layers_folded_backward_recorded(C):
     """create_graph through EdgeLinear (its recorded branch: the separate
     differentiable pieces): first and second derivatives with respect to the
-    parameters against the dense path."""
+    parameters against the dense path at 1e-5 (the dense path in fp32
+    against itself in fp64 differs by at most 4e-7 on these quantities; the
+    32,000 phi terms of this network leave an fp32 sign flip unlikely)."""
     from torchsplinekan_amd import KAN
     torch.manual_seed(2)
     net = KAN([6, 8, 4], grid_size=5, backend="cuda").to("cuda")
     x = torch.rand(400, 6, device="cuda") * 2.2 - 1.1
     f = _reg_grads(net, x.clone().requires_grad_(), "fused", create_graph=True)
     d = _reg_grads(net, x.clone().requires_grad_(), "dense", create_graph=True)
-    for a, b in zip(f, d):
-        assert normwise(np64(a), np64(b)) < 1e-4
+    errs = [normwise(np64(a), np64(b)) for a, b in zip(f, d)]
+    print("  recorded fused vs dense:", " ".join(f"{e:.1e}" for e in errs), flush=True)
+    assert max(errs) < 1e-5

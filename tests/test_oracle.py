@@ -245,6 +245,17 @@ def test_edge_abs_mean_matches_brute_force(base):
 
 
 @pytest.mark.parametrize("base", [True, False])
+def test_edge_abs_mean_by_feature_matches_edge_abs_mean(base):
+    N, I, O, R = 300, 7, 9, 6
+    s, H, bw, W = _edge(N, I, O, R, 5, base)
+    a = ko.edge_abs_mean(s, H, bw, W, chunk=64)
+    b = ko.edge_abs_mean_by_feature(s, H, bw, W, workers=3)
+    assert b.shape == a.shape and np.abs(a - b).max() < 1e-13 * np.abs(a).max()
+    sub = ko.edge_abs_mean_by_feature(s, H, bw, W, features=[5, 0, 3], workers=2)
+    assert np.abs(sub - a[:, [5, 0, 3]]).max() < 1e-13 * np.abs(a).max()
+
+
+@pytest.mark.parametrize("base", [True, False])
 def test_edge_backward_matches_finite_differences(base):
     N, I, O, R = 5, 2, 3, 4
     s, H, bw, W = _edge(N, I, O, R, 1, base)

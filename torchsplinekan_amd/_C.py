@@ -291,6 +291,17 @@ def kan_apply(x, grid, base_weight, spline_weight, spline_scaler, spline_order: 
                              has_scaler)
 
 
+def stream_probe(mode: int, a: torch.Tensor, b: torch.Tensor) -> None:
+    """Streaming probe over a's bytes (measurement support): mode 0 writes a,
+    1 reads a, 2 copies a into b (b at least as large as a for mode 2)."""
+    _req(a.is_cuda and b.is_cuda and a.is_contiguous() and b.is_contiguous(),
+         "stream_probe: contiguous device tensors")
+    nbytes = a.numel() * a.element_size() // 16 * 16
+    _req(mode != 2 or b.numel() * b.element_size() >= nbytes, "stream_probe: b too small")
+    with torch.cuda.device(a.device):
+        check(LIB.kan_hip_stream_probe(int(mode), ptr(a), ptr(b), nbytes, stream_of(a.device)))
+
+
 # ---------------------------------------------------------------------------
 # basis implementation switch (csrc/kan_cuda.cu:274-279)
 # ---------------------------------------------------------------------------

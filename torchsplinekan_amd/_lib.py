@@ -72,6 +72,7 @@ SIGNATURES = {
                                                                 _vp]),
     "kan_hip_refit_gram": (_int, [_int, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64,
                                   _vp]),
+    "kan_hip_stream_probe": (_int, [_int, _vp, _vp, _i64, _vp]),
     "kan_hip_timing_enable": (_int, [_int]),
     "kan_hip_timing_read": (_int, [_int, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_i64),
                                    ctypes.POINTER(ctypes.c_double)]),
@@ -149,7 +150,7 @@ def limits():
 
 # kernel classes of kan_hip_timing_read
 TIMING_CLASSES = {"contraction": 0, "basis": 1, "basis_grad": 2, "edge": 3, "edge_grad": 4,
-                  "other": 5}
+                  "other": 5, "stream": 6}
 
 
 def timing_enable(on: bool) -> None:

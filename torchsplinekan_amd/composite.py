@@ -45,10 +45,10 @@ def kan_forward_cpu(x, grid, base_weight, spline_weight, spline_scaler, spline_o
 
 
 def kan_backward_cpu(D, x, grid, base_weight, spline_weight, spline_scaler, basis,
-                     spline_order: int, has_scaler: bool):
+                     spline_order: int, has_scaler: bool, need_x: bool = True):
     """Analytic first-order backward from the saved basis:
     gbw = D^T silu(x); DtH = D^T H; gsw = scaler*DtH; gscaler = sum_r sw*DtH;
-    gx = sum_r (D W)[.,.,r] dB_r/dx + (D bw) silu'(x)."""
+    gx = sum_r (D W)[.,.,r] dB_r/dx + (D bw) silu'(x) (None when not need_x)."""
     B, I = x.shape
     O, _, R = spline_weight.shape
     hb = has_base(base_weight)
@@ -59,6 +59,8 @@ def kan_backward_cpu(D, x, grid, base_weight, spline_weight, spline_scaler, basi
         gsc = (spline_weight * DtH).sum(2)
     else:
         gsw, gsc = DtH, None
+    if not need_x:
+        return None, gbw, gsw, gsc
     W = _eff_weight(spline_weight, spline_scaler, has_scaler)
     DW = (D @ W.reshape(O, I * R)).reshape(B, I, R)
     gx = (DW * compute_basis_derivative(x, grid, spline_order)).sum(2)

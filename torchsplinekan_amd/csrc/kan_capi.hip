@@ -363,6 +363,17 @@ int kan_hip_timing_read(int kernel_class, double* total_ms, int64_t* launches, d
   return KAN_OK;
 }
 
+int kan_hip_stream_probe(int mode, void* a, void* b, int64_t bytes, void* stream) {
+  if (mode < 0 || mode > 2)
+    return set_error(KAN_ERR_INVALID, "stream_probe: mode must be 0 (write), 1 (read) or 2 (copy)");
+  if (bytes < 0 || bytes % 16 != 0)
+    return set_error(KAN_ERR_INVALID, "stream_probe: bytes must be a non-negative multiple of 16");
+  if (bytes > 0 && (a == nullptr || (mode != 0 && b == nullptr) ||
+                    ((uintptr_t)a % 16) != 0 || (mode == 2 && ((uintptr_t)b % 16) != 0)))
+    return set_error(KAN_ERR_INVALID, "stream_probe: buffers must be non-null and 16-byte aligned");
+  return launch_stream_probe(mode, a, b, bytes, (hipStream_t)stream);
+}
+
 int kan_hip_basis(int dtype, const void* x, const void* grid, void* basis, int64_t n, int64_t I,
                   int64_t G, int64_t k, void* stream) {
   KAN_TRY(check_dtype(dtype, "kan_basis"));

@@ -4,6 +4,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstddef>
 #include <cstdint>
 #include <string>
@@ -92,7 +93,8 @@ enum KernelClass {
   kClassEdge = 3,         // edge statistic forward
   kClassEdgeGrad = 4,     // edge statistic backward
   kClassOther = 5,        // packing / finalize kernels
-  kNumKernelClasses = 6
+  kClassStream = 6,       // streaming probes (bytes moved)
+  kNumKernelClasses = 7
 };
 
 class TimedLaunch {
@@ -106,6 +108,10 @@ class TimedLaunch {
 };
 
 // ---- launchers implemented in the .hip translation units -----------------
+
+// float4 streaming probe over `bytes` (a multiple of 16): mode 0 writes a,
+// 1 reads a, 2 copies a to b (kan_stream.hip).
+int launch_stream_probe(int mode, void* a, void* b, int64_t bytes, hipStream_t st);
 
 template <typename T>
 int launch_basis(const T* x, const T* grid, T* out, int64_t ld_out, T* silu_out, int64_t n,
