@@ -158,13 +158,15 @@ def edge_operand_grads(ga, s, H, bw, W, rows, n_total=None, extra=16):
     return arr(ds), arr(dss), np.array(dH), np.array(dHs), n_amb
 
 
-def edge_backward_full(ga, s, H, bw, W, D=None, chunk=256, extra=16):
+def edge_backward_full(ga, s, H, bw, W, D=None, chunk=256, extra=16, unit=U32):
     """All four gradients of the edge statistic (plus, with D = dL/dy, of the
     layer output y = s bw^T + <H, W>) with their slack, chunked over samples
     like ko.edge_abs_mean_backward: -> (ds, dH, dbw, dW) refs, the same four
-    slacks (ds / dbw None without a base branch) and the ambiguous count."""
+    slacks (ds / dbw None without a base branch) and the ambiguous count.
+    `unit` is the device's unit roundoff (2^-24 for float32, 2^-53 for
+    float64)."""
     N, I, R = H.shape
-    c = rounding_factor(R, extra) * U32
+    c = rounding_factor(R, extra) * unit
     dH, sH = np.empty_like(H), np.empty_like(H)
     dW, sW = np.zeros_like(W), np.zeros_like(W)
     hb = bw is not None

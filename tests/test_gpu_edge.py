@@ -79,26 +79,25 @@ def test_edge_abs_mean_and_backward_match_oracle(C, monkeypatch, shape, dtype, b
 
 
 def _check_edge_grads(got, ga, s, H, bw, W, dtype, D=None, which=(True, True, True, True)):
-    """Device edge gradients against the oracle: fp64 at 1e-12; fp32 at
-    1e-5 normwise, with the terms whose sign fp32 cannot decide (|phi|
-    within its rounding bound) counted and bounded term by term
-    (tests/_slack.py; operands shared exactly, so no extra allowance)."""
+    """Device edge gradients against the oracle: fp64 at 1e-12 and fp32 at
+    1e-5 normwise, with the terms whose sign the device's precision cannot
+    decide (|phi| within its rounding bound) counted and bounded term by
+    term (tests/_slack.py; operands shared exactly, so no extra allowance)."""
     a = lambda t: None if t is None else np64(t)
+    fp64 = dtype == torch.float64
     refs, slacks, n_amb = _slack.edge_backward_full(a(ga), a(s), a(H), a(bw), a(W), D=a(D),
-                                                    extra=0)
+                                                    extra=0, unit=2.0 ** -53 if fp64 else 2.0 ** -24)
     N, O, I = H.shape[0], W.shape[0], W.shape[1]
+    tol = 1e-12 if fp64 else 1e-5
     names = ("ds", "dH", "dbw", "dW")
     for name, want, g, ref, slack in zip(names, which, got, refs, slacks):
         if not want or ref is None:
             continue
-        if dtype == torch.float64:
-            assert normwise(np64(g), ref) < 1e-12, name
-        else:
-            e = _slack.within(np64(g), ref, slack, 1e-5)
-            assert e < 1e-5, (name, e, n_amb)
-    if dtype == torch.float32:
-        print(f"  {n_amb} of {N * O * I} terms within fp32 rounding of phi = 0", flush=True)
-        assert n_amb <= max(3, 1e-4 * N * O * I)
+        e = _slack.within(np64(g), ref, slack, tol)
+        assert e < tol, (name, e, n_amb)
+    print(f"  {n_amb} of {N * O * I} terms within {'fp64' if fp64 else 'fp32'} rounding of "
+          "phi = 0", flush=True)
+    assert n_amb <= max(3, 1e-4 * N * O * I)
 
 
 def test_edge_at_the_in_features_limit(C):
