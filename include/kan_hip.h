@@ -131,6 +131,23 @@ int kan_hip_infer(int dtype, const void* x, const void* grid, const void* weight
                   void* ws, size_t ws_bytes, int64_t n, int64_t in_features, int64_t out_features,
                   int64_t grid_size, int64_t spline_order, int has_base, void* stream);
 
+/* Allocation-free inference.  No counterpart in the reference: for callers
+ * that cannot allocate device memory (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc).  Same arguments, kernels
+ * and result as kan_hip_infer, without the workspace: the library uses a
+ * fixed device scratch of KAN_NOALLOC_SCRATCH_BYTES per GPU (held from the
+ * library's load until the process ends) and calls no allocating routine.
+ * A call whose workspace (kan_hip_infer_workspace) exceeds that size
+ * returns KAN_ERR_WORKSPACE before any launch.  All calls on one GPU share
+ * its scratch: calls that overlap in time on one GPU (other streams, other
+ * threads) race and must be serialised by the caller.  The calling
+ * thread's current device must be the one the pointers and the stream
+ * belong to. */
+#define KAN_NOALLOC_SCRATCH_BYTES (64u * 1024u * 1024u)
+int kan_hip_infer_noalloc(int dtype, const void* x, const void* grid, const void* weight_aug,
+                          void* output, int64_t n, int64_t in_features, int64_t out_features,
+                          int64_t grid_size, int64_t spline_order, int has_base, void* stream);
+
 /* Row width (elements) of the augmented basis and augmented weight buffers.
  * Returns -1 for invalid sizes.  No reference counterpart: the reference keeps
  * basis [n, I, R] and runs the SiLU branch as a second GEMM

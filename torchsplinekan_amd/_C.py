@@ -147,6 +147,31 @@ def kan_infer(x, grid, waug, spline_order: int, has_base: bool) -> torch.Tensor:
     return y
 
 
+def kan_infer_noalloc(x, grid, waug, spline_order: int, has_base: bool) -> torch.Tensor:
+    """kan_infer without a workspace: kan_hip_infer_noalloc runs the same
+    kernels on the library's fixed per-device scratch (at most
+    KAN_NOALLOC_SCRATCH_BYTES of workspace; larger calls raise).  Calls that
+    overlap on one GPU race on that scratch."""
+    _req(x.is_cuda and grid.is_cuda and waug.is_cuda, "kan_infer_noalloc: tensors must be on the device")
+    _req(x.dim() == 2 and waug.dim() == 2 and grid.dim() == 2,
+         "kan_infer_noalloc: x [B, I], waug [O, ld]")
+    _req(x.dtype == grid.dtype == waug.dtype and x.dtype in _F, "kan_infer_noalloc: dtype mismatch")
+    B, I = x.shape
+    G = grid.shape[1] - 2 * spline_order - 1
+    O = waug.shape[0]
+    ld = int(LIB.kan_hip_aug_width(I, G, spline_order, int(has_base)))
+    _req(tuple(waug.shape) == (O, ld) and grid.shape[0] == I, "kan_infer_noalloc: packed weight shape")
+    x, grid, waug = x.contiguous(), grid.contiguous(), waug.contiguous()
+    y = torch.empty(B, O, dtype=x.dtype, device=x.device)
+    if B * O == 0:
+        return y
+    with torch.cuda.device(x.device):
+        check(LIB.kan_hip_infer_noalloc(dtype_code(x.dtype), ptr(x), ptr(grid), ptr(waug), ptr(y),
+                                        B, I, O, G, spline_order, int(has_base),
+                                        stream_of(x.device)))
+    return y
+
+
 def _basis_of(aug: torch.Tensor, I: int, R: int) -> torch.Tensor:
     """basis [B, I, R] copied out of the augmented rows into its own
     contiguous tensor, the layout kan_forward_cuda returns

@@ -24,6 +24,7 @@ KAN_ERR_INVALID = 1
 KAN_ERR_LIMIT = 2
 KAN_ERR_HIP = 3
 KAN_ERR_WORKSPACE = 4
+KAN_NOALLOC_SCRATCH_BYTES = 64 * 1024 * 1024  # fixed scratch of kan_hip_infer_noalloc
 
 _i64 = ctypes.c_int64
 _int = ctypes.c_int
@@ -48,6 +49,8 @@ SIGNATURES = {
                                        ctypes.POINTER(_sz)]),
     "kan_hip_infer": (_int, [_int, _vp, _vp, _vp, _vp, _vp, _sz, _i64, _i64, _i64, _i64, _i64,
                              _int, _vp]),
+    "kan_hip_infer_noalloc": (_int, [_int, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64,
+                                     _int, _vp]),
     "kan_hip_matmul_workspace": (_int, [_int, _int, _int, _i64, _i64, _i64, ctypes.POINTER(_sz)]),
     "kan_hip_matmul": (_int, [_int, _int, _int, _i64, _i64, _i64, _vp, _i64, _vp, _i64, _vp, _i64,
                               _vp, _sz, _vp]),

@@ -305,6 +305,43 @@ size_t edge_ws_bytes(int dtype, int64_t n, int64_t I, int64_t O, int64_t R, bool
 
 using namespace kan;
 
+// ---- allocation-free inference (kan_hip_infer_noalloc) ----------------------
+// Fixed device scratch that replaces the caller workspace of kan_hip_infer.
+// Each GPU the library runs on holds its own copy until the process ends.
+// Host code never uses the array's name as an address: the per-device
+// address comes from hipGetSymbolAddress on the first call on that device.
+static __device__ __align__(256) unsigned char scratch[KAN_NOALLOC_SCRATCH_BYTES];
+
+namespace kan {
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[kMaxDevices] = {nullptr};
+
+// Address of this device's scratch (looked up once per device, with the
+// device current).
+int scratch_of_current_device(void** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess)
+    return set_error(KAN_ERR_HIP, "kan_infer_noalloc: hipGetDevice failed: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices)
+    return set_error(KAN_ERR_INVALID, "kan_infer_noalloc: device id %d out of range", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr)
+      return set_error(KAN_ERR_HIP, "kan_infer_noalloc: hipGetSymbolAddress(scratch) failed on device %d: %s",
+                       dev, hipGetErrorString(e));
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return KAN_OK;
+}
+}  // namespace
+}  // namespace kan
+
 // Digest of the sources and flags this library was built from, passed by
 // the build script; the Python loader compares it with the sources beside
 // the library and refuses a library built from other sources.
@@ -619,6 +656,35 @@ int kan_hip_infer(int dtype, const void* x, const void* grid, const void* waug, 
   if (dtype == KAN_DTYPE_F32) KAN_INFER_CALL(float);
   KAN_INFER_CALL(double);
 #undef KAN_INFER_CALL
+}
+
+int kan_hip_infer_noalloc(int dtype, const void* x, const void* grid, const void* waug, void* out,
+                          int64_t n, int64_t I, int64_t O, int64_t G, int64_t k, int has_base,
+                          void* stream) {
+  KAN_TRY(check_dtype(dtype, "kan_infer_noalloc"));
+  KAN_TRY(check_layer("kan_infer_noalloc", n, I, O, G, k));
+  if (n * O == 0) return KAN_OK;
+  const int64_t R = G + k;
+  int64_t ld, kaug, aug_elems, part_elems;
+  const size_t elem = dtype == KAN_DTYPE_F32 ? 4 : 8;
+  if (dtype == KAN_DTYPE_F32)
+    infer_plan<float>(n, I, O, R, has_base != 0, &ld, &kaug, &aug_elems, &part_elems);
+  else
+    infer_plan<double>(n, I, O, R, has_base != 0, &ld, &kaug, &aug_elems, &part_elems);
+  const size_t need = elem * (size_t)(aug_elems + part_elems);
+  if (need > (size_t)KAN_NOALLOC_SCRATCH_BYTES)
+    return set_error(KAN_ERR_WORKSPACE,
+                     "kan_infer_noalloc: %lld samples of this layer need %zu bytes of scratch, more "
+                     "than the library's fixed %zu bytes; call kan_hip_infer with a workspace "
+                     "(or split the batch)",
+                     (long long)n, need, (size_t)KAN_NOALLOC_SCRATCH_BYTES);
+  void* ws = nullptr;
+  KAN_TRY(scratch_of_current_device(&ws));
+  // Every element of the workspace that the kernels read is written first in
+  // the same call (basis columns below kaug, whole split slices), so the
+  // previous call's contents need no clearing.
+  return kan_hip_infer(dtype, x, grid, waug, out, ws, (size_t)KAN_NOALLOC_SCRATCH_BYTES, n, I, O, G,
+                       k, has_base, stream);
 }
 
 int kan_hip_pack_basis(int dtype, const void* basis, const void* x, void* aug, int64_t n,
