@@ -157,15 +157,21 @@ int64_t kan_hip_aug_width(int64_t in_features, int64_t grid_size, int64_t spline
 
 /* Forward: output = silu(x) base_weight^T + basis(x) (spline_weight*scaler)^T.
  * base_weight may be NULL (no fused base branch), spline_scaler may be NULL
- * (no scaler).  Writes output [n, O], basis_aug [n, W] (kept for backward) and
- * uses weight_aug [O, W] as workspace.  Replaces kan_forward_cuda
+ * (no scaler).  Writes output [n, O] and basis_aug [n, W] (kept for
+ * backward).  The workspace holds the augmented weight [O, W] and, for
+ * products with few output tiles (few samples or outputs against a long
+ * K), the split-K partial slices of the output, summed in a fixed order;
+ * kan_hip_forward_workspace gives its size.  Replaces kan_forward_cuda
  * (csrc/kan_cuda.cu:469-532) behind _C.kan_forward / KANFunction::forward
  * (csrc/kan_ext.cpp:10-33, csrc/kan_autograd.cpp:18-47). */
+int kan_hip_forward_workspace(int dtype, int64_t n, int64_t in_features, int64_t out_features,
+                              int64_t grid_size, int64_t spline_order, int has_base,
+                              size_t* bytes);
 int kan_hip_forward(int dtype, const void* x, const void* grid, const void* base_weight,
                     const void* spline_weight, const void* spline_scaler, void* output,
-                    void* basis_aug, void* weight_aug, int64_t n, int64_t in_features,
-                    int64_t out_features, int64_t grid_size, int64_t spline_order,
-                    void* stream);
+                    void* basis_aug, void* workspace, size_t workspace_bytes, int64_t n,
+                    int64_t in_features, int64_t out_features, int64_t grid_size,
+                    int64_t spline_order, void* stream);
 
 /* Builds basis_aug [n, W] from a caller-held basis [n, I, R] and x (silu block
  * only when has_base).  Used by the raw backward op, whose caller passes the

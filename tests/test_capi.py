@@ -82,7 +82,7 @@ def test_validation_before_launch(lib):
     assert L.kan_hip_basis(0, None, None, None, 4, 4, 66, 3, None) == lib.KAN_ERR_LIMIT
     assert "G + 2k <= 71" in lib.last_error()
     # in_features beyond the limit
-    assert L.kan_hip_forward(0, None, None, None, None, None, None, None, None,
+    assert L.kan_hip_forward(0, None, None, None, None, None, None, None, None, 0,
                              4, 65536, 4, 5, 3, None) == lib.KAN_ERR_LIMIT
     assert "in_features <= 65535" in lib.last_error()
     # spline order

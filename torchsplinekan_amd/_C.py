@@ -92,12 +92,15 @@ def _forward_device(x, grid, base_weight, spline_weight, spline_scaler, k, has_s
     B, I = x.shape
     O = sw.shape[0]
     ld = int(LIB.kan_hip_aug_width(I, G, k, int(hb)))
+    code = dtype_code(x.dtype)
     y = torch.empty(B, O, dtype=x.dtype, device=x.device)
     aug = torch.empty(B, ld, dtype=x.dtype, device=x.device)
-    waug = torch.empty(O, ld, dtype=x.dtype, device=x.device)
+    nbytes = _lib.ctypes.c_size_t(0)
+    check(LIB.kan_hip_forward_workspace(code, B, I, O, G, k, int(hb), _lib.ctypes.byref(nbytes)))
+    ws = torch.empty(max(int(nbytes.value), 1), dtype=torch.uint8, device=x.device)
     with torch.cuda.device(x.device):
-        check(LIB.kan_hip_forward(dtype_code(x.dtype), ptr(x), ptr(grid), ptr(bw), ptr(sw),
-                                  ptr(sc), ptr(y), ptr(aug), ptr(waug), B, I, O, G, k,
+        check(LIB.kan_hip_forward(code, ptr(x), ptr(grid), ptr(bw), ptr(sw), ptr(sc), ptr(y),
+                                  ptr(aug), ptr(ws), int(nbytes.value), B, I, O, G, k,
                                   stream_of(x.device)))
     return y, aug
 

@@ -58,7 +58,9 @@ SIGNATURES = {
     "kan_hip_basis_deriv_contract": (_int, [_int, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64,
                                             _i64, _vp]),
     "kan_hip_aug_width": (_i64, [_i64, _i64, _i64, _int]),
-    "kan_hip_forward": (_int, [_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
+    "kan_hip_forward_workspace": (_int, [_int, _i64, _i64, _i64, _i64, _i64, _int,
+                                         ctypes.POINTER(_sz)]),
+    "kan_hip_forward": (_int, [_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz,
                                _i64, _i64, _i64, _i64, _i64, _vp]),
     "kan_hip_pack_basis": (_int, [_int, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _int, _vp]),
     "kan_hip_backward_workspace": (_int, [_int, _i64, _i64, _i64, _i64, _i64, _int, _int, _int,

@@ -210,24 +210,41 @@ BackwardPlan plan_backward(int64_t n, int64_t I, int64_t O, int64_t G, int64_t k
   return p;
 }
 
+// Forward workspace: the augmented weight [O, ld], then the split-K partial
+// slices of the output product (elements).  Products with few output tiles
+// (few samples or outputs, long K: c5's layer, small networks) are split over
+// K and summed in a fixed order; large ones (c3) are not split.
+template <typename T>
+void forward_plan(int64_t n, int64_t I, int64_t O, int64_t R, bool has_base, int64_t* ld,
+                  int64_t* kaug, int64_t* waug_elems, int64_t* part_elems) {
+  *ld = aug_width(I, R, has_base);
+  *kaug = I * R + (has_base ? I : 0);
+  *waug_elems = round_up(O * *ld, 64);
+  *part_elems = matmul_ws_elems<T>(kLayoutNT, n, O, *kaug);
+}
+
 template <typename T>
 int forward_impl(const void* x, const void* grid, const void* bw, const void* sw,
-                 const void* scaler, void* out, void* aug, void* waug, int64_t n, int64_t I,
-                 int64_t O, int64_t G, int64_t k, hipStream_t st) {
+                 const void* scaler, void* out, void* aug, void* ws, size_t ws_bytes, int64_t n,
+                 int64_t I, int64_t O, int64_t G, int64_t k, hipStream_t st) {
   const int64_t R = G + k;
   const bool has_base = bw != nullptr;
-  const int64_t ld = aug_width(I, R, has_base);
-  const int64_t kaug = I * R + (has_base ? I : 0);
+  int64_t ld, kaug, waug_elems, part_elems;
+  forward_plan<T>(n, I, O, R, has_base, &ld, &kaug, &waug_elems, &part_elems);
+  const size_t need = sizeof(T) * (size_t)(waug_elems + part_elems);
+  if (ws_bytes < need || (need > 0 && ws == nullptr))
+    return set_error(KAN_ERR_WORKSPACE, "kan_forward: workspace of %zu bytes is smaller than the %zu required",
+                     ws_bytes, need);
   const T* tx = static_cast<const T*>(x);
   T* taug = static_cast<T*>(aug);
-  T* twaug = static_cast<T*>(waug);
+  T* twaug = static_cast<T*>(ws);
   KAN_TRY(launch_build_waug<T>(static_cast<const T*>(sw), static_cast<const T*>(scaler),
                                static_cast<const T*>(bw), twaug, ld, O, I, R, st));
   KAN_TRY(launch_basis<T>(tx, static_cast<const T*>(grid), taug, ld,
                           has_base ? taug + I * R : nullptr, n, I, (int)G, (int)k,
                           g_basis_impl.load(), st));
-  return launch_gemm<T>(kLayoutNT, n, O, kaug, taug, ld, twaug, ld, static_cast<T*>(out), O, 1,
-                        0, st);
+  return launch_matmul<T>(kLayoutNT, n, O, kaug, taug, ld, twaug, ld, static_cast<T*>(out), O,
+                          twaug + waug_elems, st);
 }
 
 template <typename T>
@@ -565,16 +582,28 @@ int64_t kan_hip_aug_width(int64_t I, int64_t G, int64_t k, int has_base) {
   return aug_width(I, G + k, has_base != 0);
 }
 
+int kan_hip_forward_workspace(int dtype, int64_t n, int64_t I, int64_t O, int64_t G, int64_t k,
+                              int has_base, size_t* bytes) {
+  KAN_TRY(check_dtype(dtype, "kan_forward_workspace"));
+  KAN_TRY(check_layer("kan_forward_workspace", n, I, O, G, k));
+  KAN_TRY(need_ptr(bytes, "kan_forward_workspace", "bytes"));
+  int64_t ld, kaug, we, pe;
+  if (dtype == KAN_DTYPE_F32) forward_plan<float>(n, I, O, G + k, has_base != 0, &ld, &kaug, &we, &pe);
+  else forward_plan<double>(n, I, O, G + k, has_base != 0, &ld, &kaug, &we, &pe);
+  *bytes = (dtype == KAN_DTYPE_F32 ? 4 : 8) * (size_t)(we + pe);
+  return KAN_OK;
+}
+
 int kan_hip_forward(int dtype, const void* x, const void* grid, const void* bw, const void* sw,
-                    const void* scaler, void* out, void* aug, void* waug, int64_t n, int64_t I,
-                    int64_t O, int64_t G, int64_t k, void* stream) {
+                    const void* scaler, void* out, void* aug, void* ws, size_t ws_bytes,
+                    int64_t n, int64_t I, int64_t O, int64_t G, int64_t k, void* stream) {
   KAN_TRY(check_dtype(dtype, "kan_forward"));
   KAN_TRY(check_layer("kan_forward", n, I, O, G, k));
   // Pointers are only required for buffers of non-zero size.
   const int64_t R = G + k;
   const int64_t ld = aug_width(I, R, bw != nullptr);
   if (O * I > 0) KAN_TRY(need_ptr(sw, "kan_forward", "spline_weight"));
-  if (O * ld > 0) KAN_TRY(need_ptr(waug, "kan_forward", "weight_aug"));
+  if (O * ld > 0) KAN_TRY(need_ptr(ws, "kan_forward", "workspace"));
   if (n * I > 0) {
     KAN_TRY(need_ptr(x, "kan_forward", "x"));
     KAN_TRY(need_ptr(grid, "kan_forward", "grid"));
@@ -583,8 +612,8 @@ int kan_hip_forward(int dtype, const void* x, const void* grid, const void* bw, 
   if (n * O > 0) KAN_TRY(need_ptr(out, "kan_forward", "output"));
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (dtype == KAN_DTYPE_F32)
-    return forward_impl<float>(x, grid, bw, sw, scaler, out, aug, waug, n, I, O, G, k, st);
-  return forward_impl<double>(x, grid, bw, sw, scaler, out, aug, waug, n, I, O, G, k, st);
+    return forward_impl<float>(x, grid, bw, sw, scaler, out, aug, ws, ws_bytes, n, I, O, G, k, st);
+  return forward_impl<double>(x, grid, bw, sw, scaler, out, aug, ws, ws_bytes, n, I, O, G, k, st);
 }
 
 int kan_hip_pack_weight(int dtype, const void* bw, const void* sw, const void* scaler, void* waug,
