@@ -140,3 +140,28 @@ def test_empty_batch(C):
     assert H.shape == (0, 4, 8)
     gx = C.basis_grad(x, grid, 3, torch.empty(0, 4, 8, device="cuda"))
     assert gx.shape == (0, 4)
+
+
+@pytest.mark.parametrize("I,G,k", [(100, 40, 3), (7, 30, 2), (64, 22, 3), (130, 69, 1)])
+def test_large_grid_paths_fp32(C, I, G, k):
+    """Grids with R = G + k >= 25 take the window-record basis kernel and the
+    window-gather gradient kernel: values, zero pattern, the gradient
+    contraction and every derivative order against the oracle, with a
+    ragged last feature block (I = 100, 130), fewer than 64 features (several
+    samples per wave step, I = 7) and exactly R = 25 (I = 64)."""
+    print(f"large-grid paths I={I} G={G} k={k}", flush=True)
+    grid = make_grid(I, G, k, "nonuniform", seed=I + G, dtype=torch.float32)
+    x = make_points(grid, n=333, seed=G)
+    H = C.basis(x.cuda(), grid.cuda(), k).cpu().numpy()
+    x64, g64 = x.double().numpy(), grid.double().numpy()
+    ref64 = ko.basis_dense(x64, g64, k)
+    assert np.array_equal(H == 0, ref64 == 0)
+    assert np.abs(H - ref64).max() < 2e-6
+    gH = torch.randn(H.shape, generator=torch.Generator().manual_seed(G))
+    gx = C.basis_grad(x.cuda(), grid.cuda(), k, gH.cuda()).cpu().double().numpy()
+    gref = (gH.double().numpy() * ko.basis_derivative(x64, g64, k)).sum(-1)
+    assert normwise(gx, gref) < 1e-5
+    for q in range(k + 1):
+        Dq = C.basis_deriv(x.cuda(), grid.cuda(), k, q).cpu().double().numpy()
+        rq = ko.basis_derivative_n(x64, g64, k, q)
+        assert normwise(Dq, rq) < 1e-5, q

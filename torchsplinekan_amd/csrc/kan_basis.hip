@@ -130,6 +130,44 @@ __device__ __forceinline__ void move_row(T* __restrict__ gmem, T* __restrict__ l
   }
 }
 
+// Record of a lane with no window (zero row): every r is outside it.
+constexpr int kNoWindow = -(1 << 20);
+
+// Writes one staged sample segment (fbv features x R values, contiguous in
+// the output) from the per-item window records: item f has its K+1 values
+// at vals[f*(K+1) ..] for r = r0[f] .. r0[f]+K, zero elsewhere.  Each lane
+// forms whole 16-byte vectors of the segment (when vec), so the stores are
+// coalesced; window entries that are not real basis functions (r < 0 or
+// r >= R near the ends of the knot vector) are never addressed.
+template <int K, typename T>
+__device__ __forceinline__ void write_window_segment(T* __restrict__ gmem,
+                                                     const T* __restrict__ vals,
+                                                     const int* __restrict__ r0, int fbv, int R,
+                                                     float inv_r, int lane, bool vec) {
+  typedef typename V16<T>::type VT;
+  constexpr int kV = V16<T>::kN;
+  const int cnt = fbv * R;
+  auto value = [&](int idx) -> T {
+    const int f = small_div(idx, inv_r);
+    const int j = idx - f * R - r0[f];
+    const int jc = j < 0 ? 0 : (j > K ? K : j);
+    const T v = vals[f * (K + 1) + jc];
+    return j == jc ? v : T(0);
+  };
+  int done = 0;
+  if (vec) {
+    const int nv = cnt / kV;
+    for (int c = lane; c < nv; c += 64) {
+      VT o;
+#pragma unroll
+      for (int e = 0; e < kV; ++e) o[e] = value(c * kV + e);
+      reinterpret_cast<VT*>(gmem)[c] = o;
+    }
+    done = nv * kV;
+  }
+  for (int c = done + lane; c < cnt; c += 64) gmem[c] = value(c);
+}
+
 // Wave-scope barrier: orders this wave's LDS writes before its following
 // LDS reads (and vice versa) at the compiler level; LDS instructions of one
 // wave complete in issue order.
@@ -144,13 +182,25 @@ __device__ __forceinline__ void wave_sync() {
 constexpr int kMaxIters = 8;
 
 // H rows (and optionally silu(x)) for a block of features x samples.
-// Each wave loads the x values of all of its steps up front, then per step
-// fills its own LDS stage (the subs sample segments exactly as they lie in
-// the output, item rows of R values back to back) and writes each segment
-// out with coalesced 16-byte stores.  Only the knot staging needs a block
-// barrier; the stages are private to their waves.
-// DER > 0 (impl 1 only) writes the order-DER derivatives instead of values.
-template <int K, typename T, int IMPL, int DER = 0>
+// Each wave loads the x values of all of its steps up front.  Per step, the
+// wave stages its items and writes each sample segment with coalesced
+// 16-byte stores.  Staging:
+//   REC (impl 1, large R): each item's window record (span start and K+1
+//     values); segments are formed from the records (write_window_segment),
+//     so the dense rows are never staged: K+2 LDS writes per item instead
+//     of R, and a small LDS footprint;
+//   dense stage (impl 1, small R): a dense R-row per item (the subs sample
+//     segments exactly as they lie in the output), zeroed once, after which
+//     each step clears only the item's previous window before writing the
+//     new one, and copied out (move_row);
+//   impl 0 (dense recurrence): the dense R-row, fully written each step.
+// Only the knot staging needs a block barrier; the stages are private to
+// their waves.  DER > 0 (impl 1 only) writes the order-DER derivatives.
+// Grid sizes above this take impl 1's window records; at or below it the
+// dense stage is cheaper (fewer VALU operations per output element).
+constexpr int kWindowRecordMinR = 25;
+
+template <int K, typename T, int IMPL, int DER = 0, bool REC = false>
 __global__ __launch_bounds__(kBasisThreads) void basis_kernel(
     const T* __restrict__ x, const T* __restrict__ grid, T* __restrict__ out, int64_t ld,
     T* __restrict__ silu_out, BasisShape sh) {
@@ -170,11 +220,27 @@ __global__ __launch_bounds__(kBasisThreads) void basis_kernel(
     xs[it] = (it < sh.iters && lane_ok && nn < sh.n) ? x[nn * sh.I + i0 + fi] : T(0);
   }
   T* knots = stage_knots<T>(smem, grid, i0, fbv, nk);
-  T* stage = knots + round_up((int64_t)sh.fb * nk, 4) + wave * 64 * R;
+  T* region = knots + round_up((int64_t)sh.fb * nk, 4);
+  // REC: K+1 window values per lane, followed by the lanes' window starts;
+  // otherwise a dense R-row per lane
+  T* stage = region + wave * 64 * (REC ? K + 1 : R);
+  int* rec_r0 = reinterpret_cast<int*>(region + sh.waves * 64 * (K + 1)) + wave * 64;
   const T* t = knots + fi * nk;
+  if (IMPL == 1 && !REC) {  // zero the wave's dense stage once
+    typedef typename V16<T>::type VT;
+    constexpr int kV = V16<T>::kN;
+    const int cnt = 64 * R;
+    if (((64 * R) % kV) == 0) {
+      for (int c = lane; c < cnt / kV; c += 64) reinterpret_cast<VT*>(stage)[c] = VT{};
+    } else {
+      for (int c = lane; c < cnt; c += 64) stage[c] = T(0);
+    }
+  }
   __syncthreads();
-  T* row = stage + lane * R;
+  T* row = stage + lane * (REC ? K + 1 : R);
   const bool vec = sh.vec != 0;
+  const float inv_r = 1.0f / (float)R;
+  int prev_m = -1;  // dense stage: span of the window this lane wrote last
 #pragma unroll
   for (int it = 0; it < kMaxIters; ++it) {
     if (it >= sh.iters) break;
@@ -183,16 +249,31 @@ __global__ __launch_bounds__(kBasisThreads) void basis_kernel(
     const bool ok = lane_ok && nn < sh.n;
     const T xv = xs[it];
     if (IMPL == 1) {
-      for (int r = 0; r < R; ++r) row[r] = T(0);
       const int m = ok ? knot_span(t, nk, xv) : -1;
-      if (m >= 0) {
-        T v[K + 1];
-        span_window<K, DER, T>(t, nk, m, xv, v);
+      T v[K + 1];
 #pragma unroll
-        for (int j = 0; j <= K; ++j) {
-          const int r = m - K + j;
-          if (r >= 0 && r < R) row[r] = v[j];
+      for (int j = 0; j <= K; ++j) v[j] = T(0);
+      if (m >= 0) span_window<K, DER, T>(t, nk, m, xv, v);
+      if (REC) {
+#pragma unroll
+        for (int j = 0; j <= K; ++j) row[j] = v[j];
+        rec_r0[lane] = m >= 0 ? m - K : kNoWindow;
+      } else {
+        if (prev_m >= 0) {
+#pragma unroll
+          for (int j = 0; j <= K; ++j) {
+            const int r = prev_m - K + j;
+            if (r >= 0 && r < R) row[r] = T(0);
+          }
         }
+        if (m >= 0) {
+#pragma unroll
+          for (int j = 0; j <= K; ++j) {
+            const int r = m - K + j;
+            if (r >= 0 && r < R) row[r] = v[j];
+          }
+        }
+        prev_m = m;
       }
     } else {
       if (ok) {
@@ -206,8 +287,12 @@ __global__ __launch_bounds__(kBasisThreads) void basis_kernel(
     for (int s = 0; s < sh.subs; ++s) {
       const int64_t ns = nb + s;
       if (ns >= sh.n) break;
-      move_row<T, true>(out + ns * ld + (int64_t)i0 * R, stage + s * sh.fb * R, fbv * R, lane,
-                        vec);
+      T* dst = out + ns * ld + (int64_t)i0 * R;
+      if (REC)
+        write_window_segment<K, T>(dst, stage + s * sh.fb * (K + 1), rec_r0 + s * sh.fb, fbv, R,
+                                   inv_r, lane, vec);
+      else
+        move_row<T, true>(dst, stage + s * sh.fb * R, fbv * R, lane, vec);
     }
     wave_sync();
   }
@@ -476,6 +561,60 @@ __global__ __launch_bounds__(kBasisThreads) void basis_grad_pf_kernel(
   }
 }
 
+// basis_grad for large grids (impl 1, R >= kWindowRecordMinR): each lane
+// loads only the K+1 gradient values of its span window straight from
+// global memory; the other R - K - 1 values of the item's row are never
+// read, so the bytes fetched per item are the window's cache lines instead
+// of the whole row.  No gradient staging in LDS (only the knot rows), so a
+// CU holds many waves to cover the load latency; the next step's x is
+// loaded while the current step is computed.  Same products in the same
+// order as basis_grad_pf_kernel (a window entry outside 0..R-1 adds +0).
+template <int K, typename T, int DER>
+__global__ __launch_bounds__(kBasisThreads) void basis_grad_window_kernel(
+    const T* __restrict__ x, const T* __restrict__ grid, const T* __restrict__ g, int64_t ld,
+    const T* __restrict__ gbase, T* __restrict__ gx, BasisShape sh) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int nk = sh.G + 2 * K + 1, R = sh.G + K;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int i0 = blockIdx.x * sh.fb;
+  const int fbv = min(sh.fb, sh.I - i0);
+  T* knots = stage_knots<T>(smem, grid, i0, fbv, nk);
+  const int sub = lane / sh.fb, fi = lane - sub * sh.fb;
+  const bool lane_ok = sub < sh.subs && fi < fbv;
+  const T* t = knots + (lane_ok ? fi : 0) * nk;
+  const int64_t step = (int64_t)sh.waves * sh.subs;
+  int64_t nn = (int64_t)blockIdx.y * sh.iters * step + (int64_t)wave * sh.subs + sub;
+  const int64_t col = (int64_t)i0 + (lane_ok ? fi : 0);
+  T xn = (lane_ok && nn < sh.n) ? x[nn * sh.I + col] : T(0);
+  __syncthreads();  // knot rows staged
+  for (int it = 0; it < sh.iters; ++it, nn += step) {
+    const bool ok = lane_ok && nn < sh.n;
+    const T xv = xn;
+    const int m = ok ? knot_span(t, nk, xv) : -1;
+    const T* grow = g + nn * ld + col * R;  // dereferenced only inside the window
+    T gw[K + 1];
+#pragma unroll
+    for (int j = 0; j <= K; ++j) {
+      const int r = m - K + j;
+      gw[j] = (m >= 0 && r >= 0 && r < R) ? grow[r] : T(0);
+    }
+    const T gb = (ok && gbase != nullptr) ? gbase[nn * ld + col] : T(0);
+    const int64_t nx = nn + step;
+    xn = (it + 1 < sh.iters && lane_ok && nx < sh.n) ? x[nx * sh.I + col] : T(0);
+    if (ok) {
+      T acc = T(0);
+      if (m >= 0) {
+        T d[K + 1];
+        span_window<K, DER, T>(t, nk, m, xv, d);
+#pragma unroll
+        for (int j = 0; j <= K; ++j) acc += gw[j] * d[j];
+      }
+      if (gbase != nullptr) acc += gb * silu_grad_of<T>(xv);
+      gx[nn * sh.I + col] = acc;
+    }
+  }
+}
+
 // Register vectors per lane the prefetching kernel needs (0 = not eligible).
 template <typename T>
 int grad_pf_vectors(const BasisShape& sh, int R) {
@@ -489,7 +628,7 @@ int grad_pf_vectors(const BasisShape& sh, int R) {
 }
 
 BasisShape make_shape(int64_t n, int64_t I, int G, int R, size_t elem, int64_t ld,
-                      const void* rows_ptr, int64_t* blocks_y) {
+                      const void* rows_ptr, int64_t* blocks_y, bool dense_stage = true) {
   BasisShape sh;
   sh.n = n;
   sh.I = (int)I;
@@ -497,7 +636,9 @@ BasisShape make_shape(int64_t n, int64_t I, int G, int R, size_t elem, int64_t l
   sh.fb = (int)(I < 64 ? I : 64);
   sh.subs = 64 / sh.fb;
   sh.waves = 4;
-  while (sh.waves > 1 && (size_t)sh.waves * 64 * R * elem > 48 * 1024) sh.waves /= 2;
+  // a dense R-row stage per lane bounds the waves of a block by LDS
+  while (dense_stage && sh.waves > 1 && (size_t)sh.waves * 64 * R * elem > 48 * 1024)
+    sh.waves /= 2;
   // 16-byte vectors: the output rows, each block's feature offset and each
   // staged sample segment must all start 16-byte aligned.
   const int64_t v = 16 / (int64_t)elem;
@@ -521,6 +662,14 @@ size_t basis_smem(const BasisShape& sh, int nk, int R) {
   return sizeof(T) * (round_up((int64_t)sh.fb * nk, 4) + (int64_t)sh.waves * 64 * R);
 }
 
+// LDS of basis_kernel with impl 1: knots, K+1 window values and the window
+// start per lane.
+template <typename T>
+size_t basis_window_smem(const BasisShape& sh, int nk, int k) {
+  return sizeof(T) * (round_up((int64_t)sh.fb * nk, 4) + (int64_t)sh.waves * 64 * (k + 1)) +
+         sizeof(int) * (size_t)sh.waves * 64;
+}
+
 inline int gs_blocks(int64_t total) {
   int64_t b = ceil_div(total, 256);
   if (b > 65536) b = 65536;
@@ -534,25 +683,30 @@ int launch_basis(const T* x, const T* grid, T* out, int64_t ld_out, T* silu_out,
                  int64_t I, int G, int k, int impl, hipStream_t st) {
   if (n == 0 || I == 0) return KAN_OK;
   const int R = G + k, nk = G + 2 * k + 1;
+  const bool rec = impl == 1 && R >= kWindowRecordMinR;
   int64_t by = 0;
-  BasisShape sh = make_shape(n, I, G, R, sizeof(T), ld_out, out, &by);
+  BasisShape sh = make_shape(n, I, G, R, sizeof(T), ld_out, out, &by, !rec);
   if (by > 2147483647LL) return set_error(KAN_ERR_LIMIT, "basis: too many samples (%lld)", (long long)n);
   dim3 grid_dim((unsigned)ceil_div(I, sh.fb), (unsigned)by);
-  const size_t smem = basis_smem<T>(sh, nk, R);
+  const size_t smem = rec ? basis_window_smem<T>(sh, nk, k) : basis_smem<T>(sh, nk, R);
   // algorithmic bytes: read x, write the R basis values (+ silu) per item
   TimedLaunch timed(kClassBasis, st,
                     (double)sizeof(T) * (double)n * (double)I * (1.0 + R + (silu_out ? 1 : 0)));
-#define KAN_BASIS_LAUNCH(KK, IM)                                                           \
-  hipLaunchKernelGGL((basis_kernel<KK, T, IM>), grid_dim, dim3(64 * sh.waves), smem, st, x, \
-                     grid, out, ld_out, silu_out, sh)
-  if (impl == 1) {
-    if (k == 1) KAN_BASIS_LAUNCH(1, 1);
-    else if (k == 2) KAN_BASIS_LAUNCH(2, 1);
-    else KAN_BASIS_LAUNCH(3, 1);
+#define KAN_BASIS_LAUNCH(KK, IM, RC)                                                     \
+  hipLaunchKernelGGL((basis_kernel<KK, T, IM, 0, RC>), grid_dim, dim3(64 * sh.waves), smem, \
+                     st, x, grid, out, ld_out, silu_out, sh)
+  if (rec) {
+    if (k == 1) KAN_BASIS_LAUNCH(1, 1, true);
+    else if (k == 2) KAN_BASIS_LAUNCH(2, 1, true);
+    else KAN_BASIS_LAUNCH(3, 1, true);
+  } else if (impl == 1) {
+    if (k == 1) KAN_BASIS_LAUNCH(1, 1, false);
+    else if (k == 2) KAN_BASIS_LAUNCH(2, 1, false);
+    else KAN_BASIS_LAUNCH(3, 1, false);
   } else {
-    if (k == 1) KAN_BASIS_LAUNCH(1, 0);
-    else if (k == 2) KAN_BASIS_LAUNCH(2, 0);
-    else KAN_BASIS_LAUNCH(3, 0);
+    if (k == 1) KAN_BASIS_LAUNCH(1, 0, false);
+    else if (k == 2) KAN_BASIS_LAUNCH(2, 0, false);
+    else KAN_BASIS_LAUNCH(3, 0, false);
   }
 #undef KAN_BASIS_LAUNCH
   return check_launch("basis");
@@ -610,6 +764,21 @@ int launch_basis_grad(const T* x, const T* grid, const T* gH, int64_t ld_g, cons
   TimedLaunch timed(kClassBasisGrad, st,
                     (double)sizeof(T) * (double)n * (double)I * (2.0 + R + (gbase ? 1 : 0)));
   int rc = KAN_OK;
+  if (impl == 1 && R >= kWindowRecordMinR) {
+    int64_t by = 0;
+    BasisShape sh = make_shape(n, I, G, R, sizeof(T), ld_g, gH, &by, false);
+    if (by > 2147483647LL) return set_error(KAN_ERR_LIMIT, "basis_grad: too many samples");
+    dim3 grid_dim((unsigned)ceil_div(I, sh.fb), (unsigned)by);
+    const size_t smem = sizeof(T) * (size_t)round_up((int64_t)sh.fb * nk, 4);
+#define KAN_BGW(KK)                                                                        \
+  hipLaunchKernelGGL((basis_grad_window_kernel<KK, T, 1>), grid_dim, dim3(64 * sh.waves), \
+                     smem, st, x, grid, gH, ld_g, gbase, gx, sh)
+    if (k == 1) KAN_BGW(1);
+    else if (k == 2) KAN_BGW(2);
+    else KAN_BGW(3);
+#undef KAN_BGW
+    return check_launch("basis_grad");
+  }
   if (impl == 1 && launch_grad_pf<T, 1>(x, grid, gH, ld_g, gbase, gx, n, I, G, k, st, &rc))
     return rc;
   int64_t by = 0;
@@ -652,15 +821,22 @@ int launch_basis_deriv(const T* x, const T* grid, T* out, int64_t n, int64_t I, 
                        n * I * R);
     return check_launch("basis_deriv (zero)");
   }
+  const bool rec = R >= kWindowRecordMinR;
   int64_t by = 0;
-  BasisShape sh = make_shape(n, I, G, R, sizeof(T), I * R, out, &by);
+  BasisShape sh = make_shape(n, I, G, R, sizeof(T), I * R, out, &by, !rec);
   if (by > 2147483647LL) return set_error(KAN_ERR_LIMIT, "basis_deriv: too many samples");
   dim3 grid_dim((unsigned)ceil_div(I, sh.fb), (unsigned)by);
-  const size_t smem = basis_smem<T>(sh, nk, R);
+  const size_t smem = rec ? basis_window_smem<T>(sh, nk, k) : basis_smem<T>(sh, nk, R);
   TimedLaunch timed(kClassBasis, st, (double)sizeof(T) * (double)n * (double)I * (1.0 + R));
-#define KAN_BDER_LAUNCH(KK, DD)                                                              \
-  hipLaunchKernelGGL((basis_kernel<KK, T, 1, DD>), grid_dim, dim3(64 * sh.waves), smem, st, x, \
-                     grid, out, (int64_t)I * R, (T*)nullptr, sh)
+#define KAN_BDER_LAUNCH(KK, DD)                                                                \
+  do {                                                                                         \
+    if (rec)                                                                                   \
+      hipLaunchKernelGGL((basis_kernel<KK, T, 1, DD, true>), grid_dim, dim3(64 * sh.waves),    \
+                         smem, st, x, grid, out, (int64_t)I * R, (T*)nullptr, sh);             \
+    else                                                                                       \
+      hipLaunchKernelGGL((basis_kernel<KK, T, 1, DD, false>), grid_dim, dim3(64 * sh.waves),   \
+                         smem, st, x, grid, out, (int64_t)I * R, (T*)nullptr, sh);             \
+  } while (0)
   if (k == 1) {
     if (order == 0) KAN_BDER_LAUNCH(1, 0);
     else KAN_BDER_LAUNCH(1, 1);

@@ -10,53 +10,53 @@ namespace kan {
 namespace {
 
 constexpr int kStreamThreads = 256;
-constexpr int kStreamUnroll = 4;  // float4 per thread per iteration, loads issued together
+constexpr int kStreamUnroll = 4;  // float4 per thread, loads issued together
+// Each workgroup covers one contiguous chunk of 256 x 4 float4 = 16 KiB:
+// pass u moves 256 consecutive float4 (4 KiB, one per lane).
+constexpr int64_t kChunk4 = (int64_t)kStreamThreads * kStreamUnroll;
 
 __global__ void __launch_bounds__(kStreamThreads)
 stream_write_kernel(float4* __restrict__ dst, int64_t n4) {
-  const int64_t stride = (int64_t)gridDim.x * kStreamThreads;
+  const int64_t base = (int64_t)blockIdx.x * kChunk4 + threadIdx.x;
   const float4 v = make_float4(1.0f, 2.0f, 3.0f, 4.0f);
-  int64_t i = (int64_t)blockIdx.x * kStreamThreads + threadIdx.x;
-  for (; i + (kStreamUnroll - 1) * stride < n4; i += kStreamUnroll * stride) {
 #pragma unroll
-    for (int u = 0; u < kStreamUnroll; ++u) dst[i + u * stride] = v;
+  for (int u = 0; u < kStreamUnroll; ++u) {
+    const int64_t i = base + u * kStreamThreads;
+    if (i < n4) dst[i] = v;
   }
-  for (; i < n4; i += stride) dst[i] = v;
 }
 
 // The sum is written only when it equals a value the inputs never produce,
 // so the loads stay and the kernel writes nothing in practice.
 __global__ void __launch_bounds__(kStreamThreads)
 stream_read_kernel(const float4* __restrict__ src, float* __restrict__ sink, int64_t n4) {
-  const int64_t stride = (int64_t)gridDim.x * kStreamThreads;
+  const int64_t base = (int64_t)blockIdx.x * kChunk4 + threadIdx.x;
+  float4 v[kStreamUnroll];
+#pragma unroll
+  for (int u = 0; u < kStreamUnroll; ++u) {
+    const int64_t i = base + u * kStreamThreads;
+    v[u] = i < n4 ? src[i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  }
   float acc = 0.0f;
-  int64_t i = (int64_t)blockIdx.x * kStreamThreads + threadIdx.x;
-  for (; i + (kStreamUnroll - 1) * stride < n4; i += kStreamUnroll * stride) {
-    float4 v[kStreamUnroll];
 #pragma unroll
-    for (int u = 0; u < kStreamUnroll; ++u) v[u] = src[i + u * stride];
-#pragma unroll
-    for (int u = 0; u < kStreamUnroll; ++u) acc += (v[u].x + v[u].y) + (v[u].z + v[u].w);
-  }
-  for (; i < n4; i += stride) {
-    const float4 v = src[i];
-    acc += (v.x + v.y) + (v.z + v.w);
-  }
+  for (int u = 0; u < kStreamUnroll; ++u) acc += (v[u].x + v[u].y) + (v[u].z + v[u].w);
   if (acc == -1234567.0f) sink[0] = acc;
 }
 
 __global__ void __launch_bounds__(kStreamThreads)
 stream_copy_kernel(const float4* __restrict__ src, float4* __restrict__ dst, int64_t n4) {
-  const int64_t stride = (int64_t)gridDim.x * kStreamThreads;
-  int64_t i = (int64_t)blockIdx.x * kStreamThreads + threadIdx.x;
-  for (; i + (kStreamUnroll - 1) * stride < n4; i += kStreamUnroll * stride) {
-    float4 v[kStreamUnroll];
+  const int64_t base = (int64_t)blockIdx.x * kChunk4 + threadIdx.x;
+  float4 v[kStreamUnroll];
 #pragma unroll
-    for (int u = 0; u < kStreamUnroll; ++u) v[u] = src[i + u * stride];
-#pragma unroll
-    for (int u = 0; u < kStreamUnroll; ++u) dst[i + u * stride] = v[u];
+  for (int u = 0; u < kStreamUnroll; ++u) {
+    const int64_t i = base + u * kStreamThreads;
+    if (i < n4) v[u] = src[i];
   }
-  for (; i < n4; i += stride) dst[i] = src[i];
+#pragma unroll
+  for (int u = 0; u < kStreamUnroll; ++u) {
+    const int64_t i = base + u * kStreamThreads;
+    if (i < n4) dst[i] = v[u];
+  }
 }
 
 }  // namespace
@@ -64,16 +64,16 @@ stream_copy_kernel(const float4* __restrict__ src, float4* __restrict__ dst, int
 int launch_stream_probe(int mode, void* a, void* b, int64_t bytes, hipStream_t st) {
   const int64_t n4 = bytes / 16;
   if (n4 <= 0) return KAN_OK;
-  const int64_t want = ceil_div(n4, (int64_t)kStreamThreads * kStreamUnroll);
-  const int blocks = (int)std::min<int64_t>(want, (int64_t)device_cu_count() * 16);
+  const int64_t blocks = ceil_div(n4, kChunk4);
+  if (blocks > 2147483647LL) return set_error(KAN_ERR_LIMIT, "stream_probe: buffer too large");
   const double moved = (double)(n4 * 16) * (mode == 2 ? 2.0 : 1.0);
   TimedLaunch t(kClassStream, st, moved);
   if (mode == 0) {
-    stream_write_kernel<<<blocks, kStreamThreads, 0, st>>>((float4*)a, n4);
+    stream_write_kernel<<<(unsigned)blocks, kStreamThreads, 0, st>>>((float4*)a, n4);
   } else if (mode == 1) {
-    stream_read_kernel<<<blocks, kStreamThreads, 0, st>>>((const float4*)a, (float*)b, n4);
+    stream_read_kernel<<<(unsigned)blocks, kStreamThreads, 0, st>>>((const float4*)a, (float*)b, n4);
   } else {
-    stream_copy_kernel<<<blocks, kStreamThreads, 0, st>>>((const float4*)a, (float4*)b, n4);
+    stream_copy_kernel<<<(unsigned)blocks, kStreamThreads, 0, st>>>((const float4*)a, (float4*)b, n4);
   }
   return check_launch("stream_probe");
 }
