@@ -252,3 +252,31 @@ def test_basis_helpers_match_oracle():
                     ko.basis_derivative(np64(x), np64(grid), 2)) < 1e-14
     with pytest.raises(ValueError):
         compute_basis(x, grid, 4)
+
+
+def test_select_keeps_the_chosen_edges():
+    """KANLinear.select: all indices reproduce the layer; a subset of outputs
+    and inputs equals the full layer evaluated with the dropped inputs'
+    edges removed, restricted to the kept outputs."""
+    torch.manual_seed(3)
+    L = KANLinear(6, 5, grid_size=4, backend="reference").double()
+    with torch.no_grad():
+        L.spline_scaler.uniform_(0.5, 1.5)
+        L.grid.add_(torch.linspace(0, 0.1, 6, dtype=torch.float64)[:, None])
+        L._ref.grid.copy_(L.grid)
+    x = torch.rand(40, 6, dtype=torch.float64) * 2 - 1
+    full = L.select()
+    assert torch.equal(full(x), L(x))
+    oi, ii = torch.tensor([4, 1]), torch.tensor([0, 3, 5])
+    sub = L.select(oi, ii)
+    assert (sub.in_features, sub.out_features) == (3, 2)
+    assert torch.equal(sub.grid, L.grid[ii]) and torch.equal(sub._ref.grid, L.grid[ii])
+    masked = L.make_like()
+    masked.load_state_dict(L.state_dict())
+    drop = [i for i in range(6) if i not in ii.tolist()]
+    with torch.no_grad():
+        masked.base_weight[:, drop] = 0
+        masked.spline_weight[:, drop] = 0
+    assert torch.allclose(sub(x[:, ii]), masked(x)[:, oi], atol=1e-13)
+    L.requires_grad_(False)
+    assert not any(p.requires_grad for p in L.select(oi, ii).parameters())

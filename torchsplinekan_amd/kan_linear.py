@@ -418,6 +418,29 @@ class KANLinear(nn.Module):
         self.grid.copy_(grid)
         self._ref.grid.copy_(grid)
 
+    @torch.no_grad()
+    def select(self, out_index: Optional[torch.Tensor] = None,
+               in_index: Optional[torch.Tensor] = None) -> "KANLinear":
+        """Independent layer restricted to the given outputs and inputs (index
+        tensors; None keeps all): the edges between them keep their weights,
+        scaler and knot rows, so on those inputs each kept output equals the
+        original's minus the removed inputs' edges.  Hyper-parameters,
+        dtype, device, training mode and requires_grad follow this layer."""
+        dev = self.grid.device
+        oi = (torch.arange(self.out_features, device=dev) if out_index is None
+              else torch.as_tensor(out_index, device=dev, dtype=torch.long))
+        ii = (torch.arange(self.in_features, device=dev) if in_index is None
+              else torch.as_tensor(in_index, device=dev, dtype=torch.long))
+        new = self.make_like(in_features=int(ii.numel()), out_features=int(oi.numel()))
+        edges = lambda t: t.index_select(0, oi).index_select(1, ii)
+        new.base_weight.copy_(edges(self.base_weight))
+        new.spline_weight.copy_(edges(self.spline_weight))
+        if self.enable_standalone_scale_spline:
+            new.spline_scaler.copy_(edges(self.spline_scaler))
+        new._copy_grid_(self.grid.index_select(0, ii))
+        new.requires_grad_(any(p.requires_grad for p in self.parameters()))
+        return new.train(self.training)
+
     def export_inference(self, requires_grad: bool = False) -> "KANLinear":
         """Independent layer computing the same function with spline_scaler
         folded into spline_weight (enable_standalone_scale_spline=False)."""
