@@ -37,7 +37,23 @@ if ROOT not in sys.path:
 METRIC = "fwd+bwd samples/s, KANLinear 1024→1024 G10 k3 N=64K; % MFMA/HBM roofline"
 PEAK_FP32_MFMA_TFLOPS = 157.3
 PEAK_HBM_GBS = 8000.0
-C3_TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "contraction_c3_traffic.json")
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "hbm_traffic_recorded.json")
+
+
+def recorded_traffic(cfg):
+    """(HBM bytes per launch of the config's dominant kernel, source) from the
+    committed rocprofv3 --pmc summaries (FETCH_SIZE + WRITE_SIZE, calibrated
+    on a 1 GiB copy); a recorded figure, not measured in this run."""
+    try:
+        with open(TRAFFIC_PROFILE) as f:
+            rec = json.load(f).get(cfg)
+    except (OSError, ValueError):
+        return None, None
+    if not rec:
+        return None, None
+    return rec.get("hbm_bytes_per_launch"), ("recorded: %s (rocprofv3 --pmc FETCH_SIZE and "
+                                              "WRITE_SIZE per dispatch, calibrated on a 1 GiB "
+                                              "copy), not measured in this run" % rec["source"])
 
 
 def parse():
@@ -395,7 +411,7 @@ def run_c2(args, dev, steps, warmup):
                  "grad)" % N,
                  _mfma_roofline(kern, "contraction", "gemm_pipe_kernel (fp32 MFMA contraction; "
                                 "forward and parameter products of both layers, input product "
-                                "of the second)"), kern)
+                                "of the second)", *recorded_traffic("c2")), kern)
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline_layers(
             [_layer_tensors(l) for l in net.layers], x, target, False, args.cpu_seconds, 1024,
@@ -428,9 +444,7 @@ def run_c4(args, dev, steps, warmup):
     # whose input needs no gradient: 4 n O I (R+1))
     roof = _mfma_roofline(kern, "edge_grad", "edge_bwd_mfma_kernel (both gradient sides, "
                           "dL/dy folded in) + edge_param_mfma_kernel (first layer): mean|phi| "
-                          "backward", traffic=None,
-                          traffic_source="profiles/edge_counters_c4.txt (rocprofv3 --pmc, per "
-                                         "kernel; not per class)")
+                          "backward", *recorded_traffic("c4"))
     e_ms, e_cnt, e_work = kern["edge"]
     line = _line("fwd+bwd samples/s, KAN([256,512,512,64]) G8 k3 N=16K forward_with_regularization",
                  N, steps, warmup, wall,
@@ -467,7 +481,8 @@ def run_c5(args, dev, steps, warmup):
                  "c5: KANLinear(4096->256, G=65, k=3) fp32, N=%d, x ~ U(-1.1, 1.1), fwd + MSE "
                  "+ bwd with dx (3 contractions)" % N,
                  _mfma_roofline(kern, "contraction", "gemm_pipe_kernel (fp32 MFMA contraction; "
-                                "forward, parameter and input products)"), kern)
+                                "forward, parameter and input products)", *recorded_traffic("c5")),
+                 kern)
     b_ms, b_cnt, b_work = kern["basis"]
     if b_cnt:
         line["basis_GBps"] = b_work / max(b_cnt, 1) / (b_ms / b_cnt * 1e-3) / 1e9
@@ -810,15 +825,10 @@ def main():
     _lib.timing_enable(False)
 
     c_ms, c_cnt, c_work = kernels["contraction"]
-    traffic = None
-    if os.path.exists(C3_TRAFFIC_PROFILE):
-        with open(C3_TRAFFIC_PROFILE) as f:
-            traffic = json.load(f).get("hbm_bytes_per_launch")
+    traffic, source = recorded_traffic("c3")
     roof = _mfma_roofline(kernels, "contraction",
                           "gemm_pipe_kernel (fp32 MFMA contraction; average over the forward, "
-                          "parameter and input launches)", traffic,
-                          "recorded: profiles/hbm_traffic_c3.txt (rocprofv3 --pmc FETCH_SIZE "
-                          "and WRITE_SIZE, calibrated on a 1 GiB copy), not measured in this run")
+                          "parameter and input launches)", traffic, source)
     b_ms, b_cnt, b_work = kernels["basis"]
     g_ms, g_cnt, g_work = kernels["basis_grad"]
     gbps = lambda w, ms, n: (w / n) / (ms / n * 1e-3) / 1e9 if n else None
