@@ -98,6 +98,37 @@ __device__ __forceinline__ float buf_ld(__amdgpu_buffer_rsrc_t rs, uint32_t off)
   return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rs, (int)off, 0, 0));
 }
 
+// KS consecutive floats at byte offset off (16-byte loads, then the rest in
+// one 12-, 8- or 4-byte load)
+typedef unsigned int u32x2v __attribute__((ext_vector_type(2)));
+typedef unsigned int u32x3v __attribute__((ext_vector_type(3)));
+typedef unsigned int u32x4v __attribute__((ext_vector_type(4)));
+template <int KS>
+__device__ __forceinline__ void buf_ld_run(__amdgpu_buffer_rsrc_t rs, uint32_t off,
+                                           float (&d)[KS]) {
+#pragma unroll
+  for (int j = 0; j + 4 <= KS; j += 4) {
+    const u32x4v v = __builtin_amdgcn_raw_buffer_load_b128(rs, (int)(off + 4 * j), 0, 0);
+    d[j] = __uint_as_float(v.x);
+    d[j + 1] = __uint_as_float(v.y);
+    d[j + 2] = __uint_as_float(v.z);
+    d[j + 3] = __uint_as_float(v.w);
+  }
+  constexpr int j = KS / 4 * 4;
+  if constexpr (KS - j == 3) {
+    const u32x3v v = __builtin_amdgcn_raw_buffer_load_b96(rs, (int)(off + 4 * j), 0, 0);
+    d[j] = __uint_as_float(v.x);
+    d[j + 1] = __uint_as_float(v.y);
+    d[j + 2] = __uint_as_float(v.z);
+  } else if constexpr (KS - j == 2) {
+    const u32x2v v = __builtin_amdgcn_raw_buffer_load_b64(rs, (int)(off + 4 * j), 0, 0);
+    d[j] = __uint_as_float(v.x);
+    d[j + 1] = __uint_as_float(v.y);
+  } else if constexpr (KS - j == 1) {
+    d[j] = buf_ld(rs, off + 4 * j);
+  }
+}
+
 // The two resources of the tile at n0 (s's covers nothing without s).
 struct HcTile {
   __amdgpu_buffer_rsrc_t h, s;
@@ -124,12 +155,44 @@ struct HcRows {
   __device__ __forceinline__ uint32_t off_s(int rr, int c) const {
     return c == 0 ? (uint32_t)((int64_t)rr * I * 4) : kBufOob;
   }
+  // byte offset of H column col of row rr within a tile
+  __device__ __forceinline__ uint32_t off_col(int rr, int col) const {
+    return (uint32_t)(((int64_t)rr * I * R + col) * 4);
+  }
 };
 
-// byte offset of row rr of s within a tile where the lane's column c is 0
-__device__ __forceinline__ uint32_t c0_off_s(int rr, int c, int64_t I) {
-  return c == 0 ? (uint32_t)((int64_t)rr * I * 4) : kBufOob;
-}
+// Contraction slots of phi = Hc Wc^T.  Slot (k-step k, lane group q) of a
+// sample row holds one augmented column c, the same in the A operand (the
+// row) and the B operand (the weights), so any assignment of columns to
+// slots gives phi.  Lane group q takes a contiguous run of KS H columns of
+// its row, loaded with one multi-dword load: its nominal run is
+// [st, st + KS), st = R - KS (q + 1), so the four runs tile the row from its
+// end.  A group whose nominal start is negative loads [0, KS) instead and
+// owns only columns [0, st + KS) of it (the rest are other groups' columns,
+// given weight 0); the group whose nominal run holds column -1 carries the
+// base column c = 0 (from s) in its last slot.  KS <= R for every k-step
+// class, so a run never leaves its feature's R columns: a tile's resource
+// holds a run wholly or not at all.  (One load per row and tile instead of
+// one per k-step: the scattered single-column loads kept the texture units
+// busy at 16 rows per quarter-wave and instruction.)
+template <int KS>
+struct PhiSlots {
+  int st;      // nominal run start R - KS (q + 1)
+  int col0;    // first H column loaded
+  bool owner;  // the last slot carries s (c = 0)
+  __device__ PhiSlots(int q, int R) : st(R - KS * (q + 1)) {
+    col0 = st > 0 ? st : 0;
+    owner = st <= -1 && st + KS > -1;
+  }
+  // augmented column of slot k (-1: none; weight 0)
+  __device__ __forceinline__ int c(int k) const {
+    if (st >= 0) return st + k + 1;
+    if (k < st + KS) return k + 1;
+    return (owner && k == KS - 1) ? 0 : -1;
+  }
+  // AND mask of the loaded value in the last slot (0 where s replaces it)
+  __device__ __forceinline__ uint32_t keep() const { return owner ? 0u : 0xffffffffu; }
+};
 
 // Where column 0 can occur a lane loads from both arrays; at most one of the
 // two is in range, so OR-ing their bits gives the value exactly.  The OR is
@@ -141,6 +204,15 @@ __device__ __forceinline__ uint32_t c0_off_s(int rr, int c, int64_t I) {
 __device__ __forceinline__ float hc_or(float h, float sv) {
   float v;
   asm volatile("v_or_b32 %0, %1, %2\n\ts_nop 4" : "=v"(v) : "v"(h), "v"(sv));
+  return v;
+}
+
+// The last slot of a phi run: the loaded H value, or s in the group that
+// carries the base column (keep = 0 there; sv reads 0 in every other group),
+// as one opaque instruction for the reasons given at hc_or.
+__device__ __forceinline__ float hc_sel(float h, uint32_t keep, float sv) {
+  float v;
+  asm volatile("v_and_or_b32 %0, %1, %2, %3\n\ts_nop 4" : "=v"(v) : "v"(h), "v"(keep), "v"(sv));
   return v;
 }
 
@@ -187,14 +259,15 @@ __global__ __launch_bounds__(kEdgeMfThreads) void edge_fwd_mfma_kernel(
   if (WS == 1 && obase >= g.O) return;  // (with WS > 1 every wave reaches the barrier)
   const int R1 = g.R + 1;
 
+  const PhiSlots<KS> ps(q, g.R);
   float w[kOT][KS];
 #pragma unroll
   for (int t = 0; t < kOT; ++t) {
     const int o = obase + t * 16 + r;
 #pragma unroll
     for (int k = 0; k < KS; ++k) {
-      const int c = 4 * k + q;
-      w[t][k] = (o < g.O && c < R1) ? wc_val(bw, W, o, g.I, i, g.R, c) : 0.0f;
+      const int c = ps.c(k);
+      w[t][k] = (o < g.O && c >= 0) ? wc_val(bw, W, o, g.I, i, g.R, c) : 0.0f;
     }
   }
   float tot[kOT];
@@ -213,16 +286,14 @@ __global__ __launch_bounds__(kEdgeMfThreads) void edge_fwd_mfma_kernel(
   // no old and new value of a slot are live together (which would cost
   // register copies that wait for the loads at the loop end).
   constexpr int S = P < 2 ? 2 : P;
-  float an[S][KS], asn[S];  // asn: the s part of k = 0
+  float an[S][KS], asn[S];  // asn: s (the group that carries c = 0)
   const HcRows hr(s, H, g.I, g.R, i);
-  uint32_t oh[KS];
-#pragma unroll
-  for (int k = 0; k < KS; ++k) oh[k] = hr.off_h(r, 4 * k + q);
-  const uint32_t os = hr.off_s(r, q);  // column 0 only at k = 0
+  const uint32_t oh = hr.off_col(r, ps.col0);
+  const uint32_t os = ps.owner ? hr.off_s(r, 0) : kBufOob;
+  const uint32_t keep = ps.keep();
   auto load_a = [&](int64_t n0, float (&dst)[KS], float& dsts) {
     const HcTile t = hr.tile(n0, ne);
-#pragma unroll
-    for (int k = 0; k < KS; ++k) dst[k] = buf_ld(t.h, oh[k]);
+    buf_ld_run<KS>(t.h, oh, dst);
     dsts = buf_ld(t.s, os);
   };
   // (slots issued in order, so that the wait for slot 0 at the loop head
@@ -245,7 +316,7 @@ __global__ __launch_bounds__(kEdgeMfThreads) void edge_fwd_mfma_kernel(
       __builtin_amdgcn_sched_barrier(0);  // the loads go out before this tile's wait
       float a[KS];
 #pragma unroll
-      for (int k = 0; k < KS; ++k) a[k] = k == 0 ? hc_or(an[p][0], asn[p]) : an[p][k];
+      for (int k = 0; k < KS; ++k) a[k] = k == KS - 1 ? hc_sel(an[p][k], keep, asn[p]) : an[p][k];
       // k outermost: the kOT accumulation chains are independent, so a wave
       // issues MFMAs back to back instead of waiting on one chain at a time
       f32x4 acc[kOT];
@@ -323,6 +394,7 @@ __global__ __launch_bounds__(kEdgeMfThreads) void edge_param_mfma_kernel(
   const int R1 = g.R + 1;
   const float inv_n = 1.0f / (float)g.n;
 
+  const PhiSlots<KS> ps(q, g.R);
   float w[kOT][KS], gav[kOT];
 #pragma unroll
   for (int t = 0; t < kOT; ++t) {
@@ -330,8 +402,8 @@ __global__ __launch_bounds__(kEdgeMfThreads) void edge_param_mfma_kernel(
     gav[t] = o < g.O ? ga[(int64_t)o * g.I + i] * inv_n : 0.0f;
 #pragma unroll
     for (int k = 0; k < KS; ++k) {
-      const int c = 4 * k + q;
-      w[t][k] = (o < g.O && c < R1) ? wc_val(bw, W, o, g.I, i, g.R, c) : 0.0f;
+      const int c = ps.c(k);
+      w[t][k] = (o < g.O && c >= 0) ? wc_val(bw, W, o, g.I, i, g.R, c) : 0.0f;
     }
   }
   f32x4 dacc[kOT][CT];
@@ -348,15 +420,15 @@ __global__ __launch_bounds__(kEdgeMfThreads) void edge_param_mfma_kernel(
     ne = min(ne, nb + per_wave);
   }
   // Operands of the next sample tile are loaded while the current one runs:
-  // A of phi (Hc[n0 + r, 4k + q]) and B of the second product
+  // A of phi (row n0 + r, the run of PhiSlots) and B of the second product
   // (Hc[n0 + 4q + v, 16ct + r]), in two register slots used alternately
   // (the slot rotation of the forward kernel with S = 2).
-  float an[2][KS], asn[2], hn[2][CT][4], hsn[2][4];  // asn, hsn: s parts (k = 0, ct = 0)
+  float an[2][KS], asn[2], hn[2][CT][4], hsn[2][4];  // asn, hsn: s parts
   const HcRows hr(s, H, g.I, g.R, i);
-  uint32_t oa[KS], ob[CT][4], obs[4];
-#pragma unroll
-  for (int k = 0; k < KS; ++k) oa[k] = hr.off_h(r, 4 * k + q);
-  const uint32_t oas = hr.off_s(r, q);  // column 0 only at k = 0
+  uint32_t ob[CT][4], obs[4];
+  const uint32_t oa = hr.off_col(r, ps.col0);
+  const uint32_t oas = ps.owner ? hr.off_s(r, 0) : kBufOob;
+  const uint32_t keep = ps.keep();
 #pragma unroll
   for (int v = 0; v < 4; ++v) {
 #pragma unroll
@@ -366,8 +438,7 @@ __global__ __launch_bounds__(kEdgeMfThreads) void edge_param_mfma_kernel(
   auto load_tile = [&](int64_t n0, float (&da)[KS], float& das, float (&dh)[CT][4],
                        float (&dhs)[4]) {
     const HcTile t = hr.tile(n0, ne);
-#pragma unroll
-    for (int k = 0; k < KS; ++k) da[k] = buf_ld(t.h, oa[k]);
+    buf_ld_run<KS>(t.h, oa, da);
     das = buf_ld(t.s, oas);
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
@@ -386,7 +457,7 @@ __global__ __launch_bounds__(kEdgeMfThreads) void edge_param_mfma_kernel(
       __builtin_amdgcn_sched_barrier(0);  // the loads go out before this tile's wait
       float a[KS], hb[CT][4];
 #pragma unroll
-      for (int k = 0; k < KS; ++k) a[k] = k == 0 ? hc_or(an[p][0], asn[p]) : an[p][k];
+      for (int k = 0; k < KS; ++k) a[k] = k == KS - 1 ? hc_sel(an[p][k], keep, asn[p]) : an[p][k];
 #pragma unroll
       for (int ct = 0; ct < CT; ++ct)
 #pragma unroll
@@ -535,13 +606,14 @@ __global__ __launch_bounds__(kEdgeMfThreads) void edge_input_mfma_kernel(
   // slots used alternately (narrow layers, where an item's few output tiles
   // cannot hide the loads; wide layers keep one slot and a wave more per
   // SIMD instead).
-  uint32_t oh[KS];
+  const PhiSlots<KS> ps(q, g.R);
+  uint32_t oh;
   {
     const HcRows hr0(s, H, g.I, g.R, 0);
-#pragma unroll
-    for (int k = 0; k < KS; ++k) oh[k] = hr0.off_h(r, 4 * k + q);
+    oh = hr0.off_col(r, ps.col0);
   }
-  const uint32_t os = c0_off_s(r, q, g.I);  // column 0 only at k = 0
+  const uint32_t os = ps.owner ? (uint32_t)((int64_t)r * g.I * 4) : kBufOob;
+  const uint32_t keep = ps.keep();
   auto load_item = [&](int64_t item, float (&dh)[NTW][KS], float (&dsv)[NTW]) {
     const bool live = item < item_hi;
     const int fi = live ? (int)(item / nblk) : 0;
@@ -550,8 +622,7 @@ __global__ __launch_bounds__(kEdgeMfThreads) void edge_input_mfma_kernel(
 #pragma unroll
     for (int j = 0; j < NTW; ++j) {
       const HcTile t = hr.tile(nbase + (int64_t)(j * 4 + wave) * 16, live ? g.n : 0);
-#pragma unroll
-      for (int k = 0; k < KS; ++k) dh[j][k] = buf_ld(t.h, oh[k]);
+      buf_ld_run<KS>(t.h, oh, dh[j]);
       dsv[j] = buf_ld(t.s, os);
     }
   };
@@ -569,7 +640,8 @@ __global__ __launch_bounds__(kEdgeMfThreads) void edge_input_mfma_kernel(
 #pragma unroll
     for (int j = 0; j < NTW; ++j)
 #pragma unroll
-      for (int k = 0; k < KS; ++k) a[j][k] = k == 0 ? hc_or(dh[j][0], dsv[j]) : dh[j][k];
+      for (int k = 0; k < KS; ++k)
+        a[j][k] = k == KS - 1 ? hc_sel(dh[j][k], keep, dsv[j]) : dh[j][k];
     f32x4 dacc[NTW][CT];
 #pragma unroll
     for (int j = 0; j < NTW; ++j)
@@ -580,12 +652,12 @@ __global__ __launch_bounds__(kEdgeMfThreads) void edge_input_mfma_kernel(
       const int orows = min(oc_rows, g.O - o0);
       if (!one_chunk) stage(o0, orows);
       for (int ot = 0; ot < orows; ot += 16) {
-        // A operand of phi^T: Wc[o = ot + r, c = 4k + q]
+        // A operand of phi^T: Wc[o = ot + r, c = slot (k, q)]
         float wa[KS];
 #pragma unroll
         for (int k = 0; k < KS; ++k) {
-          const int c = 4 * k + q;
-          wa[k] = c < R1 ? wl[(ot + r) * stride + c] : 0.0f;
+          const int c = ps.c(k);
+          wa[k] = c >= 0 ? wl[(ot + r) * stride + c] : 0.0f;
         }
         // g scale of the accumulator rows o = ot + 4q + v
         float gs[4];
@@ -722,8 +794,10 @@ __global__ __launch_bounds__(kEdgeMfThreads) void edge_bwd_mfma_kernel(
   const int R1 = g.R + 1;
   const float inv_n = 1.0f / (float)g.n;
 
-  // phi's B operand Wc[o = obase + 16t + r, c = 4k + q]; the input product's
-  // A operand Wc[o = obase + 16t + 4q + v, c = r]; ga / n of columns o.
+  // phi's B operand Wc[o = obase + 16t + r, c = slot (k, q)]; the input
+  // product's A operand Wc[o = obase + 16t + 4q + v, c = r]; ga / n of
+  // columns o.
+  const PhiSlots<KS> ps(q, g.R);
   float w[kOT][KS], wb[kOT][4], gav[kOT];
 #pragma unroll
   for (int t = 0; t < kOT; ++t) {
@@ -731,8 +805,8 @@ __global__ __launch_bounds__(kEdgeMfThreads) void edge_bwd_mfma_kernel(
     gav[t] = o < g.O ? ga[(int64_t)o * g.I + i] * inv_n : 0.0f;
 #pragma unroll
     for (int k = 0; k < KS; ++k) {
-      const int c = 4 * k + q;
-      w[t][k] = (o < g.O && c < R1) ? wc_val(bw, W, o, g.I, i, g.R, c) : 0.0f;
+      const int c = ps.c(k);
+      w[t][k] = (o < g.O && c >= 0) ? wc_val(bw, W, o, g.I, i, g.R, c) : 0.0f;
     }
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
@@ -762,10 +836,10 @@ __global__ __launch_bounds__(kEdgeMfThreads) void edge_bwd_mfma_kernel(
   static_assert(GP % S == 0, "slots divide the group");
   float an[S][KS], asn[S], hn[S][4], hsn[S][4];
   const HcRows hr(s, H, g.I, g.R, i);
-  uint32_t oa[KS], ob[4], obs[4];
-#pragma unroll
-  for (int k = 0; k < KS; ++k) oa[k] = hr.off_h(r, 4 * k + q);
-  const uint32_t oas = hr.off_s(r, q);
+  uint32_t ob[4], obs[4];
+  const uint32_t oa = hr.off_col(r, ps.col0);
+  const uint32_t oas = ps.owner ? hr.off_s(r, 0) : kBufOob;
+  const uint32_t keep = ps.keep();
 #pragma unroll
   for (int v = 0; v < 4; ++v) {
     ob[v] = hr.off_h(4 * q + v, r);
@@ -773,8 +847,7 @@ __global__ __launch_bounds__(kEdgeMfThreads) void edge_bwd_mfma_kernel(
   }
   auto load_tile = [&](int64_t n0, float (&da)[KS], float& das, float (&dh)[4], float (&dhs)[4]) {
     const HcTile t = hr.tile(n0, ne);
-#pragma unroll
-    for (int k = 0; k < KS; ++k) da[k] = buf_ld(t.h, oa[k]);
+    buf_ld_run<KS>(t.h, oa, da);
     das = buf_ld(t.s, oas);
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
@@ -818,7 +891,7 @@ __global__ __launch_bounds__(kEdgeMfThreads) void edge_bwd_mfma_kernel(
       __builtin_amdgcn_sched_barrier(0);  // the loads go out before this tile's wait
       float a[KS], hb[4];
 #pragma unroll
-      for (int k = 0; k < KS; ++k) a[k] = k == 0 ? hc_or(an[p][0], asn[p]) : an[p][k];
+      for (int k = 0; k < KS; ++k) a[k] = k == KS - 1 ? hc_sel(an[p][k], keep, asn[p]) : an[p][k];
 #pragma unroll
       for (int v = 0; v < 4; ++v) hb[v] = hc_or(hn[p][v], hsn[p][v]);
       // layer-output gradient in the accumulator layout of g,
