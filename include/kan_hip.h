@@ -277,6 +277,25 @@ int kan_hip_edge_abs_mean_double_backward(int dtype, const void* grad_a, const v
                                           int64_t n, int64_t in_features, int64_t out_features,
                                           int64_t R, void* stream);
 
+/* Regulariser of one layer from its edge means a [count] (the KAN paper's
+ * activation penalty):
+ *   reg = mu1 * T + mu2 * H,   T = sum a,   H = -sum p log p,
+ *   p = max(a / max(T, tiny), tiny)   (tiny = the type's smallest normal),
+ * written to reg[0] (device).  Replaces regularization_from_edge_means
+ * (spline_kan/reference_backend.py:149-170), an ATen expression of about
+ * ten launches, with three; block sums in double, added in a fixed order.
+ * The workspace (kan_hip_edge_reg_workspace bytes) keeps the statistics the
+ * backward reads: pass the same one, unchanged, to
+ * kan_hip_edge_reg_backward, which writes grad_a [count] =
+ * grad_reg[0] * d reg / d a, with the clamps' zero-gradient masks (what
+ * autograd takes through the reference expression). */
+int kan_hip_edge_reg_workspace(int dtype, int64_t count, size_t* bytes);
+int kan_hip_edge_reg(int dtype, const void* a, int64_t count, double mu1, double mu2, void* reg,
+                     void* workspace, size_t workspace_bytes, void* stream);
+int kan_hip_edge_reg_backward(int dtype, const void* grad_reg, const void* a, int64_t count,
+                              double mu1, double mu2, const void* workspace,
+                              size_t workspace_bytes, void* grad_a, void* stream);
+
 /* Gram matrices of the least-squares spline refit used by update_grid and
  * extend_grid, per input feature i, accumulated in float64:
  *   gram[i]  = sum_b bn(x[b,i]) bn(x[b,i])^T   [I, Rn, Rn]  (A^T A on the new grid)

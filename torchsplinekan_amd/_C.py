@@ -683,6 +683,37 @@ def edge_linear_backward(grad_a, grad_y, s, H, base_weight, W, need_s: bool, nee
     return ds, dH, dbw, dW
 
 
+def edge_regularization(a: torch.Tensor, mu1: float, mu2: float):
+    """(reg, ws): reg = mu1 * sum(a) + mu2 * entropy(a / sum(a)) as a 0-d
+    device tensor, and the workspace holding the statistics its backward
+    reads (kan_hip_edge_reg; spline_kan/reference_backend.py:149-170)."""
+    _req(a.is_cuda and a.dtype in _F, "edge_regularization: a must be a float32/float64 CUDA tensor")
+    a = a.contiguous()
+    code = dtype_code(a.dtype)
+    nb = _lib.ctypes.c_size_t(0)
+    check(LIB.kan_hip_edge_reg_workspace(code, a.numel(), _lib.ctypes.byref(nb)))
+    ws = torch.empty(int(nb.value), dtype=torch.uint8, device=a.device)
+    reg = torch.empty((), dtype=a.dtype, device=a.device)
+    with torch.cuda.device(a.device):
+        check(LIB.kan_hip_edge_reg(code, ptr(a), a.numel(), float(mu1), float(mu2), ptr(reg),
+                                   ptr(ws), int(nb.value), stream_of(a.device)))
+    return reg, ws
+
+
+def edge_regularization_backward(grad_reg: torch.Tensor, a: torch.Tensor, mu1: float, mu2: float,
+                                 ws: torch.Tensor) -> torch.Tensor:
+    """d reg / d a times grad_reg (0-d), from the workspace of the forward
+    over the same a (kan_hip_edge_reg_backward)."""
+    a = a.contiguous()
+    g = grad_reg.reshape(()).to(a.dtype).contiguous()
+    ga = torch.empty_like(a)
+    with torch.cuda.device(a.device):
+        check(LIB.kan_hip_edge_reg_backward(dtype_code(a.dtype), ptr(g), ptr(a), a.numel(),
+                                            float(mu1), float(mu2), ptr(ws), ws.numel(), ptr(ga),
+                                            stream_of(a.device)))
+    return ga
+
+
 def edge_abs_mean_double_backward(grad_a, s, H, base_weight, W, u_ds, u_dH, u_dbw, u_dW,
                                   need_ga: bool, need_s: bool, need_H: bool, need_bw: bool,
                                   need_W: bool):

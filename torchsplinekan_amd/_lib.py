@@ -78,6 +78,11 @@ SIGNATURES = {
     "kan_hip_refit_gram": (_int, [_int, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64,
                                   _vp]),
     "kan_hip_stream_probe": (_int, [_int, _vp, _vp, _i64, _vp]),
+    "kan_hip_edge_reg_workspace": (_int, [_int, _i64, ctypes.POINTER(_sz)]),
+    "kan_hip_edge_reg": (_int, [_int, _vp, _i64, ctypes.c_double, ctypes.c_double, _vp, _vp, _sz,
+                                _vp]),
+    "kan_hip_edge_reg_backward": (_int, [_int, _vp, _vp, _i64, ctypes.c_double, ctypes.c_double,
+                                         _vp, _sz, _vp, _vp]),
     "kan_hip_timing_enable": (_int, [_int]),
     "kan_hip_timing_read": (_int, [_int, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_i64),
                                    ctypes.POINTER(ctypes.c_double)]),

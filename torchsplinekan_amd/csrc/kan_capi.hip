@@ -862,6 +862,55 @@ int kan_hip_edge_linear_backward(int dtype, const void* ga, const void* gy, cons
       static_cast<hipStream_t>(stream));
 }
 
+int kan_hip_edge_reg_workspace(int dtype, int64_t count, size_t* bytes) {
+  KAN_TRY(check_dtype(dtype, "edge_reg_workspace"));
+  KAN_TRY(need_ptr(bytes, "edge_reg_workspace", "bytes"));
+  if (count < 0) return set_error(KAN_ERR_INVALID, "edge_reg_workspace: negative count");
+  *bytes = edge_reg_ws_bytes(count);
+  return KAN_OK;
+}
+
+int kan_hip_edge_reg(int dtype, const void* a, int64_t count, double mu1, double mu2, void* reg,
+                     void* ws, size_t ws_bytes, void* stream) {
+  KAN_TRY(check_dtype(dtype, "edge_reg"));
+  if (count < 0) return set_error(KAN_ERR_INVALID, "edge_reg: negative count");
+  if (count > 0) KAN_TRY(need_ptr(a, "edge_reg", "a"));
+  KAN_TRY(need_ptr(reg, "edge_reg", "reg"));
+  const size_t need = edge_reg_ws_bytes(count);
+  if (ws_bytes < need || ws == nullptr)
+    return set_error(KAN_ERR_WORKSPACE, "edge_reg: workspace of %zu bytes is smaller than the %zu required", ws_bytes, need);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  double* w = static_cast<double*>(ws);
+  if (dtype == KAN_DTYPE_F32)
+    return launch_edge_reg<float>(static_cast<const float*>(a), count, mu1, mu2,
+                                  static_cast<float*>(reg), w, st);
+  return launch_edge_reg<double>(static_cast<const double*>(a), count, mu1, mu2,
+                                 static_cast<double*>(reg), w, st);
+}
+
+int kan_hip_edge_reg_backward(int dtype, const void* grad_reg, const void* a, int64_t count,
+                              double mu1, double mu2, const void* ws, size_t ws_bytes,
+                              void* grad_a, void* stream) {
+  KAN_TRY(check_dtype(dtype, "edge_reg_backward"));
+  if (count < 0) return set_error(KAN_ERR_INVALID, "edge_reg_backward: negative count");
+  if (count == 0) return KAN_OK;
+  KAN_TRY(need_ptr(grad_reg, "edge_reg_backward", "grad_reg"));
+  KAN_TRY(need_ptr(a, "edge_reg_backward", "a"));
+  KAN_TRY(need_ptr(grad_a, "edge_reg_backward", "grad_a"));
+  const size_t need = edge_reg_ws_bytes(count);
+  if (ws_bytes < need || ws == nullptr)
+    return set_error(KAN_ERR_WORKSPACE, "edge_reg_backward: workspace of %zu bytes is smaller than the %zu required", ws_bytes, need);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const double* w = static_cast<const double*>(ws);
+  if (dtype == KAN_DTYPE_F32)
+    return launch_edge_reg_backward<float>(static_cast<const float*>(grad_reg),
+                                           static_cast<const float*>(a), count, mu1, mu2, w,
+                                           static_cast<float*>(grad_a), st);
+  return launch_edge_reg_backward<double>(static_cast<const double*>(grad_reg),
+                                          static_cast<const double*>(a), count, mu1, mu2, w,
+                                          static_cast<double*>(grad_a), st);
+}
+
 int kan_hip_edge_abs_mean_double_backward_workspace(int dtype, int64_t n, int64_t I, int64_t O,
                                                     int64_t R, size_t* bytes) {
   KAN_TRY(check_dtype(dtype, "edge_abs_mean_double_backward_workspace"));

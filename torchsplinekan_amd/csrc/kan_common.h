@@ -113,6 +113,15 @@ class TimedLaunch {
 // 1 reads a, 2 copies a to b (kan_stream.hip).
 int launch_stream_probe(int mode, void* a, void* b, int64_t bytes, hipStream_t st);
 
+// Regulariser of one layer from its edge means (kan_reg.hip).
+size_t edge_reg_ws_bytes(int64_t n);
+template <typename T>
+int launch_edge_reg(const T* a, int64_t n, double mu1, double mu2, T* reg, double* ws,
+                    hipStream_t st);
+template <typename T>
+int launch_edge_reg_backward(const T* g, const T* a, int64_t n, double mu1, double mu2,
+                             const double* ws, T* ga, hipStream_t st);
+
 template <typename T>
 int launch_basis(const T* x, const T* grid, T* out, int64_t ld_out, T* silu_out, int64_t n,
                  int64_t I, int G, int k, int impl, hipStream_t st);

@@ -143,6 +143,51 @@ class EdgeLinear(torch.autograd.Function):
                                        bool(need_bw), bool(need_W))
 
 
+def _regularization_grad(a: torch.Tensor, g: torch.Tensor, mu1: float, mu2: float) -> torch.Tensor:
+    """g * d reg / d a as differentiable tensor operations (the gradient that
+    autograd takes through regularization_from_edge_means, clamps included:
+    tc = max(T, tiny), m = [a / tc >= tiny], c = [T >= tiny],
+    U = sum (log p + 1) m a, d reg / d a = mu1 + mu2 (c U / tc^2 - (log p + 1) m / tc))."""
+    tiny = torch.finfo(a.dtype).tiny
+    total = a.sum()
+    tc = total.clamp(min=tiny)
+    q = a / tc
+    m = (q >= tiny).to(a.dtype)
+    lp1 = q.clamp(min=tiny).log() + 1
+    u = (lp1 * m * a).sum()
+    c = (total >= tiny).to(a.dtype)
+    return g * (mu1 + mu2 * (c * ((u / tc) / tc) - lp1 * m / tc))
+
+
+class EdgeRegularization(torch.autograd.Function):
+    """The layer regulariser mu1 * sum(a) + mu2 * entropy(a / sum(a)) from its
+    edge means on the device: three native launches forward and one backward
+    (kan_hip_edge_reg) in place of the ATen expression's ten and twenty
+    (spline_kan/reference_backend.py:149-170).  A recorded backward
+    (create_graph) takes the gradient as differentiable tensor operations."""
+
+    @staticmethod
+    def forward(ctx, a, mu1: float, mu2: float):
+        reg, ws = _C.edge_regularization(a, mu1, mu2)
+        ctx.save_for_backward(a)
+        ctx.ws, ctx.mu = ws, (float(mu1), float(mu2))
+        return reg
+
+    @staticmethod
+    def backward(ctx, g):
+        a, = ctx.saved_tensors
+        mu1, mu2 = ctx.mu
+        if torch.is_grad_enabled():
+            return _regularization_grad(a, g, mu1, mu2), None, None
+        return _C.edge_regularization_backward(g, a, mu1, mu2, ctx.ws), None, None
+
+
+def edge_regularization(a: torch.Tensor, mu1: float, mu2: float) -> torch.Tensor:
+    """Regulariser of one layer's edge means a on the device (see
+    EdgeRegularization)."""
+    return EdgeRegularization.apply(a, mu1, mu2)
+
+
 def edge_linear_applies(s: Optional[torch.Tensor], H: torch.Tensor, bw: Optional[torch.Tensor],
                         W: torch.Tensor) -> bool:
     """Whether edge_linear covers this layer: a base branch, and operands the

@@ -315,7 +315,7 @@ class KANLinear(nn.Module):
         impl = self._resolve_reg_impl(reg_impl, xf)
         H = self._basis(xf, impl)
         a = self._edge_abs_mean(xf, s, H, self._ref.effective_spline_weight(), impl, chunk_size)
-        return regularization_from_edge_means(a, reg_act, reg_entropy)
+        return self._regularization(a, reg_act, reg_entropy, impl)
 
     def forward_with_regularization(self, x: torch.Tensor, reg_act: float = 1.0,
                                     reg_entropy: float = 1.0, *, mode: str = "activation",
@@ -351,8 +351,17 @@ class KANLinear(nn.Module):
         self.last_backend = "cuda" if impl == "fused" else "reference"
         if a is None:
             a = self._edge_abs_mean(xf, s, H, W, impl, chunk_size)
-        reg = regularization_from_edge_means(a, reg_act, reg_entropy)
+        reg = self._regularization(a, reg_act, reg_entropy, impl)
         return y.reshape(lead + (self.out_features,)), reg
+
+    @staticmethod
+    def _regularization(a: torch.Tensor, reg_act: float, reg_entropy: float,
+                        impl: str) -> torch.Tensor:
+        """The scalar from the edge means: native on the fused path, the
+        tensor expression otherwise."""
+        if impl == "fused":
+            return _fused.edge_regularization(a, reg_act, reg_entropy)
+        return regularization_from_edge_means(a, reg_act, reg_entropy)
 
     def _resolve_reg_impl(self, reg_impl: str, x_flat: torch.Tensor) -> str:
         if reg_impl not in REG_IMPLS:
