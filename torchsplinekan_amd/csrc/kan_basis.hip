@@ -436,19 +436,54 @@ __global__ __launch_bounds__(256) void build_waug_t_kernel(
 // Parameter gradients from the (split) products G = D^T [H | s]:
 //   gsw = scaler * G_H, gscaler = sum_r sw * G_H, gbw = G_s
 // (csrc/kan_cuda.cu:576-598).  Split partials are summed in fixed order.
-// A block owns kPairs consecutive (o, i) edges of one output row o: its
-// kPairs*R partial values are contiguous, so the loads are coalesced; the
-// per-edge sum over r goes through LDS.
+// A block owns kPairs consecutive (o, i) edges of one output row o: their
+// kPairs*R partial values are contiguous, so the loads are coalesced.  The
+// pass is a pure stream (splits + 1 reads and one write per element), so
+// each thread keeps kPgUnroll vectors of V elements in flight per split;
+// V = 16 bytes when the rows, split slices and pointers allow it, else 1;
+// the host picks V only where V divides I*R, so V divides every block's
+// np*R (= I*R - i0*R, with i0 a multiple of kPairs) and there is no tail.
+// The per-edge sum over r goes through LDS rows of odd stride (conflict-free
+// for the one-thread-per-edge reads), in r order.
 constexpr int kPairs = 128;
+constexpr int kPgThreads = 256;
+constexpr int kPgUnroll = 2;
 
-template <typename T>
-__global__ __launch_bounds__(kPairs) void param_grads_kernel(
+template <typename T, int V>
+__device__ __forceinline__ void pg_load(const T* __restrict__ p, T (&e)[V]) {
+  if constexpr (V == 1) {
+    e[0] = *p;
+  } else {
+    typedef T vt __attribute__((ext_vector_type(V)));
+    const vt v = *reinterpret_cast<const vt*>(p);
+#pragma unroll
+    for (int j = 0; j < V; ++j) e[j] = v[j];
+  }
+}
+
+template <typename T, int V>
+__device__ __forceinline__ void pg_store(T* __restrict__ p, const T (&e)[V]) {
+  if constexpr (V == 1) {
+    *p = e[0];
+  } else {
+    typedef T vt __attribute__((ext_vector_type(V)));
+    vt v;
+#pragma unroll
+    for (int j = 0; j < V; ++j) v[j] = e[j];
+    *reinterpret_cast<vt*>(p) = v;
+  }
+}
+
+template <typename T, int V>
+__global__ __launch_bounds__(kPgThreads) void param_grads_kernel(
     const T* __restrict__ part, int splits, int64_t split_stride, int64_t ld,
     const T* __restrict__ sw, const T* __restrict__ scaler, T* __restrict__ gsw,
     T* __restrict__ gscaler, T* __restrict__ gbw, int64_t O, int64_t I, int64_t R,
     int64_t blocks_per_row) {
   extern __shared__ __align__(16) unsigned char smem_pg[];
+  const int rs = (int)(R | 1);  // LDS row stride
   T* prod = reinterpret_cast<T*>(smem_pg);
+  T* sc = prod + kPairs * rs;
   const int64_t o = blockIdx.x / blocks_per_row;
   const int64_t i0 = (blockIdx.x - o * blocks_per_row) * (int64_t)kPairs;
   const int np = (int)min((int64_t)kPairs, I - i0);
@@ -457,18 +492,59 @@ __global__ __launch_bounds__(kPairs) void param_grads_kernel(
   const int64_t ebase = (o * I + i0) * R;
   const float inv_r = 1.0f / (float)R;
   if (gsw != nullptr || gscaler != nullptr) {
-    for (int c = threadIdx.x; c < cnt; c += kPairs) {
-      T g = src[c];
-      for (int s = 1; s < splits; ++s) g += src[s * split_stride + c];
-      const int pr = small_div(c, inv_r);
-      if (gsw != nullptr) gsw[ebase + c] = scaler != nullptr ? scaler[o * I + i0 + pr] * g : g;
-      if (gscaler != nullptr) prod[c] = sw[ebase + c] * g;
+    if ((int)threadIdx.x < np)
+      sc[threadIdx.x] = scaler != nullptr ? scaler[o * I + i0 + threadIdx.x] : T(1);
+    __syncthreads();
+    constexpr int kStep = kPgUnroll * kPgThreads * V;
+    for (int c0 = (int)threadIdx.x * V; c0 < cnt; c0 += kStep) {
+      T g[kPgUnroll][V], w[kPgUnroll][V];
+#pragma unroll
+      for (int u = 0; u < kPgUnroll; ++u) {
+        const int c = c0 + u * kPgThreads * V;
+        if (c < cnt) {
+          pg_load<T, V>(src + c, g[u]);
+          if (gscaler != nullptr) pg_load<T, V>(sw + ebase + c, w[u]);
+        }
+      }
+      for (int s = 1; s < splits; ++s) {
+        T h[kPgUnroll][V];
+#pragma unroll
+        for (int u = 0; u < kPgUnroll; ++u) {
+          const int c = c0 + u * kPgThreads * V;
+          if (c < cnt) pg_load<T, V>(src + s * split_stride + c, h[u]);
+        }
+#pragma unroll
+        for (int u = 0; u < kPgUnroll; ++u) {
+          const int c = c0 + u * kPgThreads * V;
+          if (c < cnt) {
+#pragma unroll
+            for (int j = 0; j < V; ++j) g[u][j] += h[u][j];
+          }
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < kPgUnroll; ++u) {
+        const int c = c0 + u * kPgThreads * V;
+        if (c >= cnt) continue;
+        T out[V];
+#pragma unroll
+        for (int j = 0; j < V; ++j) {
+          const int pr = small_div(c + j, inv_r);
+          out[j] = sc[pr] * g[u][j];
+          if (gscaler != nullptr) prod[pr * rs + (c + j - pr * (int)R)] = w[u][j] * g[u][j];
+        }
+        if (gsw != nullptr) {
+          if (scaler != nullptr) pg_store<T, V>(gsw + ebase + c, out);
+          else pg_store<T, V>(gsw + ebase + c, g[u]);
+        }
+      }
     }
     if (gscaler != nullptr) {
       __syncthreads();
       if ((int)threadIdx.x < np) {
+        const T* row = prod + threadIdx.x * rs;
         T acc = T(0);
-        for (int64_t r = 0; r < R; ++r) acc += prod[threadIdx.x * R + r];
+        for (int r = 0; r < (int)R; ++r) acc += row[r];
         gscaler[o * I + i0 + threadIdx.x] = acc;
       }
     }
@@ -480,7 +556,6 @@ __global__ __launch_bounds__(kPairs) void param_grads_kernel(
     gbw[o * I + i0 + threadIdx.x] = g;
   }
 }
-
 
 // basis_grad_kernel for one sample per wave step (subs == 1) with 16-byte
 // rows: the next step's gradient segment (and x, gbase) is loaded into
@@ -948,10 +1023,21 @@ int launch_param_grads(const T* part, int splits, int64_t split_stride, int64_t 
   const int64_t per_row = ceil_div(I, kPairs);
   const int64_t blocks = O * per_row;
   if (blocks > 2147483647LL) return set_error(KAN_ERR_LIMIT, "param_grads: too many edges");
+  // 16-byte vectors when every row start, split slice and edge run is aligned
+  constexpr int V = 16 / (int)sizeof(T);
+  auto al = [](const void* q) { return q == nullptr || (reinterpret_cast<uintptr_t>(q) & 15) == 0; };
+  const bool vec = ld % V == 0 && split_stride % V == 0 && (I * R) % V == 0 && al(part) &&
+                   al(sw) && al(gsw);
+  const size_t lds = sizeof(T) * (size_t)kPairs * (size_t)((R | 1) + 1);
   TimedLaunch timed(kClassOther, st, 0.0);
-  hipLaunchKernelGGL((param_grads_kernel<T>), dim3((unsigned)blocks), dim3(kPairs),
-                     sizeof(T) * kPairs * R, st, part, splits, split_stride, ld, sw, scaler, gsw,
-                     gscaler, gbw, O, I, R, per_row);
+  if (vec)
+    hipLaunchKernelGGL((param_grads_kernel<T, V>), dim3((unsigned)blocks), dim3(kPgThreads), lds,
+                       st, part, splits, split_stride, ld, sw, scaler, gsw, gscaler, gbw, O, I, R,
+                       per_row);
+  else
+    hipLaunchKernelGGL((param_grads_kernel<T, 1>), dim3((unsigned)blocks), dim3(kPgThreads), lds,
+                       st, part, splits, split_stride, ld, sw, scaler, gsw, gscaler, gbw, O, I, R,
+                       per_row);
   return check_launch("param_grads");
 }
 
