@@ -106,3 +106,37 @@ def test_infer_rejects_short_workspace(C):
     rc = _lib.LIB.kan_hip_infer(_lib.dtype_code(torch.float32), _lib.ptr(x), _lib.ptr(grid),
                                 _lib.ptr(waug), _lib.ptr(y), None, 0, 4, 8, 6, 5, 3, 1, None)
     assert rc != 0
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
+@pytest.mark.parametrize("I,O,G,k,base,scaler", [(70, 9, 5, 3, True, True),
+                                                 (13, 5, 4, 1, False, True),
+                                                 (33, 6, 7, 2, True, False)])
+def test_pack_weight_layout_and_unaligned_output(C, dtype, I, O, G, k, base, scaler):
+    """The packed weight row [sw * scaler | base_weight | 0-padding] element
+    by element (one rounding per product, as the tensor expression), both
+    into an aligned buffer (16-byte stores) and one float past an aligned
+    address (scalar stores)."""
+    from torchsplinekan_amd import _lib
+    g = torch.Generator().manual_seed(I + O)
+    R = G + k
+    sw = torch.randn(O, I, R, generator=g, dtype=torch.float64).to(dtype).cuda()
+    bw = torch.randn(O, I, generator=g, dtype=torch.float64).to(dtype).cuda() if base else None
+    sc = (torch.rand(O, I, generator=g, dtype=torch.float64) + 0.5).to(dtype).cuda() \
+        if scaler else None
+    ld = int(_lib.LIB.kan_hip_aug_width(I, G, k, int(base)))
+    ref = torch.zeros(O, ld, dtype=dtype, device="cuda")
+    ref[:, :I * R] = (sw * sc[..., None] if scaler else sw).reshape(O, I * R)
+    if base:
+        ref[:, I * R:I * R + I] = bw
+    aligned = C.pack_weight(bw, sw, sc, k, scaler)
+    assert torch.equal(aligned, ref)
+    buf = torch.full((O * ld + 1,), float("nan"), dtype=dtype, device="cuda")
+    out = buf[1:]
+    assert out.data_ptr() % 16 != 0
+    _lib.check(_lib.LIB.kan_hip_pack_weight(
+        _lib.KAN_DTYPE_F32 if dtype == torch.float32 else _lib.KAN_DTYPE_F64,
+        _lib.ptr(bw), _lib.ptr(sw), _lib.ptr(sc), _lib.ptr(out), I, O, G, k,
+        _lib.stream_of(sw.device)))
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(O, ld), ref)

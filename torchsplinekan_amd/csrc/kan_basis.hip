@@ -376,79 +376,7 @@ __global__ void pack_basis_kernel(const T* __restrict__ basis, const T* __restri
   }
 }
 
-// waug[o, i*R + r] = sw[o,i,r] * scaler[o,i]; waug[o, I*R + i] = bw[o,i];
-// padding columns are zeroed.
-template <typename T>
-__global__ void build_waug_kernel(const T* __restrict__ sw, const T* __restrict__ scaler,
-                                  const T* __restrict__ bw, T* __restrict__ waug, int64_t ld,
-                                  int64_t O, int64_t I, int64_t R) {
-  const int64_t IR = I * R;
-  const int64_t total = O * ld;
-  for (int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; e < total;
-       e += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t o = e / ld, c = e - o * ld;
-    T v = T(0);
-    if (c < IR) {
-      v = sw[o * IR + c];
-      if (scaler != nullptr) v = v * scaler[o * I + c / R];
-    } else if (bw != nullptr && c < IR + I) {
-      v = bw[o * I + (c - IR)];
-    }
-    waug[e] = v;
-  }
-}
-
-// Transposed augmented weight, waug_t[c, o] = waug[o, c] for the kaug
-// columns c of [coef*scaler | base_weight], so that the input-side product
-// E = D waug runs with both operands K-contiguous.  The product is formed as
-// in build_waug_kernel (same rounding).  64x64 tiles are transposed through
-// LDS so that reads (along c) and writes (along o) are both coalesced.
-template <typename T>
-__global__ __launch_bounds__(256) void build_waug_t_kernel(
-    const T* __restrict__ sw, const T* __restrict__ scaler, const T* __restrict__ bw,
-    T* __restrict__ waug_t, int64_t O, int64_t I, int64_t R, int64_t kaug) {
-  __shared__ T tile[64][65];
-  const int64_t c0 = (int64_t)blockIdx.x * 64, o0 = (int64_t)blockIdx.y * 64;
-  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
-  const int64_t IR = I * R;
-#pragma unroll 4
-  for (int j = 0; j < 16; ++j) {
-    const int64_t o = o0 + ty + 4 * j, c = c0 + tx;
-    T v = T(0);
-    if (o < O && c < kaug) {
-      if (c < IR) {
-        v = sw[o * IR + c];
-        if (scaler != nullptr) v = v * scaler[o * I + c / R];
-      } else if (bw != nullptr) {
-        v = bw[o * I + (c - IR)];
-      }
-    }
-    tile[ty + 4 * j][tx] = v;
-  }
-  __syncthreads();
-#pragma unroll 4
-  for (int j = 0; j < 16; ++j) {
-    const int64_t c = c0 + ty + 4 * j, o = o0 + tx;
-    if (c < kaug && o < O) waug_t[c * O + o] = tile[tx][ty + 4 * j];
-  }
-}
-
-// Parameter gradients from the (split) products G = D^T [H | s]:
-//   gsw = scaler * G_H, gscaler = sum_r sw * G_H, gbw = G_s
-// (csrc/kan_cuda.cu:576-598).  Split partials are summed in fixed order.
-// A block owns kPairs consecutive (o, i) edges of one output row o: their
-// kPairs*R partial values are contiguous, so the loads are coalesced.  The
-// pass is a pure stream (splits + 1 reads and one write per element), so
-// each thread keeps kPgUnroll vectors of V elements in flight per split;
-// V = 16 bytes when the rows, split slices and pointers allow it, else 1;
-// the host picks V only where V divides I*R, so V divides every block's
-// np*R (= I*R - i0*R, with i0 a multiple of kPairs) and there is no tail.
-// The per-edge sum over r goes through LDS rows of odd stride (conflict-free
-// for the one-thread-per-edge reads), in r order.
-constexpr int kPairs = 128;
-constexpr int kPgThreads = 256;
-constexpr int kPgUnroll = 2;
-
+// V consecutive elements through one 16-byte access (V > 1) or one element
 template <typename T, int V>
 __device__ __forceinline__ void pg_load(const T* __restrict__ p, T (&e)[V]) {
   if constexpr (V == 1) {
@@ -473,6 +401,93 @@ __device__ __forceinline__ void pg_store(T* __restrict__ p, const T (&e)[V]) {
     *reinterpret_cast<vt*>(p) = v;
   }
 }
+
+// waug[o, i*R + r] = sw[o,i,r] * scaler[o,i]; waug[o, I*R + i] = bw[o,i];
+// padding columns are zeroed.
+template <typename T>
+__device__ __forceinline__ T waug_value(const T* __restrict__ sw, const T* __restrict__ scaler,
+                                        const T* __restrict__ bw, int64_t o, int c, int i, int r,
+                                        int64_t I, int64_t IR, int R) {
+  if (c < IR) {
+    const T v = sw[o * IR + c];
+    return scaler != nullptr ? v * scaler[o * I + i] : v;
+  }
+  if (bw != nullptr && c < IR + I) return bw[o * I + (c - IR)];
+  return T(0);
+}
+
+// waug[o, c] for one row o (blockIdx.y, strided) and V consecutive columns
+// per thread: 16 bytes and one store where the output is 16-byte aligned
+// (rows then start aligned too: ld % 4 == 0), else V = 1.  A thread divides
+// by R once; its next columns step the (feature, r) pair.
+template <typename T, int V>
+__global__ __launch_bounds__(256) void build_waug_kernel(
+    const T* __restrict__ sw, const T* __restrict__ scaler, const T* __restrict__ bw,
+    T* __restrict__ waug, int64_t ld, int64_t O, int64_t I, int64_t R) {
+  const int64_t IR = I * R;
+  const int c0 = (blockIdx.x * 256 + threadIdx.x) * V;
+  if (c0 >= ld) return;
+  const int Ri = (int)R;
+  const int f0 = c0 / Ri, r0 = c0 - f0 * Ri;
+  for (int64_t o = blockIdx.y; o < O; o += gridDim.y) {
+    T v[V];
+    int f = f0, r = r0;
+#pragma unroll
+    for (int j = 0; j < V; ++j) {
+      v[j] = waug_value<T>(sw, scaler, bw, o, c0 + j, f, r, I, IR, Ri);
+      if (++r == Ri) {
+        r = 0;
+        ++f;
+      }
+    }
+    pg_store<T, V>(waug + o * ld + c0, v);
+  }
+}
+
+// Transposed augmented weight, waug_t[c, o] = waug[o, c] for the kaug
+// columns c of [coef*scaler | base_weight], so that the input-side product
+// E = D waug runs with both operands K-contiguous.  The product is formed as
+// in build_waug_kernel (same rounding).  64x64 tiles are transposed through
+// LDS so that reads (along c) and writes (along o) are both coalesced.
+template <typename T>
+__global__ __launch_bounds__(256) void build_waug_t_kernel(
+    const T* __restrict__ sw, const T* __restrict__ scaler, const T* __restrict__ bw,
+    T* __restrict__ waug_t, int64_t O, int64_t I, int64_t R, int64_t kaug) {
+  __shared__ T tile[64][65];
+  const int64_t c0 = (int64_t)blockIdx.x * 64, o0 = (int64_t)blockIdx.y * 64;
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  const int64_t IR = I * R;
+  const int Ri = (int)R, ci = (int)(c0 + tx);  // kaug < 2^31
+  const int f = ci / Ri, r = ci - f * Ri;
+#pragma unroll 4
+  for (int j = 0; j < 16; ++j) {
+    const int64_t o = o0 + ty + 4 * j;
+    tile[ty + 4 * j][tx] =
+        o < O && ci < kaug ? waug_value<T>(sw, scaler, bw, o, ci, f, r, I, IR, Ri) : T(0);
+  }
+  __syncthreads();
+#pragma unroll 4
+  for (int j = 0; j < 16; ++j) {
+    const int64_t c = c0 + ty + 4 * j, o = o0 + tx;
+    if (c < kaug && o < O) waug_t[c * O + o] = tile[tx][ty + 4 * j];
+  }
+}
+
+// Parameter gradients from the (split) products G = D^T [H | s]:
+//   gsw = scaler * G_H, gscaler = sum_r sw * G_H, gbw = G_s
+// (csrc/kan_cuda.cu:576-598).  Split partials are summed in fixed order.
+// A block owns kPairs consecutive (o, i) edges of one output row o: their
+// kPairs*R partial values are contiguous, so the loads are coalesced.  The
+// pass is a pure stream (splits + 1 reads and one write per element), so
+// each thread keeps kPgUnroll vectors of V elements in flight per split;
+// V = 16 bytes when the rows, split slices and pointers allow it, else 1;
+// the host picks V only where V divides I*R, so V divides every block's
+// np*R (= I*R - i0*R, with i0 a multiple of kPairs) and there is no tail.
+// The per-edge sum over r goes through LDS rows of odd stride (conflict-free
+// for the one-thread-per-edge reads), in r order.
+constexpr int kPairs = 128;
+constexpr int kPgThreads = 256;
+constexpr int kPgUnroll = 2;
 
 template <typename T, int V>
 __global__ __launch_bounds__(kPgThreads) void param_grads_kernel(
@@ -995,11 +1010,18 @@ int launch_pack_basis(const T* basis, const T* x, T* aug, int64_t ld_aug, int64_
 template <typename T>
 int launch_build_waug(const T* sw, const T* scaler, const T* bw, T* waug, int64_t ld, int64_t O,
                       int64_t I, int64_t R, hipStream_t st) {
-  const int64_t total = O * ld;
-  if (total == 0) return KAN_OK;
+  if (O * ld == 0) return KAN_OK;
+  if (ld > (1LL << 30)) return set_error(KAN_ERR_LIMIT, "build_weight_aug: rows too long");
+  constexpr int V = 16 / (int)sizeof(T);
+  const bool vec = (reinterpret_cast<uintptr_t>(waug) & 15) == 0 && ld % V == 0;
+  const unsigned gy = (unsigned)std::min<int64_t>(O, 65535);
   TimedLaunch timed(kClassOther, st, 0.0);
-  hipLaunchKernelGGL((build_waug_kernel<T>), dim3(gs_blocks(total)), dim3(256), 0, st, sw,
-                     scaler, bw, waug, ld, O, I, R);
+  if (vec)
+    hipLaunchKernelGGL((build_waug_kernel<T, V>), dim3((unsigned)ceil_div(ld, 256 * V), gy),
+                       dim3(256), 0, st, sw, scaler, bw, waug, ld, O, I, R);
+  else
+    hipLaunchKernelGGL((build_waug_kernel<T, 1>), dim3((unsigned)ceil_div(ld, 256), gy), dim3(256),
+                       0, st, sw, scaler, bw, waug, ld, O, I, R);
   return check_launch("build_weight_aug");
 }
 
