@@ -41,11 +41,15 @@ def _edge_inputs(N, I, O, R, dtype, seed):
 # several sample blocks per workgroup on weights staged once.  The fused
 # backward's tilings (one chunk covering O): O <= 32 -> 2x4, 33..64 -> 4x4,
 # 65..128 -> 4x2 (100; output partials of 2 waves added per group of 2 tiles),
-# 129..256 -> 4x1 (200), 257..512 -> 8x1 (300, 512).
+# 129..256 -> 4x1 (200), 257..512 -> 8x1 (300, 512).  The forward of layers with
+# O <= 64 and R + 1 <= 16 stages groups of 4 features through LDS, with 16-byte
+# loads where I % 4 == 0 (I = 4, 8, 12, 16, 260; every k-step class) and scalar loads
+# with partial groups otherwise (I = 1, 3, 5, 7); O = 3..64.
 SHAPES = [(37, 5, 3, 4), (300, 16, 40, 8), (1000, 9, 70, 13), (64, 3, 300, 68),
           (5000, 4, 6, 11), (77, 3, 5, 1), (513, 2, 33, 20), (129, 3, 17, 29), (70, 2, 9, 44),
           (200, 2, 1300, 11), (3000, 3, 600, 7), (2000, 3, 200, 11), (4097, 5, 64, 11),
-          (8192, 260, 20, 7), (2100, 3, 512, 11), (700, 2, 300, 8), (1200, 3, 100, 3)]
+          (8192, 260, 20, 7), (2100, 3, 512, 11), (700, 2, 300, 8), (1200, 3, 100, 3),
+          (333, 7, 48, 14), (1500, 1, 64, 10), (999, 8, 50, 15), (130, 12, 10, 2)]
 
 
 @pytest.mark.parametrize("shape", SHAPES)

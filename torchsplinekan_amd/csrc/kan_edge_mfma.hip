@@ -52,6 +52,12 @@ __device__ __forceinline__ f32x4 mfma16(float a, float b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 
+// c / d for 0 <= c < 2^16 and inv_d = 1/d (d >= 1): exact, since (c + 0.5)/d
+// lies at least 0.5/d from an integer and the float product errs far less
+__device__ __forceinline__ int small_div_f(int c, float inv_d) {
+  return (int)(((float)c + 0.5f) * inv_d);
+}
+
 __device__ __forceinline__ f32x4 zero4() {
   f32x4 z;
   z[0] = z[1] = z[2] = z[3] = 0.0f;
@@ -359,6 +365,205 @@ __global__ __launch_bounds__(kEdgeMfThreads) void edge_fwd_mfma_kernel(
       const int64_t e = (int64_t)o * g.I + i;
       if (final_out) out[e] = colsum[t] / (float)g.n;
       else out[(int64_t)split * g.O * g.I + e] = colsum[t];
+    }
+  }
+}
+
+// Forward of a narrow layer (at most 4 output tiles, K = R + 1 <= 16) with
+// its sample rows staged through LDS.  Loading a 16-row MFMA operand tile
+// straight from [n, I, R] (rows I*R floats apart, R floats used per row)
+// makes every quarter-wave of a load touch 16 rows, and for a narrow layer,
+// whose rows feed only O/16 output tiles, the texture units then bound the
+// kernel.  Here a block takes kStF consecutive features, whose rows are
+// contiguous (kStF*R floats), and a chunk of kStRows samples: the block
+// loads the chunk with consecutive lanes on consecutive addresses (16-byte
+// vectors where I % 4 == 0 and the arrays are aligned) and stores it to LDS
+// rows [H(i0..i0+3, 0..R-1) | s(i0..i0+3) | 0 ...]; wave w then runs feature
+// i0 + w over the chunk's 16-row tiles, lane (q, r) reading its operand
+// column c = 4 k + q of row r at a fixed offset (s, an H column, or the zero
+// slot).  The next chunk's loads are in flight (registers) while the current
+// one is computed; two LDS buffers and one barrier per chunk.
+constexpr int kStF = 4;       // features per block (one per wave)
+constexpr int kStRows = 64;   // samples per staged chunk (= kEdgeRowQuant)
+
+template <int KS>
+struct StageGeom {
+  // row: 4R <= 4(4KS - 1) H floats, 4 s values, zero slot; the stride is
+  // 4 * odd, so the 16 rows x 4 columns a wave reads fall in distinct banks
+  static constexpr int kS = 4 * (4 * KS + 1 + ((4 * KS + 1) % 2 == 0 ? 1 : 0));
+  static constexpr int kBuf = kStRows * kS;       // floats per chunk buffer
+  static constexpr int kEPT = 4 * KS;             // scalar path: floats per thread (R <= 4KS-1)
+  static_assert(kS >= 4 * (4 * KS - 1) + 5 && (kS / 4) % 2 == 1, "row layout");
+};
+
+// The chunk at n0 (rows below ne), through resources based at the chunk
+// (rows past ne read as 0).  VEC: element v = thread + 256 j (j < KS) of the
+// chunk's 64 R H vectors then 64 s vectors (I % 4 == 0: every group is
+// whole, rows and s rows 16-byte aligned).  Scalar: H floats e = thread +
+// 256 j of the [kStRows, nf*R] block and s value thread of [kStRows, nf].
+template <int KS, bool VEC>
+struct StageLoader {
+  typedef StageGeom<KS> SG;
+  static constexpr int kN = VEC ? KS : SG::kEPT;
+  typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+  u32x4 hv4[VEC ? KS : 1];
+  float hv[VEC ? 1 : SG::kEPT], sv;
+  __device__ __forceinline__ void load(const float* __restrict__ s, const float* __restrict__ H,
+                                       int64_t n0, int64_t ne, int I, int R, int i0, int nf,
+                                       float inv_fr, float inv_nf) {
+    const int64_t IR = (int64_t)I * R;
+    const int rows = (int)min((int64_t)kStRows, ne - n0);
+    const __amdgpu_buffer_rsrc_t rh = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(H + n0 * IR + (int64_t)i0 * R), (short)0, (int)(rows * IR * 4),
+        kBufWord3);
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(s != nullptr ? s + n0 * I + i0 : H), (short)0,
+        s != nullptr ? (int)(rows * (int64_t)I * 4) : 0, kBufWord3);
+    const int t = (int)threadIdx.x;
+    if constexpr (VEC) {
+#pragma unroll
+      for (int j = 0; j < KS; ++j) {
+        const int v = t + kEdgeMfThreads * j;
+        if (v < kStRows * R) {
+          const int row = small_div_f(v, inv_fr);  // inv_fr = 1 / R here
+          hv4[j] = __builtin_amdgcn_raw_buffer_load_b128(
+              rh, (int)(((int64_t)row * IR + 4 * (v - row * R)) * 4), 0, 0);
+        } else {
+          const int row = v - kStRows * R;
+          hv4[j] = __builtin_amdgcn_raw_buffer_load_b128(
+              rs, row < kStRows ? (int)((int64_t)row * I * 4) : (int)kBufOob, 0, 0);
+        }
+      }
+    } else {
+      const int FR = nf * R, elems = kStRows * FR;
+#pragma unroll
+      for (int j = 0; j < SG::kEPT; ++j) {
+        const int e = t + kEdgeMfThreads * j;
+        const int row = small_div_f(e, inv_fr);
+        hv[j] = buf_ld(rh, e < elems ? (uint32_t)(((int64_t)row * IR + (e - row * FR)) * 4)
+                                     : kBufOob);
+      }
+      const int row = small_div_f(t, inv_nf);
+      sv = buf_ld(rs, t < kStRows * nf ? (uint32_t)(((int64_t)row * I + (t - row * nf)) * 4)
+                                       : kBufOob);
+    }
+  }
+  __device__ __forceinline__ void store(float* __restrict__ buf, int R, int nf, float inv_fr,
+                                        float inv_nf) const {
+    const int t = (int)threadIdx.x;
+    if constexpr (VEC) {
+#pragma unroll
+      for (int j = 0; j < KS; ++j) {
+        const int v = t + kEdgeMfThreads * j;
+        int off;
+        if (v < kStRows * R) {
+          const int row = small_div_f(v, inv_fr);
+          off = row * SG::kS + 4 * (v - row * R);
+        } else {
+          off = (v - kStRows * R) * SG::kS + 4 * R;
+        }
+        if (v < kStRows * (R + 1)) *reinterpret_cast<u32x4*>(buf + off) = hv4[j];
+      }
+    } else {
+      const int FR = nf * R, elems = kStRows * FR;
+#pragma unroll
+      for (int j = 0; j < SG::kEPT; ++j) {
+        const int e = t + kEdgeMfThreads * j;
+        if (e < elems) {
+          const int row = small_div_f(e, inv_fr);
+          buf[row * SG::kS + (e - row * FR)] = hv[j];
+        }
+      }
+      if (t < kStRows * nf) {
+        const int row = small_div_f(t, inv_nf);
+        buf[row * SG::kS + 4 * R + (t - row * nf)] = sv;
+      }
+    }
+  }
+};
+
+template <int KS, int OT, bool VEC>
+__global__ __launch_bounds__(kEdgeMfThreads) void edge_fwd_stage_kernel(
+    const float* __restrict__ s, const float* __restrict__ H, const float* __restrict__ bw,
+    const float* __restrict__ W, float* __restrict__ out, EdgeGeom g, int final_out) {
+  typedef StageGeom<KS> SG;
+  __shared__ float lds[2][SG::kBuf];
+  const int groups = (g.I + kStF - 1) / kStF;
+  const int64_t bid = xcd_remap((int)blockIdx.x, (int)gridDim.x);
+  const int i0 = (int)(bid % groups) * kStF;
+  const int split = (int)(bid / groups);
+  const int nf = min(kStF, g.I - i0);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int q = lane >> 4, r = lane & 15;
+  const int i = i0 + wave;
+  const bool active = wave < nf;
+  const int R = g.R;
+  const float inv_fr = 1.0f / (float)(VEC ? R : nf * R), inv_nf = 1.0f / (float)nf;
+
+  // the zero slot (and features past nf) stay zero
+  for (int e = threadIdx.x; e < 2 * SG::kBuf; e += kEdgeMfThreads) (&lds[0][0])[e] = 0.0f;
+
+  float w[OT][KS];
+#pragma unroll
+  for (int t = 0; t < OT; ++t) {
+    const int o = t * 16 + r;
+#pragma unroll
+    for (int k = 0; k < KS; ++k) {
+      const int c = 4 * k + q;
+      w[t][k] = (active && o < g.O && c <= R) ? wc_val(bw, W, o, g.I, i, R, c) : 0.0f;
+    }
+  }
+  // LDS column of operand column c = 4 k + q: s, H(i, c - 1) or the zero slot
+  int col[KS];
+#pragma unroll
+  for (int k = 0; k < KS; ++k) {
+    const int c = 4 * k + q;
+    col[k] = c == 0 ? 4 * R + wave : (c <= R ? wave * R + c - 1 : 4 * R + 4);
+  }
+  float tot[OT];
+#pragma unroll
+  for (int t = 0; t < OT; ++t) tot[t] = 0.0f;
+
+  const int64_t nb = (int64_t)split * g.per_split;
+  const int64_t ne = min(g.n, nb + g.per_split);
+  StageLoader<KS, VEC> ld;
+  if (nb < ne) ld.load(s, H, nb, ne, g.I, R, i0, nf, inv_fr, inv_nf);
+  __syncthreads();  // (the zero fill)
+  int buf = 0;
+  for (int64_t n0 = nb; n0 < ne; n0 += kStRows, buf ^= 1) {
+    ld.store(lds[buf], R, nf, inv_fr, inv_nf);
+    if (n0 + kStRows < ne) ld.load(s, H, n0 + kStRows, ne, g.I, R, i0, nf, inv_fr, inv_nf);
+    __syncthreads();
+    if (active) {
+      const float* rowp = lds[buf] + r * SG::kS;
+#pragma unroll
+      for (int tt = 0; tt < kStRows / 16; ++tt) {
+        float a[KS];
+#pragma unroll
+        for (int k = 0; k < KS; ++k) a[k] = rowp[tt * 16 * SG::kS + col[k]];
+        f32x4 acc[OT];
+#pragma unroll
+        for (int t = 0; t < OT; ++t) acc[t] = zero4();
+#pragma unroll
+        for (int k = 0; k < KS; ++k)
+#pragma unroll
+          for (int t = 0; t < OT; ++t) acc[t] = mfma16(a[k], w[t][k], acc[t]);
+#pragma unroll
+        for (int t = 0; t < OT; ++t)
+          tot[t] += (fabsf(acc[t][0]) + fabsf(acc[t][1])) + (fabsf(acc[t][2]) + fabsf(acc[t][3]));
+      }
+    }
+  }
+  if (!active) return;
+#pragma unroll
+  for (int t = 0; t < OT; ++t) {
+    const float s1 = tot[t] + __shfl_xor(tot[t], 16);
+    const float cs = s1 + __shfl_xor(s1, 32);
+    const int o = t * 16 + r;
+    if (q == 0 && o < g.O) {
+      const int64_t e = (int64_t)o * g.I + i;
+      if (final_out) out[e] = cs / (float)g.n;
+      else out[(int64_t)split * g.O * g.I + e] = cs;
     }
   }
 }
@@ -1112,6 +1317,10 @@ int edge_tiling(int64_t O, int* ot, int* ws) {
   return (4 / *ws) * *ot * 16;
 }
 
+// The forward of a narrow layer stages its rows through LDS (see
+// edge_fwd_stage_kernel): at most 4 output tiles, R + 1 <= 16.
+static bool edge_fwd_staged(int64_t O, int64_t R) { return O <= 64 && R + 1 <= 16; }
+
 // Sample splits: about 8 workgroups per CU (measured at c4's layers, where
 // longer workgroups in fewer whole rounds ran slower than many short ones the
 // hardware balances by itself).  The forward pass of a narrow layer, whose
@@ -1119,11 +1328,14 @@ int edge_tiling(int64_t O, int* ot, int* ws) {
 // many: its partial sums are only O x I per split.  At least 256 samples per
 // split, at most 64 splits.
 int edge_mfma_splits(int64_t n, int64_t I, int64_t O, int64_t R, bool backward) {
-  (void)R;
   int ot, ws;
   const int64_t ochunks = ceil_div(O, (int64_t)edge_tiling(O, &ot, &ws));
-  const int64_t blocks = I * ochunks;
-  const int64_t target = (!backward && ws > 1 ? 32LL : 8LL) * device_cu_count();
+  int64_t blocks = I * ochunks;
+  int64_t target = (!backward && ws > 1 ? 32LL : 8LL) * device_cu_count();
+  if (!backward && edge_fwd_staged(O, R)) {  // blocks of kStF features
+    blocks = ceil_div(I, (int64_t)kStF);
+    target = 8LL * device_cu_count();
+  }
   int64_t s = ceil_div(target, blocks > 0 ? blocks : 1);
   const int64_t cap = ceil_div(n, 256);
   if (s > cap) s = cap;
@@ -1148,10 +1360,30 @@ int launch_edge_forward_mfma(const float* s, const float* H, const float* bw, co
   g.per_split = round_up(ceil_div(n, splits), kEdgeRowQuant);
   int ot, ws;
   g.ochunks = (int)ceil_div(O, (int64_t)edge_tiling(O, &ot, &ws));
-  const int64_t blocks = I * g.ochunks * (int64_t)splits;
+  const bool staged = edge_fwd_staged(O, R);
+  const int64_t blocks =
+      (staged ? ceil_div(I, (int64_t)kStF) : I * g.ochunks) * (int64_t)splits;
   if (blocks > 2147483647LL) return set_error(KAN_ERR_LIMIT, "edge_abs_mean: too many blocks");
   const bool fin = splits == 1;
   TimedLaunch timed(kClassEdge, st, 2.0 * (double)n * (double)O * (double)I * (double)R1);
+  if (staged) {
+    auto al = [](const float* q) { return (reinterpret_cast<uintptr_t>(q) & 15) == 0; };
+    const bool vec = I % kStF == 0 && al(H) && (s == nullptr || al(s));
+#define KAN_EDGE_FWD_ST(OTV, VV)                                                                \
+  KAN_EDGE_MF_DISPATCH4(R1, hipLaunchKernelGGL((edge_fwd_stage_kernel<KS, OTV, VV>),            \
+                                               dim3((unsigned)blocks), dim3(kEdgeMfThreads), 0, \
+                                               st, s, H, bw, W, fin ? a : part, g, fin ? 1 : 0))
+    if (vec) {
+      if (O > 32) KAN_EDGE_FWD_ST(4, true);
+      else if (O > 16) KAN_EDGE_FWD_ST(2, true);
+      else KAN_EDGE_FWD_ST(1, true);
+    } else {
+      if (O > 32) KAN_EDGE_FWD_ST(4, false);
+      else if (O > 16) KAN_EDGE_FWD_ST(2, false);
+      else KAN_EDGE_FWD_ST(1, false);
+    }
+#undef KAN_EDGE_FWD_ST
+  } else {
 #define KAN_EDGE_FWD(OTV, WSV)                                                                  \
   KAN_EDGE_MF_DISPATCH(R1, (void)CT; hipLaunchKernelGGL((edge_fwd_mfma_kernel<KS, OTV, WSV>),   \
                                                           dim3((unsigned)blocks),                \
@@ -1163,6 +1395,7 @@ int launch_edge_forward_mfma(const float* s, const float* H, const float* bw, co
   else if (ot == 4) KAN_EDGE_FWD(4, 4);
   else KAN_EDGE_FWD(2, 4);
 #undef KAN_EDGE_FWD
+  }
   int rc = check_launch("edge_abs_mean");
   if (rc != KAN_OK || fin) return rc;
   hipLaunchKernelGGL(edge_fwd_finalize_f32, dim3(fin_blocks_f32(O * I)), dim3(256), 0, st, part,
