@@ -157,7 +157,7 @@ def test_forward_with_regularization_fused_matches_dense(C, dtype):
 # and R + 1 at 5, 12 and 16.
 LINEAR_SHAPES = [(37, 5, 4, 4), (90, 3, 7, 6), (300, 7, 64, 11), (250, 4, 33, 11),
                  (1000, 9, 100, 15), (513, 3, 200, 11), (700, 2, 300, 8), (4097, 5, 512, 11),
-                 (6000, 3, 64, 11)]
+                 (6000, 3, 64, 11), (2000, 8, 64, 11), (500, 12, 10, 3), (777, 16, 24, 14)]
 
 
 @pytest.mark.parametrize("shape", LINEAR_SHAPES)

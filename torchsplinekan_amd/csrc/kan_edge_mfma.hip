@@ -1236,6 +1236,249 @@ __global__ __launch_bounds__(kEdgeMfThreads) void edge_bwd_mfma_kernel(
   }
 }
 
+// Fused backward of a narrow layer (O <= 64, R + 1 <= 16) on staged rows:
+// the products of edge_bwd_mfma_kernel (phi, then g = ga sign(phi) / n (+ D)
+// into dWc[o, c] += sum_n g Hc and dHc^T[c, n] += sum_o Wc g), with the
+// block layout of edge_fwd_stage_kernel: kStF features (wave w: feature
+// i0 + w, every output) and chunks of kStRows samples.  Per chunk the block
+// stages the Hc rows and (with the layer-output gradient) the D rows
+// [kStRows, O] in LDS, the waves compute, and each writes its dHc values into
+// an LDS copy of the chunk's row layout, which the block then stores to ds
+// and dH with consecutive lanes on consecutive addresses.  Two barriers per
+// chunk.
+constexpr int kStDS = 68;  // LDS row stride of the staged D rows (O <= 64; 4 * odd)
+constexpr int kStDPT = kStRows * 64 / kEdgeMfThreads;  // D floats per thread per chunk
+
+template <int KS, int OT, bool HASD, bool VEC>
+__global__ __launch_bounds__(kEdgeMfThreads) void edge_bwd_stage_kernel(
+    const float* __restrict__ ga, const float* __restrict__ D, const float* __restrict__ s,
+    const float* __restrict__ H, const float* __restrict__ bw, const float* __restrict__ W,
+    float* __restrict__ ds, float* __restrict__ dH, float* __restrict__ dbw,
+    float* __restrict__ dW, float* __restrict__ part, EdgeGeom g, int final_out) {
+  typedef StageGeom<KS> SG;
+  constexpr int TS = 20;  // transposed g tile row stride
+  __shared__ __align__(16) float hs[SG::kBuf];
+  __shared__ __align__(16) float os[SG::kBuf];
+  __shared__ __align__(16) float dsm[HASD ? kStRows * kStDS : 4];
+  __shared__ __align__(16) float trans[4 * OT * 16 * TS];
+  const int groups = (g.I + kStF - 1) / kStF;
+  const int64_t bid = xcd_remap((int)blockIdx.x, (int)gridDim.x);
+  const int i0 = (int)(bid % groups) * kStF;
+  const int split = (int)(bid / groups);
+  const int nf = min(kStF, g.I - i0);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int t_ = (int)threadIdx.x;
+  const int q = lane >> 4, r = lane & 15;
+  const int i = i0 + wave;
+  const bool active = wave < nf;
+  const int R = g.R, R1 = R + 1, O = g.O, I = g.I;
+  const int64_t IR = (int64_t)I * R;
+  const float inv_n = 1.0f / (float)g.n;
+  const float inv_fr = 1.0f / (float)(VEC ? R : nf * R), inv_nf = 1.0f / (float)nf;
+  const float inv_o = 1.0f / (float)O;
+
+  // the zero slot, features past nf and D columns past O stay zero
+  for (int e = t_; e < SG::kBuf; e += kEdgeMfThreads) hs[e] = 0.0f;
+  if constexpr (HASD)
+    for (int e = t_; e < kStRows * kStDS; e += kEdgeMfThreads) dsm[e] = 0.0f;
+
+  // LDS column of augmented column c of this wave's feature
+  auto colof = [&](int c) { return c == 0 ? 4 * R + wave : (c <= R ? wave * R + c - 1 : 4 * R + 4); };
+  // phi's B operand Wc[o = 16t + r, c = 4k + q]; the input product's A
+  // operand Wc[o = 16t + 4q + v, c = r]; ga / n of columns o
+  float w[OT][KS], wb[OT][4], gav[OT];
+#pragma unroll
+  for (int t = 0; t < OT; ++t) {
+    const int o = t * 16 + r;
+    gav[t] = (active && o < O) ? ga[(int64_t)o * I + i] * inv_n : 0.0f;
+#pragma unroll
+    for (int k = 0; k < KS; ++k) {
+      const int c = 4 * k + q;
+      w[t][k] = (active && o < O && c <= R) ? wc_val(bw, W, o, I, i, R, c) : 0.0f;
+    }
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int ov = t * 16 + 4 * q + v;
+      wb[t][v] = (active && ov < O && r < R1) ? wc_val(bw, W, ov, I, i, R, r) : 0.0f;
+    }
+  }
+  int colk[KS], colo[4];
+#pragma unroll
+  for (int k = 0; k < KS; ++k) colk[k] = colof(4 * k + q);
+#pragma unroll
+  for (int v = 0; v < 4; ++v) colo[v] = colof(4 * q + v);
+  const int colr = colof(r);
+  f32x4 dacc[OT];
+#pragma unroll
+  for (int t = 0; t < OT; ++t) dacc[t] = zero4();
+
+  const int64_t nb = (int64_t)split * g.per_split;
+  const int64_t ne = min(g.n, nb + g.per_split);
+  StageLoader<KS, VEC> ld;
+  float dreg[HASD ? kStDPT : 1];
+  auto load_d = [&](int64_t n0) {
+    if constexpr (HASD) {
+      const int rows = (int)min((int64_t)kStRows, ne - n0);
+      const __amdgpu_buffer_rsrc_t rd = __builtin_amdgcn_make_buffer_rsrc(
+          const_cast<float*>(D + n0 * O), (short)0, rows * O * 4, kBufWord3);
+#pragma unroll
+      for (int j = 0; j < kStDPT; ++j) {
+        const int e = t_ + kEdgeMfThreads * j;
+        dreg[j] = buf_ld(rd, e < kStRows * O ? (uint32_t)(e * 4) : kBufOob);
+      }
+    }
+  };
+  if (nb < ne) {
+    ld.load(s, H, nb, ne, I, R, i0, nf, inv_fr, inv_nf);
+    load_d(nb);
+  }
+  float* tb = trans + wave * (OT * 16 * TS);
+  __syncthreads();  // (the zero fills)
+  for (int64_t n0 = nb; n0 < ne; n0 += kStRows) {
+    ld.store(hs, R, nf, inv_fr, inv_nf);
+    if constexpr (HASD) {
+#pragma unroll
+      for (int j = 0; j < kStDPT; ++j) {
+        const int e = t_ + kEdgeMfThreads * j;
+        if (e < kStRows * O) {
+          const int row = small_div_f(e, inv_o);
+          dsm[row * kStDS + (e - row * O)] = dreg[j];
+        }
+      }
+    }
+    if (n0 + kStRows < ne) {
+      ld.load(s, H, n0 + kStRows, ne, I, R, i0, nf, inv_fr, inv_nf);
+      load_d(n0 + kStRows);
+    }
+    __syncthreads();
+    if (active) {
+#pragma unroll 1
+      for (int tt = 0; tt < kStRows / 16; ++tt) {
+        const float* ra = hs + (16 * tt + r) * SG::kS;
+        float a[KS], hb[4];
+#pragma unroll
+        for (int k = 0; k < KS; ++k) a[k] = ra[colk[k]];
+#pragma unroll
+        for (int v = 0; v < 4; ++v) hb[v] = hs[(16 * tt + 4 * q + v) * SG::kS + colr];
+        float dq[HASD ? OT : 1][4];
+        if constexpr (HASD) {
+#pragma unroll
+          for (int t = 0; t < OT; ++t)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) dq[t][v] = dsm[(16 * tt + 4 * q + v) * kStDS + 16 * t + r];
+        }
+        f32x4 acc[OT];
+#pragma unroll
+        for (int t = 0; t < OT; ++t) acc[t] = zero4();
+#pragma unroll
+        for (int k = 0; k < KS; ++k)
+#pragma unroll
+          for (int t = 0; t < OT; ++t) acc[t] = mfma16(a[k], w[t][k], acc[t]);
+        float gv[OT][4];
+#pragma unroll
+        for (int t = 0; t < OT; ++t)
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            gv[t][v] = g_sign(gav[t], acc[t][v]);
+            if constexpr (HASD) gv[t][v] += dq[t][v];
+          }
+        // g[n = 4q + v, o = 16t + r] -> tile t at [o][n]
+#pragma unroll
+        for (int t = 0; t < OT; ++t) {
+          f32x4 gq;
+          gq[0] = gv[t][0];
+          gq[1] = gv[t][1];
+          gq[2] = gv[t][2];
+          gq[3] = gv[t][3];
+          *reinterpret_cast<f32x4*>(tb + t * 16 * TS + r * TS + 4 * q) = gq;
+        }
+#pragma unroll
+        for (int v = 0; v < 4; ++v)
+#pragma unroll
+          for (int t = 0; t < OT; ++t) dacc[t] = mfma16(gv[t][v], hb[v], dacc[t]);
+        edge_wave_sync();
+        // g[n = r, o = 16t + 4q + v]
+        float gt[OT][4];
+#pragma unroll
+        for (int t = 0; t < OT; ++t)
+#pragma unroll
+          for (int v = 0; v < 4; ++v) gt[t][v] = tb[t * 16 * TS + (4 * q + v) * TS + r];
+        edge_wave_sync();  // (the next tile's stores come after these reads)
+        f32x4 d0 = zero4(), d1 = zero4();
+#pragma unroll
+        for (int v = 0; v < 4; ++v)
+#pragma unroll
+          for (int t = 0; t < OT; t += 2) {
+            d0 = mfma16(wb[t][v], gt[t][v], d0);
+            if (t + 1 < OT) d1 = mfma16(wb[t + 1][v], gt[t + 1][v], d1);
+          }
+        // dHc[n = 16 tt + r, c = 4q + v]
+#pragma unroll
+        for (int v = 0; v < 4; ++v)
+          if (4 * q + v <= R) os[(16 * tt + r) * SG::kS + colo[v]] = d0[v] + d1[v];
+      }
+    }
+    __syncthreads();
+    // the chunk's dHc rows below ne to ds and dH
+    const int rows = (int)min((int64_t)kStRows, ne - n0);
+    if constexpr (VEC) {
+#pragma unroll
+      for (int j = 0; j < KS; ++j) {
+        const int v = t_ + kEdgeMfThreads * j;
+        if (v < kStRows * R) {
+          const int row = small_div_f(v, inv_fr);
+          const int c4 = v - row * R;
+          if (row < rows && dH != nullptr)
+            *reinterpret_cast<f32x4*>(dH + (n0 + row) * IR + (int64_t)i0 * R + 4 * c4) =
+                *reinterpret_cast<const f32x4*>(os + row * SG::kS + 4 * c4);
+        } else if (v < kStRows * (R + 1)) {
+          const int row = v - kStRows * R;
+          if (row < rows && ds != nullptr)
+            *reinterpret_cast<f32x4*>(ds + (n0 + row) * I + i0) =
+                *reinterpret_cast<const f32x4*>(os + row * SG::kS + 4 * R);
+        }
+      }
+    } else {
+      const int FR = nf * R;
+#pragma unroll
+      for (int j = 0; j < SG::kEPT; ++j) {
+        const int e = t_ + kEdgeMfThreads * j;
+        if (e < kStRows * FR) {
+          const int row = small_div_f(e, inv_fr);
+          if (row < rows && dH != nullptr)
+            dH[(n0 + row) * IR + (int64_t)i0 * R + (e - row * FR)] = os[row * SG::kS + (e - row * FR)];
+        }
+      }
+      if (t_ < kStRows * nf) {
+        const int row = small_div_f(t_, inv_nf);
+        if (row < rows && ds != nullptr)
+          ds[(n0 + row) * I + i0 + (t_ - row * nf)] = os[row * SG::kS + 4 * R + (t_ - row * nf)];
+      }
+    }
+  }
+  // dacc[t]: lane (q, r) holds column c = r, rows o = 16t + 4q + v
+  if (!active || r >= R1) return;
+#pragma unroll
+  for (int t = 0; t < OT; ++t) {
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int o = t * 16 + 4 * q + v;
+      if (o >= O) continue;
+      const int64_t e = (int64_t)o * I + i;
+      const float val = dacc[t][v];
+      if (final_out) {
+        if (r == 0) {
+          if (dbw != nullptr) dbw[e] = val;
+        } else if (dW != nullptr) {
+          dW[e * R + (r - 1)] = val;
+        }
+      } else {
+        part[((int64_t)split * O * I + e) * R1 + r] = val;
+      }
+    }
+  }
+}
+
 __global__ void edge_fwd_finalize_f32(const float* __restrict__ part, float* __restrict__ a,
                                       int splits, int64_t count, int64_t n) {
   for (int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; e < count;
@@ -1317,9 +1560,13 @@ int edge_tiling(int64_t O, int* ot, int* ws) {
   return (4 / *ws) * *ot * 16;
 }
 
-// The forward of a narrow layer stages its rows through LDS (see
-// edge_fwd_stage_kernel): at most 4 output tiles, R + 1 <= 16.
+// The forward and the fused backward of a narrow layer stage their rows
+// through LDS (edge_fwd_stage_kernel, edge_bwd_stage_kernel): at most 4
+// output tiles, R + 1 <= 16.
 static bool edge_fwd_staged(int64_t O, int64_t R) { return O <= 64 && R + 1 <= 16; }
+static bool edge_bwd_staged(int64_t O, int64_t R) {
+  return edge_fused_enabled() && O <= 64 && R + 1 <= 16;
+}
 
 // Sample splits: about 8 workgroups per CU (measured at c4's layers, where
 // longer workgroups in fewer whole rounds ran slower than many short ones the
@@ -1332,7 +1579,7 @@ int edge_mfma_splits(int64_t n, int64_t I, int64_t O, int64_t R, bool backward) 
   const int64_t ochunks = ceil_div(O, (int64_t)edge_tiling(O, &ot, &ws));
   int64_t blocks = I * ochunks;
   int64_t target = (!backward && ws > 1 ? 32LL : 8LL) * device_cu_count();
-  if (!backward && edge_fwd_staged(O, R)) {  // blocks of kStF features
+  if (backward ? edge_bwd_staged(O, R) : edge_fwd_staged(O, R)) {  // blocks of kStF features
     blocks = ceil_div(I, (int64_t)kStF);
     target = 8LL * device_cu_count();
   }
@@ -1475,11 +1722,34 @@ int launch_edge_fused(const float* ga, const float* D, const float* s, const flo
   else { ot = 8; ws = 1; }
   if (splits > 1 && part == nullptr)
     return set_error(KAN_ERR_WORKSPACE, "edge_abs_mean_backward: missing workspace");
-  const int64_t blocks = I * (int64_t)splits;
+  const bool staged = edge_bwd_staged(O, R);
+  const int64_t blocks = (staged ? ceil_div(I, (int64_t)kStF) : I) * (int64_t)splits;
   if (blocks > 2147483647LL)
     return set_error(KAN_ERR_LIMIT, "edge_abs_mean_backward: too many blocks");
   const bool fin = splits == 1;
-  {
+  if (staged) {
+    TimedLaunch timed(kClassEdgeGrad, st, 6.0 * (double)n * (double)O * (double)I * (double)R1);
+    auto al = [](const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15) == 0; };
+    const bool vec = I % kStF == 0 && al(H) && (s == nullptr || al(s)) && al(dH) && al(ds);
+#define KAN_EDGE_BWD_ST(OTV, HD, VV)                                                            \
+  KAN_EDGE_MF_DISPATCH4(R1, hipLaunchKernelGGL((edge_bwd_stage_kernel<KS, OTV, HD, VV>),        \
+                                               dim3((unsigned)blocks), dim3(kEdgeMfThreads), 0, \
+                                               st, ga, D, s, H, bw, W, ds, dH, dbw, dW, part, g, \
+                                               fin ? 1 : 0))
+#define KAN_EDGE_BWD_ST_O(HD, VV)                \
+  if (O > 32) KAN_EDGE_BWD_ST(4, HD, VV);        \
+  else if (O > 16) KAN_EDGE_BWD_ST(2, HD, VV);   \
+  else KAN_EDGE_BWD_ST(1, HD, VV)
+    if (D != nullptr) {
+      if (vec) { KAN_EDGE_BWD_ST_O(true, true); } else { KAN_EDGE_BWD_ST_O(true, false); }
+    } else {
+      if (vec) { KAN_EDGE_BWD_ST_O(false, true); } else { KAN_EDGE_BWD_ST_O(false, false); }
+    }
+#undef KAN_EDGE_BWD_ST_O
+#undef KAN_EDGE_BWD_ST
+    const int rc = check_launch("edge_abs_mean_backward(fused, staged)");
+    if (rc != KAN_OK || fin) return rc;
+  } else {
     TimedLaunch timed(kClassEdgeGrad, st, 6.0 * (double)n * (double)O * (double)I * (double)R1);
 #define KAN_EDGE_BWD(OTV, WSV, HD)                                                             \
   KAN_EDGE_MF_DISPATCH4(R1, hipLaunchKernelGGL((edge_bwd_mfma_kernel<KS, OTV, WSV, HD>),       \
