@@ -2,10 +2,13 @@
 (256x256 over 8 waves of 128x64, 256x256 over 4 waves of 128x128, and
 128x128 with 64x64 per wave), each forced through KAN_HIP_GEMM_TILE, on
 layer shapes chosen so that the
-forward (NT), input-gradient (NT against the transposed weight; both the
-two-pass route and, with KAN_HIP_FUSED_DX=1, dx contracted in the GEMM
-epilogue, where the spline columns of one feature straddle two wave blocks
-when R does not divide the block width) and parameter-gradient (TN, split
+forward (NT), input-gradient (NT against the transposed weight; the
+two-pass routes through the full E (KAN_HIP_COMPACT_E=0) and through its
+compact form (the k+1 span-window values per item; KAN_HIP_COMPACT_E=1
+forces it, by default it serves rows of R >= 25), and, with
+KAN_HIP_FUSED_DX=1, dx contracted in the GEMM epilogue, where the spline
+columns of one feature straddle two wave blocks when R does not divide the
+block width) and parameter-gradient (TN, split
 over samples) products see whole tiles, ragged row and column edges, K tails that
 are not a multiple of the 32-deep slab, unaligned leading dimensions
 (out_features not a multiple of 4) and several split-K counts.
@@ -47,7 +50,7 @@ def C():
 
 @pytest.fixture
 def tile_env():
-    names = ("KAN_HIP_GEMM_TILE", "KAN_HIP_FUSED_DX")
+    names = ("KAN_HIP_GEMM_TILE", "KAN_HIP_FUSED_DX", "KAN_HIP_COMPACT_E")
     old = {n: os.environ.get(n) for n in names}
     yield
     for n, v in old.items():
@@ -57,14 +60,15 @@ def tile_env():
             os.environ[n] = v
 
 
-@pytest.mark.parametrize("fused_dx", ["0", "1"])
+@pytest.mark.parametrize("dx_route", ["full", "compact", "fused"])
 @pytest.mark.parametrize("tile", ["256", "256w4", "128"])
 @pytest.mark.parametrize("shape", SHAPES)
-def test_contraction_configs_match_oracle(C, tile_env, tile, shape, fused_dx):
+def test_contraction_configs_match_oracle(C, tile_env, tile, shape, dx_route):
     N, I, O, G, k, kind = shape
-    print(f"contraction tile={tile} fused_dx={fused_dx} shape={shape}", flush=True)
+    print(f"contraction tile={tile} dx_route={dx_route} shape={shape}", flush=True)
     os.environ["KAN_HIP_GEMM_TILE"] = tile
-    os.environ["KAN_HIP_FUSED_DX"] = fused_dx
+    os.environ["KAN_HIP_FUSED_DX"] = "1" if dx_route == "fused" else "0"
+    os.environ["KAN_HIP_COMPACT_E"] = "1" if dx_route == "compact" else "0"
     g = torch.Generator().manual_seed(N + I)
     grid = make_grid(I, G, k, kind, seed=N)
     x = torch.rand(N, I, generator=g, dtype=torch.float64) * 2.2 - 1.1
@@ -111,3 +115,48 @@ def test_fused_dx_without_base_branch(C, tile_env, shape):
     for name, got, ref in [("y", y, ry), ("dx", gx, rgx), ("dcoef", gsw, rgsw)]:
         err = normwise(np64(got), ref)
         assert err < FP32_TOL, (name, err)
+
+
+@pytest.mark.parametrize("tile", ["256", "128"])
+@pytest.mark.parametrize("shape", [
+    (600, 37, 300, 7, 3, "uniform", True),
+    (300, 33, 19, 7, 2, "nonuniform", True),
+    (257, 33, 19, 4, 1, "repeated", False),
+    (520, 9, 70, 65, 3, "uniform", True),     # R = 68: rows across 3 wave blocks
+    (1000, 130, 64, 10, 3, "nonuniform", False),
+])
+def test_compact_input_product_matches_full_route(C, tile_env, tile, shape):
+    """dx through the compact input-side product (the k+1 span-window values
+    of E per item and the base columns, then the input gradient from them)
+    equals dx through the full E [n, ld] element for element (the same
+    products in the same order), and both hold the fp32 bar against the
+    oracle; x up to 1.1 outside [-1, 1] takes the zero-basis path, and a
+    window that crosses wave blocks is completed by each of them."""
+    N, I, O, G, k, kind, base = shape
+    print(f"compact E tile={tile} shape={shape}", flush=True)
+    os.environ["KAN_HIP_GEMM_TILE"] = tile
+    os.environ["KAN_HIP_FUSED_DX"] = "0"
+    g = torch.Generator().manual_seed(3 * N + I)
+    grid = make_grid(I, G, k, kind, seed=I)
+    x = torch.rand(N, I, generator=g, dtype=torch.float64) * 2.2 - 1.1
+    sw = torch.randn(O, I, G + k, generator=g, dtype=torch.float64) * 0.1
+    bw = (torch.rand(O, I, generator=g, dtype=torch.float64) * 2 - 1) / np.sqrt(I)
+    sc = torch.rand(O, I, generator=g, dtype=torch.float64) + 0.5
+    D = torch.randn(N, O, generator=g, dtype=torch.float64)
+    f = lambda t: t.float().cuda()
+    bwd = f(bw) if base else torch.empty(0, device="cuda")
+    y, H = C.kan_forward(f(x), f(grid), bwd, f(sw), f(sc), k, True)
+    out = {}
+    for route in ("0", "1"):
+        os.environ["KAN_HIP_COMPACT_E"] = route
+        out[route] = C.kan_backward(f(D), f(x), f(grid), bwd, f(sw), f(sc), H, k, True)
+    torch.cuda.synchronize()
+    gx_full, gx_comp = out["0"][0], out["1"][0]
+    assert torch.equal(gx_comp, gx_full)
+    for a_, b_ in zip(out["0"][1:], out["1"][1:]):
+        assert (a_ is None and b_ is None) or torch.equal(a_, b_)
+    a = lambda t: np64(t.float())
+    _, rH = ko.kan_forward(a(x), a(grid), a(bw) if base else None, a(sw), a(sc), k)
+    rgx = ko.kan_backward(a(D), a(x), a(grid), a(bw) if base else None, a(sw), a(sc), k,
+                          basis=rH)[0]
+    assert normwise(np64(gx_comp), rgx) < FP32_TOL

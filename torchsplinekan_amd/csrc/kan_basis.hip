@@ -659,7 +659,10 @@ __global__ __launch_bounds__(kBasisThreads) void basis_grad_pf_kernel(
 // CU holds many waves to cover the load latency; the next step's x is
 // loaded while the current step is computed.  Same products in the same
 // order as basis_grad_pf_kernel (a window entry outside 0..R-1 adds +0).
-template <int K, typename T, int DER>
+// CW: the gradient comes in compact form, g = Ew [n, I, K+1] (window slot j
+// of item (n, i)) and gbase = Es [n, I], as the compact input-side product
+// writes it; the same products in the same order.
+template <int K, typename T, int DER, bool CW = false>
 __global__ __launch_bounds__(kBasisThreads) void basis_grad_window_kernel(
     const T* __restrict__ x, const T* __restrict__ grid, const T* __restrict__ g, int64_t ld,
     const T* __restrict__ gbase, T* __restrict__ gx, BasisShape sh) {
@@ -681,14 +684,26 @@ __global__ __launch_bounds__(kBasisThreads) void basis_grad_window_kernel(
     const bool ok = lane_ok && nn < sh.n;
     const T xv = xn;
     const int m = ok ? knot_span(t, nk, xv) : -1;
-    const T* grow = g + nn * ld + col * R;  // dereferenced only inside the window
+    // (dereferenced only inside the window)
+    const T* grow = CW ? g + (nn * sh.I + col) * (K + 1) : g + nn * ld + col * R;
     T gw[K + 1];
+    if constexpr (CW && K == 3 && sizeof(T) == 4) {  // the window as one 16-byte load
+      typedef T vt __attribute__((ext_vector_type(4)));
+      vt v4 = {T(0), T(0), T(0), T(0)};
+      if (m >= 0) v4 = *reinterpret_cast<const vt*>(grow);
 #pragma unroll
-    for (int j = 0; j <= K; ++j) {
-      const int r = m - K + j;
-      gw[j] = (m >= 0 && r >= 0 && r < R) ? grow[r] : T(0);
+      for (int j = 0; j <= K; ++j) {
+        const int r = m - K + j;
+        gw[j] = (r >= 0 && r < R) ? v4[j] : T(0);
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j <= K; ++j) {
+        const int r = m - K + j;
+        gw[j] = (m >= 0 && r >= 0 && r < R) ? grow[CW ? j : r] : T(0);
+      }
     }
-    const T gb = (ok && gbase != nullptr) ? gbase[nn * ld + col] : T(0);
+    const T gb = (ok && gbase != nullptr) ? gbase[CW ? nn * sh.I + col : nn * ld + col] : T(0);
     const int64_t nx = nn + step;
     xn = (it + 1 < sh.iters && lane_ok && nx < sh.n) ? x[nx * sh.I + col] : T(0);
     if (ok) {
@@ -843,6 +858,34 @@ bool launch_grad_pf(const T* x, const T* grid, const T* gH, int64_t ld_g, const 
 #undef KAN_BGPF
   *rc = check_launch("basis_grad");
   return true;
+}
+
+// Input gradient from the compact input-side product (fp32, local basis):
+// gx[n, i] = sum_j Ew[n, i, j] dB_{m-k+j}/dx + Es[n, i] silu'(x).
+int launch_basis_grad_compact(const float* x, const float* grid, const float* ew,
+                              const float* es, float* gx, int64_t n, int64_t I, int G, int k,
+                              hipStream_t st) {
+  if (n == 0 || I == 0) return KAN_OK;
+  if (k < 1 || k > 3) return set_error(KAN_ERR_INVALID, "basis_grad_compact: spline order 1..3");
+  if ((reinterpret_cast<uintptr_t>(ew) & 15) != 0)
+    return set_error(KAN_ERR_INVALID, "basis_grad_compact: window values must be 16-byte aligned");
+  const int R = G + k, nk = G + 2 * k + 1;
+  // algorithmic bytes: read x, the k+1 window values (+ base), write gx
+  TimedLaunch timed(kClassBasisGrad, st,
+                    4.0 * (double)n * (double)I * (2.0 + (k + 1) + (es ? 1 : 0)));
+  int64_t by = 0;
+  BasisShape sh = make_shape(n, I, G, R, sizeof(float), 0, ew, &by, false);
+  if (by > 2147483647LL) return set_error(KAN_ERR_LIMIT, "basis_grad: too many samples");
+  dim3 grid_dim((unsigned)ceil_div(I, sh.fb), (unsigned)by);
+  const size_t smem = sizeof(float) * (size_t)round_up((int64_t)sh.fb * nk, 4);
+#define KAN_BGC(KK)                                                                           \
+  hipLaunchKernelGGL((basis_grad_window_kernel<KK, float, 1, true>), grid_dim,                \
+                     dim3(64 * sh.waves), smem, st, x, grid, ew, (int64_t)0, es, gx, sh)
+  if (k == 1) KAN_BGC(1);
+  else if (k == 2) KAN_BGC(2);
+  else KAN_BGC(3);
+#undef KAN_BGC
+  return check_launch("basis_grad_compact");
 }
 
 template <typename T>

@@ -32,6 +32,22 @@ bool fused_dx_enabled() {
   const char* v = std::getenv("KAN_HIP_FUSED_DX");
   return v != nullptr && v[0] == '1';
 }
+
+// The input-side product of the fp32 backward with the local basis can store
+// only each item's k+1 span-window values of E (and the base columns), which
+// the input gradient then reads (launch_gemm_ecomp, launch_basis_grad_compact).
+// It pays where rows are long: at R = 68 (c5) the product took 0.16 ms more
+// and the input gradient 0.80 ms less than through the full E [n, ld]; at
+// R = 13 (c3) the epilogue's span searches cost 0.54 ms against 0.39 ms
+// saved.  So by default from R >= kCompactMinR; KAN_HIP_COMPACT_E=1 takes it
+// for every R (where supported), =0 never.  Read at every plan.
+constexpr int64_t kCompactMinR = 25;
+bool compact_e_wanted(int64_t R) {
+  const char* v = std::getenv("KAN_HIP_COMPACT_E");
+  if (v != nullptr && v[0] == '0') return false;
+  if (v != nullptr && v[0] == '1') return true;
+  return R >= kCompactMinR;
+}
 }  // namespace
 
 int set_error(int code, const char* fmt, ...) {
@@ -174,9 +190,10 @@ int need_ptr(const void* p, const char* who, const char* name) {
 
 struct BackwardPlan {
   int64_t R, ld, kaug;
-  bool need_x, need_params, fused_dx;
+  bool need_x, need_params, fused_dx, compact_dx;
   int splits;
   size_t waug_elems, e_elems, part_elems;
+  size_t ew_elems;  // compact route: window values [n, I, k+1], then the base columns
 };
 
 // Inference workspace: the augmented basis [n, ld], then the split-K
@@ -200,12 +217,20 @@ BackwardPlan plan_backward(int64_t n, int64_t I, int64_t O, int64_t G, int64_t k
   p.need_x = need_x;
   p.need_params = need_params;
   p.splits = need_params ? gemm_pick_splits<T>(O, p.kaug, n) : 1;
-  p.waug_elems = need_x ? (size_t)(p.kaug * O) : 0;  // transposed weight [kaug, O]
+  // transposed weight [kaug, O] (rounded to 256 bytes: E follows it)
+  p.waug_elems = need_x ? (size_t)round_up(p.kaug * O, 64) : 0;
   // fp32 with the local basis: dx is contracted inside the input-side GEMM,
   // which leaves [n, I, 3 or 2] partial sums instead of E [n, ld]
-  p.fused_dx = need_x && std::is_same<T, float>::value && g_basis_impl.load() == 1 &&
-               fused_dx_enabled() && gemm_dx_supported(n, p.kaug, O, I, (int)G, (int)k, has_base);
-  p.e_elems = !need_x ? 0 : p.fused_dx ? (size_t)(n * I * (has_base ? 3 : 2)) : (size_t)(n * p.ld);
+  const bool local_f32 = std::is_same<T, float>::value && g_basis_impl.load() == 1;
+  p.fused_dx = need_x && local_f32 && fused_dx_enabled() &&
+               gemm_dx_supported(n, p.kaug, O, I, (int)G, (int)k, has_base);
+  p.compact_dx = need_x && local_f32 && !p.fused_dx && compact_e_wanted(p.R) &&
+                 gemm_ecomp_supported(n, p.kaug, O, I, (int)G, (int)k, has_base);
+  p.ew_elems = p.compact_dx ? (size_t)round_up(n * I * (k + 1), 64) : 0;
+  p.e_elems = !need_x         ? 0
+              : p.fused_dx   ? (size_t)(n * I * (has_base ? 3 : 2))
+              : p.compact_dx ? p.ew_elems + (size_t)(has_base ? round_up(n * I, 64) : 0)
+                             : (size_t)(n * p.ld);
   p.part_elems = need_params ? (size_t)p.splits * (size_t)(O * p.ld) : 0;
   return p;
 }
@@ -278,7 +303,20 @@ int backward_impl(const void* D, const void* x, const void* grid, const void* bw
       }
     }
   }
-  if (need_x && !p.fused_dx) {
+  if constexpr (std::is_same<T, float>::value) {
+    if (need_x && p.compact_dx) {
+      // E's span-window values and base columns only, then dx from them
+      float* ew = E;
+      float* es = has_base ? E + p.ew_elems : nullptr;
+      KAN_TRY(launch_gemm_ecomp(n, p.kaug, O, tD, O, waug, O, static_cast<const float*>(x),
+                                static_cast<const float*>(grid), I, (int)G, (int)k, has_base, ew,
+                                es, st));
+      KAN_TRY(launch_basis_grad_compact(static_cast<const float*>(x),
+                                        static_cast<const float*>(grid), ew, es,
+                                        static_cast<float*>(gx), n, I, (int)G, (int)k, st));
+    }
+  }
+  if (need_x && !p.fused_dx && !p.compact_dx) {
     // E[n, k'] = sum_o D[n, o] Waug[o, k'] = sum_o D[n, o] WaugT[k', o]  (both K-contiguous)
     KAN_TRY(launch_gemm<T>(kLayoutNT, n, p.kaug, O, tD, O, waug, O, E, p.ld, 1, 0, st));
     KAN_TRY(launch_basis_grad<T>(static_cast<const T*>(x), static_cast<const T*>(grid), E, p.ld,

@@ -129,6 +129,11 @@ int launch_basis(const T* x, const T* grid, T* out, int64_t ld_out, T* silu_out,
 template <typename T>
 int launch_basis_grad(const T* x, const T* grid, const T* gH, int64_t ld_g, const T* gbase,
                       T* gx, int64_t n, int64_t I, int G, int k, int impl, hipStream_t st);
+// The same from the compact input-side product (launch_gemm_ecomp): window
+// values ew [n, I, k+1] (16-byte aligned) and base columns es [n, I] or null.
+int launch_basis_grad_compact(const float* x, const float* grid, const float* ew,
+                              const float* es, float* gx, int64_t n, int64_t I, int G, int k,
+                              hipStream_t st);
 
 // Order-`order` derivatives of the basis, [n, I, R] (order 0 = values; order
 // > k gives zeros), and their contraction gx = sum_r gH * D^order B_r.
@@ -187,6 +192,16 @@ int launch_gemm_dx(int64_t M, int64_t N, int64_t K, const float* A, int64_t lda,
 // Whether launch_gemm_dx takes this shape (the tile configuration it would
 // pick leaves room for every block's knots and samples).
 bool gemm_dx_supported(int64_t M, int64_t N, int64_t K, int64_t I, int G, int k, bool has_base);
+
+// fp32 input-side product E = D Waug in compact form: of each (sample,
+// feature) only the k+1 span-window values of its spline columns, ew
+// [M, I, k+1], and the base columns es [M, I] (kan_gemm.hip); the input
+// gradient then takes launch_basis_grad_compact.
+int launch_gemm_ecomp(int64_t M, int64_t N, int64_t K, const float* A, int64_t lda,
+                      const float* B, int64_t ldb, const float* x, const float* grid, int64_t I,
+                      int G, int k, bool has_base, float* ew, float* es, hipStream_t st);
+bool gemm_ecomp_supported(int64_t M, int64_t N, int64_t K, int64_t I, int G, int k,
+                          bool has_base);
 
 // General product C = op(A) op(B) for any transposition pair: the split
 // count from gemm_pick_splits, partial slices in ws, then a fixed-order sum

@@ -435,7 +435,9 @@ struct SchedSeq<KMF, KMF, R, W, L> {
 struct DxParams {
   const float* x;     // [M, I] samples (the rows of the product)
   const float* grid;  // [I, nk] knot rows
-  float* part;        // [M, I, nslot] partial input gradients
+  float* part;        // [M, I, nslot] partial input gradients; compact route:
+                      // [M, I, k+1] span-window values of E
+  float* es;          // compact route: [M, I] base-column values of E
   int64_t I;
   int64_t ksp;        // I * R: first base column
   int R, nk, nslot;
@@ -586,6 +588,102 @@ __device__ __forceinline__ void dx_epilogue(const GemmParams<float>& p, const Dx
   }
 }
 
+// Compact input-side product: of E's spline columns only the K+1 that the
+// input gradient uses, those of the span window of x[n, i], are stored, as
+// Ew[n, i, 0..K] (window slot jj = column m - K + jj of feature i, the
+// columns inside 0..R-1 only), and the base columns as Es[n, i].  The
+// staging of accumulators, knot rows and x is that of dx_epilogue; each
+// item (sample, feature) of a wave block finds its span and copies the
+// window columns that lie in the block (a window that crosses a block
+// boundary is completed by the neighbouring block; every slot is written
+// by exactly one block).
+template <class C, int K>
+__device__ __forceinline__ void ecomp_epilogue(const GemmParams<float>& p, const DxParams& e,
+                                               const TileCoords& tc,
+                                               const f32x16 (&acc)[C::FM][C::FN],
+                                               float* lds_stage, float* lds_side, int side_floats,
+                                               int wave, int wm, int wn, int lane) {
+  typedef Mfma<float, 32> M;
+  constexpr int TN = C::TN, SW = C::TN + 1;  // staged row stride (odd: conflict-free columns)
+  float* stage = lds_stage + wave * 32 * SW;
+  const DxBlock blk(tc.n0 + (int64_t)wn * TN, p.N, e.ksp, e.R, TN, e.es != nullptr);
+  const int per_row = blk.nfs + blk.nbase;
+  if (per_row == 0) return;  // block lies past the last column
+  float* kn = lds_side + wave * side_floats;
+  const int nkn = blk.nfs * e.nk;
+  float* xs = kn + ((nkn + 3) & ~3);
+  static_assert(C::FM == 1 || C::FM == 2 || C::FM == 4, "tile rows per wave: 1, 2 or 4");
+  int nb = C::FM;
+  while (nb > 1 && dx_side_floats(blk, e.nk, nb) > side_floats) nb >>= 1;
+  const float* gsrc = e.grid + blk.fs * e.nk;
+  for (int b = lane; b < nkn; b += 64 * 4) {
+    float v[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int idx = b + u * 64;
+      v[u] = gsrc[idx < nkn ? idx : 0];
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      if (b + u * 64 < nkn) kn[b + u * 64] = v[u];
+  }
+  const int64_t fbase = blk.b0 - e.ksp - blk.nfs;
+  const int total = 32 * nb * per_row;
+  const float rcp = 1.0f / (float)per_row;
+#pragma unroll
+  for (int iq = 0; iq < C::FM; ++iq) {
+    const int q0 = iq & ~(nb - 1);
+    const int64_t rbase = tc.m0 + (int64_t)wm * C::TM + q0 * 32;
+    if (iq == q0) {
+      for (int b = lane; b < total; b += 64 * 8) {
+        float v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          const int el = b + u * 64;
+          const int rq = div_small(el, rcp), idx = el - rq * per_row;
+          const int64_t f = idx < blk.nfs ? blk.fs + idx : fbase + idx;
+          const int64_t n = rbase + rq;
+          const bool ok = el < total && n < p.M && idx < blk.nfs;  // (x of spline items only)
+          v[u] = ok ? e.x[n * e.I + f] : 0.0f;
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+          if (b + u * 64 < total) xs[b + u * 64] = v[u];
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < C::FN; ++j)
+#pragma unroll
+      for (int v = 0; v < M::kNAcc; ++v)
+        stage[M::out_row(lane, v) * SW + j * 32 + M::out_col(lane)] = acc[iq][j][v];
+    wave_sync_lds();
+    const float* xq = xs + (iq - q0) * 32 * per_row;
+    for (int it = lane; it < 32 * per_row; it += 64) {
+      const int row = div_small(it, rcp), idx = it - row * per_row;
+      const int64_t n = rbase + (iq - q0) * 32 + row;
+      if (n >= p.M) continue;
+      const float* srow = stage + row * SW;
+      if (idx < blk.nfs) {
+        const int64_t f = blk.fs + idx;
+        const int m = knot_span(kn + idx * e.nk, e.nk, xq[it]);
+        if (m < 0) continue;  // no spline term: the window is not read
+        const int64_t c_lo = f * e.R + m - K;  // column of window slot 0
+        float* dst = e.part + (n * e.I + f) * (K + 1);
+#pragma unroll
+        for (int jj = 0; jj <= K; ++jj) {
+          const int r = m - K + jj;
+          const int64_t col = c_lo + jj;
+          if (r >= 0 && r < e.R && col >= blk.c0 && col < blk.sp_end) dst[jj] = srow[col - blk.c0];
+        }
+      } else {
+        const int64_t col = blk.b0 + (idx - blk.nfs);
+        e.es[n * e.I + (col - e.ksp)] = srow[col - blk.c0];
+      }
+    }
+    wave_sync_lds();
+  }
+}
+
 template <class C, bool AK, bool BKC, int EPIK>
 __global__ __launch_bounds__(C::kThreads, C::MINB) void gemm_pipe_kernel(GemmParams<float> p,
                                                                          DxParams e) {
@@ -718,7 +816,11 @@ __global__ __launch_bounds__(C::kThreads, C::MINB) void gemm_pipe_kernel(GemmPar
     constexpr int kSide = 2 * SB::kElems / (C::WM * C::WN);
     static_assert(kSide + 512 <= 8192, "div_small covers the side buffer's indices");
     __syncthreads();  // every wave is done with the slab buffers
-    dx_epilogue<C, EPIK>(p, e, tc, acc, &lds_a[0][0], &lds_b[0][0], kSide, wave, wm, wn, lane);
+    if constexpr (EPIK > 0)
+      dx_epilogue<C, EPIK>(p, e, tc, acc, &lds_a[0][0], &lds_b[0][0], kSide, wave, wm, wn, lane);
+    else
+      ecomp_epilogue<C, -EPIK>(p, e, tc, acc, &lds_a[0][0], &lds_b[0][0], kSide, wave, wm, wn,
+                               lane);
   }
 }
 
@@ -871,6 +973,25 @@ int launch_dx_cfg(const GemmParams<float>& p, const DxParams& e, int k, hipStrea
   if (k == 1) return launch_cfg<C, true, true, 1>(p, 1, st, &e);
   if (k == 2) return launch_cfg<C, true, true, 2>(p, 1, st, &e);
   return launch_cfg<C, true, true, 3>(p, 1, st, &e);
+}
+
+// Every wave block's side buffer fits (the compact route has no bound on R:
+// a window crossing blocks is completed by each of them).
+template <class C>
+bool ecomp_cfg_fits(int64_t N, int64_t I, int R, int nk, bool has_base) {
+  typedef Slab<C::BN, C::BK, true> SB;
+  constexpr int64_t kSide = 2 * SB::kElems / (C::WM * C::WN);
+  const int64_t ksp = I * R;
+  for (int64_t c0 = 0; c0 < N; c0 += C::TN)
+    if (dx_side_floats(DxBlock(c0, N, ksp, R, C::TN, has_base), nk, 1) > kSide) return false;
+  return true;
+}
+
+template <class C>
+int launch_ecomp_cfg(const GemmParams<float>& p, const DxParams& e, int k, hipStream_t st) {
+  if (k == 1) return launch_cfg<C, true, true, -1>(p, 1, st, &e);
+  if (k == 2) return launch_cfg<C, true, true, -2>(p, 1, st, &e);
+  return launch_cfg<C, true, true, -3>(p, 1, st, &e);
 }
 
 }  // namespace
@@ -1036,6 +1157,7 @@ int launch_gemm_dx(int64_t M, int64_t N, int64_t K, const float* A, int64_t lda,
   e.R = G + k;
   e.ksp = I * e.R;
   e.nk = G + 2 * k + 1;
+  e.es = nullptr;
   e.nslot = has_base ? 3 : 2;
   int rc;
   {
@@ -1055,6 +1177,57 @@ int launch_gemm_dx(int64_t M, int64_t N, int64_t K, const float* A, int64_t lda,
   hipLaunchKernelGGL(dx_finalize_kernel, dim3((unsigned)blocks), dim3(256), 0, st, part, gx,
                      count, e.nslot);
   return check_launch("dx_finalize");
+}
+
+bool gemm_ecomp_supported(int64_t M, int64_t N, int64_t K, int64_t I, int G, int k,
+                          bool has_base) {
+  if (k < 1 || k > 3) return false;
+  const int R = G + k, nk = G + 2 * k + 1;
+  const int cfg = pick_cfg_f32(M, N, K, 1);
+  if (cfg == 0) return ecomp_cfg_fits<CfgF32Big>(N, I, R, nk, has_base);
+  if (cfg == 3) return ecomp_cfg_fits<CfgF32Big4>(N, I, R, nk, has_base);
+  return ecomp_cfg_fits<CfgF32Small>(N, I, R, nk, has_base);
+}
+
+// Input-side product in compact form (NT layout: A = D [M, K], B = Waug^T
+// [N, K]): the span-window values Ew [M, I, k+1] and the base columns Es
+// [M, I] (has_base) through ecomp_epilogue; no [M, N] output.
+int launch_gemm_ecomp(int64_t M, int64_t N, int64_t K, const float* A, int64_t lda,
+                      const float* B, int64_t ldb, const float* x, const float* grid, int64_t I,
+                      int G, int k, bool has_base, float* ew, float* es, hipStream_t st) {
+  if (M <= 0 || I <= 0) return KAN_OK;
+  if (!gemm_ecomp_supported(M, N, K, I, G, k, has_base))
+    return set_error(KAN_ERR_LIMIT, "gemm_ecomp: layer shape not supported by the compact epilogue");
+  GemmParams<float> p;
+  p.A = A;
+  p.B = B;
+  p.C = nullptr;
+  p.M = M;
+  p.N = N;
+  p.K = K;
+  p.lda = lda;
+  p.ldb = ldb;
+  p.ldc = 0;
+  p.split_stride = 0;
+  p.vec = vec_ok(A, lda) && vec_ok(B, ldb);
+  DxParams e;
+  e.x = x;
+  e.grid = grid;
+  e.part = ew;
+  e.es = has_base ? es : nullptr;
+  e.I = I;
+  e.R = G + k;
+  e.ksp = I * e.R;
+  e.nk = G + 2 * k + 1;
+  e.nslot = k + 1;
+  TimedLaunch timed(kClassContraction, st, 2.0 * (double)M * (double)N * (double)K);
+  const int cfg = pick_cfg_f32(M, N, K, 1);
+  int rc;
+  if (cfg == 0) rc = launch_ecomp_cfg<CfgF32Big>(p, e, k, st);
+  else if (cfg == 3) rc = launch_ecomp_cfg<CfgF32Big4>(p, e, k, st);
+  else rc = launch_ecomp_cfg<CfgF32Small>(p, e, k, st);
+  if (rc != KAN_OK) return rc;
+  return check_launch("gemm_ecomp");
 }
 
 template int launch_gemm<float>(int, int64_t, int64_t, int64_t, const float*, int64_t,
