@@ -591,12 +591,15 @@ __device__ __forceinline__ void dx_epilogue(const GemmParams<float>& p, const Dx
 // Compact input-side product: of E's spline columns only the K+1 that the
 // input gradient uses, those of the span window of x[n, i], are stored, as
 // Ew[n, i, 0..K] (window slot jj = column m - K + jj of feature i, the
-// columns inside 0..R-1 only), and the base columns as Es[n, i].  The
-// staging of accumulators, knot rows and x is that of dx_epilogue; each
-// item (sample, feature) of a wave block finds its span and copies the
-// window columns that lie in the block (a window that crosses a block
-// boundary is completed by the neighbouring block; every slot is written
-// by exactly one block).
+// columns inside 0..R-1 only), and the base columns as Es[n, i].  Base
+// columns go from the accumulators straight to Es.  For the spline columns
+// a wave block stages the knot rows of its features and x of its items
+// (all its tile rows at once when the side buffer holds them), finds every
+// item's span (four interleaved searches per lane) and keeps it in x's
+// place; then per tile row it stages the accumulators in LDS and each item
+// copies the window columns that lie in the block (a window that crosses a
+// block boundary is completed by the neighbouring block; every slot is
+// written by exactly one block).
 template <class C, int K>
 __device__ __forceinline__ void ecomp_epilogue(const GemmParams<float>& p, const DxParams& e,
                                                const TileCoords& tc,
@@ -607,48 +610,99 @@ __device__ __forceinline__ void ecomp_epilogue(const GemmParams<float>& p, const
   constexpr int TN = C::TN, SW = C::TN + 1;  // staged row stride (odd: conflict-free columns)
   float* stage = lds_stage + wave * 32 * SW;
   const DxBlock blk(tc.n0 + (int64_t)wn * TN, p.N, e.ksp, e.R, TN, e.es != nullptr);
-  const int per_row = blk.nfs + blk.nbase;
-  if (per_row == 0) return;  // block lies past the last column
+  if (blk.nbase > 0) {  // base columns of the block: accumulators -> Es
+#pragma unroll
+    for (int iq = 0; iq < C::FM; ++iq)
+#pragma unroll
+      for (int j = 0; j < C::FN; ++j) {
+        const int64_t col = blk.c0 + j * 32 + M::out_col(lane);
+        if (col < e.ksp || col >= e.ksp + e.I) continue;
+#pragma unroll
+        for (int v = 0; v < M::kNAcc; ++v) {
+          const int64_t row = tc.m0 + (int64_t)wm * C::TM + iq * 32 + M::out_row(lane, v);
+          if (row < p.M) e.es[row * e.I + (col - e.ksp)] = acc[iq][j][v];
+        }
+      }
+  }
+  const int nfs = blk.nfs;
+  if (nfs == 0) return;
   float* kn = lds_side + wave * side_floats;
-  const int nkn = blk.nfs * e.nk;
+  const int nkn = nfs * e.nk;
   float* xs = kn + ((nkn + 3) & ~3);
   static_assert(C::FM == 1 || C::FM == 2 || C::FM == 4, "tile rows per wave: 1, 2 or 4");
   int nb = C::FM;
-  while (nb > 1 && dx_side_floats(blk, e.nk, nb) > side_floats) nb >>= 1;
+  while (nb > 1 && (((int64_t)nkn + 3) & ~(int64_t)3) + (int64_t)32 * nb * nfs > side_floats)
+    nb >>= 1;
   const float* gsrc = e.grid + blk.fs * e.nk;
-  for (int b = lane; b < nkn; b += 64 * 4) {
-    float v[4];
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int idx = b + u * 64;
-      v[u] = gsrc[idx < nkn ? idx : 0];
-    }
-#pragma unroll
-    for (int u = 0; u < 4; ++u)
-      if (b + u * 64 < nkn) kn[b + u * 64] = v[u];
-  }
-  const int64_t fbase = blk.b0 - e.ksp - blk.nfs;
-  const int total = 32 * nb * per_row;
-  const float rcp = 1.0f / (float)per_row;
+  const float rcp = 1.0f / (float)nfs;
 #pragma unroll
   for (int iq = 0; iq < C::FM; ++iq) {
     const int q0 = iq & ~(nb - 1);
     const int64_t rbase = tc.m0 + (int64_t)wm * C::TM + q0 * 32;
+    const int total = 32 * nb * nfs;  // spline items of tile rows q0 .. q0 + nb - 1
     if (iq == q0) {
+      // knot rows (first batch only; nfs * nk <= 256) and x, sample-major
+      // xs[rq * nfs + idx], loaded together
+      float kv[4];
+      if (iq == 0) {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) kv[u] = lane + 64 * u < nkn ? gsrc[lane + 64 * u] : 0.0f;
+      }
       for (int b = lane; b < total; b += 64 * 8) {
         float v[8];
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
           const int el = b + u * 64;
-          const int rq = div_small(el, rcp), idx = el - rq * per_row;
-          const int64_t f = idx < blk.nfs ? blk.fs + idx : fbase + idx;
+          const int rq = div_small(el, rcp), idx = el - rq * nfs;
           const int64_t n = rbase + rq;
-          const bool ok = el < total && n < p.M && idx < blk.nfs;  // (x of spline items only)
-          v[u] = ok ? e.x[n * e.I + f] : 0.0f;
+          v[u] = (el < total && n < p.M) ? e.x[n * e.I + blk.fs + idx] : 0.0f;
         }
 #pragma unroll
         for (int u = 0; u < 8; ++u)
           if (b + u * 64 < total) xs[b + u * 64] = v[u];
+      }
+      if (iq == 0) {
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+          if (lane + 64 * u < nkn) kn[lane + 64 * u] = kv[u];
+      }
+      wave_sync_lds();
+      // spans (knot_span of kan_spline.h as 7 fixed halving steps, nk <= 128:
+      // the largest m <= nk - 2 with t[m] <= x for t[0] <= x < t[nk-1], the
+      // last non-degenerate span at x == t[nk-1], -1 outside or NaN), four
+      // interleaved searches per lane, stored over x
+      for (int b = lane; b < total; b += 64 * 4) {
+        float xv[4];
+        const float* tk[4];
+        int lo[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const int el = b + u * 64 < total ? b + u * 64 : total - 1;
+          const int rq = div_small(el, rcp);
+          xv[u] = xs[el];
+          tk[u] = kn + (el - rq * nfs) * e.nk;
+          lo[u] = 0;
+        }
+#pragma unroll
+        for (int step = 64; step >= 1; step >>= 1)
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            const int c = lo[u] + step;
+            if (c <= e.nk - 2 && tk[u][c <= e.nk - 2 ? c : e.nk - 2] <= xv[u]) lo[u] = c;
+          }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const float* t = tk[u];
+          const float x = xv[u], tl = t[e.nk - 1];
+          int m = lo[u];
+          if (!(x >= t[0]) || x > tl) {
+            m = -1;
+          } else if (x == tl) {
+            m = e.nk - 2;
+            while (m > 0 && t[m] == tl) --m;
+          }
+          if (b + u * 64 < total) xs[b + u * 64] = __int_as_float(m);
+        }
       }
     }
 #pragma unroll
@@ -657,27 +711,21 @@ __device__ __forceinline__ void ecomp_epilogue(const GemmParams<float>& p, const
       for (int v = 0; v < M::kNAcc; ++v)
         stage[M::out_row(lane, v) * SW + j * 32 + M::out_col(lane)] = acc[iq][j][v];
     wave_sync_lds();
-    const float* xq = xs + (iq - q0) * 32 * per_row;
-    for (int it = lane; it < 32 * per_row; it += 64) {
-      const int row = div_small(it, rcp), idx = it - row * per_row;
+    const float* sq = xs + (iq - q0) * 32 * nfs;
+    for (int it = lane; it < 32 * nfs; it += 64) {
+      const int row = div_small(it, rcp), idx = it - row * nfs;
       const int64_t n = rbase + (iq - q0) * 32 + row;
-      if (n >= p.M) continue;
+      const int m = __float_as_int(sq[it]);
+      if (n >= p.M || m < 0) continue;  // (no spline term: the window is not read)
       const float* srow = stage + row * SW;
-      if (idx < blk.nfs) {
-        const int64_t f = blk.fs + idx;
-        const int m = knot_span(kn + idx * e.nk, e.nk, xq[it]);
-        if (m < 0) continue;  // no spline term: the window is not read
-        const int64_t c_lo = f * e.R + m - K;  // column of window slot 0
-        float* dst = e.part + (n * e.I + f) * (K + 1);
+      const int64_t f = blk.fs + idx;
+      const int64_t c_lo = f * e.R + m - K;  // column of window slot 0
+      float* dst = e.part + (n * e.I + f) * (K + 1);
 #pragma unroll
-        for (int jj = 0; jj <= K; ++jj) {
-          const int r = m - K + jj;
-          const int64_t col = c_lo + jj;
-          if (r >= 0 && r < e.R && col >= blk.c0 && col < blk.sp_end) dst[jj] = srow[col - blk.c0];
-        }
-      } else {
-        const int64_t col = blk.b0 + (idx - blk.nfs);
-        e.es[n * e.I + (col - e.ksp)] = srow[col - blk.c0];
+      for (int jj = 0; jj <= K; ++jj) {
+        const int r = m - K + jj;
+        const int64_t col = c_lo + jj;
+        if (r >= 0 && r < e.R && col >= blk.c0 && col < blk.sp_end) dst[jj] = srow[col - blk.c0];
       }
     }
     wave_sync_lds();
@@ -981,9 +1029,14 @@ template <class C>
 bool ecomp_cfg_fits(int64_t N, int64_t I, int R, int nk, bool has_base) {
   typedef Slab<C::BN, C::BK, true> SB;
   constexpr int64_t kSide = 2 * SB::kElems / (C::WM * C::WN);
+  if (nk > 128) return false;  // (the epilogue's span search takes 7 halving steps)
   const int64_t ksp = I * R;
-  for (int64_t c0 = 0; c0 < N; c0 += C::TN)
-    if (dx_side_floats(DxBlock(c0, N, ksp, R, C::TN, has_base), nk, 1) > kSide) return false;
+  for (int64_t c0 = 0; c0 < N; c0 += C::TN) {
+    const DxBlock b(c0, N, ksp, R, C::TN, has_base);
+    if (b.nfs * nk > 256 ||
+        (((int64_t)b.nfs * nk + 3) & ~(int64_t)3) + 32 * (int64_t)b.nfs > kSide)
+      return false;
+  }
   return true;
 }
 
