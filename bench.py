@@ -443,8 +443,9 @@ def run_c4(args, dev, steps, warmup):
     # products, 6 n O I (R+1) flops; parameter kernel for the first layer,
     # whose input needs no gradient: 4 n O I (R+1))
     roof = _mfma_roofline(kern, "edge_grad", "edge_bwd_mfma_kernel (both gradient sides, "
-                          "dL/dy folded in) + edge_param_mfma_kernel (first layer): mean|phi| "
-                          "backward", *recorded_traffic("c4"))
+                          "dL/dy folded in; edge_bwd_stage_kernel for the 64-wide layer) + "
+                          "edge_param_mfma_kernel (first layer): mean|phi| backward",
+                          *recorded_traffic("c4"))
     e_ms, e_cnt, e_work = kern["edge"]
     line = _line("fwd+bwd samples/s, KAN([256,512,512,64]) G8 k3 N=16K forward_with_regularization",
                  N, steps, warmup, wall,
