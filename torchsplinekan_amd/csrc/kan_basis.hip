@@ -659,10 +659,7 @@ __global__ __launch_bounds__(kBasisThreads) void basis_grad_pf_kernel(
 // CU holds many waves to cover the load latency; the next step's x is
 // loaded while the current step is computed.  Same products in the same
 // order as basis_grad_pf_kernel (a window entry outside 0..R-1 adds +0).
-// CW: the gradient comes in compact form, g = Ew [n, I, K+1] (window slot j
-// of item (n, i)) and gbase = Es [n, I], as the compact input-side product
-// writes it; the same products in the same order.
-template <int K, typename T, int DER, bool CW = false>
+template <int K, typename T, int DER>
 __global__ __launch_bounds__(kBasisThreads) void basis_grad_window_kernel(
     const T* __restrict__ x, const T* __restrict__ grid, const T* __restrict__ g, int64_t ld,
     const T* __restrict__ gbase, T* __restrict__ gx, BasisShape sh) {
@@ -684,26 +681,14 @@ __global__ __launch_bounds__(kBasisThreads) void basis_grad_window_kernel(
     const bool ok = lane_ok && nn < sh.n;
     const T xv = xn;
     const int m = ok ? knot_span(t, nk, xv) : -1;
-    // (dereferenced only inside the window)
-    const T* grow = CW ? g + (nn * sh.I + col) * (K + 1) : g + nn * ld + col * R;
+    const T* grow = g + nn * ld + col * R;  // dereferenced only inside the window
     T gw[K + 1];
-    if constexpr (CW && K == 3 && sizeof(T) == 4) {  // the window as one 16-byte load
-      typedef T vt __attribute__((ext_vector_type(4)));
-      vt v4 = {T(0), T(0), T(0), T(0)};
-      if (m >= 0) v4 = *reinterpret_cast<const vt*>(grow);
 #pragma unroll
-      for (int j = 0; j <= K; ++j) {
-        const int r = m - K + j;
-        gw[j] = (r >= 0 && r < R) ? v4[j] : T(0);
-      }
-    } else {
-#pragma unroll
-      for (int j = 0; j <= K; ++j) {
-        const int r = m - K + j;
-        gw[j] = (m >= 0 && r >= 0 && r < R) ? grow[CW ? j : r] : T(0);
-      }
+    for (int j = 0; j <= K; ++j) {
+      const int r = m - K + j;
+      gw[j] = (m >= 0 && r >= 0 && r < R) ? grow[r] : T(0);
     }
-    const T gb = (ok && gbase != nullptr) ? gbase[CW ? nn * sh.I + col : nn * ld + col] : T(0);
+    const T gb = (ok && gbase != nullptr) ? gbase[nn * ld + col] : T(0);
     const int64_t nx = nn + step;
     xn = (it + 1 < sh.iters && lane_ok && nx < sh.n) ? x[nx * sh.I + col] : T(0);
     if (ok) {
@@ -715,6 +700,72 @@ __global__ __launch_bounds__(kBasisThreads) void basis_grad_window_kernel(
         for (int j = 0; j <= K; ++j) acc += gw[j] * d[j];
       }
       if (gbase != nullptr) acc += gb * silu_grad_of<T>(xv);
+      gx[nn * sh.I + col] = acc;
+    }
+  }
+}
+
+// Input gradient from the compact input-side product: Ew [n, I, K+1]
+// (window slot j of item (n, i)) and Es [n, I].  The same products in the
+// same order as basis_grad_window_kernel (a slot outside 0..R-1 adds +0), so
+// the result equals the route through the full E.  An item's slots lie at a
+// fixed place whatever its span, so the next step's window values, base
+// value and x are all loaded while the current step is computed (one
+// 16-byte load for the window with k = 3).
+template <int K>
+__global__ __launch_bounds__(kBasisThreads) void basis_grad_compact_kernel(
+    const float* __restrict__ x, const float* __restrict__ grid, const float* __restrict__ ew,
+    const float* __restrict__ es, float* __restrict__ gx, BasisShape sh) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int nk = sh.G + 2 * K + 1, R = sh.G + K;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int i0 = blockIdx.x * sh.fb;
+  const int fbv = min(sh.fb, sh.I - i0);
+  float* knots = stage_knots<float>(smem, grid, i0, fbv, nk);
+  const int sub = lane / sh.fb, fi = lane - sub * sh.fb;
+  const bool lane_ok = sub < sh.subs && fi < fbv;
+  const float* t = knots + (lane_ok ? fi : 0) * nk;
+  const int64_t step = (int64_t)sh.waves * sh.subs;
+  int64_t nn = (int64_t)blockIdx.y * sh.iters * step + (int64_t)wave * sh.subs + sub;
+  const int64_t col = (int64_t)i0 + (lane_ok ? fi : 0);
+  typedef float f4 __attribute__((ext_vector_type(4)));
+  float xn = 0.0f, bn = 0.0f, wn[K + 1];
+  auto fetch = [&](int64_t n_, bool ok_) {
+    const int64_t e = n_ * sh.I + col;
+    xn = ok_ ? x[e] : 0.0f;
+    if constexpr (K == 3) {
+      const f4 v = ok_ ? *reinterpret_cast<const f4*>(ew + e * 4) : f4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) wn[j] = v[j];
+    } else {
+#pragma unroll
+      for (int j = 0; j <= K; ++j) wn[j] = ok_ ? ew[e * (K + 1) + j] : 0.0f;
+    }
+    bn = (ok_ && es != nullptr) ? es[e] : 0.0f;
+  };
+  fetch(nn, lane_ok && nn < sh.n);
+  __syncthreads();  // knot rows staged
+  for (int it = 0; it < sh.iters; ++it, nn += step) {
+    const bool ok = lane_ok && nn < sh.n;
+    const float xv = xn, gb = bn;
+    float gw[K + 1];
+#pragma unroll
+    for (int j = 0; j <= K; ++j) gw[j] = wn[j];
+    const int64_t nx = nn + step;
+    fetch(nx, it + 1 < sh.iters && lane_ok && nx < sh.n);
+    if (ok) {
+      const int m = knot_span(t, nk, xv);
+      float acc = 0.0f;
+      if (m >= 0) {
+        float d[K + 1];
+        span_window<K, 1, float>(t, nk, m, xv, d);
+#pragma unroll
+        for (int j = 0; j <= K; ++j) {
+          const int r = m - K + j;
+          acc += (r >= 0 && r < R ? gw[j] : 0.0f) * d[j];
+        }
+      }
+      if (es != nullptr) acc += gb * silu_grad_of<float>(xv);
       gx[nn * sh.I + col] = acc;
     }
   }
@@ -879,8 +930,8 @@ int launch_basis_grad_compact(const float* x, const float* grid, const float* ew
   dim3 grid_dim((unsigned)ceil_div(I, sh.fb), (unsigned)by);
   const size_t smem = sizeof(float) * (size_t)round_up((int64_t)sh.fb * nk, 4);
 #define KAN_BGC(KK)                                                                           \
-  hipLaunchKernelGGL((basis_grad_window_kernel<KK, float, 1, true>), grid_dim,                \
-                     dim3(64 * sh.waves), smem, st, x, grid, ew, (int64_t)0, es, gx, sh)
+  hipLaunchKernelGGL((basis_grad_compact_kernel<KK>), grid_dim, dim3(64 * sh.waves), smem, st, \
+                     x, grid, ew, es, gx, sh)
   if (k == 1) KAN_BGC(1);
   else if (k == 2) KAN_BGC(2);
   else KAN_BGC(3);
