@@ -104,12 +104,17 @@ def _check_edge_grads(got, ga, s, H, bw, W, dtype, D=None, which=(True, True, Tr
     assert n_amb <= max(3, 1e-4 * N * O * I)
 
 
-def test_edge_at_the_in_features_limit(C):
-    """in_features = 65535 and R = 72 (the widest augmented rows, k-steps 19 and
-    5 column tiles): the fp32 kernels' per-tile buffer offsets reach 15 rows x
-    I x R x 4 bytes = 283 MB, and the last feature's rows end at the end of H.
-    Forward and backward against the oracle."""
-    N, I, O, R = 23, 65535, 2, 72
+@pytest.mark.parametrize("shape", [(23, 65535, 2, 72), (23, 65535, 5, 11), (70, 65532, 40, 14)])
+def test_edge_at_the_in_features_limit(C, shape):
+    """in_features at the limit.  R = 72 (the widest augmented rows, k-steps 19
+    and 5 column tiles): the fp32 kernels' per-tile buffer offsets reach 15
+    rows x I x R x 4 bytes = 283 MB, and the last feature's rows end at the
+    end of H.  O <= 64 with R + 1 <= 16 takes the kernels staged through LDS:
+    I = 65535 (scalar loads, a last group of 3 features; chunk offsets up to
+    22 rows x I x R x 4 bytes) and I = 65532 (16-byte loads, two chunks per
+    split with a ragged second one).  Forward and backward against the
+    oracle."""
+    N, I, O, R = shape
     print(f"edge at the limit {(N, I, O, R)}", flush=True)
     s, H, bw, W, ga = _edge_inputs(N, I, O, R, torch.float32, seed=11)
     a = C.edge_abs_mean(s.cuda(), H.cuda(), bw.cuda(), W.cuda())
