@@ -136,6 +136,24 @@ def test_edge_backward_partial_requests(C):
     assert dH is None and dbw is not None and dW is not None
 
 
+@pytest.mark.parametrize("shape", [(700, 8, 40, 11), (300, 7, 64, 11)])
+def test_edge_backward_partial_requests_fp32(C, shape):
+    """fp32 requests of some gradients only (narrow layers, whose full
+    request takes the backward staged through LDS with 16-byte or scalar
+    row stores; a one-sided request takes the input or the parameter
+    kernel): the requested gradients hold the oracle bar, the others are not
+    returned."""
+    N, I, O, R = shape
+    s, H, bw, W, ga = _edge_inputs(N, I, O, R, torch.float32, seed=I + O)
+    d = [t.cuda() for t in (s, H, bw, W, ga)]
+    for which in ((True, True, True, True), (True, False, False, False),
+                  (False, True, False, False), (True, True, False, False),
+                  (False, False, True, True), (True, False, False, True)):
+        got = C.edge_abs_mean_backward(d[4], d[0], d[1], d[2], d[3], *which)
+        assert all((g is None) == (not w) for g, w in zip(got, which)), which
+        _check_edge_grads(got, ga, s, H, bw, W, torch.float32, which=which)
+
+
 @pytest.mark.parametrize("dtype", [torch.float64, torch.float32])
 def test_forward_with_regularization_fused_matches_dense(C, dtype):
     from torchsplinekan_amd import KAN
