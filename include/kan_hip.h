@@ -74,6 +74,23 @@ int kan_hip_basis_grad(int dtype, const void* x, const void* grid, const void* g
                        void* grad_x, int64_t n, int64_t in_features, int64_t grid_size,
                        int64_t spline_order, void* stream);
 
+/* basis[n, I, R] and silu[n, I] = x * sigmoid(x) in one pass over x: the two
+ * operands that forward_with_regularization's native path takes from
+ * base_activation (SiLU) and the native basis separately
+ * (spline_kan/kan_linear.py:380-381; the native path requires SiLU,
+ * kan_linear.py:213). */
+int kan_hip_basis_silu(int dtype, const void* x, const void* grid, void* basis, void* silu,
+                       int64_t n, int64_t in_features, int64_t grid_size, int64_t spline_order,
+                       void* stream);
+
+/* grad_x[n, i] = sum_r grad_basis[n, i, r] * dB_r/dx(x[n, i])
+ *              + grad_silu[n, i] * silu'(x[n, i]): the gradients that autograd
+ * takes through the basis and SiLU of those call sites and adds, in one
+ * pass. */
+int kan_hip_basis_silu_grad(int dtype, const void* x, const void* grid, const void* grad_basis,
+                            const void* grad_silu, void* grad_x, int64_t n, int64_t in_features,
+                            int64_t grid_size, int64_t spline_order, void* stream);
+
 /* out[n, i, r] = d^order B_r / dx^order at x[n, i] (order >= 0; order 0 is the
  * basis itself, order > spline_order gives zeros), with the span, boundary
  * and zero-denominator conventions of kan_hip_basis.  Replaces the

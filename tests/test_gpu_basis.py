@@ -165,3 +165,31 @@ def test_large_grid_paths_fp32(C, I, G, k):
         Dq = C.basis_deriv(x.cuda(), grid.cuda(), k, q).cpu().double().numpy()
         rq = ko.basis_derivative_n(x64, g64, k, q)
         assert normwise(Dq, rq) < 1e-5, q
+
+
+@pytest.mark.parametrize("dtype,tol", [(torch.float64, 1e-12), (torch.float32, 1e-5)])
+@pytest.mark.parametrize("G,k,kind", [(5, 3, "uniform"), (17, 2, "nonuniform"), (30, 3, "repeated"),
+                                      (4, 1, "uniform")])
+def test_basis_silu_and_grad_match_oracle(C, dtype, tol, G, k, kind):
+    """kan_hip_basis_silu: the basis equals kan_hip_basis element for element
+    and silu(x) holds the bar against the oracle; kan_hip_basis_silu_grad
+    equals kan_hip_basis_grad plus gs * silu'(x), against the oracle's
+    basis_derivative and silu_grad (R = 30 takes the window-record kernels;
+    x up to 1.2 outside the grid)."""
+    I, N = 37, 700
+    grid = make_grid(I, G, k, kind, seed=G).to(dtype)
+    g = torch.Generator().manual_seed(G + k)
+    x = ((torch.rand(N, I, generator=g, dtype=torch.float64) * 2.4 - 1.2)).to(dtype)
+    gH = torch.randn(N, I, G + k, generator=g, dtype=torch.float64).to(dtype)
+    gs = torch.randn(N, I, generator=g, dtype=torch.float64).to(dtype)
+    xd, gd = x.cuda(), grid.cuda()
+    s, H = C.basis_silu(xd, gd, k)
+    assert torch.equal(H, C.basis(xd, gd, k))
+    assert normwise(np64(s), ko.silu(np64(x))) < tol
+    gx = C.basis_silu_grad(xd, gd, k, gH.cuda(), gs.cuda())
+    dB = ko.basis_derivative(np64(x), np64(grid), k)
+    ref = np.einsum("nir,nir->ni", np64(gH), dB) + np64(gs) * ko.silu_grad(np64(x))
+    assert normwise(np64(gx), ref) < tol
+    # the spline part alone is kan_hip_basis_grad's
+    gx0 = C.basis_silu_grad(xd, gd, k, gH.cuda(), torch.zeros_like(gs).cuda())
+    assert torch.equal(gx0, C.basis_grad(xd, gd, k, gH.cuda()))

@@ -397,6 +397,42 @@ def basis_grad(x, grid, spline_order: int, grad_basis) -> torch.Tensor:
     return gx
 
 
+def basis_silu(x, grid, spline_order: int) -> Tuple[torch.Tensor, torch.Tensor]:
+    """(silu(x) [B, I], basis H [B, I, R]) from one pass over x (device)."""
+    G = _check_basis_args(x, grid, spline_order)
+    x, grid = x.contiguous(), grid.contiguous()
+    B, I = x.shape
+    H = torch.empty(B, I, G + spline_order, dtype=x.dtype, device=x.device)
+    s = torch.empty(B, I, dtype=x.dtype, device=x.device)
+    if B == 0:
+        return s, H
+    with torch.cuda.device(x.device):
+        check(LIB.kan_hip_basis_silu(dtype_code(x.dtype), ptr(x), ptr(grid), ptr(H), ptr(s), B, I,
+                                     G, spline_order, stream_of(x.device)))
+    return s, H
+
+
+def basis_silu_grad(x, grid, spline_order: int, grad_basis, grad_silu) -> torch.Tensor:
+    """gx = sum_r grad_basis dB_r/dx + grad_silu silu'(x) in one pass (device)."""
+    G = _check_basis_args(x, grid, spline_order)
+    B, I = x.shape
+    R = G + spline_order
+    _req(grad_basis.dim() == 3 and tuple(grad_basis.shape) == (B, I, R),
+         "kan_basis_silu_grad: gH must be [B, I, G+k]")
+    _req(tuple(grad_silu.shape) == (B, I), "kan_basis_silu_grad: gs must be [B, I]")
+    x, grid = x.contiguous(), grid.contiguous()
+    gH = grad_basis.contiguous().to(x.dtype)
+    gs = grad_silu.contiguous().to(x.dtype)
+    gx = torch.empty(B, I, dtype=x.dtype, device=x.device)
+    if B == 0:
+        return gx
+    with torch.cuda.device(x.device):
+        check(LIB.kan_hip_basis_silu_grad(dtype_code(x.dtype), ptr(x), ptr(grid), ptr(gH),
+                                          ptr(gs), ptr(gx), B, I, G, spline_order,
+                                          stream_of(x.device)))
+    return gx
+
+
 def basis_deriv(x, grid, spline_order: int, order: int) -> torch.Tensor:
     """d^order B / dx^order [B, I, R] (device; order 0 = basis, order > k = 0)."""
     G = _check_basis_args(x, grid, spline_order)

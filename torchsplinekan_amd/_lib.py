@@ -40,6 +40,9 @@ SIGNATURES = {
     "kan_hip_get_basis_impl": (_i64, []),
     "kan_hip_basis": (_int, [_int, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp]),
     "kan_hip_basis_grad": (_int, [_int, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp]),
+    "kan_hip_basis_silu": (_int, [_int, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp]),
+    "kan_hip_basis_silu_grad": (_int, [_int, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64,
+                                       _vp]),
     "kan_hip_edge_abs_mean_double_backward_workspace": (_int, [_int, _i64, _i64, _i64, _i64,
                                                                 ctypes.POINTER(_sz)]),
     "kan_hip_edge_abs_mean_double_backward": (_int, [_int] + [_vp] * 15 + [_sz, _i64, _i64, _i64,

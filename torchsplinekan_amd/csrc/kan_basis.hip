@@ -90,6 +90,7 @@ struct BasisShape {
   int iters;  // wave steps per block
   int waves;  // waves per block
   int vec;    // 16-byte vector path for the staged rows (alignment holds)
+  int64_t ld_aux;  // row stride of silu(x) (basis) or of its gradient (basis_grad)
 };
 
 // 16-byte vector of T.
@@ -282,7 +283,7 @@ __global__ __launch_bounds__(kBasisThreads) void basis_kernel(
         for (int r = 0; r < R; ++r) row[r] = T(0);
       }
     }
-    if (silu_out != nullptr && ok) silu_out[nn * ld + i0 + fi] = silu_of<T>(xv);
+    if (silu_out != nullptr && ok) silu_out[nn * sh.ld_aux + i0 + fi] = silu_of<T>(xv);
     wave_sync();
     for (int s = 0; s < sh.subs; ++s) {
       const int64_t ns = nb + s;
@@ -334,7 +335,7 @@ __global__ __launch_bounds__(kBasisThreads) void basis_grad_kernel(
     const int64_t nn = nbase + sub;
     const bool ok = lane_ok && nn < sh.n;
     const T xv = ok ? x[nn * sh.I + i0 + fi] : T(0);
-    const T gb = (ok && gbase != nullptr) ? gbase[nn * ld + i0 + fi] : T(0);
+    const T gb = (ok && gbase != nullptr) ? gbase[nn * sh.ld_aux + i0 + fi] : T(0);
     __syncthreads();
     if (ok) {
       T acc = T(0);
@@ -618,7 +619,7 @@ __global__ __launch_bounds__(kBasisThreads) void basis_grad_pf_kernel(
     }
     if (rem > 0) tail = base[segv * kV + (lane < rem ? lane : 0)];
     xn = x[nc * sh.I + i0 + fi];
-    gbn = gbase != nullptr ? gbase[nc * ld + i0 + fi] : T(0);
+    gbn = gbase != nullptr ? gbase[nc * sh.ld_aux + i0 + fi] : T(0);
   };
   issue(nn);
   __syncthreads();  // knot rows staged
@@ -688,7 +689,7 @@ __global__ __launch_bounds__(kBasisThreads) void basis_grad_window_kernel(
       const int r = m - K + j;
       gw[j] = (m >= 0 && r >= 0 && r < R) ? grow[r] : T(0);
     }
-    const T gb = (ok && gbase != nullptr) ? gbase[nn * ld + col] : T(0);
+    const T gb = (ok && gbase != nullptr) ? gbase[nn * sh.ld_aux + col] : T(0);
     const int64_t nx = nn + step;
     xn = (it + 1 < sh.iters && lane_ok && nx < sh.n) ? x[nx * sh.I + col] : T(0);
     if (ok) {
@@ -789,6 +790,7 @@ BasisShape make_shape(int64_t n, int64_t I, int G, int R, size_t elem, int64_t l
   sh.n = n;
   sh.I = (int)I;
   sh.G = G;
+  sh.ld_aux = ld;
   sh.fb = (int)(I < 64 ? I : 64);
   sh.subs = 64 / sh.fb;
   sh.waves = 4;
@@ -836,12 +838,13 @@ inline int gs_blocks(int64_t total) {
 
 template <typename T>
 int launch_basis(const T* x, const T* grid, T* out, int64_t ld_out, T* silu_out, int64_t n,
-                 int64_t I, int G, int k, int impl, hipStream_t st) {
+                 int64_t I, int G, int k, int impl, hipStream_t st, int64_t ld_silu) {
   if (n == 0 || I == 0) return KAN_OK;
   const int R = G + k, nk = G + 2 * k + 1;
   const bool rec = impl == 1 && R >= kWindowRecordMinR;
   int64_t by = 0;
   BasisShape sh = make_shape(n, I, G, R, sizeof(T), ld_out, out, &by, !rec);
+  if (ld_silu >= 0) sh.ld_aux = ld_silu;
   if (by > 2147483647LL) return set_error(KAN_ERR_LIMIT, "basis: too many samples (%lld)", (long long)n);
   dim3 grid_dim((unsigned)ceil_div(I, sh.fb), (unsigned)by);
   const size_t smem = rec ? basis_window_smem<T>(sh, nk, k) : basis_smem<T>(sh, nk, R);
@@ -872,11 +875,13 @@ int launch_basis(const T* x, const T* grid, T* out, int64_t ld_out, T* silu_out,
 // false (nothing launched) otherwise.
 template <typename T, int DER>
 bool launch_grad_pf(const T* x, const T* grid, const T* gH, int64_t ld_g, const T* gbase, T* gx,
-                    int64_t n, int64_t I, int G, int k, hipStream_t st, int* rc) {
+                    int64_t n, int64_t I, int G, int k, hipStream_t st, int* rc,
+                    int64_t ld_base = -1) {
   if (k < DER) return false;
   const int R = G + k, nk = G + 2 * k + 1;
   int64_t by = 0;
   BasisShape sh = make_shape(n, I, G, R, sizeof(T), ld_g, gH, &by);
+  if (ld_base >= 0) sh.ld_aux = ld_base;
   const int pv = grad_pf_vectors<T>(sh, R);
   if (pv == 0) return false;
   // two steps per block: more blocks in flight, each still overlapping one load
@@ -941,7 +946,8 @@ int launch_basis_grad_compact(const float* x, const float* grid, const float* ew
 
 template <typename T>
 int launch_basis_grad(const T* x, const T* grid, const T* gH, int64_t ld_g, const T* gbase,
-                      T* gx, int64_t n, int64_t I, int G, int k, int impl, hipStream_t st) {
+                      T* gx, int64_t n, int64_t I, int G, int k, int impl, hipStream_t st,
+                      int64_t ld_base) {
   if (n == 0 || I == 0) return KAN_OK;
   const int R = G + k, nk = G + 2 * k + 1;
   // algorithmic bytes: read x and the R gradient values (+ base), write gx
@@ -951,6 +957,7 @@ int launch_basis_grad(const T* x, const T* grid, const T* gH, int64_t ld_g, cons
   if (impl == 1 && R >= kWindowRecordMinR) {
     int64_t by = 0;
     BasisShape sh = make_shape(n, I, G, R, sizeof(T), ld_g, gH, &by, false);
+    if (ld_base >= 0) sh.ld_aux = ld_base;
     if (by > 2147483647LL) return set_error(KAN_ERR_LIMIT, "basis_grad: too many samples");
     dim3 grid_dim((unsigned)ceil_div(I, sh.fb), (unsigned)by);
     const size_t smem = sizeof(T) * (size_t)round_up((int64_t)sh.fb * nk, 4);
@@ -963,10 +970,12 @@ int launch_basis_grad(const T* x, const T* grid, const T* gH, int64_t ld_g, cons
 #undef KAN_BGW
     return check_launch("basis_grad");
   }
-  if (impl == 1 && launch_grad_pf<T, 1>(x, grid, gH, ld_g, gbase, gx, n, I, G, k, st, &rc))
+  if (impl == 1 && launch_grad_pf<T, 1>(x, grid, gH, ld_g, gbase, gx, n, I, G, k, st, &rc,
+                                        ld_base))
     return rc;
   int64_t by = 0;
   BasisShape sh = make_shape(n, I, G, R, sizeof(T), ld_g, gH, &by);
+  if (ld_base >= 0) sh.ld_aux = ld_base;
   if (by > 2147483647LL) return set_error(KAN_ERR_LIMIT, "basis_grad: too many samples");
   dim3 grid_dim((unsigned)ceil_div(I, sh.fb), (unsigned)by);
   const size_t smem = basis_smem<T>(sh, nk, R);
@@ -1159,9 +1168,9 @@ int launch_param_grads(const T* part, int splits, int64_t split_stride, int64_t 
 
 #define KAN_INST(T)                                                                          \
   template int launch_basis<T>(const T*, const T*, T*, int64_t, T*, int64_t, int64_t, int, int, \
-                               int, hipStream_t);                                            \
+                               int, hipStream_t, int64_t);                                   \
   template int launch_basis_grad<T>(const T*, const T*, const T*, int64_t, const T*, T*,       \
-                                    int64_t, int64_t, int, int, int, hipStream_t);           \
+                                    int64_t, int64_t, int, int, int, hipStream_t, int64_t);  \
   template int launch_pack_basis<T>(const T*, const T*, T*, int64_t, int64_t, int64_t,        \
                                     int64_t, bool, hipStream_t);                             \
   template int launch_build_waug<T>(const T*, const T*, const T*, T*, int64_t, int64_t,       \

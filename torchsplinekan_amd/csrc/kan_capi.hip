@@ -615,6 +615,50 @@ int kan_hip_basis_grad(int dtype, const void* x, const void* grid, const void* g
                                    static_cast<double*>(gx), n, I, (int)G, (int)k, 1, st);
 }
 
+int kan_hip_basis_silu(int dtype, const void* x, const void* grid, void* basis, void* silu,
+                       int64_t n, int64_t I, int64_t G, int64_t k, void* stream) {
+  KAN_TRY(check_dtype(dtype, "kan_basis_silu"));
+  KAN_TRY(check_layer("kan_basis_silu", n, I, 0, G, k));
+  if (n == 0 || I == 0) return KAN_OK;
+  KAN_TRY(need_ptr(x, "kan_basis_silu", "x"));
+  KAN_TRY(need_ptr(grid, "kan_basis_silu", "grid"));
+  KAN_TRY(need_ptr(basis, "kan_basis_silu", "basis"));
+  KAN_TRY(need_ptr(silu, "kan_basis_silu", "silu"));
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int64_t R = G + k;
+  if (dtype == KAN_DTYPE_F32)
+    return launch_basis<float>(static_cast<const float*>(x), static_cast<const float*>(grid),
+                               static_cast<float*>(basis), I * R, static_cast<float*>(silu), n, I,
+                               (int)G, (int)k, g_basis_impl.load(), st, I);
+  return launch_basis<double>(static_cast<const double*>(x), static_cast<const double*>(grid),
+                              static_cast<double*>(basis), I * R, static_cast<double*>(silu), n, I,
+                              (int)G, (int)k, g_basis_impl.load(), st, I);
+}
+
+int kan_hip_basis_silu_grad(int dtype, const void* x, const void* grid, const void* gH,
+                            const void* gs, void* gx, int64_t n, int64_t I, int64_t G, int64_t k,
+                            void* stream) {
+  KAN_TRY(check_dtype(dtype, "kan_basis_silu_grad"));
+  KAN_TRY(check_layer("kan_basis_silu_grad", n, I, 0, G, k));
+  if (n == 0 || I == 0) return KAN_OK;
+  KAN_TRY(need_ptr(x, "kan_basis_silu_grad", "x"));
+  KAN_TRY(need_ptr(grid, "kan_basis_silu_grad", "grid"));
+  KAN_TRY(need_ptr(gH, "kan_basis_silu_grad", "grad_basis"));
+  KAN_TRY(need_ptr(gs, "kan_basis_silu_grad", "grad_silu"));
+  KAN_TRY(need_ptr(gx, "kan_basis_silu_grad", "grad_x"));
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int64_t R = G + k;
+  if (dtype == KAN_DTYPE_F32)
+    return launch_basis_grad<float>(static_cast<const float*>(x), static_cast<const float*>(grid),
+                                    static_cast<const float*>(gH), I * R,
+                                    static_cast<const float*>(gs), static_cast<float*>(gx), n, I,
+                                    (int)G, (int)k, 1, st, I);
+  return launch_basis_grad<double>(static_cast<const double*>(x), static_cast<const double*>(grid),
+                                   static_cast<const double*>(gH), I * R,
+                                   static_cast<const double*>(gs), static_cast<double*>(gx), n, I,
+                                   (int)G, (int)k, 1, st, I);
+}
+
 int64_t kan_hip_aug_width(int64_t I, int64_t G, int64_t k, int has_base) {
   if (I < 0 || G < 1 || k < 1 || k > 3) return -1;
   return aug_width(I, G + k, has_base != 0);

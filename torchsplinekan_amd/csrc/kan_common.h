@@ -124,11 +124,12 @@ int launch_edge_reg_backward(const T* g, const T* a, int64_t n, double mu1, doub
 
 template <typename T>
 int launch_basis(const T* x, const T* grid, T* out, int64_t ld_out, T* silu_out, int64_t n,
-                 int64_t I, int G, int k, int impl, hipStream_t st);
+                 int64_t I, int G, int k, int impl, hipStream_t st, int64_t ld_silu = -1);
 
 template <typename T>
 int launch_basis_grad(const T* x, const T* grid, const T* gH, int64_t ld_g, const T* gbase,
-                      T* gx, int64_t n, int64_t I, int G, int k, int impl, hipStream_t st);
+                      T* gx, int64_t n, int64_t I, int G, int k, int impl, hipStream_t st,
+                      int64_t ld_base = -1);
 // The same from the compact input-side product (launch_gemm_ecomp): window
 // values ew [n, I, k+1] (16-byte aligned) and base columns es [n, I] or null.
 int launch_basis_grad_compact(const float* x, const float* grid, const float* ew,

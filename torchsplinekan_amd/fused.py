@@ -52,6 +52,37 @@ class NativeBasis(torch.autograd.Function):
         return _C.basis_grad(x.contiguous(), grid, ctx.k, gH.contiguous()), None, None
 
 
+class NativeBasisSilu(torch.autograd.Function):
+    """(s, H) = (silu(x), basis(x)) from one device pass over x, the two
+    operands forward_with_regularization's native path takes from
+    base_activation and the native basis separately
+    (spline_kan/kan_linear.py:380-381).  The backward adds both inputs'
+    contributions, sum_r gH dB_r/dx + gs silu'(x), in one pass as well;
+    recorded backwards (create_graph) use the differentiable pieces."""
+
+    @staticmethod
+    def forward(ctx, x, grid, k: int):
+        ctx.k = k
+        ctx.save_for_backward(x, grid)
+        return _C.basis_silu(x, grid, k)
+
+    @staticmethod
+    def backward(ctx, gs, gH):
+        x, grid = ctx.saved_tensors
+        if not ctx.needs_input_grad[0]:
+            return None, None, None
+        B, I = x.shape
+        if gs is None:
+            gs = x.new_zeros(B, I)
+        if gH is None:
+            gH = x.new_zeros(B, I, grid.shape[1] - ctx.k - 1)
+        if torch.is_grad_enabled():
+            sg = torch.sigmoid(x)
+            gx = _C.DerivContract.apply(x, grid, gH, ctx.k, 1) + gs * (sg * (1 + x * (1 - sg)))
+            return gx, None, None
+        return _C.basis_silu_grad(x, grid, ctx.k, gH, gs), None, None
+
+
 class EdgeAbsMean(torch.autograd.Function):
     """a[o,i] = mean_n |s*bw + <H, W>| without materialising [N, O, I]."""
 
@@ -204,6 +235,11 @@ def edge_linear(s: torch.Tensor, H: torch.Tensor, bw: torch.Tensor, W: torch.Ten
 
 def native_basis(x: torch.Tensor, grid: torch.Tensor, k: int) -> torch.Tensor:
     return NativeBasis.apply(x, grid, k)
+
+
+def native_basis_silu(x: torch.Tensor, grid: torch.Tensor, k: int):
+    """(silu(x), basis(x)) of a device input in one pass (NativeBasisSilu)."""
+    return NativeBasisSilu.apply(x, grid, k)
 
 
 def edge_abs_mean(s: Optional[torch.Tensor], H: torch.Tensor, bw: Optional[torch.Tensor],

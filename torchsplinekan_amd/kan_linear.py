@@ -333,8 +333,12 @@ class KANLinear(nn.Module):
         lead = x.shape[:-1]
         xf = x.reshape(-1, self.in_features)
         impl = self._resolve_reg_impl(reg_impl, xf)
-        s = self._ref.base_activation(xf)
-        H = self._basis(xf, impl)
+        if impl == "fused" and self._native_fuses_base and xf.shape[0] > 0:
+            # SiLU and the basis from one pass over x (gradients likewise)
+            s, H = _fused.native_basis_silu(xf, self.grid, self.spline_order)
+        else:
+            s = self._ref.base_activation(xf)
+            H = self._basis(xf, impl)
         W = self._ref.effective_spline_weight()
         B, R = xf.shape[0], self.grid_size + self.spline_order
         a = None
