@@ -1241,16 +1241,17 @@ __global__ __launch_bounds__(kEdgeMfThreads) void edge_bwd_mfma_kernel(
 // into dWc[o, c] += sum_n g Hc and dHc^T[c, n] += sum_o Wc g), with the
 // block layout of edge_fwd_stage_kernel: kStF features (wave w: feature
 // i0 + w, every output) and chunks of kStRows samples.  Per chunk the block
-// stages the Hc rows and (with the layer-output gradient) the D rows
-// [kStRows, O] in LDS, the waves compute, and each writes its dHc values into
-// an LDS copy of the chunk's row layout, which the block then stores to ds
-// and dH with consecutive lanes on consecutive addresses.  Two barriers per
-// chunk.
-constexpr int kStDS = 68;  // LDS row stride of the staged D rows (O <= 64; 4 * odd)
-constexpr int kStDPT = kStRows * 64 / kEdgeMfThreads;  // D floats per thread per chunk
+// stages the Hc rows in LDS, the waves compute, and each writes its dHc
+// values into an LDS copy of the chunk's row layout, which the block then
+// stores to ds and dH with consecutive lanes on consecutive addresses.  Two
+// barriers per chunk.  The layer-output gradient D is read per sample tile
+// straight from global memory in the accumulator layout of g (4 rows of 16
+// consecutive columns per load), so the block needs no LDS for it: with
+// 16-byte staging (VEC) three blocks fit a CU (46 KB of LDS, at most 168
+// VGPRs per lane).
 
 template <int KS, int OT, bool HASD, bool VEC>
-__global__ __launch_bounds__(kEdgeMfThreads) void edge_bwd_stage_kernel(
+__global__ __launch_bounds__(kEdgeMfThreads, VEC ? 3 : 1) void edge_bwd_stage_kernel(
     const float* __restrict__ ga, const float* __restrict__ D, const float* __restrict__ s,
     const float* __restrict__ H, const float* __restrict__ bw, const float* __restrict__ W,
     float* __restrict__ ds, float* __restrict__ dH, float* __restrict__ dbw,
@@ -1259,7 +1260,6 @@ __global__ __launch_bounds__(kEdgeMfThreads) void edge_bwd_stage_kernel(
   constexpr int TS = 20;  // transposed g tile row stride
   __shared__ __align__(16) float hs[SG::kBuf];
   __shared__ __align__(16) float os[SG::kBuf];
-  __shared__ __align__(16) float dsm[HASD ? kStRows * kStDS : 4];
   __shared__ __align__(16) float trans[4 * OT * 16 * TS];
   const int groups = (g.I + kStF - 1) / kStF;
   const int64_t bid = xcd_remap((int)blockIdx.x, (int)gridDim.x);
@@ -1275,12 +1275,9 @@ __global__ __launch_bounds__(kEdgeMfThreads) void edge_bwd_stage_kernel(
   const int64_t IR = (int64_t)I * R;
   const float inv_n = 1.0f / (float)g.n;
   const float inv_fr = 1.0f / (float)(VEC ? R : nf * R), inv_nf = 1.0f / (float)nf;
-  const float inv_o = 1.0f / (float)O;
 
-  // the zero slot, features past nf and D columns past O stay zero
+  // the zero slot and features past nf stay zero
   for (int e = t_; e < SG::kBuf; e += kEdgeMfThreads) hs[e] = 0.0f;
-  if constexpr (HASD)
-    for (int e = t_; e < kStRows * kStDS; e += kEdgeMfThreads) dsm[e] = 0.0f;
 
   // LDS column of augmented column c of this wave's feature
   auto colof = [&](int c) { return c == 0 ? 4 * R + wave : (c <= R ? wave * R + c - 1 : 4 * R + 4); };
@@ -1315,41 +1312,21 @@ __global__ __launch_bounds__(kEdgeMfThreads) void edge_bwd_stage_kernel(
   const int64_t nb = (int64_t)split * g.per_split;
   const int64_t ne = min(g.n, nb + g.per_split);
   StageLoader<KS, VEC> ld;
-  float dreg[HASD ? kStDPT : 1];
-  auto load_d = [&](int64_t n0) {
-    if constexpr (HASD) {
-      const int rows = (int)min((int64_t)kStRows, ne - n0);
-      const __amdgpu_buffer_rsrc_t rd = __builtin_amdgcn_make_buffer_rsrc(
-          const_cast<float*>(D + n0 * O), (short)0, rows * O * 4, kBufWord3);
+  // dL/dy offsets in the accumulator layout of g: D[n0 + 16 tt + 4q + v, 16t + r]
+  uint32_t doff[HASD ? OT : 1][4];
+  if constexpr (HASD) {
 #pragma unroll
-      for (int j = 0; j < kStDPT; ++j) {
-        const int e = t_ + kEdgeMfThreads * j;
-        dreg[j] = buf_ld(rd, e < kStRows * O ? (uint32_t)(e * 4) : kBufOob);
-      }
-    }
-  };
-  if (nb < ne) {
-    ld.load(s, H, nb, ne, I, R, i0, nf, inv_fr, inv_nf);
-    load_d(nb);
+    for (int t = 0; t < OT; ++t)
+#pragma unroll
+      for (int v = 0; v < 4; ++v)
+        doff[t][v] = 16 * t + r < O ? (uint32_t)(((4 * q + v) * O + 16 * t + r) * 4) : kBufOob;
   }
+  if (nb < ne) ld.load(s, H, nb, ne, I, R, i0, nf, inv_fr, inv_nf);
   float* tb = trans + wave * (OT * 16 * TS);
   __syncthreads();  // (the zero fills)
   for (int64_t n0 = nb; n0 < ne; n0 += kStRows) {
     ld.store(hs, R, nf, inv_fr, inv_nf);
-    if constexpr (HASD) {
-#pragma unroll
-      for (int j = 0; j < kStDPT; ++j) {
-        const int e = t_ + kEdgeMfThreads * j;
-        if (e < kStRows * O) {
-          const int row = small_div_f(e, inv_o);
-          dsm[row * kStDS + (e - row * O)] = dreg[j];
-        }
-      }
-    }
-    if (n0 + kStRows < ne) {
-      ld.load(s, H, n0 + kStRows, ne, I, R, i0, nf, inv_fr, inv_nf);
-      load_d(n0 + kStRows);
-    }
+    if (n0 + kStRows < ne) ld.load(s, H, n0 + kStRows, ne, I, R, i0, nf, inv_fr, inv_nf);
     __syncthreads();
     if (active) {
 #pragma unroll 1
@@ -1362,10 +1339,12 @@ __global__ __launch_bounds__(kEdgeMfThreads) void edge_bwd_stage_kernel(
         for (int v = 0; v < 4; ++v) hb[v] = hs[(16 * tt + 4 * q + v) * SG::kS + colr];
         float dq[HASD ? OT : 1][4];
         if constexpr (HASD) {
+          const int64_t nt = n0 + 16 * tt;
+          const __amdgpu_buffer_rsrc_t rd = tile_rsrc(D + nt * O, ne - nt, O);
 #pragma unroll
           for (int t = 0; t < OT; ++t)
 #pragma unroll
-            for (int v = 0; v < 4; ++v) dq[t][v] = dsm[(16 * tt + 4 * q + v) * kStDS + 16 * t + r];
+            for (int v = 0; v < 4; ++v) dq[t][v] = buf_ld(rd, doff[t][v]);
         }
         f32x4 acc[OT];
 #pragma unroll
