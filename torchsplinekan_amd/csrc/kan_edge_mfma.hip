@@ -72,14 +72,6 @@ __device__ __forceinline__ float g_sign(float g, float v) {
   return v != 0.0f ? __uint_as_float(bits) : 0.0f;
 }
 
-// augmented sample value Hc[n, c]
-__device__ __forceinline__ float hc_val(const float* __restrict__ s, const float* __restrict__ H,
-                                        int64_t n, int I, int i, int R, int c) {
-  const int64_t f = n * I + i;
-  if (c == 0) return s != nullptr ? s[f] : 0.0f;
-  return H[f * R + (c - 1)];
-}
-
 // Buffer-resource loads of the augmented sample values Hc[n, c] of feature
 // i, one tile of 16 rows at a time (n0 wave-uniform): H rows lie I*R floats
 // apart, s rows I floats apart.  A tile's resource covers only its rows below
@@ -263,7 +255,6 @@ __global__ __launch_bounds__(kEdgeMfThreads) void edge_fwd_mfma_kernel(
   const int q = lane >> 4, r = lane & 15;
   const int obase = oc * Tl::kBlockOut + wo * kOT * 16;
   if (WS == 1 && obase >= g.O) return;  // (with WS > 1 every wave reaches the barrier)
-  const int R1 = g.R + 1;
 
   const PhiSlots<KS> ps(q, g.R);
   float w[kOT][KS];
@@ -1247,11 +1238,11 @@ __global__ __launch_bounds__(kEdgeMfThreads) void edge_bwd_mfma_kernel(
 // barriers per chunk.  The layer-output gradient D is read per sample tile
 // straight from global memory in the accumulator layout of g (4 rows of 16
 // consecutive columns per load), so the block needs no LDS for it: with
-// 16-byte staging (VEC) three blocks fit a CU (46 KB of LDS, at most 168
-// VGPRs per lane).
+// 16-byte staging (VEC) and R + 1 <= 12 three blocks fit a CU (46 KB of LDS,
+// at most 168 VGPRs per lane).
 
 template <int KS, int OT, bool HASD, bool VEC>
-__global__ __launch_bounds__(kEdgeMfThreads, VEC ? 3 : 1) void edge_bwd_stage_kernel(
+__global__ __launch_bounds__(kEdgeMfThreads, VEC && KS <= 3 ? 3 : 1) void edge_bwd_stage_kernel(
     const float* __restrict__ ga, const float* __restrict__ D, const float* __restrict__ s,
     const float* __restrict__ H, const float* __restrict__ bw, const float* __restrict__ W,
     float* __restrict__ ds, float* __restrict__ dH, float* __restrict__ dbw,
