@@ -192,10 +192,18 @@ def _view(t, trans):
 
 @pytest.mark.parametrize("dtype,tol", [(torch.float64, 1e-12), (torch.float32, 1e-5)])
 @pytest.mark.parametrize("M,K,N", [(5, 3, 7), (128, 16384, 1408), (300, 37, 19), (1, 10, 64),
-                                   (64, 10, 1), (7, 0, 5), (257, 4100, 33)])
+                                   (64, 10, 1), (7, 0, 5), (257, 4100, 33),
+                                   # thin products (an output side or K of at most 16)
+                                   (4096, 2304, 10), (10, 4096, 2304), (4096, 10, 2304),
+                                   (16, 777, 1001), (1003, 300, 16), (17, 300, 17),
+                                   (3, 5000, 1), (1, 4099, 5), (513, 16, 77), (2, 17, 3),
+                                   (4097, 1, 6)])
 def test_native_matmul_matches_torch(C, dtype, tol, M, K, N):
-    """kan_hip_matmul on all four transposition pairs, long-K (split) and
-    degenerate shapes, against the float64 product of the same operands."""
+    """kan_hip_matmul on all four transposition pairs, long-K (split),
+    degenerate and thin shapes (an output side or a contraction of at most 16,
+    as in a classifier's output layer, with ragged edges and split slices),
+    against the float64 product of the same operands; two calls agree bit for
+    bit."""
     print(f"matmul M={M} K={K} N={N} {dtype}", flush=True)
     g = torch.Generator().manual_seed(M + K + N)
     a = torch.randn(M, K, generator=g, dtype=torch.float64).to(dtype)
