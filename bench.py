@@ -409,9 +409,11 @@ def run_c2(args, dev, steps, warmup):
     line = _line("fwd+bwd samples/s, KAN([784,256,10]) G5 k3 N=4096", N, steps, warmup, wall,
                  "c2: KAN([784,256,10], G=5, k=3) fp32, N=%d, fwd + MSE + bwd (x without "
                  "grad)" % N,
-                 _mfma_roofline(kern, "contraction", "gemm_pipe_kernel (fp32 MFMA contraction; "
-                                "forward and parameter products of both layers, input product "
-                                "of the second)", *recorded_traffic("c2")), kern)
+                 _mfma_roofline(kern, "contraction", "contraction: gemm_pipe_kernel (fp32 MFMA; "
+                                "forward and parameter products of the first layer) and the "
+                                "thin-product kernels (thin_wide_cols/thin_wide_rows/"
+                                "thin_short_k: forward, parameter and input products of the "
+                                "10-wide output layer)", *recorded_traffic("c2")), kern)
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline_layers(
             [_layer_tensors(l) for l in net.layers], x, target, False, args.cpu_seconds, 1024,

@@ -1047,6 +1047,391 @@ int launch_ecomp_cfg(const GemmParams<float>& p, const DxParams& e, int k, hipSt
   return launch_cfg<C, true, true, -3>(p, 1, st, &e);
 }
 
+
+// ---------------------------------------------------------------------------
+// Thin products: an output side of at most kThinMax (a classifier's or a
+// PINN's output layer, and that layer's parameter product) or a contraction
+// of at most kThinMax (the input-side product of such a layer).  MFMA tiles
+// would be mostly padding there, and the product is bound by the traffic of
+// its wide operand (with a short K, of C).  These kernels stream that operand
+// with 16-byte loads and accumulate with FMAs in a fixed order (k ascending
+// within a lane, then fixed partial-sum orders), so results are
+// deterministic.  Element (m, n) of a layout is addressed through strides:
+// A(m, k) = A[m * as_m + k * as_k], B(k, n) = B[k * bs_k + n * bs_n].
+constexpr int kThinMax = 16;
+constexpr int kThinThreads = 256;
+constexpr int kThinChunk = 256;  // k rows (or k columns) of the thin operand staged at a time
+constexpr int kThinUnroll = 8;   // wide-operand loads in flight per lane
+constexpr int kThinRowChunk = 64;  // rows of A staged per wave (short contraction)
+
+template <typename T>
+struct ThinVec {
+  static constexpr int kW = 16 / sizeof(T);  // elements per 16-byte vector
+  typedef T type __attribute__((ext_vector_type(16 / sizeof(T))));
+};
+
+struct ThinStrides {
+  int64_t as_m, as_k, bs_k, bs_n;
+};
+inline ThinStrides thin_strides(int layout, int64_t lda, int64_t ldb) {
+  ThinStrides t;
+  const bool ta = layout == kLayoutTN || layout == kLayoutTT;
+  const bool tb = layout == kLayoutNT || layout == kLayoutTT;
+  t.as_m = ta ? 1 : lda;
+  t.as_k = ta ? lda : 1;
+  t.bs_k = tb ? 1 : ldb;
+  t.bs_n = tb ? ldb : 1;
+  return t;
+}
+
+// LDS of the wide-rows kernel: the staged thin rows, then the partial sums of
+// waves 1..3 (48 KB either way at P = 16)
+template <typename T, int P>
+struct ThinRowsLds {
+  static constexpr int kW = ThinVec<T>::kW;
+  static constexpr int kStage = kThinChunk * P;
+  static constexpr int kRed = 3 * 64 * kW * P;
+  static constexpr int kElems = kStage > kRed ? kStage : kRed;
+};
+
+// out(p, q) = sum_k X[k * ldx + q] * Y[k * ys_k + p * ys_p] over split s's k
+// range, for p < np (<= P) and q < nq, written to C[s * sstride + p * cp +
+// q * cq].  The wide operand X is contiguous along q.  A block's 4 waves take
+// the same 64 * W wide indices (W per lane); the split's k range goes in
+// chunks of kThinChunk rows whose thin values the block stages in LDS, and
+// wave w takes the w-th quarter of each chunk.  The waves' sums are added in
+// wave order through LDS.
+template <typename T, int P, bool VEC>
+__global__ __launch_bounds__(kThinThreads) void thin_wide_rows_kernel(
+    const T* __restrict__ X, int64_t ldx, const T* __restrict__ Y, int64_t ys_k, int64_t ys_p,
+    T* __restrict__ C, int64_t cp, int64_t cq, int64_t sstride, int np, int64_t nq, int64_t K,
+    int64_t kper) {
+  typedef ThinVec<T> TV;
+  typedef ThinRowsLds<T, P> L;
+  constexpr int W = TV::kW;
+  __shared__ __align__(16) T lds[L::kElems];
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int64_t q0 = (int64_t)blockIdx.x * (64 * W) + lane * W;
+  const int split = blockIdx.y;
+  const int64_t kb = (int64_t)split * kper, ke = min(K, kb + kper);
+  const bool whole_block = VEC && ((int64_t)blockIdx.x + 1) * (64 * W) <= nq;
+  T acc[W][P];
+#pragma unroll
+  for (int j = 0; j < W; ++j)
+#pragma unroll
+    for (int pp = 0; pp < P; ++pp) acc[j][pp] = T(0);
+  auto rows = [&](int64_t c0, int r0, int r1, auto whole_c) {
+    constexpr bool kWhole = decltype(whole_c)::value;
+    auto load_row = [&](int r, T (&x)[W]) {
+      const T* src = X + (c0 + r) * ldx + q0;
+      if constexpr (kWhole) {
+        const typename TV::type v = *reinterpret_cast<const typename TV::type*>(src);
+#pragma unroll
+        for (int j = 0; j < W; ++j) x[j] = v[j];
+      } else {
+#pragma unroll
+        for (int j = 0; j < W; ++j) x[j] = q0 + j < nq ? src[j] : T(0);
+      }
+    };
+    auto fma_row = [&](int r, const T (&x)[W]) {
+      const T* yr = lds + r * P;  // (the same address in every lane: a broadcast)
+#pragma unroll
+      for (int pp = 0; pp < P; ++pp) {
+        const T y = yr[pp];
+#pragma unroll
+        for (int j = 0; j < W; ++j) acc[j][pp] += x[j] * y;
+      }
+    };
+    const int rfull = r0 + (r1 - r0) / kThinUnroll * kThinUnroll;
+    for (int r = r0; r < rfull; r += kThinUnroll) {
+      T x[kThinUnroll][W];
+#pragma unroll
+      for (int u = 0; u < kThinUnroll; ++u) load_row(r + u, x[u]);
+      // (row by row: the thin values of one row at a time in registers)
+#pragma unroll
+      for (int u = 0; u < kThinUnroll; ++u) {
+        __builtin_amdgcn_sched_barrier(0);
+        fma_row(r + u, x[u]);
+      }
+    }
+    for (int r = rfull; r < r1; ++r) {
+      T x[W];
+      load_row(r, x);
+      fma_row(r, x);
+    }
+  };
+  for (int64_t c0 = kb; c0 < ke; c0 += kThinChunk) {
+    const int nr = (int)min((int64_t)kThinChunk, ke - c0);
+    __syncthreads();  // (the previous chunk's reads of the stage are done)
+    for (int e = threadIdx.x; e < nr * P; e += kThinThreads) {
+      const int r = e / P, pp = e - r * P;
+      lds[e] = pp < np ? Y[(c0 + r) * ys_k + pp * ys_p] : T(0);
+    }
+    __syncthreads();
+    const int quarter = (nr + 3) / 4;
+    const int r0 = min(nr, wave * quarter), r1 = min(nr, r0 + quarter);
+    if (whole_block) rows(c0, r0, r1, std::integral_constant<bool, VEC>());
+    else rows(c0, r0, r1, std::false_type());
+  }
+  __syncthreads();  // (the stage is reused for the partial sums)
+  if (wave > 0) {
+    T* dst = lds + (wave - 1) * (64 * W * P) + lane;
+#pragma unroll
+    for (int j = 0; j < W; ++j)
+#pragma unroll
+      for (int pp = 0; pp < P; ++pp) dst[(j * P + pp) * 64] = acc[j][pp];
+  }
+  __syncthreads();
+  if (wave != 0) return;
+  // (one row of P values at a time: the loads need few registers)
+#pragma unroll 1
+  for (int w = 0; w < 3; ++w) {
+    const T* src = lds + w * (64 * W * P) + lane;
+#pragma unroll
+    for (int j = 0; j < W; ++j) {
+      T v[P];
+#pragma unroll
+      for (int pp = 0; pp < P; ++pp) v[pp] = src[(j * P + pp) * 64];
+#pragma unroll
+      for (int pp = 0; pp < P; ++pp) acc[j][pp] += v[pp];
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+  T* out = C + (int64_t)split * sstride;
+#pragma unroll
+  for (int j = 0; j < W; ++j) {
+    if (q0 + j >= nq) continue;
+#pragma unroll
+    for (int pp = 0; pp < P; ++pp)
+      if (pp < np) out[pp * cp + (q0 + j) * cq] = acc[j][pp];
+  }
+}
+
+// out(p, q) = sum_k X[q * ldx + k] * Y[p * ys_p + k * ys_k] over split s's k
+// range: the wide operand X is contiguous along k.  A block takes 16 wide
+// indices (4 per wave, 16 lanes each) of one split; per chunk of kThinChunk
+// columns it stages the thin rows Y(0..P-1, chunk) in LDS, and each lane
+// covers W consecutive k per stripe of 16 lanes.  The 16 lanes' sums are added
+// by a fixed butterfly.
+template <typename T, int P, bool VEC>
+__global__ __launch_bounds__(kThinThreads) void thin_wide_cols_kernel(
+    const T* __restrict__ X, int64_t ldx, const T* __restrict__ Y, int64_t ys_k, int64_t ys_p,
+    T* __restrict__ C, int64_t cp, int64_t cq, int64_t sstride, int np, int64_t nq, int64_t K,
+    int64_t kper) {
+  typedef ThinVec<T> TV;
+  constexpr int W = TV::kW;
+  constexpr int kStripes = kThinChunk / (16 * W);  // per lane and chunk
+  __shared__ __align__(16) T ys[P * kThinChunk];
+  const int lane = threadIdx.x & 63, sub = lane & 15;
+  const int64_t q = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
+  const int split = blockIdx.y;
+  const int64_t kb = (int64_t)split * kper, ke = min(K, kb + kper);
+  const T* xr = X + min(q, nq - 1) * ldx;
+  T acc[P];
+#pragma unroll
+  for (int pp = 0; pp < P; ++pp) acc[pp] = T(0);
+  for (int64_t c0 = kb; c0 < ke; c0 += kThinChunk) {
+    const int nc = (int)min((int64_t)kThinChunk, ke - c0);
+    __syncthreads();  // (the previous chunk's reads of the stage are done)
+    for (int e = threadIdx.x; e < P * kThinChunk; e += kThinThreads) {
+      const int pp = e / kThinChunk, c = e - pp * kThinChunk;
+      ys[e] = (pp < np && c < nc) ? Y[pp * ys_p + (c0 + c) * ys_k] : T(0);
+    }
+    __syncthreads();
+    T x[kStripes][W];
+    const bool whole = VEC && nc == kThinChunk;  // (block-uniform)
+#pragma unroll
+    for (int t = 0; t < kStripes; ++t) {
+      const int c = (t * 16 + sub) * W;
+      if (whole) {
+        const typename TV::type v = *reinterpret_cast<const typename TV::type*>(xr + c0 + c);
+#pragma unroll
+        for (int j = 0; j < W; ++j) x[t][j] = v[j];
+      } else {
+#pragma unroll
+        for (int j = 0; j < W; ++j) x[t][j] = c + j < nc ? xr[c0 + c + j] : T(0);
+      }
+    }
+#pragma unroll
+    for (int t = 0; t < kStripes; ++t) {
+      const int c = (t * 16 + sub) * W;
+#pragma unroll
+      for (int pp = 0; pp < P; ++pp) {
+        const typename TV::type y = *reinterpret_cast<const typename TV::type*>(ys + pp * kThinChunk + c);
+#pragma unroll
+        for (int j = 0; j < W; ++j) acc[pp] += x[t][j] * y[j];
+      }
+    }
+  }
+#pragma unroll
+  for (int pp = 0; pp < P; ++pp) {
+#pragma unroll
+    for (int off = 8; off >= 1; off >>= 1) acc[pp] += __shfl_xor(acc[pp], off, 16);
+  }
+  if (q < nq && sub == 0) {
+    T* out = C + (int64_t)split * sstride + q * cq;
+#pragma unroll
+    for (int pp = 0; pp < P; ++pp)
+      if (pp < np) out[pp * cp] = acc[pp];
+  }
+}
+
+// C[m, n] = sum_{k < K} A(m, k) B(k, n) for K <= kThinMax: a block's waves
+// share 64 * W columns, whose B(0..K-1, ·) the block stages in LDS once and
+// each lane then keeps in registers (W columns); a wave walks its row range in
+// chunks of kThinRowChunk rows whose A values it stages in LDS.
+template <typename T, bool VEC>
+__global__ __launch_bounds__(kThinThreads) void thin_short_k_kernel(
+    const T* __restrict__ A, ThinStrides st, const T* __restrict__ B, T* __restrict__ C,
+    int64_t ldc, int64_t M, int64_t N, int K, int64_t rows_per_wave) {
+  typedef ThinVec<T> TV;
+  constexpr int W = TV::kW;
+  __shared__ T as[kThinThreads / 64][kThinRowChunk * kThinMax];
+  __shared__ T bs[kThinMax * 64 * W];
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int64_t nb = (int64_t)blockIdx.x * (64 * W), n0 = nb + lane * W;
+  const int64_t m0 = ((int64_t)blockIdx.y * (kThinThreads / 64) + wave) * rows_per_wave;
+  const int64_t m1 = min(M, m0 + rows_per_wave);
+  // B(k, nb + c) at bs[k * 64W + c], loaded with consecutive threads on
+  // consecutive addresses of whichever of k and n is contiguous in B
+  for (int e = threadIdx.x; e < kThinMax * 64 * W; e += kThinThreads) {
+    int k, c;
+    if (st.bs_k == 1) {
+      c = e / kThinMax;
+      k = e - c * kThinMax;
+    } else {
+      k = e / (64 * W);
+      c = e - k * (64 * W);
+    }
+    bs[k * (64 * W) + c] = (k < K && nb + c < N) ? B[k * st.bs_k + (nb + c) * st.bs_n] : T(0);
+  }
+  __syncthreads();
+  T b[kThinMax][W];
+#pragma unroll
+  for (int k = 0; k < kThinMax; ++k)
+#pragma unroll
+    for (int j = 0; j < W; ++j) b[k][j] = bs[k * (64 * W) + lane * W + j];
+  const bool whole = VEC && n0 + W <= N;
+  T* aw = as[wave];
+  for (int64_t mc = m0; mc < m1; mc += kThinRowChunk) {
+    const int nr = (int)min((int64_t)kThinRowChunk, m1 - mc);
+    // (wave-private stage: the wave's own loads and reads, in order)
+    for (int e = lane; e < nr * kThinMax; e += 64) {
+      const int r = e / kThinMax, k = e - r * kThinMax;
+      aw[e] = k < K ? A[(mc + r) * st.as_m + k * st.as_k] : T(0);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    for (int r = 0; r < nr; ++r) {
+      const T* ar = aw + r * kThinMax;  // (a broadcast read)
+      T acc[W];
+#pragma unroll
+      for (int j = 0; j < W; ++j) acc[j] = T(0);
+#pragma unroll
+      for (int k = 0; k < kThinMax; ++k) {
+        const T a = ar[k];
+#pragma unroll
+        for (int j = 0; j < W; ++j) acc[j] += a * b[k][j];
+      }
+      T* cr = C + (mc + r) * ldc + n0;
+      if (whole) {
+        typename TV::type v;
+#pragma unroll
+        for (int j = 0; j < W; ++j) v[j] = acc[j];
+        *reinterpret_cast<typename TV::type*>(cr) = v;
+      } else {
+#pragma unroll
+        for (int j = 0; j < W; ++j)
+          if (n0 + j < N) cr[j] = acc[j];
+      }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  }
+}
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+// Split count of a thin product (one side <= kThinMax, K > kThinMax): about
+// 1024 waves over the wide side's 256-wide groups, at least 256 k per split.
+int thin_splits(int64_t M, int64_t N, int64_t K) {
+  const int64_t groups = ceil_div(max(M, N), (int64_t)256);
+  int64_t s = ceil_div((int64_t)256, groups);
+  s = min(s, K / 256);
+  s = min(s, (int64_t)64);
+  return (int)max(s, (int64_t)1);
+}
+
+template <typename T, int P>
+int launch_thin_p(int layout, int64_t M, int64_t N, int64_t K, const T* A, int64_t lda,
+                  const T* B, int64_t ldb, T* C, int64_t ldc, int splits, int64_t sstride,
+                  hipStream_t st) {
+  constexpr int W = ThinVec<T>::kW;
+  const ThinStrides t = thin_strides(layout, lda, ldb);
+  const int64_t kper = ceil_div(K, (int64_t)splits);
+  // thin side p, wide side q: X(.., q) the wide operand, Y(p, k) the thin one
+  const bool thin_m = M <= N;
+  const T* X = thin_m ? B : A;
+  const T* Y = thin_m ? A : B;
+  const int np = (int)(thin_m ? M : N);
+  const int64_t nq = thin_m ? N : M;
+  const int64_t x_q = thin_m ? t.bs_n : t.as_m, x_k = thin_m ? t.bs_k : t.as_k;
+  const int64_t y_p = thin_m ? t.as_m : t.bs_n, y_k = thin_m ? t.as_k : t.bs_k;
+  const int64_t cp = thin_m ? ldc : 1, cq = thin_m ? 1 : ldc;
+  if (x_q == 1) {  // wide operand contiguous along the wide index
+    const bool vec = aligned16(X) && x_k % W == 0;
+    const dim3 grid((unsigned)ceil_div(nq, (int64_t)(64 * W)), (unsigned)splits);
+    if (vec)
+      hipLaunchKernelGGL((thin_wide_rows_kernel<T, P, true>), grid, dim3(kThinThreads), 0, st, X,
+                         x_k, Y, y_k, y_p, C, cp, cq, sstride, np, nq, K, kper);
+    else
+      hipLaunchKernelGGL((thin_wide_rows_kernel<T, P, false>), grid, dim3(kThinThreads), 0, st, X,
+                         x_k, Y, y_k, y_p, C, cp, cq, sstride, np, nq, K, kper);
+  } else {  // contiguous along k
+    const bool vec = aligned16(X) && x_q % W == 0 && kper % W == 0;
+    const dim3 grid((unsigned)ceil_div(nq, (int64_t)16), (unsigned)splits);
+    if (vec)
+      hipLaunchKernelGGL((thin_wide_cols_kernel<T, P, true>), grid, dim3(kThinThreads), 0, st, X,
+                         x_q, Y, y_k, y_p, C, cp, cq, sstride, np, nq, K, kper);
+    else
+      hipLaunchKernelGGL((thin_wide_cols_kernel<T, P, false>), grid, dim3(kThinThreads), 0, st, X,
+                         x_q, Y, y_k, y_p, C, cp, cq, sstride, np, nq, K, kper);
+  }
+  return KAN_OK;
+}
+
+template <typename T>
+int launch_thin(int layout, int64_t M, int64_t N, int64_t K, const T* A, int64_t lda, const T* B,
+                int64_t ldb, T* C, int64_t ldc, int splits, int64_t sstride, hipStream_t st) {
+  constexpr int W = ThinVec<T>::kW;
+  if (K <= kThinMax) {  // short contraction: bound by the writes of C
+    const ThinStrides t = thin_strides(layout, lda, ldb);
+    const bool vec = aligned16(C) && ldc % W == 0;
+    const int64_t ncol = ceil_div(N, (int64_t)(64 * W));
+    const int64_t rpw = ceil_div(M * ncol, (int64_t)1024);
+    const int64_t wave_rows = ceil_div(M, rpw);
+    const dim3 grid((unsigned)ncol, (unsigned)ceil_div(wave_rows, (int64_t)(kThinThreads / 64)));
+    if (vec)
+      hipLaunchKernelGGL((thin_short_k_kernel<T, true>), grid, dim3(kThinThreads), 0, st, A, t, B,
+                         C, ldc, M, N, (int)K, rpw);
+    else
+      hipLaunchKernelGGL((thin_short_k_kernel<T, false>), grid, dim3(kThinThreads), 0, st, A, t,
+                         B, C, ldc, M, N, (int)K, rpw);
+    return KAN_OK;
+  }
+  const int64_t p = min(M, N);
+  if (p <= 1) return launch_thin_p<T, 1>(layout, M, N, K, A, lda, B, ldb, C, ldc, splits, sstride, st);
+  if (p <= 2) return launch_thin_p<T, 2>(layout, M, N, K, A, lda, B, ldb, C, ldc, splits, sstride, st);
+  if (p <= 4) return launch_thin_p<T, 4>(layout, M, N, K, A, lda, B, ldb, C, ldc, splits, sstride, st);
+  if (p <= 8) return launch_thin_p<T, 8>(layout, M, N, K, A, lda, B, ldb, C, ldc, splits, sstride, st);
+  return launch_thin_p<T, 16>(layout, M, N, K, A, lda, B, ldb, C, ldc, splits, sstride, st);
+}
+
+inline bool gemm_is_thin(int64_t M, int64_t N, int64_t K) {
+  return K <= kThinMax || M <= kThinMax || N <= kThinMax;
+}
 }  // namespace
 
 // Split-K factor: the split count in 1..64 with the smallest estimated time
@@ -1056,6 +1441,7 @@ int launch_ecomp_cfg(const GemmParams<float>& p, const DxParams& e, int k, hipSt
 // (the parameter product, sample reductions, small-batch inference) split.
 template <typename T>
 int gemm_pick_splits(int64_t M, int64_t N, int64_t K) {
+  if (gemm_is_thin(M, N, K)) return K <= kThinMax ? 1 : thin_splits(M, N, K);
   int best = 1;
   double best_t = 0.0;
   for (int s = 1; s <= 64; ++s) {
@@ -1094,7 +1480,12 @@ int launch_gemm(int layout, int64_t M, int64_t N, int64_t K, const T* A, int64_t
   p.vec = vec_ok(A, lda) && vec_ok(B, ldb);
   TimedLaunch timed(kClassContraction, st, 2.0 * (double)M * (double)N * (double)K);
   int rc;
-  if constexpr (std::is_same<T, float>::value) {
+  if (gemm_is_thin(M, N, K) && K > 0) {
+    if (K <= kThinMax && splits > 1)
+      return set_error(KAN_ERR_INVALID, "gemm: a contraction of K <= %d is not split", kThinMax);
+    rc = launch_thin<T>(layout, M, N, K, A, lda, B, ldb, C, ldc, splits < 1 ? 1 : splits,
+                        split_stride, st);
+  } else if constexpr (std::is_same<T, float>::value) {
     const int cfg = pick_cfg_f32(M, N, K, splits < 1 ? 1 : splits);
     if (cfg == 0) rc = launch_layout<CfgF32Big>(layout, p, splits, st);
     else if (cfg == 3) rc = launch_layout<CfgF32Big4>(layout, p, splits, st);
