@@ -959,6 +959,11 @@ int pick_cfg_f32(int64_t M, int64_t N, int64_t K, int splits) {
       best_t = t;
     }
   }
+  // Split over K, the small tile ran slower than the model says, and slower
+  // than the big tile with its own split count (c2's first layer, K = 7056 and
+  // 4096: 176 and 197 us against 139 and 158 us); unsplit it matches the model
+  // (c4's layers).  So a split product takes the big tile.
+  if (best == 1 && splits > 1) best = 0;
   return best;
 }
 
