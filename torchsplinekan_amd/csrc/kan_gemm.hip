@@ -959,11 +959,6 @@ int pick_cfg_f32(int64_t M, int64_t N, int64_t K, int splits) {
       best_t = t;
     }
   }
-  // Split over K, the small tile ran slower than the model says, and slower
-  // than the big tile with its own split count (c2's first layer, K = 7056 and
-  // 4096: 176 and 197 us against 139 and 158 us); unsplit it matches the model
-  // (c4's layers).  So a split product takes the big tile.
-  if (best == 1 && splits > 1) best = 0;
   return best;
 }
 
@@ -1359,17 +1354,15 @@ __global__ __launch_bounds__(kThinThreads) void thin_short_k_kernel(
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
-// Split count of a thin product (one side <= kThinMax, K > kThinMax) over the
-// wide side's 256-wide groups.  A thin M (a parameter product: the wide
-// operand streams along its rows) aims at about 2048 waves with at least 64 k
-// per split; a thin N (a forward product: every block stages the thin rows
-// of its k range) at about 1024 waves with at least 256 k per split (at c2's
-// output layer: 17 us against 21 us, and 22 us against 53 us).
+// Split count of a thin product (one side <= kThinMax, K > kThinMax): about
+// 1024 waves over the wide side's 256-wide groups, at least 256 k per split.
+// (Finer splits of a parameter product shortened the product but lengthened
+// the fixed-order sum of its slices by more: at c2's output layer 17 + 29 us
+// against 21 + 9 us.)
 int thin_splits(int64_t M, int64_t N, int64_t K) {
   const int64_t groups = ceil_div(max(M, N), (int64_t)256);
-  const bool thin_m = M <= kThinMax;
-  int64_t s = ceil_div(thin_m ? (int64_t)512 : (int64_t)256, groups);
-  s = min(s, K / (thin_m ? 64 : 256));
+  int64_t s = ceil_div((int64_t)256, groups);
+  s = min(s, K / 256);
   s = min(s, (int64_t)64);
   return (int)max(s, (int64_t)1);
 }
