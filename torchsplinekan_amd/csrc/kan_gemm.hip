@@ -1413,7 +1413,7 @@ int launch_thin(int layout, int64_t M, int64_t N, int64_t K, const T* A, int64_t
     const ThinStrides t = thin_strides(layout, lda, ldb);
     const bool vec = aligned16(C) && ldc % W == 0;
     const int64_t ncol = ceil_div(N, (int64_t)(64 * W));
-    const int64_t rpw = ceil_div(M * ncol, (int64_t)1024);
+    const int64_t rpw = ceil_div(M * ncol, (int64_t)4096);
     const int64_t wave_rows = ceil_div(M, rpw);
     const dim3 grid((unsigned)ncol, (unsigned)ceil_div(wave_rows, (int64_t)(kThinThreads / 64)));
     if (vec)
