@@ -62,6 +62,30 @@ int kan_hip_limits(int64_t* max_deg0_basis, int64_t* max_in_features);
 int kan_hip_set_basis_impl(int64_t impl);
 int64_t kan_hip_get_basis_impl(void);
 
+/* Routing switches of the native path (no reference counterpart: they choose
+ * between kernel routes that give the same results, for tests and tuning).
+ * Each starts from its environment variable, read once when the library is
+ * loaded; kan_hip_set_route changes it for the whole process.  A workspace
+ * query and the launch it sizes must see the same routes.
+ *   KAN_ROUTE_FUSED_DX   (KAN_HIP_FUSED_DX)   0 off (default), 1 dx contracted
+ *                        in the input-side product's epilogue
+ *   KAN_ROUTE_COMPACT_E  (KAN_HIP_COMPACT_E)  -1 automatic (R >= 25, default),
+ *                        0 never, 1 always: span-window form of E
+ *   KAN_ROUTE_EDGE_FUSED (KAN_HIP_EDGE_FUSED) 1 (default) both gradient sides
+ *                        of the edge statistic in one kernel, 0 separate
+ *   KAN_ROUTE_GEMM_TILE  (KAN_HIP_GEMM_TILE)  -1 cost model (default), 0 256x256
+ *                        ("256"), 1 128x128 ("128"), 2 256x64 ("256x64"),
+ *                        3 4-wave 256x256 ("256w4")
+ * kan_hip_set_route returns KAN_ERR_INVALID for an unknown route or value;
+ * kan_hip_get_route returns -2 for an unknown route. */
+#define KAN_ROUTE_FUSED_DX 0
+#define KAN_ROUTE_COMPACT_E 1
+#define KAN_ROUTE_EDGE_FUSED 2
+#define KAN_ROUTE_GEMM_TILE 3
+#define KAN_ROUTE_COUNT 4
+int kan_hip_set_route(int route, int value);
+int kan_hip_get_route(int route);
+
 /* basis[n, I, R] = B-spline basis of x.  Replaces _C.basis / kan_basis_cuda
  * (csrc/kan_ext.cpp:196-197, csrc/kan_cuda.cu:666-680). */
 int kan_hip_basis(int dtype, const void* x, const void* grid, void* basis, int64_t n,

@@ -58,6 +58,33 @@ def test_library_matches_its_sources(lib, tmp_path, monkeypatch):
 
 def test_limits(lib):
     assert lib.limits() == (71, 65535)
+
+
+def test_routes_are_set_explicitly(lib, routes):
+    """Routing switches: defaults from the environment at load, changed only
+    through kan_hip_set_route; out-of-range values and unknown routes are
+    rejected with KAN_ERR_INVALID and leave the switch unchanged."""
+    env_default = {"fused_dx": 0, "compact_e": -1, "edge_fused": 1, "gemm_tile": -1}
+    for name, want in env_default.items():
+        var = "KAN_HIP_" + name.upper()
+        if var not in os.environ:
+            assert lib.get_route(name) == want, name
+    for name, good, bad in [("fused_dx", 1, 2), ("compact_e", -1, -2), ("edge_fused", 0, 3),
+                            ("gemm_tile", 3, 4)]:
+        lib.set_route(name, good)
+        assert lib.get_route(name) == good
+        assert lib.LIB.kan_hip_set_route(lib.ROUTES[name], bad) == lib.KAN_ERR_INVALID
+        assert "route" in lib.last_error()
+        assert lib.get_route(name) == good
+    assert lib.LIB.kan_hip_set_route(7, 0) == lib.KAN_ERR_INVALID
+    assert lib.LIB.kan_hip_get_route(7) == -2
+    # a changed environment is not read again
+    os.environ["KAN_HIP_GEMM_TILE"] = "128"
+    try:
+        lib.set_route("gemm_tile", -1)
+        assert lib.get_route("gemm_tile") == -1
+    finally:
+        del os.environ["KAN_HIP_GEMM_TILE"]
     from torchsplinekan_amd import _C
     assert _C.CUDA_MAX_DEG0_BASIS == 71 and _C.CUDA_MAX_IN_FEATURES == 65535
     assert _C.HAS_FUSED_KERNELS is True

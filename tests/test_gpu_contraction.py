@@ -1,12 +1,12 @@
 """GPU parity of the fp32 contraction engine in its tile configurations
 (256x256 over 8 waves of 128x64, 256x256 over 4 waves of 128x128, and
-128x128 with 64x64 per wave), each forced through KAN_HIP_GEMM_TILE, on
+128x128 with 64x64 per wave), each forced through the gemm_tile route, on
 layer shapes chosen so that the
 forward (NT), input-gradient (NT against the transposed weight; the
-two-pass routes through the full E (KAN_HIP_COMPACT_E=0) and through its
-compact form (the k+1 span-window values per item; KAN_HIP_COMPACT_E=1
+two-pass routes through the full E (compact_e route 0) and through its
+compact form (the k+1 span-window values per item; compact_e route 1
 forces it, by default it serves rows of R >= 25), and, with
-KAN_HIP_FUSED_DX=1, dx contracted in the GEMM epilogue, where the spline
+fused_dx route 1, dx contracted in the GEMM epilogue, where the spline
 columns of one feature straddle two wave blocks when R does not divide the
 block width) and parameter-gradient (TN, split
 over samples) products see whole tiles, ragged row and column edges, K tails that
@@ -48,27 +48,15 @@ def C():
     return _C
 
 
-@pytest.fixture
-def tile_env():
-    names = ("KAN_HIP_GEMM_TILE", "KAN_HIP_FUSED_DX", "KAN_HIP_COMPACT_E")
-    old = {n: os.environ.get(n) for n in names}
-    yield
-    for n, v in old.items():
-        if v is None:
-            os.environ.pop(n, None)
-        else:
-            os.environ[n] = v
-
-
 @pytest.mark.parametrize("dx_route", ["full", "compact", "fused"])
 @pytest.mark.parametrize("tile", ["256", "256w4", "128"])
 @pytest.mark.parametrize("shape", SHAPES)
-def test_contraction_configs_match_oracle(C, tile_env, tile, shape, dx_route):
+def test_contraction_configs_match_oracle(C, routes, tile, shape, dx_route):
     N, I, O, G, k, kind = shape
     print(f"contraction tile={tile} dx_route={dx_route} shape={shape}", flush=True)
-    os.environ["KAN_HIP_GEMM_TILE"] = tile
-    os.environ["KAN_HIP_FUSED_DX"] = "1" if dx_route == "fused" else "0"
-    os.environ["KAN_HIP_COMPACT_E"] = "1" if dx_route == "compact" else "0"
+    routes.set_route("gemm_tile", routes.GEMM_TILES[tile])
+    routes.set_route("fused_dx", 1 if dx_route == "fused" else 0)
+    routes.set_route("compact_e", 1 if dx_route == "compact" else 0)
     g = torch.Generator().manual_seed(N + I)
     grid = make_grid(I, G, k, kind, seed=N)
     x = torch.rand(N, I, generator=g, dtype=torch.float64) * 2.2 - 1.1
@@ -92,12 +80,12 @@ def test_contraction_configs_match_oracle(C, tile_env, tile, shape, dx_route):
 
 
 @pytest.mark.parametrize("shape", [(300, 37, 96, 7, 3, "uniform"), (257, 33, 19, 4, 1, "repeated")])
-def test_fused_dx_without_base_branch(C, tile_env, shape):
+def test_fused_dx_without_base_branch(C, routes, shape):
     """The fused input gradient with two partial slots per feature (no base
     columns), spline features straddling wave blocks (R = 10 and R = 5)."""
     N, I, O, G, k, kind = shape
     print(f"fused dx, no base branch, shape={shape}", flush=True)
-    os.environ["KAN_HIP_FUSED_DX"] = "1"
+    routes.set_route("fused_dx", 1)
     g = torch.Generator().manual_seed(N)
     grid = make_grid(I, G, k, kind, seed=N)
     x = torch.rand(N, I, generator=g, dtype=torch.float64) * 2.2 - 1.1
@@ -125,7 +113,7 @@ def test_fused_dx_without_base_branch(C, tile_env, shape):
     (520, 9, 70, 65, 3, "uniform", True),     # R = 68: rows across 3 wave blocks
     (1000, 130, 64, 10, 3, "nonuniform", False),
 ])
-def test_compact_input_product_matches_full_route(C, tile_env, tile, shape):
+def test_compact_input_product_matches_full_route(C, routes, tile, shape):
     """dx through the compact input-side product (the k+1 span-window values
     of E per item and the base columns, then the input gradient from them)
     equals dx through the full E [n, ld] element for element (the same
@@ -134,8 +122,8 @@ def test_compact_input_product_matches_full_route(C, tile_env, tile, shape):
     window that crosses wave blocks is completed by each of them."""
     N, I, O, G, k, kind, base = shape
     print(f"compact E tile={tile} shape={shape}", flush=True)
-    os.environ["KAN_HIP_GEMM_TILE"] = tile
-    os.environ["KAN_HIP_FUSED_DX"] = "0"
+    routes.set_route("gemm_tile", routes.GEMM_TILES[tile])
+    routes.set_route("fused_dx", 0)
     g = torch.Generator().manual_seed(3 * N + I)
     grid = make_grid(I, G, k, kind, seed=I)
     x = torch.rand(N, I, generator=g, dtype=torch.float64) * 2.2 - 1.1
@@ -148,7 +136,7 @@ def test_compact_input_product_matches_full_route(C, tile_env, tile, shape):
     y, H = C.kan_forward(f(x), f(grid), bwd, f(sw), f(sc), k, True)
     out = {}
     for route in ("0", "1"):
-        os.environ["KAN_HIP_COMPACT_E"] = route
+        routes.set_route("compact_e", int(route))
         out[route] = C.kan_backward(f(D), f(x), f(grid), bwd, f(sw), f(sc), H, k, True)
     torch.cuda.synchronize()
     gx_full, gx_comp = out["0"][0], out["1"][0]

@@ -56,14 +56,14 @@ SHAPES = [(37, 5, 3, 4), (300, 16, 40, 8), (1000, 9, 70, 13), (64, 3, 300, 68),
 @pytest.mark.parametrize("dtype", [torch.float64, torch.float32])
 @pytest.mark.parametrize("base", [True, False])
 @pytest.mark.parametrize("route", ["auto", "separate"])
-def test_edge_abs_mean_and_backward_match_oracle(C, monkeypatch, shape, dtype, base, route):
+def test_edge_abs_mean_and_backward_match_oracle(C, routes, shape, dtype, base, route):
     """route "auto": fp32 layers with O <= 512 and R + 1 <= 16 take the fused
     backward kernel (both gradient sides from one phi); "separate" forces the
-    parameter and input kernels (KAN_HIP_EDGE_FUSED=0)."""
+    parameter and input kernels (edge_fused route 0)."""
     N, I, O, R = shape
     if route == "separate" and dtype == torch.float64:
         pytest.skip("the route applies to the fp32 MFMA kernels only")
-    monkeypatch.setenv("KAN_HIP_EDGE_FUSED", "0" if route == "separate" else "1")
+    routes.set_route("edge_fused", 0 if route == "separate" else 1)
     print(f"edge {shape} {dtype} base={base} route={route}", flush=True)
     s, H, bw, W, ga = _edge_inputs(N, I, O, R, dtype, seed=N + O)
     empty = torch.empty(0, dtype=dtype, device="cuda")

@@ -222,13 +222,13 @@ def test_native_matmul_matches_torch(C, dtype, tol, M, K, N):
 @pytest.mark.parametrize("tile", ["256x64", "128", "256", "256w4"])
 @pytest.mark.parametrize("M,K,N", [(600, 5632, 64), (513, 407, 61), (16384, 64, 64),
                                    (333, 16384, 19), (64, 100, 3)])
-def test_matmul_tile_configs_match_torch(C, monkeypatch, tile, M, K, N):
-    """The fp32 tile configurations forced through KAN_HIP_GEMM_TILE on
+def test_matmul_tile_configs_match_torch(C, routes, tile, M, K, N):
+    """The fp32 tile configurations forced through the gemm_tile route on
     narrow products (N <= 64, the narrow 256x64 tile's range): ragged rows,
     K tails past the 32-deep slab, unaligned leading dimensions and split-K,
     all four transposition pairs, against the float64 product."""
     print(f"matmul tile={tile} M={M} K={K} N={N}", flush=True)
-    monkeypatch.setenv("KAN_HIP_GEMM_TILE", tile)
+    routes.set_route("gemm_tile", routes.GEMM_TILES[tile])
     g = torch.Generator().manual_seed(M + 3 * K + N)
     a = torch.randn(M, K, generator=g, dtype=torch.float64).float()
     b = torch.randn(K, N, generator=g, dtype=torch.float64).float()

@@ -280,3 +280,62 @@ def test_select_keeps_the_chosen_edges():
     assert torch.allclose(sub(x[:, ii]), masked(x)[:, oi], atol=1e-13)
     L.requires_grad_(False)
     assert not any(p.requires_grad for p in L.select(oi, ii).parameters())
+
+
+def test_select_index_arguments():
+    """select takes boolean masks as masks (not as 0/1 indices) and rejects
+    out-of-range indices, masks of the wrong length and float indices."""
+    torch.manual_seed(5)
+    L = KANLinear(4, 3, grid_size=3, backend="reference").double()
+    x = torch.rand(10, 4, dtype=torch.float64) * 2 - 1
+    by_mask = L.select(torch.tensor([False, True, True]), torch.tensor([True, False, True, True]))
+    by_index = L.select(torch.tensor([1, 2]), torch.tensor([0, 2, 3]))
+    assert (by_mask.out_features, by_mask.in_features) == (2, 3)
+    assert torch.equal(by_mask(x[:, [0, 2, 3]]), by_index(x[:, [0, 2, 3]]))
+    assert L.select([True, False, True]).out_features == 2
+    with pytest.raises(IndexError):
+        L.select(torch.tensor([0, 3]))
+    with pytest.raises(IndexError):
+        L.select(None, [-1])
+    with pytest.raises(ValueError):
+        L.select(torch.tensor([True, False]))
+    with pytest.raises(TypeError):
+        L.select(torch.tensor([0.0, 1.0]))
+
+
+@pytest.mark.parametrize("with_base", [True, False])
+def test_chunked_edge_statistic_gradients(with_base):
+    """reg_impl="checkpoint" statistic: value, all four first derivatives and
+    second derivatives (gradgradcheck) against the dense phi formulation."""
+    from torchsplinekan_amd.fused import edge_abs_mean_chunked
+    from torchsplinekan_amd.reference_backend import compute_basis, edge_abs_mean_dense
+    g = torch.Generator().manual_seed(11)
+    N, I, O, G, k = 23, 3, 4, 4, 3
+    x = (torch.rand(N, I, generator=g, dtype=torch.float64) * 2.6 - 1.3).requires_grad_()
+    grid = torch.linspace(-1, 1, G + 1, dtype=torch.float64)
+    h = grid[1] - grid[0]
+    grid = torch.cat([grid[0] - h * torch.arange(k, 0, -1), grid,
+                      grid[-1] + h * torch.arange(1, k + 1)]).repeat(I, 1)
+    W = torch.randn(O, I, G + k, generator=g, dtype=torch.float64).requires_grad_()
+    bw = torch.randn(O, I, generator=g, dtype=torch.float64).requires_grad_() if with_base else None
+    s = torch.nn.functional.silu(x) if with_base else None
+
+    def chunked(x_, W_, bw_):
+        s_ = torch.nn.functional.silu(x_) if with_base else None
+        return edge_abs_mean_chunked(s_, x_, grid, k, bw_, W_, 5)
+
+    def dense(x_, W_, bw_):
+        s_ = torch.nn.functional.silu(x_) if with_base else None
+        return edge_abs_mean_dense(s_, compute_basis(x_, grid, k), bw_, W_)
+
+    args = (x, W, bw) if with_base else (x, W)
+    f_c = (lambda a, b, c: chunked(a, b, c)) if with_base else (lambda a, b: chunked(a, b, None))
+    f_d = (lambda a, b, c: dense(a, b, c)) if with_base else (lambda a, b: dense(a, b, None))
+    a_c, a_d = f_c(*args), f_d(*args)
+    assert normwise(np64(a_c), np64(a_d)) < 1e-14
+    ga = torch.randn(O, I, generator=g, dtype=torch.float64)
+    gc = torch.autograd.grad(a_c, args, ga)
+    gd = torch.autograd.grad(a_d, args, ga)
+    for u, v in zip(gc, gd):
+        assert normwise(np64(u), np64(v)) < 1e-12
+    assert torch.autograd.gradgradcheck(f_c, args, (ga,))

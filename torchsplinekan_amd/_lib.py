@@ -38,6 +38,8 @@ SIGNATURES = {
     "kan_hip_limits": (_int, [ctypes.POINTER(_i64), ctypes.POINTER(_i64)]),
     "kan_hip_set_basis_impl": (_int, [_i64]),
     "kan_hip_get_basis_impl": (_i64, []),
+    "kan_hip_set_route": (_int, [_int, _int]),
+    "kan_hip_get_route": (_int, [_int]),
     "kan_hip_basis": (_int, [_int, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp]),
     "kan_hip_basis_grad": (_int, [_int, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp]),
     "kan_hip_basis_silu": (_int, [_int, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp]),
@@ -153,6 +155,39 @@ def ptr(t):
 def stream_of(device: torch.device) -> int:
     """hipStream_t handle of the current torch stream on `device`."""
     return torch.cuda.current_stream(device).cuda_stream
+
+
+# routing switches of kan_hip_set_route (KAN_ROUTE_* in include/kan_hip.h) and
+# the values each takes
+ROUTES = {"fused_dx": 0, "compact_e": 1, "edge_fused": 2, "gemm_tile": 3}
+GEMM_TILES = {"auto": -1, "256": 0, "128": 1, "256x64": 2, "256w4": 3}
+
+
+def set_route(name: str, value: int) -> None:
+    """Sets one routing switch for the whole process (a choice between
+    kernel routes with the same results; see include/kan_hip.h)."""
+    check(LIB.kan_hip_set_route(ROUTES[name], int(value)))
+
+
+def get_route(name: str) -> int:
+    return int(LIB.kan_hip_get_route(ROUTES[name]))
+
+
+class route:
+    """Context manager: `with route("gemm_tile", 1): ...` sets a switch and
+    restores its previous value on exit."""
+
+    def __init__(self, name: str, value: int):
+        self.name, self.value = name, int(value)
+
+    def __enter__(self):
+        self.saved = get_route(self.name)
+        set_route(self.name, self.value)
+        return self
+
+    def __exit__(self, *exc):
+        set_route(self.name, self.saved)
+        return False
 
 
 def limits():

@@ -7,6 +7,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstdlib>
+#include <cstring>
 #include <map>
 #include <mutex>
 #include <type_traits>
@@ -23,30 +24,65 @@ std::mutex g_cu_mutex;
 int g_cu_count[64] = {0};
 std::map<std::pair<int, const void*>, int> g_resident;  // (device, kernel) -> blocks per CU
 
-// KAN_HIP_FUSED_DX=1 contracts dx inside the input-side GEMM (no E buffer:
-// the workspace shrinks by n * (ld - 3 I) floats, at about 10% more time for
-// that GEMM, whose epilogue then evaluates dB/dx at one wave per SIMD).
-// Unset or any other value keeps the two-pass route (E, then basis_grad).
-// Read at every plan, so a caller can switch it between calls.
-bool fused_dx_enabled() {
-  const char* v = std::getenv("KAN_HIP_FUSED_DX");
-  return v != nullptr && v[0] == '1';
+// Routing switches (KAN_ROUTE_* in kan_hip.h).  Each starts from its
+// environment variable, read once when the library is loaded, and changes
+// only through kan_hip_set_route, so a workspace query and the launch it
+// sizes see the same route unless the caller switches it in between.
+//  * FUSED_DX (KAN_HIP_FUSED_DX=1): contract dx inside the input-side GEMM
+//    (no E buffer: the workspace shrinks by n * (ld - 3 I) floats, at about
+//    10% more time for that GEMM).  Default off.
+//  * COMPACT_E (KAN_HIP_COMPACT_E=1 always, =0 never, else automatic): the
+//    input-side product of the fp32 backward with the local basis stores only
+//    each item's k+1 span-window values of E (and the base columns), which the
+//    input gradient then reads.  It pays where rows are long: at R = 68 (c5)
+//    the product took 0.16 ms more and the input gradient 0.80 ms less than
+//    through the full E [n, ld]; at R = 13 (c3) the epilogue's span searches
+//    cost 0.54 ms against 0.39 ms saved.  Automatic means R >= kCompactMinR.
+//  * EDGE_FUSED (KAN_HIP_EDGE_FUSED=0 turns it off): both gradient sides of
+//    an edge-statistic layer in one kernel where it applies.
+//  * GEMM_TILE (KAN_HIP_GEMM_TILE=256, 128, 256x64 or 256w4): forces the fp32
+//    tile configuration; otherwise the cost model picks it.
+constexpr int64_t kCompactMinR = 25;
+
+int route_from_env(int route) {
+  switch (route) {
+    case KAN_ROUTE_FUSED_DX: {
+      const char* v = std::getenv("KAN_HIP_FUSED_DX");
+      return v != nullptr && v[0] == '1' ? 1 : 0;
+    }
+    case KAN_ROUTE_COMPACT_E: {
+      const char* v = std::getenv("KAN_HIP_COMPACT_E");
+      if (v != nullptr && v[0] == '0') return 0;
+      if (v != nullptr && v[0] == '1') return 1;
+      return -1;
+    }
+    case KAN_ROUTE_EDGE_FUSED: {
+      const char* v = std::getenv("KAN_HIP_EDGE_FUSED");
+      return v != nullptr && std::strcmp(v, "0") == 0 ? 0 : 1;
+    }
+    case KAN_ROUTE_GEMM_TILE: {
+      const char* v = std::getenv("KAN_HIP_GEMM_TILE");
+      if (v == nullptr) return -1;
+      if (std::strcmp(v, "256") == 0) return 0;
+      if (std::strcmp(v, "128") == 0) return 1;
+      if (std::strcmp(v, "256x64") == 0) return 2;
+      if (std::strcmp(v, "256w4") == 0) return 3;
+      return -1;
+    }
+    default:
+      return 0;
+  }
 }
 
-// The input-side product of the fp32 backward with the local basis can store
-// only each item's k+1 span-window values of E (and the base columns), which
-// the input gradient then reads (launch_gemm_ecomp, launch_basis_grad_compact).
-// It pays where rows are long: at R = 68 (c5) the product took 0.16 ms more
-// and the input gradient 0.80 ms less than through the full E [n, ld]; at
-// R = 13 (c3) the epilogue's span searches cost 0.54 ms against 0.39 ms
-// saved.  So by default from R >= kCompactMinR; KAN_HIP_COMPACT_E=1 takes it
-// for every R (where supported), =0 never.  Read at every plan.
-constexpr int64_t kCompactMinR = 25;
+std::atomic<int> g_route[KAN_ROUTE_COUNT] = {
+    {route_from_env(KAN_ROUTE_FUSED_DX)}, {route_from_env(KAN_ROUTE_COMPACT_E)},
+    {route_from_env(KAN_ROUTE_EDGE_FUSED)}, {route_from_env(KAN_ROUTE_GEMM_TILE)}};
+
+bool fused_dx_enabled() { return g_route[KAN_ROUTE_FUSED_DX].load() == 1; }
+
 bool compact_e_wanted(int64_t R) {
-  const char* v = std::getenv("KAN_HIP_COMPACT_E");
-  if (v != nullptr && v[0] == '0') return false;
-  if (v != nullptr && v[0] == '1') return true;
-  return R >= kCompactMinR;
+  const int v = g_route[KAN_ROUTE_COMPACT_E].load();
+  return v < 0 ? R >= kCompactMinR : v == 1;
 }
 }  // namespace
 
@@ -424,6 +460,22 @@ int kan_hip_set_basis_impl(int64_t impl) {
 }
 
 int64_t kan_hip_get_basis_impl(void) { return g_basis_impl.load(); }
+
+int kan_hip_set_route(int route, int value) {
+  static const int lo[KAN_ROUTE_COUNT] = {0, -1, 0, -1};
+  static const int hi[KAN_ROUTE_COUNT] = {1, 1, 1, 3};
+  if (route < 0 || route >= KAN_ROUTE_COUNT)
+    return set_error(KAN_ERR_INVALID, "unknown route %d", route);
+  if (value < lo[route] || value > hi[route])
+    return set_error(KAN_ERR_INVALID, "route %d takes values %d..%d, got %d", route, lo[route],
+                     hi[route], value);
+  g_route[route].store(value);
+  return KAN_OK;
+}
+
+int kan_hip_get_route(int route) {
+  return route >= 0 && route < KAN_ROUTE_COUNT ? g_route[route].load() : -2;
+}
 
 int kan_hip_timing_enable(int on) {
   std::lock_guard<std::mutex> lock(g_timing_mutex);

@@ -1510,13 +1510,10 @@ inline int fin_blocks_f32(int64_t total) {
 
 }  // namespace
 
-// Both gradient sides of a layer in one fused kernel where it applies (set
-// KAN_HIP_EDGE_FUSED=0 to take the separate parameter and input kernels; read
-// at every call, so a test can switch it between calls).
-bool edge_fused_enabled() {
-  const char* v = std::getenv("KAN_HIP_EDGE_FUSED");
-  return v == nullptr || std::strcmp(v, "0") != 0;
-}
+// Both gradient sides of a layer in one fused kernel where it applies
+// (route KAN_ROUTE_EDGE_FUSED; 0 takes the separate parameter and input
+// kernels).
+bool edge_fused_enabled() { return kan_hip_get_route(KAN_ROUTE_EDGE_FUSED) != 0; }
 
 // (OT, WS) of the forward and parameter kernels for a layer width O; see
 // EdgeTiling.  Returns the block's output coverage.

@@ -667,40 +667,24 @@ __device__ __forceinline__ void ecomp_epilogue(const GemmParams<float>& p, const
           if (lane + 64 * u < nkn) kn[lane + 64 * u] = kv[u];
       }
       wave_sync_lds();
-      // spans (knot_span of kan_spline.h as 7 fixed halving steps, nk <= 128:
-      // the largest m <= nk - 2 with t[m] <= x for t[0] <= x < t[nk-1], the
-      // last non-degenerate span at x == t[nk-1], -1 outside or NaN), four
+      // spans through knot_spans (kan_spline.h), the routine
+      // basis_grad_compact_kernel uses to read the window slots back; four
       // interleaved searches per lane, stored over x
       for (int b = lane; b < total; b += 64 * 4) {
         float xv[4];
         const float* tk[4];
-        int lo[4];
+        int ms[4];
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
           const int el = b + u * 64 < total ? b + u * 64 : total - 1;
           const int rq = div_small(el, rcp);
           xv[u] = xs[el];
           tk[u] = kn + (el - rq * nfs) * e.nk;
-          lo[u] = 0;
         }
-#pragma unroll
-        for (int step = 64; step >= 1; step >>= 1)
-#pragma unroll
-          for (int u = 0; u < 4; ++u) {
-            const int c = lo[u] + step;
-            if (c <= e.nk - 2 && tk[u][c <= e.nk - 2 ? c : e.nk - 2] <= xv[u]) lo[u] = c;
-          }
+        knot_spans<4, float>(tk, e.nk, xv, ms);
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
-          const float* t = tk[u];
-          const float x = xv[u], tl = t[e.nk - 1];
-          int m = lo[u];
-          if (!(x >= t[0]) || x > tl) {
-            m = -1;
-          } else if (x == tl) {
-            m = e.nk - 2;
-            while (m > 0 && t[m] == tl) --m;
-          }
+          const int m = ms[u];
           if (b + u * 64 < total) xs[b + u * 64] = __int_as_float(m);
         }
       }
@@ -928,20 +912,10 @@ double est_seconds(const CfgModel& c, double peak_per_cu, int64_t M, int64_t N, 
   return t;
 }
 
-// Test override of the fp32 tile configuration: KAN_HIP_GEMM_TILE=256, 128,
-// 256x64 or 256w4 forces the big, the small, the narrow or the 4-wave
-// 256x256 configuration (read at every launch, so a test can switch it
-// between calls); unset or any other value leaves the choice to the cost
+// Forced fp32 tile configuration (route KAN_ROUTE_GEMM_TILE: 0 big, 1 small,
+// 2 narrow, 3 the 4-wave 256x256), or -1 to leave the choice to the cost
 // model.
-int forced_cfg_f32() {
-  const char* v = std::getenv("KAN_HIP_GEMM_TILE");
-  if (v == nullptr) return -1;
-  if (std::strcmp(v, "256") == 0) return 0;
-  if (std::strcmp(v, "128") == 0) return 1;
-  if (std::strcmp(v, "256x64") == 0) return 2;
-  if (std::strcmp(v, "256w4") == 0) return 3;
-  return -1;
-}
+int forced_cfg_f32() { return kan_hip_get_route(KAN_ROUTE_GEMM_TILE); }
 
 // fp32 configuration (0 = big, 1 = small, 2 = narrow, 3 = 4-wave big, only
 // when forced) for a given split count; the narrow one only where N fits its

@@ -8,26 +8,56 @@
 
 namespace kan {
 
-// Span index m with t[m] <= x < t[m+1] (x == t[nk-1]: last non-degenerate
-// span), or -1 when x lies outside [t[0], t[nk-1]] or is NaN.
-// Follows find_span, csrc/kan_cuda.cu:207-221.
+// Span search.  For W values x[u] on knot rows t[u] of nk knots each, m[u]
+// is the span index with t[m] <= x < t[m+1] (x == t[nk-1]: the last
+// non-degenerate span), or -1 when x lies outside [t[0], t[nk-1]] or is NaN
+// (the conventions of find_span, csrc/kan_cuda.cu:207-221).  Inside the
+// knots the index is found by greedy binary lifting: starting from 0, add
+// each power of two below nk - 1, largest first, wherever the knot reached
+// is still <= x.  On a sorted row that gives the largest m <= nk - 2 with
+// t[m] <= x.  The step count depends on nk alone, so lanes never diverge,
+// and W independent searches interleave for latency.  Every kernel finds its
+// spans through this one routine, so kernels that exchange span-indexed data
+// (the compact input-side product writes window slots that
+// basis_grad_compact_kernel reads) agree on any knot row, sorted or not.
+__host__ __device__ __forceinline__ int lift_top_step(int nk) {
+  return nk > 2 ? 1 << (31 - __builtin_clz((unsigned)(nk - 2))) : 0;
+}
+
+template <int W, typename T>
+__host__ __device__ __forceinline__ void knot_spans(const T* const (&t)[W], int nk,
+                                                    const T (&x)[W], int (&m)[W]) {
+  const int last = nk - 2;
+#pragma unroll
+  for (int u = 0; u < W; ++u) m[u] = 0;
+  for (int step = lift_top_step(nk); step > 0; step >>= 1) {
+#pragma unroll
+    for (int u = 0; u < W; ++u) {
+      const int c = m[u] + step;
+      const T knot = t[u][c <= last ? c : last];   // in range whether or not c is
+      if (c <= last && knot <= x[u]) m[u] = c;
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < W; ++u) {
+    const T top = t[u][nk - 1];
+    if (!(x[u] >= t[u][0]) || x[u] > top) {
+      m[u] = -1;
+    } else if (x[u] == top) {
+      int q = last;
+      while (q > 0 && t[u][q] == top) --q;
+      m[u] = q;
+    }
+  }
+}
+
 template <typename T>
-__device__ __forceinline__ int knot_span(const T* __restrict__ t, int nk, T x) {
-  const T lo_knot = t[0];
-  const T hi_knot = t[nk - 1];
-  if (!(x >= lo_knot) || x > hi_knot) return -1;
-  if (x == hi_knot) {
-    int m = nk - 2;
-    while (m > 0 && t[m] == hi_knot) --m;
-    return m;
-  }
-  int lo = 0, hi = nk - 1;  // t[lo] <= x < t[hi]
-  while (hi - lo > 1) {
-    const int mid = (lo + hi) >> 1;
-    if (t[mid] <= x) lo = mid;
-    else hi = mid;
-  }
-  return lo;
+__host__ __device__ __forceinline__ int knot_span(const T* t, int nk, T x) {
+  const T* const rows[1] = {t};
+  const T xs[1] = {x};
+  int m[1];
+  knot_spans<1, T>(rows, nk, xs, m);
+  return m[0];
 }
 
 template <typename T>

@@ -22,7 +22,7 @@ from typing import Optional
 
 import torch
 
-from .reference_backend import compute_basis, edge_abs_mean_dense
+from .reference_backend import compute_basis, compute_basis_derivative
 
 try:
     from . import _C
@@ -99,7 +99,7 @@ class EdgeAbsMean(torch.autograd.Function):
         s, H, bw, W = ctx.saved_tensors
         has_base = ctx.has_base
         need_s, need_H, need_bw, need_W = ctx.needs_input_grad
-        if torch.is_grad_enabled() and H.is_cuda:
+        if torch.is_grad_enabled():
             # Recorded backward: a differentiable native function of the
             # saved tensors themselves (mixed input x weight terms kept),
             # whose own backward runs the native double-backward kernels.
@@ -107,19 +107,6 @@ class EdgeAbsMean(torch.autograd.Function):
                 ga, s if has_base else None, H, bw if has_base else None, W)
             return (ds if need_s and has_base else None, dH if need_H else None,
                     dbw if need_bw and has_base else None, dW if need_W else None)
-        if torch.is_grad_enabled():
-            # Partial derivatives written in the saved tensors themselves, so
-            # that double backward keeps the mixed (input x weight) terms;
-            # sign(0) = 0 matches the subgradient of abs.
-            phi = torch.einsum("oir,nir->noi", W, H)
-            if has_base:
-                phi = s.unsqueeze(1) * bw.unsqueeze(0) + phi
-            g = phi.sign() * ga.unsqueeze(0) / H.shape[0]
-            ds = (g * bw.unsqueeze(0)).sum(1) if need_s and has_base else None
-            dH = torch.einsum("noi,oir->nir", g, W) if need_H else None
-            dbw = (g * s.unsqueeze(1)).sum(0) if need_bw and has_base else None
-            dW = torch.einsum("noi,nir->oir", g, H) if need_W else None
-            return ds, dH, dbw, dW
         ds, dH, dbw, dW = _C.edge_abs_mean_backward(
             ga, s, H, bw, W, bool(need_s and has_base), bool(need_H),
             bool(need_bw and has_base), bool(need_W))
@@ -258,23 +245,79 @@ def native_linear(s: torch.Tensor, bw: torch.Tensor, H2: torch.Tensor,
     return y + _C.NativeMatmul.apply(H2, W2.t())
 
 
+class ChunkedEdgeAbsMean(torch.autograd.Function):
+    """a[o, i] = mean_n |phi[n, o, i]| on any device with at most `chunk`
+    samples' worth of phi (and of the basis) alive at once.  The forward
+    accumulates sum_n |phi| chunk by chunk under no_grad and keeps only its
+    inputs.  The backward visits the chunks again: it evaluates the chunk's
+    basis, takes g = sign(phi) ga / N, and forms the four gradients in closed
+    form (dW = sum_n g H, dbw = sum_n g s, ds = sum_o g bw, dx = sum_r
+    (sum_o g W) dB_r/dx).  Those are differentiable operations on the saved
+    inputs, so a recorded backward (create_graph) can be differentiated again;
+    sign(phi) is constant almost everywhere and enters as data.  The reference
+    bounds memory the same way through activation checkpointing
+    (spline_kan/fused.py:114-137)."""
+
+    @staticmethod
+    def forward(ctx, x, s, bw, W, grid, k: int, chunk: int):
+        N = x.shape[0]
+        total = W.new_zeros(W.shape[:2])
+        for lo in range(0, N, chunk):
+            hi = min(lo + chunk, N)
+            phi = _chunk_phi(x[lo:hi], None if s is None else s[lo:hi], grid, k, bw, W)
+            total += phi.abs().sum(0)
+        ctx.k, ctx.chunk = k, chunk
+        ctx.save_for_backward(x, s, bw, W, grid)
+        return total / N
+
+    @staticmethod
+    def backward(ctx, ga):
+        x, s, bw, W, grid = ctx.saved_tensors
+        k, chunk, N = ctx.k, ctx.chunk, x.shape[0]
+        need_x, need_s, need_bw, need_W = ctx.needs_input_grad[:4]
+        has_base = bw is not None
+        dx, ds, dbw, dW = [], [], None, None
+        for lo in range(0, N, chunk):
+            hi = min(lo + chunk, N)
+            xc = x[lo:hi]
+            sc = s[lo:hi] if has_base else None
+            Hc = compute_basis(xc, grid, k)
+            with torch.no_grad():
+                sgn = _chunk_phi(xc, sc, grid, k, bw, W, Hc).sign()
+            g = sgn * (ga / N)                                           # [n, O, I]
+            if need_W:
+                part = torch.einsum("noi,nir->oir", g, Hc)
+                dW = part if dW is None else dW + part
+            if need_bw and has_base:
+                part = torch.einsum("noi,ni->oi", g, sc)
+                dbw = part if dbw is None else dbw + part
+            if need_s and has_base:
+                ds.append(torch.einsum("noi,oi->ni", g, bw))
+            if need_x:
+                gH = torch.einsum("noi,oir->nir", g, W)
+                if k >= 1:
+                    dx.append((gH * compute_basis_derivative(xc, grid, k)).sum(-1))
+                else:                        # piecewise constant basis: dB/dx = 0
+                    dx.append(torch.zeros_like(xc))
+        return (torch.cat(dx) if need_x else None,
+                torch.cat(ds) if need_s and has_base else None,
+                dbw, dW, None, None, None)
+
+
+def _chunk_phi(xc, sc, grid, k, bw, W, Hc=None):
+    """phi [n, O, I] of a sample chunk: sc bw + <basis(xc), W>."""
+    if Hc is None:
+        Hc = compute_basis(xc, grid, k)
+    phi = torch.einsum("nir,oir->noi", Hc, W)
+    if bw is not None:
+        phi = phi + sc[:, None, :] * bw[None]
+    return phi
+
+
 def edge_abs_mean_chunked(s: Optional[torch.Tensor], x: torch.Tensor, grid: torch.Tensor, k: int,
                           bw: Optional[torch.Tensor], W: torch.Tensor,
                           chunk_size: int) -> torch.Tensor:
-    """Pure-PyTorch low-memory variant: activation checkpointing over sample
-    chunks, so peak memory scales with chunk_size * O * I instead of N * O * I
-    (spline_kan/fused.py:114-137)."""
-    from torch.utils.checkpoint import checkpoint
-
-    N = x.shape[0]
-
-    def chunk_sum(xc, sc, bw_, W_):
-        return edge_abs_mean_dense(sc, compute_basis(xc, grid, k), bw_, W_) * xc.shape[0]
-
-    total = None
-    for n0 in range(0, N, chunk_size):
-        xc = x[n0:n0 + chunk_size]
-        sc = s[n0:n0 + chunk_size] if s is not None else None
-        part = checkpoint(chunk_sum, xc, sc, bw, W, use_reentrant=False)
-        total = part if total is None else total + part
-    return total / N
+    """Low-memory edge statistic on any device (reg_impl="checkpoint"):
+    ChunkedEdgeAbsMean over chunks of chunk_size samples."""
+    return ChunkedEdgeAbsMean.apply(x, s if bw is not None else None, bw, W, grid, k,
+                                    chunk_size)

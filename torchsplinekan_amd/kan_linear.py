@@ -66,6 +66,42 @@ def native_config_supported(in_features: int, grid_size: int, spline_order: int)
     return True, ""
 
 
+def _uniform_knot_rows(span: torch.Tensor, G: int, k: int) -> torch.Tensor:
+    """[I, G+2k+1] knot rows with G equal intervals between span[:, 0] and
+    span[:, 1] and k more of the same width beyond each end."""
+    lo, hi = span.unbind(1)
+    offsets = torch.arange(-k, G + k + 1, device=span.device, dtype=span.dtype)
+    return lo[:, None] + offsets[None] * ((hi - lo) / G)[:, None]
+
+
+def _interior_points(grid: torch.Tensor, G: int, k: int, count: int) -> torch.Tensor:
+    """[count, I] evenly spaced points from t_k to t_{k+G} of every knot row."""
+    a, b = grid[:, k], grid[:, k + G]
+    frac = torch.linspace(0, 1, count, device=grid.device, dtype=grid.dtype)
+    return a[None] + frac[:, None] * (b - a)[None]
+
+
+def _index_list(index, size: int, name: str, device) -> torch.Tensor:
+    """Long index tensor for KANLinear.select: None keeps all `size` entries;
+    a boolean mask of length `size` keeps its True positions; integer indices
+    must lie in [0, size)."""
+    if index is None:
+        return torch.arange(size, device=device)
+    t = torch.as_tensor(index, device=device)
+    if t.dtype == torch.bool:
+        if t.dim() != 1 or t.numel() != size:
+            raise ValueError(f"{name}: a boolean mask must have shape [{size}], "
+                             f"got {list(t.shape)}")
+        return t.nonzero().flatten()
+    if t.is_floating_point() or t.is_complex():
+        raise TypeError(f"{name}: expected integer indices or a boolean mask, got {t.dtype}")
+    t = t.to(torch.long).flatten()
+    if t.numel() and (int(t.min()) < 0 or int(t.max()) >= size):
+        raise IndexError(f"{name}: indices must lie in [0, {size}), got "
+                         f"[{int(t.min())}, {int(t.max())}]")
+    return t
+
+
 class KANLinear(nn.Module):
     """B-spline KAN layer.
 
@@ -265,35 +301,40 @@ class KANLinear(nn.Module):
         if adapt_knots:
             new_grid = new._ref.grid_from_samples(x_flat, new_grid_size, margin)
         else:
-            lo0, hi0 = self.grid[:, k], self.grid[:, k + self.grid_size]
-            xmin, xmax = x_flat.amin(0), x_flat.amax(0)
-            lo = torch.where(xmin < lo0, xmin - margin, lo0)
-            hi = torch.where(xmax > hi0, xmax + margin, hi0)
-            lo = torch.maximum(lo, self.grid[:, 0])     # the old spline is 0 beyond its support
-            hi = torch.minimum(hi, self.grid[:, -1])
-            r = torch.arange(new_grid_size + 2 * k + 1, device=lo.device, dtype=lo.dtype) - k
-            new_grid = lo[:, None] + r[None] * ((hi - lo) / new_grid_size)[:, None]
-        xs = x_flat
+            new_grid = _uniform_knot_rows(self._extension_span(x_flat, margin), new_grid_size, k)
+        fit_x = x_flat
         if n_dense > 0:
-            lo, hi = new_grid[:, k], new_grid[:, k + new_grid_size]
-            t = torch.linspace(0, 1, n_dense, device=lo.device, dtype=lo.dtype)
-            xs = torch.cat([x_flat, lo[None] + t[:, None] * (hi - lo)[None]], 0)
-        native = (self.backend_for(x) == "cuda"
-                  and native_config_supported(self.in_features, new_grid_size, k)[0])
-        if native:
+            fit_x = torch.cat([x_flat, _interior_points(new_grid, new_grid_size, k, n_dense)], 0)
+        if (self.backend_for(x) == "cuda"
+                and native_config_supported(self.in_features, new_grid_size, k)[0]):
             from . import refit as _refit
-            gram, cross = _refit.refit_gram(xs.double(), self.grid.double(), new_grid.double(), k)
+            gram, cross = _refit.refit_gram(fit_x.double(), self.grid.double(),
+                                            new_grid.double(), k)
             coeffs = _refit.solve_ridge(gram, cross, self.spline_weight, ridge)
         else:
-            H_old = compute_basis(xs, self.grid, k)
-            y_old = torch.einsum("oir,bir->obi", self.spline_weight, H_old)   # unscaled curves
-            coeffs = fit_spline_coeffs(xs, y_old, new_grid, k, ridge=ridge)
+            curves = torch.einsum("bir,oir->obi", compute_basis(fit_x, self.grid, k),
+                                  self.spline_weight)          # unscaled curves [O, B, I]
+            coeffs = fit_spline_coeffs(fit_x, curves, new_grid, k, ridge=ridge)
         new.base_weight.copy_(self.base_weight)
         new.spline_weight.copy_(coeffs.to(new.spline_weight.dtype))
         if self.enable_standalone_scale_spline:
             new.spline_scaler.copy_(self.spline_scaler)
         new._copy_grid_(new_grid)
         return new.train(self.training)
+
+    def _extension_span(self, x_flat: torch.Tensor, margin: float) -> torch.Tensor:
+        """[I, 2] end points of extend_grid's uniform knots: the current
+        interior [t_k, t_{k+G}], moved out to min(x) - margin (max(x) + margin)
+        on a side where samples lie beyond it, and clipped to the outermost
+        current knots, past which the current spline is identically zero
+        (spline_kan/kan_linear.py:562-570)."""
+        k, g = self.spline_order, self.grid
+        interior = g[:, [k, k + self.grid_size]]
+        xmin, xmax = torch.aminmax(x_flat, dim=0)
+        outside = torch.stack((xmin < interior[:, 0], xmax > interior[:, 1]), 1)
+        widened = torch.stack((xmin - margin, xmax + margin), 1)
+        span = torch.where(outside, widened, interior)
+        return torch.clamp(span, min=g[:, :1], max=g[:, -1:])
 
     # ------------------------------------------------------------------ regularisation
 
@@ -440,10 +481,8 @@ class KANLinear(nn.Module):
         original's minus the removed inputs' edges.  Hyper-parameters,
         dtype, device, training mode and requires_grad follow this layer."""
         dev = self.grid.device
-        oi = (torch.arange(self.out_features, device=dev) if out_index is None
-              else torch.as_tensor(out_index, device=dev, dtype=torch.long))
-        ii = (torch.arange(self.in_features, device=dev) if in_index is None
-              else torch.as_tensor(in_index, device=dev, dtype=torch.long))
+        oi = _index_list(out_index, self.out_features, "out_index", dev)
+        ii = _index_list(in_index, self.in_features, "in_index", dev)
         new = self.make_like(in_features=int(ii.numel()), out_features=int(oi.numel()))
         edges = lambda t: t.index_select(0, oi).index_select(1, ii)
         new.base_weight.copy_(edges(self.base_weight))

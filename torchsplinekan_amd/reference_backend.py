@@ -110,34 +110,43 @@ def curve2coeff(x_samples: torch.Tensor, y_samples: torch.Tensor, grid: torch.Te
     return out.to(dtype=x_samples.dtype, device=x_samples.device)
 
 
+def ridge_solve(gram: torch.Tensor, rhs: torch.Tensor, ridge: float) -> torch.Tensor:
+    """Solutions [I, R, M] of (G_i + lam * mean(diag G_i) * Id) X_i = rhs_i for a
+    batch of symmetric positive semi-definite G [I, R, R] (float64).
+
+    lam runs through the ladder ridge, 1e3 ridge, 1e6 ridge, 1e9 ridge and
+    stops at the first rung where every G_i's shifted matrix factors by
+    Cholesky; the batch shares one lam.  If none does, the top rung's systems
+    are solved by least squares.  This is the shift schedule of the
+    reference's fit (spline_kan/reference_backend.py:197-215)."""
+    if ridge <= 0:
+        raise ValueError(f"ridge must be positive, got {ridge}")
+    R = gram.shape[-1]
+    mean_diag = torch.diagonal(gram, dim1=-2, dim2=-1).sum(-1).clamp(min=1e-300) / R
+    shifted = gram
+    for rung in range(4):
+        lam = ridge * 1e3 ** rung
+        shifted = gram + torch.diag_embed((lam * mean_diag)[:, None].expand(-1, R))
+        factor, info = torch.linalg.cholesky_ex(shifted)
+        if int(info.count_nonzero()) == 0:
+            return torch.cholesky_solve(rhs, factor)
+    return torch.linalg.lstsq(shifted, rhs).solution
+
+
 def fit_spline_coeffs(x_samples: torch.Tensor, y_samples: torch.Tensor, grid: torch.Tensor,
                       k: int, ridge: float = 1e-12) -> torch.Tensor:
     """Ridge-regularised least-squares coefficients [O, I, R] of the curves
-    y [O, B, I] at x [B, I] on `grid`, per feature through the normal
-    equations in float64 on the samples' device: Cholesky of
-    A^T A + lam * (tr(A^T A)/R) I with lam = ridge, raised 1e3-fold (up to
-    three times) while the factorisation fails, then a general solve
+    y [O, B, I] sampled at x [B, I] on the knot rows `grid`, in float64 on
+    the samples' device: per feature, the normal equations A^T A c = A^T y of
+    the float64 basis A [B, R], solved by ridge_solve
     (spline_kan/reference_backend.py:173-215)."""
     if ridge <= 0:
         raise ValueError(f"ridge must be positive, got {ridge}")
-    A = compute_basis(x_samples.double(), grid.double(), k)                 # [B, I, R]
-    y = y_samples.double()                                                   # [O, B, I]
-    R = A.shape[-1]
-    AtA = torch.einsum("bir,bis->irs", A, A)
-    Aty = torch.einsum("bir,obi->iro", A, y)                                 # [I, R, O]
-    scale = AtA.diagonal(dim1=-2, dim2=-1).sum(-1).clamp(min=1e-300) / R
-    eye = torch.eye(R, dtype=torch.float64, device=A.device)
-    lam = ridge
-    for _ in range(4):
-        M = AtA + (lam * scale)[:, None, None] * eye
-        L, info = torch.linalg.cholesky_ex(M)
-        if not bool((info != 0).any()):
-            sol = torch.cholesky_solve(Aty, L)
-            break
-        lam *= 1e3
-    else:
-        sol = torch.linalg.lstsq(M, Aty).solution
-    return sol.permute(2, 0, 1).to(dtype=x_samples.dtype)
+    basis = compute_basis(x_samples.double(), grid.double(), k).transpose(0, 1)   # [I, B, R]
+    curves = y_samples.double().permute(2, 1, 0)                                 # [I, B, O]
+    gram = basis.transpose(1, 2) @ basis                                         # [I, R, R]
+    coeffs = ridge_solve(gram, basis.transpose(1, 2) @ curves, ridge)            # [I, R, O]
+    return coeffs.permute(2, 0, 1).to(dtype=x_samples.dtype)
 
 
 class ReferenceKANLayer(nn.Module):

@@ -31,6 +31,7 @@ in float64 on the same device:
 import torch
 
 from . import _lib
+from .reference_backend import ridge_solve
 
 
 def refit_gram(x_flat: torch.Tensor, grid_old: torch.Tensor, grid_new: torch.Tensor, k: int):
@@ -75,21 +76,7 @@ def solve_min_norm(gram: torch.Tensor, cross: torch.Tensor, coef: torch.Tensor,
 def solve_ridge(gram: torch.Tensor, cross: torch.Tensor, coef: torch.Tensor,
                 ridge: float = 1e-12) -> torch.Tensor:
     """Ridge-regularised normal-equation coefficients [O, I, Rn] (float64) of
-    fit_spline_coeffs (spline_kan/reference_backend.py:173-215)."""
-    if ridge <= 0:
-        raise ValueError(f"ridge must be positive, got {ridge}")
-    Rn = gram.shape[-1]
-    aty = torch.einsum("irs,ois->iro", cross, coef.to(torch.float64))    # [I, Rn, O]
-    scale = gram.diagonal(dim1=-2, dim2=-1).sum(-1).clamp(min=1e-300) / Rn
-    eye = torch.eye(Rn, dtype=torch.float64, device=gram.device)
-    lam = ridge
-    for _ in range(4):
-        M = gram + (lam * scale)[:, None, None] * eye
-        L, info = torch.linalg.cholesky_ex(M)
-        if not bool((info != 0).any()):
-            sol = torch.cholesky_solve(aty, L)
-            break
-        lam *= 1e3
-    else:
-        sol = torch.linalg.lstsq(M, aty).solution
-    return sol.permute(2, 0, 1)                                      # [O, I, Rn]
+    fit_spline_coeffs (spline_kan/reference_backend.py:173-215): the right-hand
+    side A_i^T y_old is C_i coef[:, i, :]^T, solved by the same shift ladder."""
+    rhs = cross @ coef.to(torch.float64).permute(1, 2, 0)            # [I, Rn, O]
+    return ridge_solve(gram, rhs, ridge).permute(2, 0, 1)            # [O, I, Rn]
