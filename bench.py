@@ -344,25 +344,60 @@ def _layer_tensors(layer):
 # timed GPU steps
 # ---------------------------------------------------------------------------
 
-def timed_steps(step, steps, warmup, classes):
+def timed_steps(step, steps, warmup, classes, params=()):
     """warmup untimed steps, then `steps` timed ones between two device
-    synchronisations, with the library's per-launch HIP-event timing on:
-    -> (wall seconds, {class: (ms, launches, work)})."""
+    synchronisations with nothing else running (the library's per-launch
+    timing off), then one more step for the memory figures and `steps`
+    instrumented ones for the per-kernel times (HIP events the library
+    records around each launch on its own stream):
+    -> (wall seconds of the timed steps, {class: (ms, launches, work)},
+        memory figures)."""
     import torch
     from torchsplinekan_amd import _lib
     for _ in range(warmup):
         step()
-    torch.cuda.synchronize()
-    _lib.timing_enable(True)
+    _lib.timing_enable(False)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(steps):
         step()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
+    mem = measure_memory(step, params)
+    _lib.timing_enable(True)
+    torch.cuda.synchronize()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
     kern = {c: _lib.timing_read(c) for c in classes}
     _lib.timing_enable(False)
-    return wall, kern
+    return wall, kern, mem
+
+
+def measure_memory(step, params):
+    """Device memory of one step as the reference's benchmark measures it
+    (benchmarks/bench_kan.py:308-329): gradients cleared, allocator peak
+    reset, one step; the peak over the step, its increment over what was
+    allocated before (parameters, inputs, targets), what the step leaves
+    allocated, and the gradients' bytes."""
+    import gc
+    import torch
+    for p in params:
+        p.grad = None
+    gc.collect()
+    torch.cuda.synchronize()
+    base = torch.cuda.memory_allocated()
+    torch.cuda.reset_peak_memory_stats()
+    step()
+    torch.cuda.synchronize()
+    peak = torch.cuda.max_memory_allocated()
+    after = torch.cuda.memory_allocated()
+    grads = sum(p.grad.numel() * p.grad.element_size() for p in params if p.grad is not None)
+    return {"peak_mem_bytes": peak, "baseline_bytes": base, "peak_increment_bytes": peak - base,
+            "retained_after_bytes": after - base, "grad_bytes": grads,
+            "method": "torch.cuda.max_memory_allocated over one step after "
+                      "reset_peak_memory_stats (benchmarks/bench_kan.py:308-329); every "
+                      "library workspace is a torch allocation"}
 
 
 def _mfma_roofline(kern, cls, kernel_name, traffic=None, traffic_source=None):
@@ -375,7 +410,7 @@ def _mfma_roofline(kern, cls, kernel_name, traffic=None, traffic_source=None):
             "launches": cnt}
 
 
-def _line(metric, N, steps, warmup, wall, workload, roofline, kern, **extra):
+def _line(metric, N, steps, warmup, wall, workload, roofline, kern, mem, **extra):
     line = {
         "metric": metric, "value": N * steps / wall, "unit": "samples/s", "n_gpus": 1,
         "steps": steps, "warmup": warmup, "ms_per_step": wall * 1e3 / steps,
@@ -384,8 +419,98 @@ def _line(metric, N, steps, warmup, wall, workload, roofline, kern, **extra):
         "config": {"workload": workload}, "roofline": roofline,
         "kernels": {c: {"ms_per_step": v[0] / steps, "launches_per_step": v[1] / steps}
                     for c, v in kern.items()},
+        "kernel_times": "from a separate instrumented pass of the same step count",
+        "peak_mem_bytes": mem["peak_mem_bytes"], "memory": mem,
     }
     line.update(extra)
+    return line
+
+
+def run_c3(args, dev, steps, warmup, need_dx=True):
+    """c3: KANLinear(1024 -> 1024, G=10, k=3) fp32, N = 65536, fwd + MSE +
+    bwd; with dx (three contractions: the metric's workload) or, as the
+    reference's benchmark runs it (benchmarks/bench_kan.py:168-175), with x
+    not requiring grad (two contractions)."""
+    import torch
+    import torch.nn.functional as F
+    N = args.n or 65536
+    L, xd, td, cpu_inputs = build_c3(dev, N, need_dx)
+    I, O, R = L.in_features, L.out_features, L.grid_size + L.spline_order
+    torch.cuda.synchronize()
+
+    def step():
+        for p in L.parameters():
+            p.grad = None
+        xd.grad = None
+        y = L(xd)
+        loss = F.mse_loss(y, td)
+        loss.backward()
+
+    wall, kernels, mem = timed_steps(step, steps, warmup,
+                                     ("contraction", "basis", "basis_grad", "other"),
+                                     list(L.parameters()) + [xd])
+    if L.last_backend != "cuda":
+        raise RuntimeError("the timed steps did not run on the native backend")
+    # per-step spans with events on the step's stream, outside the timed region
+    stream = torch.cuda.current_stream(dev)
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(steps)]
+    for i in range(steps):
+        ev[i][0].record(stream)
+        step()
+        ev[i][1].record(stream)
+    torch.cuda.synchronize()
+    step_ms = [a.elapsed_time(b) for a, b in ev]
+
+    traffic, source = recorded_traffic("c3" if need_dx else "c3-nodx")
+    roof = _mfma_roofline(kernels, "contraction",
+                          "gemm_pipe_kernel (fp32 MFMA contraction; average over the forward, "
+                          "parameter%s launches)" % (" and input" if need_dx else ""),
+                          traffic, source)
+    b_ms, b_cnt, b_work = kernels["basis"]
+    g_ms, g_cnt, g_work = kernels["basis_grad"]
+    c_ms = kernels["contraction"][0]
+    gbps = lambda w, ms, n: (w / n) / (ms / n * 1e-3) / 1e9 if n else None
+    line = {
+        "metric": METRIC if need_dx else
+        "fwd+bwd samples/s, KANLinear 1024->1024 G10 k3 N=64K, x without grad (2 contractions)",
+        "value": N * steps / wall,
+        "unit": "samples/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": warmup,
+        "ms_per_step": wall * 1e3 / steps,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded torch.Generator draws, random-init weights of the config)",
+        "config": {
+            "workload": ("c3: KANLinear(1024->1024, grid_size=10, spline_order=3) fp32, N=%d, "
+                         "fwd + MSE + bwd %s" % (N, "with dx (3 contractions)" if need_dx
+                                                 else "without dx (2 contractions; the "
+                                                 "reference benchmark's fwd_bwd)")),
+            "in_features": I, "out_features": O, "grid_size": L.grid_size,
+            "spline_order": L.spline_order, "samples_per_step": N, "x_requires_grad": need_dx,
+        },
+        "roofline": roof,
+        "step_ms_median_events": statistics.median(step_ms),
+        "kernels": {
+            "basis": {"avg_ms": b_ms / max(b_cnt, 1), "launches": b_cnt,
+                      "GB/s": gbps(b_work, b_ms, b_cnt)},
+            "basis_grad": {"avg_ms": g_ms / max(g_cnt, 1), "launches": g_cnt,
+                           "GB/s": gbps(g_work, g_ms, g_cnt)},
+            "contraction_ms_per_step": c_ms / steps,
+            "other_ms_per_step": kernels["other"][0] / steps,
+        },
+        "kernel_times": "from a separate instrumented pass of the same step count",
+        "peak_mem_bytes": mem["peak_mem_bytes"],
+        "memory": mem,
+    }
+    if not args.no_cpu_baseline:
+        x, coef, bw, scaler, target, grid = cpu_inputs
+        line["cpu_baseline"] = cpu_baseline_layers([(grid, bw, coef, scaler)], x, target, need_dx,
+                                                   args.cpu_seconds, 2048, "c3")
     return line
 
 
@@ -403,7 +528,9 @@ def run_c2(args, dev, steps, warmup):
             p.grad = None
         F.mse_loss(net(xd), td).backward()
 
-    wall, kern = timed_steps(step, steps, warmup, ("contraction", "basis", "basis_grad", "other"))
+    wall, kern, mem = timed_steps(step, steps, warmup,
+                                  ("contraction", "basis", "basis_grad", "other"),
+                                  list(net.parameters()))
     if any(l.last_backend != "cuda" for l in net.layers):
         raise RuntimeError("c2 did not run on the native backend")
     line = _line("fwd+bwd samples/s, KAN([784,256,10]) G5 k3 N=4096", N, steps, warmup, wall,
@@ -413,7 +540,7 @@ def run_c2(args, dev, steps, warmup):
                                 "forward and parameter products of the first layer) and the "
                                 "thin-product kernels (thin_wide_cols/thin_wide_rows/"
                                 "thin_short_k: forward, parameter and input products of the "
-                                "10-wide output layer)", *recorded_traffic("c2")), kern)
+                                "10-wide output layer)", *recorded_traffic("c2")), kern, mem)
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline_layers(
             [_layer_tensors(l) for l in net.layers], x, target, False, args.cpu_seconds, 1024,
@@ -436,8 +563,9 @@ def run_c4(args, dev, steps, warmup):
         y, reg = net.forward_with_regularization(xd, 1e-2, 1e-2, reg_impl="auto")
         (F.mse_loss(y, td) + reg).backward()
 
-    wall, kern = timed_steps(step, steps, warmup, ("edge", "edge_grad", "basis", "basis_grad",
-                                                   "contraction", "other"))
+    wall, kern, mem = timed_steps(step, steps, warmup, ("edge", "edge_grad", "basis",
+                                                        "basis_grad", "contraction", "other"),
+                                  list(net.parameters()))
     if any(l.last_backend != "cuda" for l in net.layers):
         raise RuntimeError("c4 did not run the fused native path")
     # dominant kernel class: the edge-statistic backward on FP32 MFMA (fused
@@ -453,7 +581,7 @@ def run_c4(args, dev, steps, warmup):
                  N, steps, warmup, wall,
                  "c4: KAN([256,512,512,64], G=8, k=3) fp32, N=%d, update_grid knots, "
                  "forward_with_regularization(1e-2, 1e-2, 'auto') + MSE + backward" % N, roof,
-                 kern, edge_forward_tflops=e_work / (e_ms * 1e-3) / 1e12 if e_cnt else 0.0)
+                 kern, mem, edge_forward_tflops=e_work / (e_ms * 1e-3) / 1e12 if e_cnt else 0.0)
     if not args.no_cpu_baseline:
         from torchsplinekan_amd import KAN
         net_cpu = KAN([256, 512, 512, 64], grid_size=8, spline_order=3, backend="reference")
@@ -477,7 +605,9 @@ def run_c5(args, dev, steps, warmup):
         xd.grad = None
         F.mse_loss(L(xd), td).backward()
 
-    wall, kern = timed_steps(step, steps, warmup, ("contraction", "basis", "basis_grad", "other"))
+    wall, kern, mem = timed_steps(step, steps, warmup,
+                                  ("contraction", "basis", "basis_grad", "other"),
+                                  list(L.parameters()) + [xd])
     if L.last_backend != "cuda":
         raise RuntimeError("c5 did not run on the native backend")
     line = _line("fwd+bwd samples/s, KANLinear 4096->256 G65 k3 N=8192", N, steps, warmup, wall,
@@ -485,7 +615,7 @@ def run_c5(args, dev, steps, warmup):
                  "+ bwd with dx (3 contractions)" % N,
                  _mfma_roofline(kern, "contraction", "gemm_pipe_kernel (fp32 MFMA contraction; "
                                 "forward, parameter and input products)", *recorded_traffic("c5")),
-                 kern)
+                 kern, mem)
     b_ms, b_cnt, b_work = kern["basis"]
     if b_cnt:
         line["basis_GBps"] = b_work / max(b_cnt, 1) / (b_ms / b_cnt * 1e-3) / 1e9
@@ -789,92 +919,12 @@ def main():
         other[args.workload](args)
         return
 
-    N = args.n or 65536
-    need_dx = args.workload == "c3"
-    L, xd, td, cpu_inputs = build_c3(dev, N, need_dx)
-    I, O, R = L.in_features, L.out_features, L.grid_size + L.spline_order
-    torch.cuda.synchronize()
-
-    def step():
-        for p in L.parameters():
-            p.grad = None
-        xd.grad = None
-        y = L(xd)
-        loss = F.mse_loss(y, td)
-        loss.backward()
-
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-
-    from torchsplinekan_amd import _lib
-    stream = torch.cuda.current_stream(dev)
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-          for _ in range(args.steps)]
-    _lib.timing_enable(True)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for i in range(args.steps):
-        ev[i][0].record(stream)
-        step()
-        ev[i][1].record(stream)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    if L.last_backend != "cuda":
-        raise RuntimeError("the timed steps did not run on the native backend")
-    step_ms = [a.elapsed_time(b) for a, b in ev]
-    kernels = {cls: _lib.timing_read(cls) for cls in ("contraction", "basis", "basis_grad",
-                                                       "other")}
-    _lib.timing_enable(False)
-
-    c_ms, c_cnt, c_work = kernels["contraction"]
-    traffic, source = recorded_traffic("c3")
-    roof = _mfma_roofline(kernels, "contraction",
-                          "gemm_pipe_kernel (fp32 MFMA contraction; average over the forward, "
-                          "parameter and input launches)", traffic, source)
-    b_ms, b_cnt, b_work = kernels["basis"]
-    g_ms, g_cnt, g_work = kernels["basis_grad"]
-    gbps = lambda w, ms, n: (w / n) / (ms / n * 1e-3) / 1e9 if n else None
-    line = {
-        "metric": METRIC,
-        "value": N * args.steps / wall,
-        "unit": "samples/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": wall * 1e3 / args.steps,
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "f32",
-        "data": "synthetic (seeded torch.Generator draws, random-init weights of the config)",
-        "config": {
-            "workload": ("c3: KANLinear(1024->1024, grid_size=10, spline_order=3) fp32, N=%d, "
-                         "fwd + MSE + bwd %s" % (N, "with dx (3 contractions)" if need_dx
-                                                 else "without dx (2 contractions)")),
-            "in_features": I, "out_features": O, "grid_size": L.grid_size,
-            "spline_order": L.spline_order, "samples_per_step": N, "x_requires_grad": need_dx,
-        },
-        "roofline": roof,
-        "step_ms_median_events": statistics.median(step_ms),
-        "kernels": {
-            "basis": {"avg_ms": b_ms / max(b_cnt, 1), "launches": b_cnt,
-                      "GB/s": gbps(b_work, b_ms, b_cnt)},
-            "basis_grad": {"avg_ms": g_ms / max(g_cnt, 1), "launches": g_cnt,
-                           "GB/s": gbps(g_work, g_ms, g_cnt)},
-            "contraction_ms_per_step": c_ms / args.steps,
-            "other_ms_per_step": kernels["other"][0] / args.steps,
-        },
-    }
-    if not args.no_cpu_baseline:
-        x, coef, bw, scaler, target, grid = cpu_inputs
-        line["cpu_baseline"] = cpu_baseline_layers([(grid, bw, coef, scaler)], x, target, need_dx,
-                                                   args.cpu_seconds, 2048, "c3")
+    line = run_c3(args, dev, args.steps, args.warmup, need_dx=args.workload == "c3")
     if args.workload == "c3" and not args.no_other_configs and not args.n:
-        del L, xd, td, cpu_inputs
         torch.cuda.empty_cache()
         line["other_configs"] = {}
-        for name, fn in (("c2", run_c2), ("c4", run_c4), ("c5", run_c5)):
+        nodx = lambda a, d, st, w: run_c3(a, d, st, w, need_dx=False)
+        for name, fn in (("c3-nodx", nodx), ("c2", run_c2), ("c4", run_c4), ("c5", run_c5)):
             try:
                 line["other_configs"][name] = fn(args, dev, args.steps, args.warmup)
             except Exception as exc:  # reported in the line; the metric stands on its own

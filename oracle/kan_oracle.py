@@ -376,7 +376,8 @@ def kan_forward(x, grid, base_weight, spline_weight, spline_scaler, k, basis=Non
     return y, H
 
 
-def kan_backward(D, x, grid, base_weight, spline_weight, spline_scaler, k, basis=None):
+def kan_backward(D, x, grid, base_weight, spline_weight, spline_scaler, k, basis=None,
+                 basis_deriv=None):
     """Analytic first-order backward -> (gx, gbw | None, gsw, gscaler | None):
       gbw     = D^T silu(x)
       DtH     = D^T H;  gsw = scaler * DtH;  gscaler = sum_r sw * DtH
@@ -394,7 +395,8 @@ def kan_backward(D, x, grid, base_weight, spline_weight, spline_scaler, k, basis
         gsw, gsc = DtH, None
     W = _eff_weight(spline_weight, spline_scaler)
     DW = (D @ W.reshape(O, I * R)).reshape(N, I, R)
-    gx = (DW * basis_derivative(x, grid, k)).sum(axis=2)
+    dB = basis_derivative(x, grid, k) if basis_deriv is None else basis_deriv
+    gx = (DW * dB).sum(axis=2)
     if base_weight is not None:
         gx = gx + (D @ base_weight) * silu_grad(x)
     return gx, gbw, gsw, gsc

@@ -2,12 +2,14 @@
 functions bench.py times (bench.build_c2 .. build_c5), against the fp64
 oracle at the north star's fp32 bar (normwise relative 1e-5):
 
-* c3: KANLinear 1024 -> 1024 G10 k3, N = 65536, x with grad: y and dx on 64
-  rows, dcoef / dscaler / dbase_w on 64 edges over all samples.
+* c3: KANLinear 1024 -> 1024 G10 k3, N = 65536, x with grad: every element
+  of y, dx, dcoef, dscaler and dbase_w (tests/_fullcheck.py: the oracle in
+  row chunks; each tensor held to the bar block by block, so one faulty
+  output tile of the c3 schedule cannot hide in the whole-tensor norm).
 * c5: KANLinear 4096 -> 256 G65 k3, N = 8192 (N I (G + 2k) = 2.38e9, past
-  the reference's 32-bit guard): the same checks, exact zero basis rows
-  outside the knot span, and the edge statistic on the c5 basis (2.28e9
-  elements) with its backward.
+  the reference's 32-bit guard): the same whole-tensor checks, exact zero
+  basis rows outside the knot span, and the edge statistic on the c5 basis
+  (2.28e9 elements) with its backward.
 * c4: KAN([256, 512, 512, 64]) G8 with update_grid knots on the Gaussian
   mixture, forward_with_regularization(1e-2, 1e-2, "auto") + MSE + backward:
   per layer, outputs on rows, the regulariser from the oracle's edge means
@@ -55,27 +57,10 @@ _params = _netcheck.params
 basis_threaded = _netcheck.basis_threaded
 
 
-def _edge_param_oracle(D, x, grid, bw, sw, sc, k, edges):
-    """dbw, dcoef, dscaler of sampled edges over all samples, each edge as a
-    1 x 1 sub-layer of the oracle's kan_backward_params (an edge's gradients
-    depend only on its own input column and output column of D)."""
-    gbw, gsw, gsc = [], [], []
-    for o, i in edges:
-        Hi = ko.basis_dense(x[:, i:i + 1], grid[i:i + 1], k)
-        b, w, c = ko.kan_backward_params(D[:, o:o + 1], x[:, i:i + 1], bw[o:o + 1, i:i + 1],
-                                         sw[o:o + 1, i:i + 1], sc[o:o + 1, i:i + 1], Hi)
-        gbw.append(b[0, 0])
-        gsw.append(w[0, 0])
-        gsc.append(c[0, 0])
-    return np.array(gbw), np.array(gsw), np.array(gsc)
-
-
-_sample_edges = _netcheck.sample_edges
-
-
-def _check_single_layer(L, xd, td, x_cpu, k, n_rows, n_edges, tag):
-    """One training step of a single KANLinear (the bench's step) and its
-    outputs against the oracle on rows and sampled edges."""
+def _check_whole_step(L, xd, td, x_cpu, k, tag):
+    """One training step of a single KANLinear (the bench's step); every
+    element of its outputs against the oracle (tests/_fullcheck.py)."""
+    from tests import _fullcheck
     for p in L.parameters():
         p.grad = None
     y = L(xd)
@@ -83,36 +68,21 @@ def _check_single_layer(L, xd, td, x_cpu, k, n_rows, n_edges, tag):
     torch.cuda.synchronize()
     assert L.last_backend == "cuda"
     N, O = y.shape
-    I = xd.shape[1]
-    grid, bw, sw, sc = _params(L)
-    x = x_cpu.detach().double().numpy()
     D = 2.0 * (np64(y) - np64(td)) / (N * O)
-    rows = np.unique(np.linspace(0, N - 1, n_rows).astype(int))
-    ry, H = ko.kan_forward(x[rows], grid, bw, sw, sc, k)
-    e = normwise(np64(y[rows]), ry)
-    _say(f"{tag}: y rows {e:.2e}")
-    assert e < TOL
-    rgx, _, _, _ = ko.kan_backward(D[rows], x[rows], grid, bw, sw, sc, k, basis=H)
-    e = normwise(np64(xd.grad[rows]), rgx)
-    _say(f"{tag}: dx rows {e:.2e}")
-    assert e < TOL
-    edges = _sample_edges(O, I, n_edges, seed=N)
-    gbw, gsw, gsc = _edge_param_oracle(D, x, grid, bw, sw, sc, k, edges)
-    oo, ii = map(list, zip(*edges))
-    for name, got, ref in (("dbase_w", L.base_weight.grad[oo, ii], gbw),
-                           ("dcoef", L.spline_weight.grad[oo, ii], gsw),
-                           ("dscaler", L.spline_scaler.grad[oo, ii], gsc)):
-        e = normwise(np64(got), ref)
-        _say(f"{tag}: {name} on {len(edges)} edges {e:.2e}")
-        assert e < TOL, name
+    errs = _fullcheck.check_layer_step(L, x_cpu, y.detach(), xd.grad, D, k,
+                                       lambda m: _say(f"{tag}: {m}"))
+    for name, (worst, block, whole) in errs.items():
+        _say(f"{tag}: {name} whole-tensor {whole:.2e}, worst block {worst:.2e} at {block}")
+    for name, (worst, block, whole) in errs.items():
+        assert worst < TOL, (name, worst, block)
 
 
 @pytest.mark.timeout(900)
 def test_c3_training_step_matches_oracle(bench):
     dev = torch.device("cuda", 0)
     L, xd, td, cpu = bench.build_c3(dev, 65536, need_dx=True)
-    _say("c3: KANLinear 1024->1024 G10 k3 N=65536 fwd+MSE+bwd with dx")
-    _check_single_layer(L, xd, td, cpu[0], 3, n_rows=64, n_edges=64, tag="c3")
+    _say("c3: KANLinear 1024->1024 G10 k3 N=65536 fwd+MSE+bwd with dx, every element")
+    _check_whole_step(L, xd, td, cpu[0], 3, tag="c3")
 
 
 @pytest.mark.timeout(900)
@@ -123,8 +93,8 @@ def test_c5_kernel_limit_layer_full_size(bench):
     k = 3
     assert N * I * (L.grid_size + 2 * k) > 2 ** 31 - 1   # past the reference's guard
     xd, td = x.to(dev).requires_grad_(), target.to(dev)
-    _say("c5: KANLinear 4096->256 G65 k3 N=8192 fwd+MSE+bwd with dx")
-    _check_single_layer(L, xd, td, x, k, n_rows=32, n_edges=48, tag="c5")
+    _say("c5: KANLinear 4096->256 G65 k3 N=8192 fwd+MSE+bwd with dx, every element")
+    _check_whole_step(L, xd, td, x, k, tag="c5")
     # basis past 2^31 elements: exact zero rows outside [t_0, t_71], values on rows
     from torchsplinekan_amd import _C
     with torch.no_grad():
