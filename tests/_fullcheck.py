@@ -55,7 +55,7 @@ def block_error(got, ref, bm, bn):
     return float(err[worst]), (int(worst[0]) * bm, int(worst[1]) * bn), whole
 
 
-def check_layer_step(layer, x_cpu, y_dev, gx_dev, D, k, say, chunk=4096):
+def check_layer_step(layer, x_cpu, y_dev, gx_dev, D, k, say, chunk=None):
     """Errors of every output of one layer step against the oracle.
 
     layer: the KANLinear after backward (its .grad fields filled); x_cpu the
@@ -67,7 +67,9 @@ def check_layer_step(layer, x_cpu, y_dev, gx_dev, D, k, say, chunk=4096):
     bw, sw, sc = np64(layer.base_weight), np64(layer.spline_weight), np64(layer.spline_scaler)
     x = x_cpu.detach().double().numpy()
     N, I = x.shape
-    O = sw.shape[0]
+    O, _, R = sw.shape
+    if chunk is None:       # about 1 GB of float64 basis per chunk
+        chunk = max(256, min(4096, (1 << 27) // (I * R)))
     y_got = np64(y_dev)
     gx_got = np64(gx_dev) if gx_dev is not None else None
     y_ref = np.empty((N, O))
@@ -93,7 +95,6 @@ def check_layer_step(layer, x_cpu, y_dev, gx_dev, D, k, say, chunk=4096):
         if (n0 // chunk) % 4 == 3:
             say(f"oracle rows {n1}/{N}, {time.time() - t0:.1f} s")
     say(f"oracle over {N} rows in {time.time() - t0:.1f} s")
-    R = sw.shape[2]
     out = {"y": block_error(y_got, y_ref, 256, 256)}
     if gx_ref is not None:
         out["dx"] = block_error(gx_got, gx_ref, 256, 256)
