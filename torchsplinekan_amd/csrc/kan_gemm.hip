@@ -1003,7 +1003,6 @@ template <class C>
 bool ecomp_cfg_fits(int64_t N, int64_t I, int R, int nk, bool has_base) {
   typedef Slab<C::BN, C::BK, true> SB;
   constexpr int64_t kSide = 2 * SB::kElems / (C::WM * C::WN);
-  if (nk > 128) return false;  // (the epilogue's span search takes 7 halving steps)
   const int64_t ksp = I * R;
   for (int64_t c0 = 0; c0 < N; c0 += C::TN) {
     const DxBlock b(c0, N, ksp, R, C::TN, has_base);
