@@ -91,7 +91,25 @@ struct BasisShape {
   int waves;  // waves per block
   int vec;    // 16-byte vector path for the staged rows (alignment holds)
   int64_t ld_aux;  // row stride of silu(x) (basis) or of its gradient (basis_grad)
+  int nfb;    // feature blocks (ceil(I / fb))
 };
+
+// Block of a basis launch: feature block f and sample-row group g.  The
+// launch is a 1-D grid of nfb x (row groups) workgroups whose ids are
+// remapped (xcd_remap) so that each XCD takes a contiguous range of logical
+// blocks, feature block fastest.  An XCD then streams whole consecutive
+// sample rows of the [n, ld] rows; with the 2-D grid dealt round-robin, XCD
+// j took feature blocks j and j + 8 of every row, a strided eighth of the
+// whole buffer.  Measured at c3: basis 0.757 -> 0.713 ms, basis_grad 0.839
+// -> 0.810 ms.
+struct BasisBlock {
+  int f;
+  int64_t g;
+};
+__device__ __forceinline__ BasisBlock basis_block(const BasisShape& sh) {
+  const int id = xcd_remap((int)blockIdx.x, (int)gridDim.x);
+  return {id % sh.nfb, (int64_t)(id / sh.nfb)};
+}
 
 // 16-byte vector of T.
 template <typename T>
@@ -208,12 +226,13 @@ __global__ __launch_bounds__(kBasisThreads) void basis_kernel(
   extern __shared__ __align__(16) unsigned char smem[];
   const int nk = sh.G + 2 * K + 1, R = sh.G + K;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int i0 = blockIdx.x * sh.fb;
+  const BasisBlock bb = basis_block(sh);
+  const int i0 = bb.f * sh.fb;
   const int fbv = min(sh.fb, sh.I - i0);
   const int sub = lane / sh.fb, fi = lane - sub * sh.fb;
   const bool lane_ok = sub < sh.subs && fi < fbv;
   const int64_t step = (int64_t)sh.waves * sh.subs;
-  const int64_t nbase = (int64_t)blockIdx.y * sh.iters * step + (int64_t)wave * sh.subs;
+  const int64_t nbase = bb.g * sh.iters * step + (int64_t)wave * sh.subs;
   T xs[kMaxIters];
 #pragma unroll
   for (int it = 0; it < kMaxIters; ++it) {
@@ -311,7 +330,8 @@ __global__ __launch_bounds__(kBasisThreads) void basis_grad_kernel(
   extern __shared__ __align__(16) unsigned char smem[];
   const int nk = sh.G + 2 * K + 1, R = sh.G + K;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int i0 = blockIdx.x * sh.fb;
+  const BasisBlock bb = basis_block(sh);
+  const int i0 = bb.f * sh.fb;
   const int fbv = min(sh.fb, sh.I - i0);
   T* knots = stage_knots<T>(smem, grid, i0, fbv, nk);
   T* stage = knots + round_up((int64_t)sh.fb * nk, 4) + wave * 64 * R;
@@ -321,7 +341,7 @@ __global__ __launch_bounds__(kBasisThreads) void basis_grad_kernel(
   const bool lane_ok = sub < sh.subs && fi < fbv;
   const T* t = knots + fi * nk;
   const int64_t step = (int64_t)sh.waves * sh.subs;
-  int64_t nbase = (int64_t)blockIdx.y * sh.iters * step + (int64_t)wave * sh.subs;
+  int64_t nbase = bb.g * sh.iters * step + (int64_t)wave * sh.subs;
   const T* row = stage + lane * R;
   const bool vec = sh.vec != 0;
 
@@ -589,7 +609,8 @@ __global__ __launch_bounds__(kBasisThreads) void basis_grad_pf_kernel(
   extern __shared__ __align__(16) unsigned char smem[];
   const int nk = sh.G + 2 * K + 1, R = sh.G + K;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int i0 = blockIdx.x * sh.fb;
+  const BasisBlock bb = basis_block(sh);
+  const int i0 = bb.f * sh.fb;
   const int fbv = min(sh.fb, sh.I - i0);
   T* knots = stage_knots<T>(smem, grid, i0, fbv, nk);
   T* stage = knots + round_up((int64_t)sh.fb * nk, 4) + wave * 64 * R;
@@ -601,7 +622,7 @@ __global__ __launch_bounds__(kBasisThreads) void basis_grad_pf_kernel(
   const int fi = lane_ok ? lane : 0;
   const T* t = knots + fi * nk;
   const int64_t step = sh.waves;
-  int64_t nn = (int64_t)blockIdx.y * sh.iters * step + wave;
+  int64_t nn = bb.g * sh.iters * step + wave;
   const T* row = stage + lane * R;
   VT pf[PV];
   T tail = T(0), xn = T(0), gbn = T(0);
@@ -667,14 +688,15 @@ __global__ __launch_bounds__(kBasisThreads) void basis_grad_window_kernel(
   extern __shared__ __align__(16) unsigned char smem[];
   const int nk = sh.G + 2 * K + 1, R = sh.G + K;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int i0 = blockIdx.x * sh.fb;
+  const BasisBlock bb = basis_block(sh);
+  const int i0 = bb.f * sh.fb;
   const int fbv = min(sh.fb, sh.I - i0);
   T* knots = stage_knots<T>(smem, grid, i0, fbv, nk);
   const int sub = lane / sh.fb, fi = lane - sub * sh.fb;
   const bool lane_ok = sub < sh.subs && fi < fbv;
   const T* t = knots + (lane_ok ? fi : 0) * nk;
   const int64_t step = (int64_t)sh.waves * sh.subs;
-  int64_t nn = (int64_t)blockIdx.y * sh.iters * step + (int64_t)wave * sh.subs + sub;
+  int64_t nn = bb.g * sh.iters * step + (int64_t)wave * sh.subs + sub;
   const int64_t col = (int64_t)i0 + (lane_ok ? fi : 0);
   T xn = (lane_ok && nn < sh.n) ? x[nn * sh.I + col] : T(0);
   __syncthreads();  // knot rows staged
@@ -720,14 +742,15 @@ __global__ __launch_bounds__(kBasisThreads) void basis_grad_compact_kernel(
   extern __shared__ __align__(16) unsigned char smem[];
   const int nk = sh.G + 2 * K + 1, R = sh.G + K;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int i0 = blockIdx.x * sh.fb;
+  const BasisBlock bb = basis_block(sh);
+  const int i0 = bb.f * sh.fb;
   const int fbv = min(sh.fb, sh.I - i0);
   float* knots = stage_knots<float>(smem, grid, i0, fbv, nk);
   const int sub = lane / sh.fb, fi = lane - sub * sh.fb;
   const bool lane_ok = sub < sh.subs && fi < fbv;
   const float* t = knots + (lane_ok ? fi : 0) * nk;
   const int64_t step = (int64_t)sh.waves * sh.subs;
-  int64_t nn = (int64_t)blockIdx.y * sh.iters * step + (int64_t)wave * sh.subs + sub;
+  int64_t nn = bb.g * sh.iters * step + (int64_t)wave * sh.subs + sub;
   const int64_t col = (int64_t)i0 + (lane_ok ? fi : 0);
   typedef float f4 __attribute__((ext_vector_type(4)));
   float xn = 0.0f, bn = 0.0f, wn[K + 1];
@@ -792,6 +815,7 @@ BasisShape make_shape(int64_t n, int64_t I, int G, int R, size_t elem, int64_t l
   sh.G = G;
   sh.ld_aux = ld;
   sh.fb = (int)(I < 64 ? I : 64);
+  sh.nfb = (int)ceil_div(I, sh.fb);
   sh.subs = 64 / sh.fb;
   sh.waves = 4;
   // a dense R-row stage per lane bounds the waves of a block by LDS
@@ -845,8 +869,8 @@ int launch_basis(const T* x, const T* grid, T* out, int64_t ld_out, T* silu_out,
   int64_t by = 0;
   BasisShape sh = make_shape(n, I, G, R, sizeof(T), ld_out, out, &by, !rec);
   if (ld_silu >= 0) sh.ld_aux = ld_silu;
-  if (by > 2147483647LL) return set_error(KAN_ERR_LIMIT, "basis: too many samples (%lld)", (long long)n);
-  dim3 grid_dim((unsigned)ceil_div(I, sh.fb), (unsigned)by);
+  if (sh.nfb * by > 2147483647LL) return set_error(KAN_ERR_LIMIT, "basis: too many samples (%lld)", (long long)n);
+  const dim3 grid_dim((unsigned)(sh.nfb * by));
   const size_t smem = rec ? basis_window_smem<T>(sh, nk, k) : basis_smem<T>(sh, nk, R);
   // algorithmic bytes: read x, write the R basis values (+ silu) per item
   TimedLaunch timed(kClassBasis, st,
@@ -888,11 +912,11 @@ bool launch_grad_pf(const T* x, const T* grid, const T* gH, int64_t ld_g, const 
   const int64_t steps = ceil_div(n, (int64_t)sh.waves);
   sh.iters = 2;
   by = ceil_div(steps, (int64_t)sh.iters);
-  if (by > 2147483647LL) {
+  if (sh.nfb * by > 2147483647LL) {
     *rc = set_error(KAN_ERR_LIMIT, "basis_grad: too many samples");
     return true;
   }
-  dim3 grid_dim((unsigned)ceil_div(I, sh.fb), (unsigned)by);
+  const dim3 grid_dim((unsigned)(sh.nfb * by));
   const size_t smem = basis_smem<T>(sh, nk, R);
 #define KAN_BGPF(KK, PVV)                                                                         \
   hipLaunchKernelGGL((basis_grad_pf_kernel<KK, T, DER, PVV>), grid_dim, dim3(64 * sh.waves), smem, \
@@ -931,8 +955,8 @@ int launch_basis_grad_compact(const float* x, const float* grid, const float* ew
                     4.0 * (double)n * (double)I * (2.0 + (k + 1) + (es ? 1 : 0)));
   int64_t by = 0;
   BasisShape sh = make_shape(n, I, G, R, sizeof(float), 0, ew, &by, false);
-  if (by > 2147483647LL) return set_error(KAN_ERR_LIMIT, "basis_grad: too many samples");
-  dim3 grid_dim((unsigned)ceil_div(I, sh.fb), (unsigned)by);
+  if (sh.nfb * by > 2147483647LL) return set_error(KAN_ERR_LIMIT, "basis_grad: too many samples");
+  const dim3 grid_dim((unsigned)(sh.nfb * by));
   const size_t smem = sizeof(float) * (size_t)round_up((int64_t)sh.fb * nk, 4);
 #define KAN_BGC(KK)                                                                           \
   hipLaunchKernelGGL((basis_grad_compact_kernel<KK>), grid_dim, dim3(64 * sh.waves), smem, st, \
@@ -958,8 +982,8 @@ int launch_basis_grad(const T* x, const T* grid, const T* gH, int64_t ld_g, cons
     int64_t by = 0;
     BasisShape sh = make_shape(n, I, G, R, sizeof(T), ld_g, gH, &by, false);
     if (ld_base >= 0) sh.ld_aux = ld_base;
-    if (by > 2147483647LL) return set_error(KAN_ERR_LIMIT, "basis_grad: too many samples");
-    dim3 grid_dim((unsigned)ceil_div(I, sh.fb), (unsigned)by);
+    if (sh.nfb * by > 2147483647LL) return set_error(KAN_ERR_LIMIT, "basis_grad: too many samples");
+    const dim3 grid_dim((unsigned)(sh.nfb * by));
     const size_t smem = sizeof(T) * (size_t)round_up((int64_t)sh.fb * nk, 4);
 #define KAN_BGW(KK)                                                                        \
   hipLaunchKernelGGL((basis_grad_window_kernel<KK, T, 1>), grid_dim, dim3(64 * sh.waves), \
@@ -976,8 +1000,8 @@ int launch_basis_grad(const T* x, const T* grid, const T* gH, int64_t ld_g, cons
   int64_t by = 0;
   BasisShape sh = make_shape(n, I, G, R, sizeof(T), ld_g, gH, &by);
   if (ld_base >= 0) sh.ld_aux = ld_base;
-  if (by > 2147483647LL) return set_error(KAN_ERR_LIMIT, "basis_grad: too many samples");
-  dim3 grid_dim((unsigned)ceil_div(I, sh.fb), (unsigned)by);
+  if (sh.nfb * by > 2147483647LL) return set_error(KAN_ERR_LIMIT, "basis_grad: too many samples");
+  const dim3 grid_dim((unsigned)(sh.nfb * by));
   const size_t smem = basis_smem<T>(sh, nk, R);
 #define KAN_BGRAD_LAUNCH(KK, IM)                                                             \
   hipLaunchKernelGGL((basis_grad_kernel<KK, T, IM>), grid_dim, dim3(64 * sh.waves), smem, st, \
@@ -1017,8 +1041,8 @@ int launch_basis_deriv(const T* x, const T* grid, T* out, int64_t n, int64_t I, 
   const bool rec = R >= kWindowRecordMinR;
   int64_t by = 0;
   BasisShape sh = make_shape(n, I, G, R, sizeof(T), I * R, out, &by, !rec);
-  if (by > 2147483647LL) return set_error(KAN_ERR_LIMIT, "basis_deriv: too many samples");
-  dim3 grid_dim((unsigned)ceil_div(I, sh.fb), (unsigned)by);
+  if (sh.nfb * by > 2147483647LL) return set_error(KAN_ERR_LIMIT, "basis_deriv: too many samples");
+  const dim3 grid_dim((unsigned)(sh.nfb * by));
   const size_t smem = rec ? basis_window_smem<T>(sh, nk, k) : basis_smem<T>(sh, nk, R);
   TimedLaunch timed(kClassBasis, st, (double)sizeof(T) * (double)n * (double)I * (1.0 + R));
 #define KAN_BDER_LAUNCH(KK, DD)                                                                \
@@ -1066,8 +1090,8 @@ int launch_basis_deriv_contract(const T* x, const T* grid, const T* gH, T* gx, i
     return rc;
   int64_t by = 0;
   BasisShape sh = make_shape(n, I, G, R, sizeof(T), I * R, gH, &by);
-  if (by > 2147483647LL) return set_error(KAN_ERR_LIMIT, "basis_deriv_contract: too many samples");
-  dim3 grid_dim((unsigned)ceil_div(I, sh.fb), (unsigned)by);
+  if (sh.nfb * by > 2147483647LL) return set_error(KAN_ERR_LIMIT, "basis_deriv_contract: too many samples");
+  const dim3 grid_dim((unsigned)(sh.nfb * by));
   const size_t smem = basis_smem<T>(sh, nk, R);
 #define KAN_BDC_LAUNCH(KK, DD)                                                                  \
   hipLaunchKernelGGL((basis_grad_kernel<KK, T, 1, DD>), grid_dim, dim3(64 * sh.waves), smem, st, \
