@@ -36,6 +36,7 @@ if ROOT not in sys.path:
 
 METRIC = "fwd+bwd samples/s, KANLinear 1024→1024 G10 k3 N=64K; % MFMA/HBM roofline"
 PEAK_FP32_MFMA_TFLOPS = 157.3
+PEAK_FP64_TFLOPS = 78.6  # FP64 MFMA and FP64 vector alike
 PEAK_HBM_GBS = 8000.0
 TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "hbm_traffic_recorded.json")
 
@@ -73,6 +74,9 @@ def parse():
                          "KAN([2,128,128,1]) through create_graph) or infer (c3's layer, "
                          "exported, inference forward); all but c3 are reported separately, "
                          "not the metric")
+    ap.add_argument("--dtype", default="f32", choices=["f32", "f64"],
+                    help="arithmetic type of c3, c3-nodx and c4 (the metric is f32; f64 lines "
+                         "are reported against the FP64 peak)")
     ap.add_argument("--n", type=int, default=0, help="samples per step (default: the config's)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-other-configs", action="store_true",
@@ -113,9 +117,10 @@ def make_inputs(N, I, O, G, k, seed=0):
     return x, coef, bw, scaler, target
 
 
-def build_c3(dev, N=65536, need_dx=True):
+def build_c3(dev, N=65536, need_dx=True, dtype=None):
     """(layer on dev, x on dev with requires_grad=need_dx, target on dev,
-    CPU copies of (x, coef, bw, scaler, target, grid)) for c3."""
+    CPU copies of (x, coef, bw, scaler, target, grid)) for c3; dtype float64
+    casts the same draws (layer, x and target) after they are made."""
     import torch
     from torchsplinekan_amd import KANLinear
     I = O = 1024
@@ -127,9 +132,10 @@ def build_c3(dev, N=65536, need_dx=True):
         L.base_weight.copy_(bw)
         L.spline_scaler.copy_(scaler)
     grid_cpu = L.grid.detach().clone()
-    L = L.to(dev)
-    xd = x.to(dev).requires_grad_(need_dx)
-    return L, xd, target.to(dev), (x, coef, bw, scaler, target, grid_cpu)
+    dt = dtype or torch.float32
+    L = L.to(dev, dt)
+    xd = x.to(dev, dt).requires_grad_(need_dx)
+    return L, xd, target.to(dev, dt), (x, coef, bw, scaler, target, grid_cpu)
 
 
 def build_c2(dev, N=4096):
@@ -151,7 +157,7 @@ def build_c2(dev, N=4096):
     return net.to(dev), x, target
 
 
-def build_c4(dev, N=16384):
+def build_c4(dev, N=16384, dtype=None):
     """c4: KAN([256, 512, 512, 64], G=8, k=3) fp32; x [N, 256] from a
     4-component Gaussian mixture (means +-0.5, +-0.8, sd 0.1, equal weights);
     coef ~ N(0, 0.1); knots and coefficients then set by the network's
@@ -170,10 +176,11 @@ def build_c4(dev, N=16384):
     with torch.no_grad():
         for layer in net.layers:
             layer.spline_weight.normal_(0.0, 0.1, generator=g)
-    net = net.to(dev)
-    xd = x.to(dev)
+    dt = dtype or torch.float32
+    net = net.to(dev, dt)
+    xd = x.to(dev, dt)
     net.update_grid(xd)
-    return net, xd, target.to(dev)
+    return net, xd, target.to(dev, dt)
 
 
 def build_c5(dev, N=8192):
@@ -400,11 +407,12 @@ def measure_memory(step, params):
                       "library workspace is a torch allocation"}
 
 
-def _mfma_roofline(kern, cls, kernel_name, traffic=None, traffic_source=None):
+def _mfma_roofline(kern, cls, kernel_name, traffic=None, traffic_source=None,
+                   peak=PEAK_FP32_MFMA_TFLOPS):
     ms, cnt, work = kern[cls]
     ach = work / (ms * 1e-3) / 1e12 if cnt else 0.0
     return {"bound": "mfma", "kernel": kernel_name, "achieved": ach,
-            "peak": PEAK_FP32_MFMA_TFLOPS, "unit": "TFLOP/s", "frac": ach / PEAK_FP32_MFMA_TFLOPS,
+            "peak": peak, "unit": "TFLOP/s", "frac": ach / peak,
             "traffic": traffic, "traffic_source": traffic_source,
             "flop_per_launch": work / max(cnt, 1), "avg_launch_ms": ms / max(cnt, 1),
             "launches": cnt}
@@ -426,15 +434,16 @@ def _line(metric, N, steps, warmup, wall, workload, roofline, kern, mem, **extra
     return line
 
 
-def run_c3(args, dev, steps, warmup, need_dx=True):
+def run_c3(args, dev, steps, warmup, need_dx=True, f64=False):
     """c3: KANLinear(1024 -> 1024, G=10, k=3) fp32, N = 65536, fwd + MSE +
     bwd; with dx (three contractions: the metric's workload) or, as the
     reference's benchmark runs it (benchmarks/bench_kan.py:168-175), with x
-    not requiring grad (two contractions)."""
+    not requiring grad (two contractions).  f64: the same in float64 (the
+    reference dispatches every kernel on both types), against the FP64 peak."""
     import torch
     import torch.nn.functional as F
     N = args.n or 65536
-    L, xd, td, cpu_inputs = build_c3(dev, N, need_dx)
+    L, xd, td, cpu_inputs = build_c3(dev, N, need_dx, torch.float64 if f64 else None)
     I, O, R = L.in_features, L.out_features, L.grid_size + L.spline_order
     torch.cuda.synchronize()
 
@@ -462,18 +471,23 @@ def run_c3(args, dev, steps, warmup, need_dx=True):
     torch.cuda.synchronize()
     step_ms = [a.elapsed_time(b) for a, b in ev]
 
-    traffic, source = recorded_traffic("c3" if need_dx else "c3-nodx")
+    tag = ("c3" if need_dx else "c3-nodx") + ("-f64" if f64 else "")
+    traffic, source = recorded_traffic(tag)
     roof = _mfma_roofline(kernels, "contraction",
-                          "gemm_pipe_kernel (fp32 MFMA contraction; average over the forward, "
-                          "parameter%s launches)" % (" and input" if need_dx else ""),
-                          traffic, source)
+                          "%s (%s MFMA contraction; average over the forward, parameter%s "
+                          "launches)" % ("gemm_kernel" if f64 else "gemm_pipe_kernel",
+                                         "fp64" if f64 else "fp32",
+                                         " and input" if need_dx else ""),
+                          traffic, source, PEAK_FP64_TFLOPS if f64 else PEAK_FP32_MFMA_TFLOPS)
     b_ms, b_cnt, b_work = kernels["basis"]
     g_ms, g_cnt, g_work = kernels["basis_grad"]
     c_ms = kernels["contraction"][0]
     gbps = lambda w, ms, n: (w / n) / (ms / n * 1e-3) / 1e9 if n else None
     line = {
-        "metric": METRIC if need_dx else
-        "fwd+bwd samples/s, KANLinear 1024->1024 G10 k3 N=64K, x without grad (2 contractions)",
+        "metric": (METRIC if need_dx and not f64 else
+                   "fwd+bwd samples/s, KANLinear 1024->1024 G10 k3 N=64K%s%s"
+                   % ("" if need_dx else ", x without grad (2 contractions)",
+                      ", float64" if f64 else "")),
         "value": N * steps / wall,
         "unit": "samples/s",
         "n_gpus": 1,
@@ -483,11 +497,12 @@ def run_c3(args, dev, steps, warmup, need_dx=True):
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32",
+        "dtype": "f64" if f64 else "f32",
         "data": "synthetic (seeded torch.Generator draws, random-init weights of the config)",
         "config": {
-            "workload": ("c3: KANLinear(1024->1024, grid_size=10, spline_order=3) fp32, N=%d, "
-                         "fwd + MSE + bwd %s" % (N, "with dx (3 contractions)" if need_dx
+            "workload": ("c3: KANLinear(1024->1024, grid_size=10, spline_order=3) %s, N=%d, "
+                         "fwd + MSE + bwd %s" % ("fp64" if f64 else "fp32", N,
+                                                 "with dx (3 contractions)" if need_dx
                                                  else "without dx (2 contractions; the "
                                                  "reference benchmark's fwd_bwd)")),
             "in_features": I, "out_features": O, "grid_size": L.grid_size,
@@ -507,7 +522,7 @@ def run_c3(args, dev, steps, warmup, need_dx=True):
         "peak_mem_bytes": mem["peak_mem_bytes"],
         "memory": mem,
     }
-    if not args.no_cpu_baseline:
+    if not args.no_cpu_baseline and not f64:
         x, coef, bw, scaler, target, grid = cpu_inputs
         line["cpu_baseline"] = cpu_baseline_layers([(grid, bw, coef, scaler)], x, target, need_dx,
                                                    args.cpu_seconds, 2048, "c3")
@@ -555,7 +570,8 @@ def run_c4(args, dev, steps, warmup):
     import torch
     import torch.nn.functional as F
     N = args.n or 16384
-    net, xd, td = build_c4(dev, N)
+    f64 = getattr(args, "dtype", "f32") == "f64"
+    net, xd, td = build_c4(dev, N, torch.float64 if f64 else None)
 
     def step():
         for p in net.parameters():
@@ -572,17 +588,26 @@ def run_c4(args, dev, steps, warmup):
     # kernel for the layers that need both gradient sides: phi once plus two
     # products, 6 n O I (R+1) flops; parameter kernel for the first layer,
     # whose input needs no gradient: 4 n O I (R+1))
-    roof = _mfma_roofline(kern, "edge_grad", "edge_bwd_mfma_kernel (both gradient sides, "
-                          "dL/dy folded in; edge_bwd_stage_kernel for the 64-wide layer) + "
-                          "edge_param_mfma_kernel (first layer): mean|phi| backward",
-                          *recorded_traffic("c4"))
+    if f64:
+        roof = _mfma_roofline(kern, "edge_grad", "edge_param_grad_kernel + "
+                              "edge_input_grad_kernel (fp64): mean|phi| backward",
+                              None, None, PEAK_FP64_TFLOPS)
+        roof["bound"] = "fp64"
+    else:
+        roof = _mfma_roofline(kern, "edge_grad", "edge_bwd_mfma_kernel (both gradient sides, "
+                              "dL/dy folded in; edge_bwd_stage_kernel for the 64-wide layer) + "
+                              "edge_param_mfma_kernel (first layer): mean|phi| backward",
+                              *recorded_traffic("c4"))
     e_ms, e_cnt, e_work = kern["edge"]
-    line = _line("fwd+bwd samples/s, KAN([256,512,512,64]) G8 k3 N=16K forward_with_regularization",
-                 N, steps, warmup, wall,
-                 "c4: KAN([256,512,512,64], G=8, k=3) fp32, N=%d, update_grid knots, "
-                 "forward_with_regularization(1e-2, 1e-2, 'auto') + MSE + backward" % N, roof,
+    line = _line("fwd+bwd samples/s, KAN([256,512,512,64]) G8 k3 N=16K forward_with_regularization"
+                 + (", float64" if f64 else ""), N, steps, warmup, wall,
+                 "c4: KAN([256,512,512,64], G=8, k=3) %s, N=%d, update_grid knots, "
+                 "forward_with_regularization(1e-2, 1e-2, 'auto') + MSE + backward"
+                 % ("fp64" if f64 else "fp32", N), roof,
                  kern, mem, edge_forward_tflops=e_work / (e_ms * 1e-3) / 1e12 if e_cnt else 0.0)
-    if not args.no_cpu_baseline:
+    if f64:
+        line["dtype"] = "f64"
+    if not args.no_cpu_baseline and not f64:
         from torchsplinekan_amd import KAN
         net_cpu = KAN([256, 512, 512, 64], grid_size=8, spline_order=3, backend="reference")
         net_cpu.load_state_dict({k_: v.detach().cpu() for k_, v in net.state_dict().items()})
@@ -919,12 +944,21 @@ def main():
         other[args.workload](args)
         return
 
-    line = run_c3(args, dev, args.steps, args.warmup, need_dx=args.workload == "c3")
-    if args.workload == "c3" and not args.no_other_configs and not args.n:
+    line = run_c3(args, dev, args.steps, args.warmup, need_dx=args.workload == "c3",
+                  f64=args.dtype == "f64")
+    if args.workload == "c3" and args.dtype == "f32" and not args.no_other_configs and not args.n:
         torch.cuda.empty_cache()
         line["other_configs"] = {}
         nodx = lambda a, d, st, w: run_c3(a, d, st, w, need_dx=False)
-        for name, fn in (("c3-nodx", nodx), ("c2", run_c2), ("c4", run_c4), ("c5", run_c5)):
+        c3_64 = lambda a, d, st, w: run_c3(a, d, max(3, st // 4), min(w, 2), f64=True)
+
+        def c4_64(a, d, st, w):
+            a64 = argparse.Namespace(**vars(a))
+            a64.dtype = "f64"
+            return run_c4(a64, d, st, w)
+
+        for name, fn in (("c3-nodx", nodx), ("c2", run_c2), ("c4", run_c4), ("c5", run_c5),
+                         ("c3-f64", c3_64), ("c4-f64", c4_64)):
             try:
                 line["other_configs"][name] = fn(args, dev, args.steps, args.warmup)
             except Exception as exc:  # reported in the line; the metric stands on its own
