@@ -1,15 +1,17 @@
 """kan_hip_infer_noalloc (the inference entry point that allocates nothing)
-against kan_hip_infer, both through the C-ABI: identical outputs on two
-calls in a row (the second on a smaller batch, so the scratch holds the
-first call's larger contents), fp32 and fp64; a call whose workspace
-exceeds the fixed scratch is refused before any launch."""
+against kan_hip_infer, both through the C-ABI, on two calls in a row (the
+second on a smaller batch, so the scratch holds the first call's larger
+contents), fp32 and fp64: identical outputs where both plan the same split
+count, within rounding (1e-6 fp32, 1e-14 fp64) where the fixed scratch
+bounds the split slices; a call whose basis and output exceed the fixed
+scratch is refused before any launch."""
 
 import ctypes
 
 import pytest
 import torch
 
-from tests._util import make_grid
+from tests._util import make_grid, normwise, np64
 
 pytestmark = pytest.mark.gpu
 
@@ -60,15 +62,21 @@ def test_noalloc_matches_infer_on_two_calls(lib, dtype):
     I, O, G, k = 1024, 1024, 10, 3
     grid, waug = _packed_layer(I, O, G, k, dtype, seed=3)
     g = torch.Generator().manual_seed(4)
-    for n in (512 if dtype == torch.float32 else 256, 7):   # 60 MiB of scratch, then less
+    for n in (512 if dtype == torch.float32 else 256, 7):   # most of the scratch, then less
         print(f"noalloc vs infer {dtype} n={n}", flush=True)
         x = ((torch.rand(n, I, generator=g, dtype=torch.float64) * 2.2 - 1.1)
              .to(dtype).cuda())
         ref, need = _infer(lib, x, grid, waug, O, G, k)
-        assert need <= lib.KAN_NOALLOC_SCRATCH_BYTES
         got = _infer_noalloc(lib, x, grid, waug, O, G, k)
         torch.cuda.synchronize()
-        assert torch.equal(got, ref)
+        if need <= lib.KAN_NOALLOC_SCRATCH_BYTES:
+            # the same plan (split count, tiles) as the workspace call
+            assert torch.equal(got, ref)
+        else:
+            # the scratch bounds the split slices: another split count, the
+            # same product summed in another order
+            tol = 1e-6 if dtype == torch.float32 else 1e-14
+            assert normwise(np64(got), np64(ref)) < tol
 
 
 def test_noalloc_refuses_beyond_the_scratch(lib):

@@ -234,13 +234,23 @@ struct BackwardPlan {
 
 // Inference workspace: the augmented basis [n, ld], then the split-K
 // partial slices of the product (elements).
+// A non-negative scratch_elems (the allocation-free call's fixed scratch)
+// bounds the product's split slices to what the scratch holds after the
+// basis; the cost model then picks among the split counts that fit.  The
+// launch must pass the same bound (infer_slice_cap).
+inline int64_t infer_slice_cap(int64_t scratch_elems, int64_t aug_elems) {
+  return scratch_elems < 0 ? -1 : std::max<int64_t>(0, scratch_elems - aug_elems);
+}
+
 template <typename T>
 void infer_plan(int64_t n, int64_t I, int64_t O, int64_t R, bool has_base, int64_t* ld,
-                int64_t* kaug, int64_t* aug_elems, int64_t* part_elems) {
+                int64_t* kaug, int64_t* aug_elems, int64_t* part_elems,
+                int64_t scratch_elems = -1) {
   *ld = aug_width(I, R, has_base);
   *kaug = I * R + (has_base ? I : 0);
   *aug_elems = round_up(n * *ld, 64);
-  *part_elems = matmul_ws_elems<T>(kLayoutNT, n, O, *kaug);
+  *part_elems = matmul_ws_elems<T>(kLayoutNT, n, O, *kaug,
+                                   infer_slice_cap(scratch_elems, *aug_elems));
 }
 
 template <typename T>
@@ -783,12 +793,11 @@ int kan_hip_infer_workspace(int dtype, int64_t n, int64_t I, int64_t O, int64_t 
   return KAN_OK;
 }
 
-int kan_hip_infer(int dtype, const void* x, const void* grid, const void* waug, void* out,
-                  void* ws, size_t ws_bytes, int64_t n, int64_t I, int64_t O, int64_t G, int64_t k,
-                  int has_base, void* stream) {
-  KAN_TRY(check_dtype(dtype, "kan_infer"));
-  KAN_TRY(check_layer("kan_infer", n, I, O, G, k));
-  if (n * O == 0) return KAN_OK;
+namespace {
+// kan_hip_infer with the split slices bounded by scratch_elems (-1: none).
+int infer_run(int dtype, const void* x, const void* grid, const void* waug, void* out, void* ws,
+              size_t ws_bytes, int64_t n, int64_t I, int64_t O, int64_t G, int64_t k,
+              int has_base, void* stream, int64_t scratch_elems) {
   KAN_TRY(need_ptr(out, "kan_infer", "output"));
   KAN_TRY(need_ptr(waug, "kan_infer", "weight_aug"));
   if (n * I > 0) {
@@ -799,9 +808,12 @@ int kan_hip_infer(int dtype, const void* x, const void* grid, const void* waug, 
   int64_t ld, kaug, aug_elems, part_elems;
   const size_t elem = dtype == KAN_DTYPE_F32 ? 4 : 8;
   if (dtype == KAN_DTYPE_F32)
-    infer_plan<float>(n, I, O, R, has_base != 0, &ld, &kaug, &aug_elems, &part_elems);
+    infer_plan<float>(n, I, O, R, has_base != 0, &ld, &kaug, &aug_elems, &part_elems,
+                      scratch_elems);
   else
-    infer_plan<double>(n, I, O, R, has_base != 0, &ld, &kaug, &aug_elems, &part_elems);
+    infer_plan<double>(n, I, O, R, has_base != 0, &ld, &kaug, &aug_elems, &part_elems,
+                       scratch_elems);
+  const int64_t cap = infer_slice_cap(scratch_elems, aug_elems);
   const size_t need = elem * (size_t)(aug_elems + part_elems);
   if (ws_bytes < need || ws == nullptr)
     return set_error(KAN_ERR_WORKSPACE, "kan_infer: workspace of %zu bytes is smaller than the %zu required",
@@ -814,11 +826,21 @@ int kan_hip_infer(int dtype, const void* x, const void* grid, const void* waug, 
                             has_base ? aug + I * R : nullptr, n, I, (int)G, (int)k,              \
                             g_basis_impl.load(), st));                                           \
     return launch_matmul<T>(kLayoutNT, n, O, kaug, aug, ld, static_cast<const T*>(waug), ld,     \
-                            static_cast<T*>(out), O, aug + aug_elems, st);                       \
+                            static_cast<T*>(out), O, aug + aug_elems, st, cap);                  \
   } while (0)
   if (dtype == KAN_DTYPE_F32) KAN_INFER_CALL(float);
   KAN_INFER_CALL(double);
 #undef KAN_INFER_CALL
+}
+}  // namespace
+
+int kan_hip_infer(int dtype, const void* x, const void* grid, const void* waug, void* out,
+                  void* ws, size_t ws_bytes, int64_t n, int64_t I, int64_t O, int64_t G, int64_t k,
+                  int has_base, void* stream) {
+  KAN_TRY(check_dtype(dtype, "kan_infer"));
+  KAN_TRY(check_layer("kan_infer", n, I, O, G, k));
+  if (n * O == 0) return KAN_OK;
+  return infer_run(dtype, x, grid, waug, out, ws, ws_bytes, n, I, O, G, k, has_base, stream, -1);
 }
 
 int kan_hip_infer_noalloc(int dtype, const void* x, const void* grid, const void* waug, void* out,
@@ -830,10 +852,13 @@ int kan_hip_infer_noalloc(int dtype, const void* x, const void* grid, const void
   const int64_t R = G + k;
   int64_t ld, kaug, aug_elems, part_elems;
   const size_t elem = dtype == KAN_DTYPE_F32 ? 4 : 8;
+  const int64_t scratch_elems = (int64_t)(KAN_NOALLOC_SCRATCH_BYTES / elem);
   if (dtype == KAN_DTYPE_F32)
-    infer_plan<float>(n, I, O, R, has_base != 0, &ld, &kaug, &aug_elems, &part_elems);
+    infer_plan<float>(n, I, O, R, has_base != 0, &ld, &kaug, &aug_elems, &part_elems,
+                      scratch_elems);
   else
-    infer_plan<double>(n, I, O, R, has_base != 0, &ld, &kaug, &aug_elems, &part_elems);
+    infer_plan<double>(n, I, O, R, has_base != 0, &ld, &kaug, &aug_elems, &part_elems,
+                       scratch_elems);
   const size_t need = elem * (size_t)(aug_elems + part_elems);
   if (need > (size_t)KAN_NOALLOC_SCRATCH_BYTES)
     return set_error(KAN_ERR_WORKSPACE,
@@ -846,8 +871,8 @@ int kan_hip_infer_noalloc(int dtype, const void* x, const void* grid, const void
   // Every element of the workspace that the kernels read is written first in
   // the same call (basis columns below kaug, whole split slices), so the
   // previous call's contents need no clearing.
-  return kan_hip_infer(dtype, x, grid, waug, out, ws, (size_t)KAN_NOALLOC_SCRATCH_BYTES, n, I, O, G,
-                       k, has_base, stream);
+  return infer_run(dtype, x, grid, waug, out, ws, (size_t)KAN_NOALLOC_SCRATCH_BYTES, n, I, O, G, k,
+                   has_base, stream, scratch_elems);
 }
 
 int kan_hip_pack_basis(int dtype, const void* basis, const void* x, void* aug, int64_t n,

@@ -206,16 +206,21 @@ bool gemm_ecomp_supported(int64_t M, int64_t N, int64_t K, int64_t I, int G, int
 
 // General product C = op(A) op(B) for any transposition pair: the split
 // count from gemm_pick_splits, partial slices in ws, then a fixed-order sum
-// into C (kan_gemm.hip).  ws must hold matmul_ws_elems(...) elements.
+// into C (kan_gemm.hip).  ws must hold matmul_ws_elems(...) elements, with
+// the same max_slice_elems: a non-negative value bounds the split slices'
+// total elements (the allocation-free inference's fixed scratch), -1 leaves
+// the split count to the cost model alone.
 template <typename T>
-int64_t matmul_ws_elems(int layout, int64_t M, int64_t N, int64_t K);
+int64_t matmul_ws_elems(int layout, int64_t M, int64_t N, int64_t K,
+                        int64_t max_slice_elems = -1);
 template <typename T>
 int launch_matmul(int layout, int64_t M, int64_t N, int64_t K, const T* A, int64_t lda,
-                  const T* B, int64_t ldb, T* C, int64_t ldc, T* ws, hipStream_t st);
+                  const T* B, int64_t ldb, T* C, int64_t ldc, T* ws, hipStream_t st,
+                  int64_t max_slice_elems = -1);
 
 // Split count the GEMM scheduler would choose for a problem (1 = no split).
 template <typename T>
-int gemm_pick_splits(int64_t M, int64_t N, int64_t K);
+int gemm_pick_splits(int64_t M, int64_t N, int64_t K, int64_t max_slice_elems = -1);
 
 template <typename T>
 int launch_edge_forward(const T* s, const T* H, const T* bw, const T* W, T* a, T* part,

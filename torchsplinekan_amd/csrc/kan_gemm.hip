@@ -875,41 +875,67 @@ bool vec_ok(const T* ptr, int64_t ld) {
 
 // ---- planning ----------------------------------------------------------------
 
-// Tile configuration as seen by the cost model: block tile, slab depth,
-// resident blocks per CU and the measured fraction of the MFMA peak that one
-// CU sustains on whole tiles of this configuration (MI355X, c3 shapes).
+// Cost model of the fp32 tile configurations, fitted to a sweep of every
+// configuration and split count over the products of BASELINE's workloads
+// (c2's first layer, c3's and c5's parameter products, c4's and c5's
+// forward products) on MI355X.  The dispatcher spreads workgroups over CUs,
+// so the busiest CU runs ceil(tiles / CUs) blocks one after another (two
+// small blocks that share a CU run at half speed each, the same total);
+// a block costs its MFMA work at the configuration's sustained efficiency
+// plus a fixed start-up and write-out time.  The 128 x 128 tile loses most
+// of its efficiency when it runs alone on a CU (one wave per SIMD: the slab
+// barriers idle the MFMA pipes), which is why the earlier whole-wave model
+// (eff 0.85 at two blocks per CU, a 256-k overhead) split c2's and c5's
+// products onto small tiles that ran 10-30 % slower than the 256 x 256 tile
+// with more splits, and c3's parameter product 4 ways instead of 8.
 struct CfgModel {
+  int bm, bn, bk;
+  double eff;       // sustained fraction of the per-CU peak, blocks sharing CUs
+  double eff_lone;  // the same when every block has a CU of its own
+  double block_s;   // fixed seconds per block (start-up, epilogue)
+};
+constexpr CfgModel kModelF32[4] = {
+    {256, 256, 32, 0.89, 0.89, 5e-6}, {128, 128, 32, 0.88, 0.40, 10e-6},
+    {256, 64, 32, 0.75, 0.75, 5e-6}, {256, 256, 32, 0.89, 0.89, 5e-6}};
+constexpr double kPeakPerCuF32 = 157.3e12 / 256.0;  // FP32 MFMA flop/s per CU
+constexpr double kStreamBytesPerS = 5.0e12;          // split-K partial-sum traffic
+
+// fp64 (one configuration): whole waves of resident blocks times one block's
+// k range plus a 256-k start-up and write-out term.
+struct CfgModelF64 {
   int bm, bn, bk, blocks_per_cu;
   double eff;
 };
-constexpr CfgModel kModelF32[4] = {
-    {256, 256, 32, 1, 0.89}, {128, 128, 32, 2, 0.85}, {256, 64, 32, 1, 0.75},
-    {256, 256, 32, 1, 0.89}};
-constexpr CfgModel kModelF64 = {128, 128, 16, 1, 0.80};
-constexpr double kPeakPerCuF32 = 157.3e12 / 256.0;  // FP32 MFMA flop/s per CU
+constexpr CfgModelF64 kModelF64 = {128, 128, 16, 1, 0.80};
 constexpr double kPeakPerCuF64 = 78.6e12 / 256.0;
-constexpr double kStreamBytesPerS = 5.0e12;          // split-K partial-sum traffic
-// Per-block start-up and write-out, as the k-extent that would take as long:
-// a block that runs a short k range (a split of a moderate K) is charged for
-// it (measured at c4's layers: a 256 x 256 tile split twice over K = 5632
-// ran 10 % slower than 128 x 128 tiles over the whole K).
-constexpr double kKOverhead = 256.0;
+constexpr double kKOverheadF64 = 256.0;
 
-// Estimated seconds for M x N x K with `splits` K-slices: whole waves of
-// resident blocks times the duration of one block (its k range plus
-// kKOverhead), plus the split-K partial traffic (written once, read once by
-// the caller's reduction).
-double est_seconds(const CfgModel& c, double peak_per_cu, int64_t M, int64_t N, int64_t K,
-                   int splits, size_t elem) {
+double split_traffic_s(int64_t M, int64_t N, int splits, size_t elem) {
+  return splits > 1 ? 2.0 * (double)splits * (double)(M * N) * (double)elem / kStreamBytesPerS
+                    : 0.0;
+}
+
+// Estimated seconds for M x N x K with `splits` K-slices on fp32 tiles of c,
+// plus the split-K partial traffic (written once, read once by the sum).
+double est_seconds(const CfgModel& c, int64_t M, int64_t N, int64_t K, int splits) {
+  const int64_t cus = device_cu_count();
+  const int64_t tiles = ceil_div(M, c.bm) * ceil_div(N, c.bn) * splits;
+  const int64_t per_cu = ceil_div(tiles, cus);
+  const int64_t kper = round_up(ceil_div(K > 0 ? K : 1, splits), c.bk);
+  const double eff = tiles <= cus ? c.eff_lone : c.eff;
+  const double block = 2.0 * c.bm * c.bn * (double)kper / (kPeakPerCuF32 * eff) + c.block_s;
+  return (double)per_cu * block + split_traffic_s(M, N, splits, 4);
+}
+
+double est_seconds_f64(int64_t M, int64_t N, int64_t K, int splits) {
+  const CfgModelF64& c = kModelF64;
   const int64_t cus = device_cu_count();
   const int64_t tiles = ceil_div(M, c.bm) * ceil_div(N, c.bn) * splits;
   const int64_t waves = ceil_div(tiles, cus * c.blocks_per_cu);
   const int64_t kper = round_up(ceil_div(K > 0 ? K : 1, splits), c.bk);
-  const double block_s = 2.0 * c.bm * c.bn * ((double)kper + kKOverhead) * c.blocks_per_cu /
-                         (peak_per_cu * c.eff);
-  double t = (double)waves * block_s;
-  if (splits > 1) t += 2.0 * (double)splits * (double)(M * N) * (double)elem / kStreamBytesPerS;
-  return t;
+  const double block_s = 2.0 * c.bm * c.bn * ((double)kper + kKOverheadF64) * c.blocks_per_cu /
+                         (kPeakPerCuF64 * c.eff);
+  return (double)waves * block_s + split_traffic_s(M, N, splits, 8);
 }
 
 // Forced fp32 tile configuration (route KAN_ROUTE_GEMM_TILE: 0 big, 1 small,
@@ -925,9 +951,9 @@ int pick_cfg_f32(int64_t M, int64_t N, int64_t K, int splits) {
   if (forced >= 0) return forced;
   const int last = N <= 64 ? 2 : 1;
   int best = 0;
-  double best_t = est_seconds(kModelF32[0], kPeakPerCuF32, M, N, K, splits, 4);
+  double best_t = est_seconds(kModelF32[0], M, N, K, splits);
   for (int c = 1; c <= last; ++c) {
-    const double t = est_seconds(kModelF32[c], kPeakPerCuF32, M, N, K, splits, 4);
+    const double t = est_seconds(kModelF32[c], M, N, K, splits);
     if (t < best_t) {
       best = c;
       best_t = t;
@@ -1416,18 +1442,19 @@ inline bool gemm_is_thin(int64_t M, int64_t N, int64_t K) {
 // all splits fill their last wave of resident blocks.  Long-K products with few output tiles
 // (the parameter product, sample reductions, small-batch inference) split.
 template <typename T>
-int gemm_pick_splits(int64_t M, int64_t N, int64_t K) {
+int gemm_pick_splits(int64_t M, int64_t N, int64_t K, int64_t max_slice_elems) {
   if (gemm_is_thin(M, N, K)) return K <= kThinMax ? 1 : thin_splits(M, N, K);
   int best = 1;
   double best_t = 0.0;
   for (int s = 1; s <= 64; ++s) {
+    if (s > 1 && max_slice_elems >= 0 && (int64_t)s * M * N > max_slice_elems) break;
     double t;
     if (std::is_same<T, float>::value) {
       if (s > 1 && K / s < 8 * kModelF32[0].bk) break;
-      t = est_seconds(kModelF32[pick_cfg_f32(M, N, K, s)], kPeakPerCuF32, M, N, K, s, sizeof(T));
+      t = est_seconds(kModelF32[pick_cfg_f32(M, N, K, s)], M, N, K, s);
     } else {
       if (s > 1 && K / s < 8 * kModelF64.bk) break;
-      t = est_seconds(kModelF64, kPeakPerCuF64, M, N, K, s, sizeof(T));
+      t = est_seconds_f64(M, N, K, s);
     }
     if (s == 1 || t < best_t * (1.0 - 1e-9)) {
       best = s;
@@ -1507,23 +1534,24 @@ inline unsigned flat_blocks(int64_t count) {
 }  // namespace
 
 template <typename T>
-int64_t matmul_ws_elems(int layout, int64_t M, int64_t N, int64_t K) {
+int64_t matmul_ws_elems(int layout, int64_t M, int64_t N, int64_t K, int64_t max_slice_elems) {
   (void)layout;
   if (M <= 0 || N <= 0 || K <= 0) return 0;
-  const int s = gemm_pick_splits<T>(M, N, K);
+  const int s = gemm_pick_splits<T>(M, N, K, max_slice_elems);
   return s > 1 ? (int64_t)s * M * N : 0;
 }
 
 template <typename T>
 int launch_matmul(int layout, int64_t M, int64_t N, int64_t K, const T* A, int64_t lda,
-                  const T* B, int64_t ldb, T* C, int64_t ldc, T* ws, hipStream_t st) {
+                  const T* B, int64_t ldb, T* C, int64_t ldc, T* ws, hipStream_t st,
+                  int64_t max_slice_elems) {
   if (M <= 0 || N <= 0) return KAN_OK;
   if (K <= 0) {
     hipLaunchKernelGGL(fill_rows_kernel<T>, dim3(flat_blocks(M * N)), dim3(256), 0, st, C, M, N,
                        ldc);
     return check_launch("matmul (K = 0)");
   }
-  const int s = gemm_pick_splits<T>(M, N, K);
+  const int s = gemm_pick_splits<T>(M, N, K, max_slice_elems);
   if (s <= 1) return launch_gemm<T>(layout, M, N, K, A, lda, B, ldb, C, ldc, 1, 0, st);
   const int rc = launch_gemm<T>(layout, M, N, K, A, lda, B, ldb, ws, N, s, M * N, st);
   if (rc != KAN_OK) return rc;
@@ -1532,12 +1560,14 @@ int launch_matmul(int layout, int64_t M, int64_t N, int64_t K, const T* A, int64
   return check_launch("matmul split sum");
 }
 
-template int64_t matmul_ws_elems<float>(int, int64_t, int64_t, int64_t);
-template int64_t matmul_ws_elems<double>(int, int64_t, int64_t, int64_t);
+template int64_t matmul_ws_elems<float>(int, int64_t, int64_t, int64_t, int64_t);
+template int64_t matmul_ws_elems<double>(int, int64_t, int64_t, int64_t, int64_t);
 template int launch_matmul<float>(int, int64_t, int64_t, int64_t, const float*, int64_t,
-                                  const float*, int64_t, float*, int64_t, float*, hipStream_t);
+                                  const float*, int64_t, float*, int64_t, float*, hipStream_t,
+                                  int64_t);
 template int launch_matmul<double>(int, int64_t, int64_t, int64_t, const double*, int64_t,
-                                   const double*, int64_t, double*, int64_t, double*, hipStream_t);
+                                   const double*, int64_t, double*, int64_t, double*, hipStream_t,
+                                   int64_t);
 
 bool gemm_dx_supported(int64_t M, int64_t N, int64_t K, int64_t I, int G, int k, bool has_base) {
   if (k < 1 || k > 3) return false;
@@ -1656,7 +1686,7 @@ template int launch_gemm<float>(int, int64_t, int64_t, int64_t, const float*, in
 template int launch_gemm<double>(int, int64_t, int64_t, int64_t, const double*, int64_t,
                                  const double*, int64_t, double*, int64_t, int, int64_t,
                                  hipStream_t);
-template int gemm_pick_splits<float>(int64_t, int64_t, int64_t);
-template int gemm_pick_splits<double>(int64_t, int64_t, int64_t);
+template int gemm_pick_splits<float>(int64_t, int64_t, int64_t, int64_t);
+template int gemm_pick_splits<double>(int64_t, int64_t, int64_t, int64_t);
 
 }  // namespace kan
