@@ -115,27 +115,40 @@ int kan_hip_basis_silu_grad(int dtype, const void* x, const void* grid, const vo
                             const void* grad_silu, void* grad_x, int64_t n, int64_t in_features,
                             int64_t grid_size, int64_t spline_order, void* stream);
 
-/* out[n, i, r] = d^order B_r / dx^order at x[n, i] (order >= 0; order 0 is the
- * basis itself, order > spline_order gives zeros), with the span, boundary
- * and zero-denominator conventions of kan_hip_basis.  Replaces the
- * differentiable basis derivatives that the reference builds from ATen ops
- * when the backward is recorded (create_graph=True):
- * compute_basis_derivative (spline_kan/reference_backend.py:99-125) and
- * autograd through compute_basis (reference_backend.py:69-94), as used by
+/* out[n, i, r] = scale[n, i] * d^order B_r / dx^order at x[n, i] (order >= 0;
+ * order 0 is the basis itself, order > spline_order gives zeros; scale may be
+ * NULL for 1), with the span, boundary and zero-denominator conventions of
+ * kan_hip_basis.  Replaces the differentiable basis derivatives that the
+ * reference builds from ATen ops when the backward is recorded
+ * (create_graph=True): compute_basis_derivative
+ * (spline_kan/reference_backend.py:99-125) and autograd through
+ * compute_basis (reference_backend.py:69-94), as used by
  * kan_backward_composite (csrc/kan_cpu.cpp:301-345) and NativeBasis
- * (spline_kan/fused.py:57-60). */
-int kan_hip_basis_deriv(int dtype, const void* x, const void* grid, void* out, int64_t n,
-                        int64_t in_features, int64_t grid_size, int64_t spline_order,
+ * (spline_kan/fused.py:57-60); the scale folds the elementwise product the
+ * recorded backward applies to them (g * D^q B). */
+int kan_hip_basis_deriv(int dtype, const void* x, const void* grid, const void* scale, void* out,
+                        int64_t n, int64_t in_features, int64_t grid_size, int64_t spline_order,
                         int64_t order, void* stream);
 
-/* grad_x[n, i] = sum_r grad_basis[n, i, r] * d^order B_r/dx^order(x[n, i])
- * (order 1 is kan_hip_basis_grad).  The contraction behind the higher-order
- * derivatives of the same reference call sites, without forming the
- * derivative tensor. */
+/* grad_x[n, i] = scale[n, i] * (sum_r grad_basis[n, i, r] * d^order B_r/dx^order(x[n, i])
+ *                + grad_base[n, i] * silu^(order)(x[n, i]))
+ * (order 1 without base or scale is kan_hip_basis_grad; grad_base and scale
+ * may be NULL; with grad_base, order <= 4).  The contraction behind the
+ * higher-order derivatives of the same reference call sites, without forming
+ * the derivative tensor; the base term is the SiLU branch of
+ * kan_backward_composite (csrc/kan_cpu.cpp:335-342) and its derivatives. */
 int kan_hip_basis_deriv_contract(int dtype, const void* x, const void* grid,
-                                 const void* grad_basis, void* grad_x, int64_t n,
+                                 const void* grad_basis, const void* grad_base,
+                                 const void* scale, void* grad_x, int64_t n,
                                  int64_t in_features, int64_t grid_size, int64_t spline_order,
                                  int64_t order, void* stream);
+
+/* out[e] = scale[e] * silu^(order)(x[e]) for count elements (order 0..4;
+ * scale may be NULL).  The SiLU terms of the recorded backward (silu(x) and
+ * silu'(x) of kan_backward_composite, csrc/kan_cpu.cpp:335-342, and their
+ * derivatives) as one launch each. */
+int kan_hip_silu_deriv(int dtype, const void* x, const void* scale, void* out, int64_t count,
+                       int64_t order, void* stream);
 
 /* C[M, N] = op(A) op(B) on the MFMA contraction engine, for the products
  * of the recorded (create_graph=True) backward.  op(A) is A [M, K] with row

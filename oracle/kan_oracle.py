@@ -285,10 +285,11 @@ def basis_derivative_n(x, grid, k, q, chunk=1 << 14):
 
 
 def silu_derivative(x, q):
-    """q-th derivative of silu(x) = x sigmoid(x), q = 0..3, with s = sigmoid(x):
+    """q-th derivative of silu(x) = x sigmoid(x), q = 0..4, with s = sigmoid(x):
     q=1  s (1 + x (1 - s))              (silu_grad; csrc/kan_cpu.cpp:279-281)
     q=2  s (1 - s) (2 + x (1 - 2s))
     q=3  s (1 - s) (3 (1 - 2s) + x (1 - 6s + 6s^2))
+    q=4  s (1 - s) (4 (1 - 6s + 6s^2) + x (1 - 2s) (1 - 12s + 12s^2))
     (from s' = s (1 - s))."""
     x = np.asarray(x)
     if q == 0:
@@ -300,7 +301,10 @@ def silu_derivative(x, q):
         return s * (1 - s) * (2 + x * (1 - 2 * s))
     if q == 3:
         return s * (1 - s) * (3 * (1 - 2 * s) + x * (1 - 6 * s + 6 * s * s))
-    raise ValueError("silu_derivative: q must be 0..3")
+    if q == 4:
+        return s * (1 - s) * (4 * (1 - 6 * s + 6 * s * s)
+                              + x * (1 - 2 * s) * (1 - 12 * s + 12 * s * s))
+    raise ValueError("silu_derivative: q must be 0..4")
 
 
 def kan_edge_derivative(x, grid, base_weight, spline_weight, spline_scaler, k, q):

@@ -65,6 +65,64 @@ def test_basis_derivatives_match_oracle(C, dtype, k, G, kind):
     assert torch.equal(C.basis_deriv(xd, gd, k, 0), C.basis(xd, gd, k))
 
 
+@pytest.mark.parametrize("dtype", [torch.float64, torch.float32])
+@pytest.mark.parametrize("k,G,kind", [(2, 7, "nonuniform"), (3, 10, "uniform")])
+def test_scaled_and_base_derivative_terms_match_oracle(C, dtype, k, G, kind):
+    """basis_deriv with a per-item factor, basis_deriv_contract with the SiLU
+    base term and a factor, and silu_deriv, for every order the recorded
+    backward reaches, against the oracle; order 1 with the base term and no
+    factor is the first-order kernel (kan_hip_basis_silu_grad) bit for bit."""
+    print(f"scaled/base derivative terms k={k} G={G} {kind} {dtype}", flush=True)
+    I, N = 45, 257
+    grid = make_grid(I, G, k, kind, seed=G + 1).to(dtype)
+    g = torch.Generator().manual_seed(11 * k)
+    x = (torch.rand(N, I, generator=g, dtype=torch.float64) * 2.4 - 1.2).to(dtype)
+    gH = torch.randn(N, I, G + k, generator=g, dtype=torch.float64).to(dtype)
+    gb = torch.randn(N, I, generator=g, dtype=torch.float64).to(dtype)
+    w = (torch.rand(N, I, generator=g, dtype=torch.float64) + 0.5).to(dtype)
+    xd, gd = x.cuda(), grid.cuda()
+    xs = np64(x)
+    for q in range(0, 5):
+        silu_q = ko.silu_derivative(xs, q)
+        tol = 1e-12 if dtype == torch.float64 else 1e-5
+        assert normwise(np64(C.silu_deriv(xd, q)), silu_q) < tol, q
+        assert normwise(np64(C.silu_deriv(xd, q, w.cuda())), np64(w) * silu_q) < tol, q
+        Dq = ko.basis_derivative_n(xs, np64(grid), k, q)
+        got = np64(C.basis_deriv(xd, gd, k, q, w.cuda()))
+        ref = np64(w)[:, :, None] * Dq
+        if q > k:
+            assert not got.any()
+        else:
+            assert normwise(got, ref) < _tol(dtype, q), q
+        gx = np64(C.basis_deriv_contract(xd, gd, k, gH.cuda(), q, gb.cuda(), w.cuda()))
+        rgx = np64(w) * (np.einsum("nir,nir->ni", np64(gH), Dq) + np64(gb) * silu_q)
+        assert normwise(gx, rgx) < max(_tol(dtype, q), tol), q
+    assert torch.equal(C.basis_deriv_contract(xd, gd, k, gH.cuda(), 1, gb.cuda()),
+                       C.basis_silu_grad(xd, gd, k, gH.cuda(), gb.cuda()))
+    with pytest.raises(RuntimeError):
+        C.silu_deriv(xd, 5)
+
+
+def test_deriv_contract_gradients(C):
+    """deriv_contract with the base term and a factor: first and second
+    derivatives in every operand (gradcheck, gradgradcheck, float64)."""
+    torch.manual_seed(2)
+    I, N, G, k = 3, 9, 5, 3
+    grid = make_grid(I, G, k, "nonuniform", seed=4).double().cuda()
+    x = (torch.rand(N, I, dtype=torch.float64) * 1.6 - 0.8).cuda().requires_grad_()
+    Gs = torch.randn(N, I, G + k, dtype=torch.float64).cuda().requires_grad_()
+    Gb = torch.randn(N, I, dtype=torch.float64).cuda().requires_grad_()
+    w = (torch.rand(N, I, dtype=torch.float64) + 0.5).cuda().requires_grad_()
+    for q in (0, 1, 2):
+        f = lambda a, b, c, d: C.deriv_contract(a, grid, b, k, q, c, d)
+        assert torch.autograd.gradcheck(f, (x, Gs, Gb, w), eps=1e-6, atol=1e-6)
+        assert torch.autograd.gradgradcheck(f, (x, Gs, Gb, w), eps=1e-6, atol=1e-5)
+    h = lambda a, d: C.BasisDeriv.apply(a, grid, k, 1, d)
+    assert torch.autograd.gradgradcheck(h, (x, w), eps=1e-6, atol=1e-5)
+    s = lambda a, d: C.SiluDeriv.apply(a, 2, d)
+    assert torch.autograd.gradgradcheck(s, (x, w), eps=1e-6, atol=1e-5)
+
+
 def test_deriv_entry_points_reject_bad_orders(C):
     x = torch.rand(4, 3, device="cuda")
     grid = make_grid(3, 5, 3, "uniform").float().cuda()

@@ -433,23 +433,35 @@ def basis_silu_grad(x, grid, spline_order: int, grad_basis, grad_silu) -> torch.
     return gx
 
 
-def basis_deriv(x, grid, spline_order: int, order: int) -> torch.Tensor:
-    """d^order B / dx^order [B, I, R] (device; order 0 = basis, order > k = 0)."""
+def _optional_operand(t, like, name):
+    """A [B, I] factor of the derivative kernels (or None), contiguous in x's dtype."""
+    if t is None:
+        return None
+    _req(tuple(t.shape) == tuple(like.shape), f"{name} must be [B, I]")
+    return t.contiguous().to(like.dtype)
+
+
+def basis_deriv(x, grid, spline_order: int, order: int, scale=None) -> torch.Tensor:
+    """scale[b, i] * d^order B / dx^order [B, I, R] (device; order 0 = basis,
+    order > k = 0; scale None = 1)."""
     G = _check_basis_args(x, grid, spline_order)
     _req(order >= 0, "kan_basis_deriv: order must be >= 0")
     x, grid = x.contiguous(), grid.contiguous()
     B, I = x.shape
+    w = _optional_operand(scale, x, "kan_basis_deriv: scale")
     out = torch.empty(B, I, G + spline_order, dtype=x.dtype, device=x.device)
     if B == 0:
         return out
     with torch.cuda.device(x.device):
-        check(LIB.kan_hip_basis_deriv(dtype_code(x.dtype), ptr(x), ptr(grid), ptr(out), B, I, G,
-                                      spline_order, int(order), stream_of(x.device)))
+        check(LIB.kan_hip_basis_deriv(dtype_code(x.dtype), ptr(x), ptr(grid), ptr(w), ptr(out), B,
+                                      I, G, spline_order, int(order), stream_of(x.device)))
     return out
 
 
-def basis_deriv_contract(x, grid, spline_order: int, grad_basis, order: int) -> torch.Tensor:
-    """gx[b, i] = sum_r grad_basis[b, i, r] d^order B_r/dx^order (device)."""
+def basis_deriv_contract(x, grid, spline_order: int, grad_basis, order: int, grad_base=None,
+                         scale=None) -> torch.Tensor:
+    """gx[b, i] = scale * (sum_r grad_basis[b, i, r] d^order B_r/dx^order
+    + grad_base[b, i] silu^(order)(x)) (device; grad_base and scale optional)."""
     G = _check_basis_args(x, grid, spline_order)
     _req(order >= 0, "kan_basis_deriv_contract: order must be >= 0")
     B, I = x.shape
@@ -458,14 +470,34 @@ def basis_deriv_contract(x, grid, spline_order: int, grad_basis, order: int) -> 
          "kan_basis_deriv_contract: gH must be [B, I, G+k]")
     x, grid = x.contiguous(), grid.contiguous()
     gH = grad_basis.contiguous().to(x.dtype)
+    gb = _optional_operand(grad_base, x, "kan_basis_deriv_contract: grad_base")
+    w = _optional_operand(scale, x, "kan_basis_deriv_contract: scale")
     gx = torch.empty(B, I, dtype=x.dtype, device=x.device)
     if B == 0:
         return gx
     with torch.cuda.device(x.device):
         check(LIB.kan_hip_basis_deriv_contract(dtype_code(x.dtype), ptr(x), ptr(grid), ptr(gH),
-                                               ptr(gx), B, I, G, spline_order, int(order),
-                                               stream_of(x.device)))
+                                               ptr(gb), ptr(w), ptr(gx), B, I, G, spline_order,
+                                               int(order), stream_of(x.device)))
     return gx
+
+
+SILU_MAX_ORDER = 4   # native orders of silu_deriv (the base term of the kernels above)
+
+
+def silu_deriv(x, order: int, scale=None) -> torch.Tensor:
+    """scale * silu^(order)(x), elementwise on the device (order 0..4)."""
+    _req(x.is_cuda and x.dtype in _F, "kan_silu_deriv: x must be a float32/float64 CUDA tensor")
+    _req(0 <= order <= SILU_MAX_ORDER, "kan_silu_deriv: order must lie in 0..", SILU_MAX_ORDER)
+    xc = x.contiguous()
+    w = _optional_operand(scale, xc, "kan_silu_deriv: scale")
+    out = torch.empty_like(xc)
+    if xc.numel() == 0:
+        return out
+    with torch.cuda.device(x.device):
+        check(LIB.kan_hip_silu_deriv(dtype_code(x.dtype), ptr(xc), ptr(w), ptr(out), xc.numel(),
+                                     int(order), stream_of(x.device)))
+    return out
 
 
 def _mm_operand(t: torch.Tensor):
@@ -526,48 +558,112 @@ class NativeMatmul(torch.autograd.Function):
 
 
 class BasisDeriv(torch.autograd.Function):
-    """D^q B(x) [B, I, R] on the device kernels, differentiable to any order:
-    its x-gradient is DerivContract of order q + 1.  Together with
-    DerivContract it replaces the differentiable ATen recurrences the
-    reference records under create_graph=True (compute_basis and
-    compute_basis_derivative, spline_kan/reference_backend.py:69-125)."""
+    """Y = w[:, :, None] * D^q B(x) [B, I, R] on the device kernels (w None
+    for 1), differentiable to any order: dx = DerivContract(x, gY; q + 1, w),
+    dw = DerivContract(x, gY; q).  Together with DerivContract and SiluDeriv
+    it replaces the differentiable ATen recurrences the reference records
+    under create_graph=True (compute_basis and compute_basis_derivative,
+    spline_kan/reference_backend.py:69-125); w folds the elementwise factor
+    a recorded backward puts on them, so no [B, I, R] product is launched."""
 
     @staticmethod
-    def forward(ctx, x, grid, k: int, order: int):
+    def forward(ctx, x, grid, k: int, order: int, w):
         ctx.k, ctx.order = k, order
-        ctx.save_for_backward(x, grid)
-        return basis_deriv(x, grid, k, order)
+        ctx.save_for_backward(x, grid, w)
+        return basis_deriv(x, grid, k, order, w)
 
     @staticmethod
-    def backward(ctx, gH):
-        x, grid = ctx.saved_tensors
-        if not ctx.needs_input_grad[0]:
-            return None, None, None, None
-        return DerivContract.apply(x, grid, gH, ctx.k, ctx.order + 1), None, None, None
+    def backward(ctx, gY):
+        x, grid, w = ctx.saved_tensors
+        need_x, need_w = ctx.needs_input_grad[0], ctx.needs_input_grad[4]
+        gx = deriv_contract(x, grid, gY, ctx.k, ctx.order + 1, None, w) if need_x else None
+        gw = (deriv_contract(x, grid, gY, ctx.k, ctx.order, None, None)
+              if need_w and w is not None else None)
+        return gx, None, None, None, gw
 
 
-class DerivContract(torch.autograd.Function):
-    """gx[b, i] = sum_r G[b, i, r] D^q B_r(x[b, i]) on the device kernels; the
-    derivative tensor is never formed.  Gradients: w.r.t. G, g * D^q B(x)
-    (BasisDeriv); w.r.t. x, g * DerivContract of order q + 1.  Past q = k the
-    spline is constant between knots and every term is zero."""
+def _silu_sigmoid_poly(q: int):
+    """Coefficients c with d^q sigmoid / dx^q = sum_j c[j] s^j (s = sigmoid):
+    d/dx s^j = j s^j (1 - s)."""
+    c = [0.0, 1.0]                     # s
+    for _ in range(q):
+        nxt = [0.0] * (len(c) + 1)
+        for j, a in enumerate(c):
+            nxt[j] += j * a
+            nxt[j + 1] -= j * a
+        c = nxt
+    return c
+
+
+def _silu_deriv_torch(x, q: int):
+    """silu^(q)(x) = x s^(q) + q s^(q-1) from differentiable ATen operations,
+    for the orders past the native kernels."""
+    s = torch.sigmoid(x)
+    poly = lambda c: sum(a * s ** j for j, a in enumerate(c) if a != 0.0)
+    return x * poly(_silu_sigmoid_poly(q)) + q * poly(_silu_sigmoid_poly(q - 1))
+
+
+def silu_deriv_any(x, q: int, w=None):
+    """w * silu^(q)(x), differentiable: native for q <= 4, ATen beyond."""
+    if q <= SILU_MAX_ORDER:
+        return SiluDeriv.apply(x, q, w)
+    out = _silu_deriv_torch(x, q)
+    return out if w is None else out * w
+
+
+class SiluDeriv(torch.autograd.Function):
+    """Y = w * silu^(q)(x) on the device (w None for 1): dx = w g silu^(q+1)(x),
+    dw = g silu^(q)(x), each one launch (silu_deriv)."""
 
     @staticmethod
-    def forward(ctx, x, grid, G, k: int, order: int):
-        ctx.k, ctx.order = k, order
-        ctx.save_for_backward(x, grid, G)
-        return basis_deriv_contract(x, grid, k, G, order)
+    def forward(ctx, x, q: int, w):
+        ctx.q = q
+        ctx.save_for_backward(x, w)
+        return silu_deriv(x, q, w)
 
     @staticmethod
     def backward(ctx, g):
-        x, grid, G = ctx.saved_tensors
-        need_x, _, need_G = ctx.needs_input_grad[:3]
-        gx = gG = None
-        if need_x:
-            gx = g * DerivContract.apply(x, grid, G, ctx.k, ctx.order + 1)
-        if need_G:
-            gG = g.unsqueeze(-1) * BasisDeriv.apply(x, grid, ctx.k, ctx.order)
-        return gx, None, gG, None, None
+        x, w = ctx.saved_tensors
+        need_x, need_w = ctx.needs_input_grad[0], ctx.needs_input_grad[2]
+        gx = silu_deriv_any(x, ctx.q + 1, g if w is None else g * w) if need_x else None
+        gw = silu_deriv_any(x, ctx.q, g) if need_w and w is not None else None
+        return gx, None, gw
+
+
+def deriv_contract(x, grid, G, k: int, order: int, Gb=None, w=None):
+    """w * (sum_r G D^order B_r(x) + Gb silu^(order)(x)), differentiable;
+    Gb and w optional."""
+    if Gb is not None and order > SILU_MAX_ORDER:
+        spline = DerivContract.apply(x, grid, G, k, order, None, None)
+        out = spline + silu_deriv_any(x, order, Gb)
+        return out if w is None else out * w
+    return DerivContract.apply(x, grid, G, k, order, Gb, w)
+
+
+class DerivContract(torch.autograd.Function):
+    """gx[b, i] = w * (sum_r G[b, i, r] D^q B_r(x[b, i]) + Gb[b, i] silu^(q)(x))
+    on the device kernels (Gb, w optional); the derivative tensor is never
+    formed.  With v = g w: dx = DerivContract(x, G, Gb; q + 1, v),
+    dG = BasisDeriv(x; q, v), dGb = SiluDeriv(x; q, v), dw = DerivContract(x,
+    G, Gb; q, g).  Past q = k the spline part is zero between knots."""
+
+    @staticmethod
+    def forward(ctx, x, grid, G, k: int, order: int, Gb, w):
+        ctx.k, ctx.order = k, order
+        ctx.save_for_backward(x, grid, G, Gb, w)
+        return basis_deriv_contract(x, grid, k, G, order, Gb, w)
+
+    @staticmethod
+    def backward(ctx, g):
+        x, grid, G, Gb, w = ctx.saved_tensors
+        need_x, _, need_G, _, _, need_Gb, need_w = ctx.needs_input_grad
+        v = g if w is None else g * w
+        gx = deriv_contract(x, grid, G, ctx.k, ctx.order + 1, Gb, v) if need_x else None
+        gG = BasisDeriv.apply(x, grid, ctx.k, ctx.order, v) if need_G else None
+        gGb = silu_deriv_any(x, ctx.order, v) if need_Gb and Gb is not None else None
+        gw = (deriv_contract(x, grid, G, ctx.k, ctx.order, Gb, g)
+              if need_w and w is not None else None)
+        return gx, None, gG, None, None, gGb, gw
 
 
 def kan_backward_composite_device(D, x, grid, base_weight, spline_weight, spline_scaler,
@@ -578,15 +674,16 @@ def kan_backward_composite_device(D, x, grid, base_weight, spline_weight, spline
     basis is a function of x again, so the recorded graph carries the exact
     spline curvature.  Here the basis and its derivative come from the native
     kernels through BasisDeriv / DerivContract (dB/dx is contracted in
-    registers, never stored), and the products run on the MFMA contraction
-    engine through NativeMatmul (split over the sample axis where the output
-    is small), differentiable in turn.
+    registers, never stored; the SiLU branch's (D bw) silu'(x) is added in the
+    same launch), silu(x) from SiluDeriv, and the products run on the MFMA
+    contraction engine through NativeMatmul (split over the sample axis where
+    the output is small), differentiable in turn.
     """
     B, I = x.shape
     O, _, R = spline_weight.shape
     hb = _cmp.has_base(base_weight)
     mm = NativeMatmul.apply
-    H = BasisDeriv.apply(x, grid, spline_order, 0)
+    H = BasisDeriv.apply(x, grid, spline_order, 0, None)
     DtH = mm(D.t(), H.reshape(B, I * R)).reshape(O, I, R)
     if has_scaler:
         gsw = spline_scaler.unsqueeze(2) * DtH
@@ -595,11 +692,12 @@ def kan_backward_composite_device(D, x, grid, base_weight, spline_weight, spline
         gsw, gsc = DtH, None
     W = _cmp._eff_weight(spline_weight, spline_scaler, has_scaler)
     DW = mm(D, W.reshape(O, I * R)).reshape(B, I, R)
-    gx = DerivContract.apply(x, grid, DW, spline_order, 1)
     gbw = None
     if hb:
-        gbw = mm(D.t(), torch.nn.functional.silu(x))
-        gx = gx + mm(D, base_weight) * _cmp._silu_grad(x)
+        gbw = mm(D.t(), SiluDeriv.apply(x, 0, None))
+        gx = deriv_contract(x, grid, DW, spline_order, 1, mm(D, base_weight), None)
+    else:
+        gx = deriv_contract(x, grid, DW, spline_order, 1, None, None)
     return gx, gbw, gsw, gsc
 
 

@@ -59,9 +59,11 @@ SIGNATURES = {
     "kan_hip_matmul_workspace": (_int, [_int, _int, _int, _i64, _i64, _i64, ctypes.POINTER(_sz)]),
     "kan_hip_matmul": (_int, [_int, _int, _int, _i64, _i64, _i64, _vp, _i64, _vp, _i64, _vp, _i64,
                               _vp, _sz, _vp]),
-    "kan_hip_basis_deriv": (_int, [_int, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _vp]),
-    "kan_hip_basis_deriv_contract": (_int, [_int, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64,
-                                            _i64, _vp]),
+    "kan_hip_basis_deriv": (_int, [_int, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64,
+                                   _vp]),
+    "kan_hip_basis_deriv_contract": (_int, [_int, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64,
+                                            _i64, _i64, _i64, _vp]),
+    "kan_hip_silu_deriv": (_int, [_int, _vp, _vp, _vp, _i64, _i64, _vp]),
     "kan_hip_aug_width": (_i64, [_i64, _i64, _i64, _int]),
     "kan_hip_forward_workspace": (_int, [_int, _i64, _i64, _i64, _i64, _i64, _int,
                                          ctypes.POINTER(_sz)]),

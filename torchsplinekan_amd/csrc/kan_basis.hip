@@ -92,6 +92,7 @@ struct BasisShape {
   int vec;    // 16-byte vector path for the staged rows (alignment holds)
   int64_t ld_aux;  // row stride of silu(x) (basis) or of its gradient (basis_grad)
   int nfb;    // feature blocks (ceil(I / fb))
+  const void* scale;  // optional [n, I] factor of every item's output (T)
 };
 
 // Block of a basis launch: feature block f and sample-row group g.  The
@@ -274,6 +275,11 @@ __global__ __launch_bounds__(kBasisThreads) void basis_kernel(
 #pragma unroll
       for (int j = 0; j <= K; ++j) v[j] = T(0);
       if (m >= 0) span_window<K, DER, T>(t, nk, m, xv, v);
+      if (sh.scale != nullptr && m >= 0) {
+        const T w = static_cast<const T*>(sh.scale)[nn * sh.I + i0 + fi];
+#pragma unroll
+        for (int j = 0; j <= K; ++j) v[j] *= w;
+      }
       if (REC) {
 #pragma unroll
         for (int j = 0; j <= K; ++j) row[j] = v[j];
@@ -375,7 +381,8 @@ __global__ __launch_bounds__(kBasisThreads) void basis_grad_kernel(
         dense_derivative<T>(t, nk, xv, K, d);
         for (int r = 0; r < R; ++r) acc += row[r] * d[r];
       }
-      if (gbase != nullptr) acc += gb * silu_grad_of<T>(xv);
+      if (gbase != nullptr) acc += gb * silu_deriv_of<T>(xv, DER);
+      if (sh.scale != nullptr) acc *= static_cast<const T*>(sh.scale)[nn * sh.I + i0 + fi];
       gx[nn * sh.I + i0 + fi] = acc;
     }
     __syncthreads();
@@ -667,7 +674,8 @@ __global__ __launch_bounds__(kBasisThreads) void basis_grad_pf_kernel(
           if (r >= 0 && r < R) acc += row[r] * d[j];
         }
       }
-      if (gbase != nullptr) acc += gb * silu_grad_of<T>(xv);
+      if (gbase != nullptr) acc += gb * silu_deriv_of<T>(xv, DER);
+      if (sh.scale != nullptr) acc *= static_cast<const T*>(sh.scale)[nn * sh.I + i0 + lane];
       gx[nn * sh.I + i0 + lane] = acc;
     }
   }
@@ -816,6 +824,7 @@ BasisShape make_shape(int64_t n, int64_t I, int G, int R, size_t elem, int64_t l
   sh.ld_aux = ld;
   sh.fb = (int)(I < 64 ? I : 64);
   sh.nfb = (int)ceil_div(I, sh.fb);
+  sh.scale = nullptr;
   sh.subs = 64 / sh.fb;
   sh.waves = 4;
   // a dense R-row stage per lane bounds the waves of a block by LDS
@@ -900,12 +909,13 @@ int launch_basis(const T* x, const T* grid, T* out, int64_t ld_out, T* silu_out,
 template <typename T, int DER>
 bool launch_grad_pf(const T* x, const T* grid, const T* gH, int64_t ld_g, const T* gbase, T* gx,
                     int64_t n, int64_t I, int G, int k, hipStream_t st, int* rc,
-                    int64_t ld_base = -1) {
+                    int64_t ld_base = -1, const T* scale = nullptr) {
   if (k < DER) return false;
   const int R = G + k, nk = G + 2 * k + 1;
   int64_t by = 0;
   BasisShape sh = make_shape(n, I, G, R, sizeof(T), ld_g, gH, &by);
   if (ld_base >= 0) sh.ld_aux = ld_base;
+  sh.scale = scale;
   const int pv = grad_pf_vectors<T>(sh, R);
   if (pv == 0) return false;
   // two steps per block: more blocks in flight, each still overlapping one load
@@ -1026,11 +1036,44 @@ __global__ void zero_fill_kernel(T* __restrict__ out, int64_t count) {
        e += (int64_t)gridDim.x * blockDim.x)
     out[e] = T(0);
 }
+
+// out[e] = silu^(q)(x[e]) * w1[e] * w2[e] (factors optional)
+template <typename T>
+__global__ void silu_deriv_kernel(const T* __restrict__ x, const T* __restrict__ w1,
+                                  const T* __restrict__ w2, T* __restrict__ out, int64_t count,
+                                  int q) {
+  for (int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; e < count;
+       e += (int64_t)gridDim.x * blockDim.x) {
+    T v = silu_deriv_of<T>(x[e], q);
+    if (w1 != nullptr) v *= w1[e];
+    if (w2 != nullptr) v *= w2[e];
+    out[e] = v;
+  }
+}
 }  // namespace
 
 template <typename T>
-int launch_basis_deriv(const T* x, const T* grid, T* out, int64_t n, int64_t I, int G, int k,
-                       int order, hipStream_t st) {
+int launch_silu_deriv(const T* x, const T* w1, const T* w2, T* out, int64_t count, int order,
+                      hipStream_t st) {
+  if (count == 0) return KAN_OK;
+  if (order < 0 || order > kMaxSiluOrder)
+    return set_error(KAN_ERR_INVALID, "silu_deriv: order must lie in 0..%d, got %d",
+                     kMaxSiluOrder, order);
+  TimedLaunch timed(kClassOther, st,
+                    (double)sizeof(T) * (double)count * (2.0 + (w1 ? 1 : 0) + (w2 ? 1 : 0)));
+  hipLaunchKernelGGL(silu_deriv_kernel<T>, dim3(gs_blocks(count)), dim3(256), 0, st, x, w1, w2,
+                     out, count, order);
+  return check_launch("silu_deriv");
+}
+
+template int launch_silu_deriv<float>(const float*, const float*, const float*, float*, int64_t,
+                                      int, hipStream_t);
+template int launch_silu_deriv<double>(const double*, const double*, const double*, double*,
+                                       int64_t, int, hipStream_t);
+
+template <typename T>
+int launch_basis_deriv(const T* x, const T* grid, const T* scale, T* out, int64_t n, int64_t I,
+                       int G, int k, int order, hipStream_t st) {
   if (n == 0 || I == 0) return KAN_OK;
   const int R = G + k, nk = G + 2 * k + 1;
   if (order > k) {  // a degree-k piecewise polynomial: zero almost everywhere
@@ -1041,6 +1084,7 @@ int launch_basis_deriv(const T* x, const T* grid, T* out, int64_t n, int64_t I, 
   const bool rec = R >= kWindowRecordMinR;
   int64_t by = 0;
   BasisShape sh = make_shape(n, I, G, R, sizeof(T), I * R, out, &by, !rec);
+  sh.scale = scale;
   if (sh.nfb * by > 2147483647LL) return set_error(KAN_ERR_LIMIT, "basis_deriv: too many samples");
   const dim3 grid_dim((unsigned)(sh.nfb * by));
   const size_t smem = rec ? basis_window_smem<T>(sh, nk, k) : basis_smem<T>(sh, nk, R);
@@ -1072,30 +1116,40 @@ int launch_basis_deriv(const T* x, const T* grid, T* out, int64_t n, int64_t I, 
 }
 
 template <typename T>
-int launch_basis_deriv_contract(const T* x, const T* grid, const T* gH, T* gx, int64_t n,
-                                int64_t I, int G, int k, int order, hipStream_t st) {
+int launch_basis_deriv_contract(const T* x, const T* grid, const T* gH, const T* gbase,
+                                const T* scale, T* gx, int64_t n, int64_t I, int G, int k,
+                                int order, hipStream_t st) {
   if (n == 0 || I == 0) return KAN_OK;
   const int R = G + k, nk = G + 2 * k + 1;
-  if (order > k) {
+  if (order > k) {  // the spline part is zero; the base part (if any) remains
+    if (gbase != nullptr) return launch_silu_deriv<T>(x, gbase, scale, gx, n * I, order, st);
     hipLaunchKernelGGL(zero_fill_kernel<T>, dim3(gs_blocks(n * I)), dim3(256), 0, st, gx, n * I);
     return check_launch("basis_deriv_contract (zero)");
   }
-  TimedLaunch timed(kClassBasisGrad, st, (double)sizeof(T) * (double)n * (double)I * (2.0 + R));
+  TimedLaunch timed(kClassBasisGrad, st,
+                    (double)sizeof(T) * (double)n * (double)I *
+                        (2.0 + R + (gbase ? 1 : 0) + (scale ? 1 : 0)));
   int rc = KAN_OK;
-  const T* none = nullptr;
-  if ((order == 0 && launch_grad_pf<T, 0>(x, grid, gH, I * R, none, gx, n, I, G, k, st, &rc)) ||
-      (order == 1 && launch_grad_pf<T, 1>(x, grid, gH, I * R, none, gx, n, I, G, k, st, &rc)) ||
-      (order == 2 && launch_grad_pf<T, 2>(x, grid, gH, I * R, none, gx, n, I, G, k, st, &rc)) ||
-      (order == 3 && launch_grad_pf<T, 3>(x, grid, gH, I * R, none, gx, n, I, G, k, st, &rc)))
+  const int64_t lb = I;  // gbase is [n, I]
+  if ((order == 0 &&
+       launch_grad_pf<T, 0>(x, grid, gH, I * R, gbase, gx, n, I, G, k, st, &rc, lb, scale)) ||
+      (order == 1 &&
+       launch_grad_pf<T, 1>(x, grid, gH, I * R, gbase, gx, n, I, G, k, st, &rc, lb, scale)) ||
+      (order == 2 &&
+       launch_grad_pf<T, 2>(x, grid, gH, I * R, gbase, gx, n, I, G, k, st, &rc, lb, scale)) ||
+      (order == 3 &&
+       launch_grad_pf<T, 3>(x, grid, gH, I * R, gbase, gx, n, I, G, k, st, &rc, lb, scale)))
     return rc;
   int64_t by = 0;
   BasisShape sh = make_shape(n, I, G, R, sizeof(T), I * R, gH, &by);
+  sh.ld_aux = I;
+  sh.scale = scale;
   if (sh.nfb * by > 2147483647LL) return set_error(KAN_ERR_LIMIT, "basis_deriv_contract: too many samples");
   const dim3 grid_dim((unsigned)(sh.nfb * by));
   const size_t smem = basis_smem<T>(sh, nk, R);
 #define KAN_BDC_LAUNCH(KK, DD)                                                                  \
   hipLaunchKernelGGL((basis_grad_kernel<KK, T, 1, DD>), grid_dim, dim3(64 * sh.waves), smem, st, \
-                     x, grid, gH, (int64_t)I * R, (const T*)nullptr, gx, sh)
+                     x, grid, gH, (int64_t)I * R, gbase, gx, sh)
   if (k == 1) {
     if (order == 0) KAN_BDC_LAUNCH(1, 0);
     else KAN_BDC_LAUNCH(1, 1);
@@ -1113,15 +1167,16 @@ int launch_basis_deriv_contract(const T* x, const T* grid, const T* gH, T* gx, i
   return check_launch("basis_deriv_contract");
 }
 
-template int launch_basis_deriv<float>(const float*, const float*, float*, int64_t, int64_t, int,
-                                       int, int, hipStream_t);
-template int launch_basis_deriv<double>(const double*, const double*, double*, int64_t, int64_t,
-                                        int, int, int, hipStream_t);
-template int launch_basis_deriv_contract<float>(const float*, const float*, const float*, float*,
-                                                int64_t, int64_t, int, int, int, hipStream_t);
+template int launch_basis_deriv<float>(const float*, const float*, const float*, float*,
+                                       int64_t, int64_t, int, int, int, hipStream_t);
+template int launch_basis_deriv<double>(const double*, const double*, const double*, double*,
+                                        int64_t, int64_t, int, int, int, hipStream_t);
+template int launch_basis_deriv_contract<float>(const float*, const float*, const float*,
+                                                const float*, const float*, float*, int64_t,
+                                                int64_t, int, int, int, hipStream_t);
 template int launch_basis_deriv_contract<double>(const double*, const double*, const double*,
-                                                 double*, int64_t, int64_t, int, int, int,
-                                                 hipStream_t);
+                                                 const double*, const double*, double*, int64_t,
+                                                 int64_t, int, int, int, hipStream_t);
 
 template <typename T>
 int launch_pack_basis(const T* basis, const T* x, T* aug, int64_t ld_aug, int64_t n, int64_t I,

@@ -608,8 +608,9 @@ int kan_hip_matmul(int dtype, int trans_a, int trans_b, int64_t M, int64_t N, in
                                static_cast<double*>(ws), st);
 }
 
-int kan_hip_basis_deriv(int dtype, const void* x, const void* grid, void* out, int64_t n,
-                        int64_t I, int64_t G, int64_t k, int64_t order, void* stream) {
+int kan_hip_basis_deriv(int dtype, const void* x, const void* grid, const void* scale, void* out,
+                        int64_t n, int64_t I, int64_t G, int64_t k, int64_t order,
+                        void* stream) {
   KAN_TRY(check_dtype(dtype, "kan_basis_deriv"));
   KAN_TRY(check_layer("kan_basis_deriv", n, I, 0, G, k));
   if (order < 0 || order > 64)
@@ -622,22 +623,27 @@ int kan_hip_basis_deriv(int dtype, const void* x, const void* grid, void* out, i
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (dtype == KAN_DTYPE_F32)
     return launch_basis_deriv<float>(static_cast<const float*>(x), static_cast<const float*>(grid),
-                                     static_cast<float*>(out), n, I, (int)G, (int)k, (int)order,
-                                     st);
+                                     static_cast<const float*>(scale), static_cast<float*>(out),
+                                     n, I, (int)G, (int)k, (int)order, st);
   return launch_basis_deriv<double>(static_cast<const double*>(x),
-                                    static_cast<const double*>(grid), static_cast<double*>(out),
+                                    static_cast<const double*>(grid),
+                                    static_cast<const double*>(scale), static_cast<double*>(out),
                                     n, I, (int)G, (int)k, (int)order, st);
 }
 
 int kan_hip_basis_deriv_contract(int dtype, const void* x, const void* grid, const void* gH,
-                                 void* gx, int64_t n, int64_t I, int64_t G, int64_t k,
-                                 int64_t order, void* stream) {
+                                 const void* gbase, const void* scale, void* gx, int64_t n,
+                                 int64_t I, int64_t G, int64_t k, int64_t order, void* stream) {
   KAN_TRY(check_dtype(dtype, "kan_basis_deriv_contract"));
   KAN_TRY(check_layer("kan_basis_deriv_contract", n, I, 0, G, k));
   if (order < 0 || order > 64)
     return set_error(KAN_ERR_INVALID,
                      "kan_basis_deriv_contract: order must lie in 0..64, got %lld",
                      (long long)order);
+  if (gbase != nullptr && order > kMaxSiluOrder)
+    return set_error(KAN_ERR_INVALID,
+                     "kan_basis_deriv_contract: the base term supports orders 0..%d, got %lld",
+                     kMaxSiluOrder, (long long)order);
   if (n == 0 || I == 0) return KAN_OK;
   KAN_TRY(need_ptr(x, "kan_basis_deriv_contract", "x"));
   KAN_TRY(need_ptr(grid, "kan_basis_deriv_contract", "grid"));
@@ -647,12 +653,33 @@ int kan_hip_basis_deriv_contract(int dtype, const void* x, const void* grid, con
   if (dtype == KAN_DTYPE_F32)
     return launch_basis_deriv_contract<float>(
         static_cast<const float*>(x), static_cast<const float*>(grid),
-        static_cast<const float*>(gH), static_cast<float*>(gx), n, I, (int)G, (int)k,
+        static_cast<const float*>(gH), static_cast<const float*>(gbase),
+        static_cast<const float*>(scale), static_cast<float*>(gx), n, I, (int)G, (int)k,
         (int)order, st);
   return launch_basis_deriv_contract<double>(
       static_cast<const double*>(x), static_cast<const double*>(grid),
-      static_cast<const double*>(gH), static_cast<double*>(gx), n, I, (int)G, (int)k, (int)order,
-      st);
+      static_cast<const double*>(gH), static_cast<const double*>(gbase),
+      static_cast<const double*>(scale), static_cast<double*>(gx), n, I, (int)G, (int)k,
+      (int)order, st);
+}
+
+int kan_hip_silu_deriv(int dtype, const void* x, const void* scale, void* out, int64_t count,
+                       int64_t order, void* stream) {
+  KAN_TRY(check_dtype(dtype, "kan_silu_deriv"));
+  if (count < 0) return set_error(KAN_ERR_INVALID, "kan_silu_deriv: negative count");
+  if (order < 0 || order > kMaxSiluOrder)
+    return set_error(KAN_ERR_INVALID, "kan_silu_deriv: order must lie in 0..%d, got %lld",
+                     kMaxSiluOrder, (long long)order);
+  if (count == 0) return KAN_OK;
+  KAN_TRY(need_ptr(x, "kan_silu_deriv", "x"));
+  KAN_TRY(need_ptr(out, "kan_silu_deriv", "out"));
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (dtype == KAN_DTYPE_F32)
+    return launch_silu_deriv<float>(static_cast<const float*>(x), static_cast<const float*>(scale),
+                                     nullptr, static_cast<float*>(out), count, (int)order, st);
+  return launch_silu_deriv<double>(static_cast<const double*>(x),
+                                   static_cast<const double*>(scale), nullptr,
+                                   static_cast<double*>(out), count, (int)order, st);
 }
 
 int kan_hip_basis_grad(int dtype, const void* x, const void* grid, const void* gH, void* gx,

@@ -81,6 +81,26 @@ __device__ __forceinline__ float silu_grad_of<float>(float x) {
   return sg * (1.0f + x * (1.0f - sg));
 }
 
+// Order-q derivative of silu(x) = x s(x), s the logistic sigmoid, q = 0..4:
+//   silu^(q) = x s^(q) + q s^(q-1), with d = s (1 - s) and
+//   s^(1) = d, s^(2) = d (1 - 2 s), s^(3) = d (1 - 6 d),
+//   s^(4) = d (1 - 2 s) (1 - 12 d).
+// q = 0 and 1 are silu_of and silu_grad_of themselves, so the first-order
+// kernels and this one agree bit for bit.  Higher q returns NaN.
+constexpr int kMaxSiluOrder = 4;
+template <typename T>
+__device__ __forceinline__ T silu_deriv_of(T x, int q) {
+  if (q == 0) return silu_of<T>(x);
+  if (q == 1) return silu_grad_of<T>(x);
+  const T sg = T(1) / (T(1) + exp(-x));
+  const T d = sg * (T(1) - sg);
+  if (q == 2) return x * (d * (T(1) - T(2) * sg)) + T(2) * d;
+  if (q == 3) return x * (d * (T(1) - T(6) * d)) + T(3) * (d * (T(1) - T(2) * sg));
+  if (q == 4)
+    return x * (d * (T(1) - T(2) * sg) * (T(1) - T(12) * d)) + T(4) * (d * (T(1) - T(6) * d));
+  return T(NAN);
+}
+
 // ---- optional HIP-event timing of kernel launches ---------------------------
 // When enabled (kan_hip_timing_enable), every launch below records a pair of
 // events on its stream together with the launch's algorithmic work (flops
@@ -137,14 +157,22 @@ int launch_basis_grad_compact(const float* x, const float* grid, const float* ew
                               hipStream_t st);
 
 // Order-`order` derivatives of the basis, [n, I, R] (order 0 = values; order
-// > k gives zeros), and their contraction gx = sum_r gH * D^order B_r.
+// > k gives zeros), each item's row times scale[n, i] when scale is given;
+// and their contraction gx = scale * (sum_r gH * D^order B_r
+// + gbase * silu^(order)(x)), gbase and scale optional ([n, I] each).
 template <typename T>
-int launch_basis_deriv(const T* x, const T* grid, T* out, int64_t n, int64_t I, int G, int k,
-                       int order, hipStream_t st);
+int launch_basis_deriv(const T* x, const T* grid, const T* scale, T* out, int64_t n, int64_t I,
+                       int G, int k, int order, hipStream_t st);
 
 template <typename T>
-int launch_basis_deriv_contract(const T* x, const T* grid, const T* gH, T* gx, int64_t n,
-                                int64_t I, int G, int k, int order, hipStream_t st);
+int launch_basis_deriv_contract(const T* x, const T* grid, const T* gH, const T* gbase,
+                                const T* scale, T* gx, int64_t n, int64_t I, int G, int k,
+                                int order, hipStream_t st);
+
+// out[e] = silu^(order)(x[e]) * w1[e] * w2[e] (w1, w2 optional; order <= 4).
+template <typename T>
+int launch_silu_deriv(const T* x, const T* w1, const T* w2, T* out, int64_t count, int order,
+                      hipStream_t st);
 
 template <typename T>
 int launch_pack_basis(const T* basis, const T* x, T* aug, int64_t ld_aug, int64_t n, int64_t I,

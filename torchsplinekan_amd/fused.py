@@ -48,7 +48,7 @@ class NativeBasis(torch.autograd.Function):
             return None, None, None
         if torch.is_grad_enabled():
             # recorded backward: the native contraction, itself differentiable
-            return _C.DerivContract.apply(x, grid, gH, ctx.k, 1), None, None
+            return _C.deriv_contract(x, grid, gH, ctx.k, 1), None, None
         return _C.basis_grad(x.contiguous(), grid, ctx.k, gH.contiguous()), None, None
 
 
@@ -77,9 +77,8 @@ class NativeBasisSilu(torch.autograd.Function):
         if gH is None:
             gH = x.new_zeros(B, I, grid.shape[1] - ctx.k - 1)
         if torch.is_grad_enabled():
-            sg = torch.sigmoid(x)
-            gx = _C.DerivContract.apply(x, grid, gH, ctx.k, 1) + gs * (sg * (1 + x * (1 - sg)))
-            return gx, None, None
+            # recorded backward: spline and SiLU terms in one differentiable native call
+            return _C.deriv_contract(x, grid, gH, ctx.k, 1, gs), None, None
         return _C.basis_silu_grad(x, grid, ctx.k, gH, gs), None, None
 
 
