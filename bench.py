@@ -79,6 +79,9 @@ def parse():
                          "are reported against the FP64 peak)")
     ap.add_argument("--n", type=int, default=0, help="samples per step (default: the config's)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--native-only", action="store_true",
+                    help="pinn: skip the reference formulation's run on the same GPU (for "
+                         "profiling the native step alone)")
     ap.add_argument("--no-other-configs", action="store_true",
                     help="c3 only: skip the c2, c4 and c5 figures of the JSON line")
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
@@ -764,12 +767,14 @@ def bench_pinn(args):
     kern = {c: _lib.timing_read(c) for c in ("basis", "basis_grad", "contraction", "other")}
     _lib.timing_enable(False)
     # the reference's recorded backward (dense differentiable recurrences) on the same GPU
-    native_fn = _C.kan_backward_composite_device
-    _C.kan_backward_composite_device = cmp.kan_backward_composite
-    try:
-        dense_s = timed(max(2, args.steps // 2))
-    finally:
-        _C.kan_backward_composite_device = native_fn
+    dense_s = float("nan")
+    if not args.native_only:
+        native_fn = _C.kan_backward_composite_device
+        _C.kan_backward_composite_device = cmp.kan_backward_composite
+        try:
+            dense_s = timed(max(2, args.steps // 2))
+        finally:
+            _C.kan_backward_composite_device = native_fn
     cpu = None
     if not args.no_cpu_baseline:
         ref = KAN(widths, grid_size=G, spline_order=k, backend="reference").double()

@@ -124,6 +124,9 @@ using CfgF32Small = Cfg<float, 128, 128, 32, 2, 2, 32, 2>;
 // 64 x 64 each, so no wave computes padding columns.
 using CfgF32Narrow = Cfg<float, 256, 64, 32, 4, 1, 32, 1>;
 using CfgF64 = Cfg<double, 128, 128, 16, 2, 2, 16, 1>;
+// fp64, 256 x 128 block tiles: 8 waves of 64 x 64, two per SIMD (while one
+// wave waits at the slab barrier the other issues MFMAs)
+using CfgF64Big = Cfg<double, 256, 128, 16, 4, 2, 16, 1>;
 
 template <typename T>
 struct GemmParams {
@@ -906,7 +909,9 @@ struct CfgModelF64 {
   int bm, bn, bk, blocks_per_cu;
   double eff;
 };
-constexpr CfgModelF64 kModelF64 = {128, 128, 16, 1, 0.80};
+// (measured at c3's shapes: 0.81-0.83 of the FP64 peak for the 8-wave tile,
+// 0.75-0.82 for the 4-wave one, whose parameter product lost most)
+constexpr CfgModelF64 kModelF64[2] = {{256, 128, 16, 1, 0.84}, {128, 128, 16, 1, 0.80}};
 constexpr double kPeakPerCuF64 = 78.6e12 / 256.0;
 constexpr double kKOverheadF64 = 256.0;
 
@@ -927,8 +932,7 @@ double est_seconds(const CfgModel& c, int64_t M, int64_t N, int64_t K, int split
   return (double)per_cu * block + split_traffic_s(M, N, splits, 4);
 }
 
-double est_seconds_f64(int64_t M, int64_t N, int64_t K, int splits) {
-  const CfgModelF64& c = kModelF64;
+double est_seconds_f64(const CfgModelF64& c, int64_t M, int64_t N, int64_t K, int splits) {
   const int64_t cus = device_cu_count();
   const int64_t tiles = ceil_div(M, c.bm) * ceil_div(N, c.bn) * splits;
   const int64_t waves = ceil_div(tiles, cus * c.blocks_per_cu);
@@ -942,6 +946,17 @@ double est_seconds_f64(int64_t M, int64_t N, int64_t K, int splits) {
 // 2 narrow, 3 the 4-wave 256x256), or -1 to leave the choice to the cost
 // model.
 int forced_cfg_f32() { return kan_hip_get_route(KAN_ROUTE_GEMM_TILE); }
+
+// fp64 configuration (0 = 256 x 128 with 8 waves, 1 = 128 x 128 with 4) for
+// a split count; the route forces 0 for "256" and 1 for "128".
+int pick_cfg_f64(int64_t M, int64_t N, int64_t K, int splits) {
+  const int forced = kan_hip_get_route(KAN_ROUTE_GEMM_TILE);
+  if (forced == 0 || forced == 1) return forced;
+  return est_seconds_f64(kModelF64[0], M, N, K, splits) <=
+                 est_seconds_f64(kModelF64[1], M, N, K, splits)
+             ? 0
+             : 1;
+}
 
 // fp32 configuration (0 = big, 1 = small, 2 = narrow, 3 = 4-wave big, only
 // when forced) for a given split count; the narrow one only where N fits its
@@ -1453,8 +1468,8 @@ int gemm_pick_splits(int64_t M, int64_t N, int64_t K, int64_t max_slice_elems) {
       if (s > 1 && K / s < 8 * kModelF32[0].bk) break;
       t = est_seconds(kModelF32[pick_cfg_f32(M, N, K, s)], M, N, K, s);
     } else {
-      if (s > 1 && K / s < 8 * kModelF64.bk) break;
-      t = est_seconds_f64(M, N, K, s);
+      if (s > 1 && K / s < 8 * kModelF64[1].bk) break;
+      t = est_seconds_f64(kModelF64[pick_cfg_f64(M, N, K, s)], M, N, K, s);
     }
     if (s == 1 || t < best_t * (1.0 - 1e-9)) {
       best = s;
@@ -1495,7 +1510,10 @@ int launch_gemm(int layout, int64_t M, int64_t N, int64_t K, const T* A, int64_t
     else if (cfg == 2) rc = launch_layout<CfgF32Narrow>(layout, p, splits, st);
     else rc = launch_layout<CfgF32Small>(layout, p, splits, st);
   } else {
-    rc = launch_layout<CfgF64>(layout, p, splits, st);
+    if (pick_cfg_f64(M, N, K, splits < 1 ? 1 : splits) == 0)
+      rc = launch_layout<CfgF64Big>(layout, p, splits, st);
+    else
+      rc = launch_layout<CfgF64>(layout, p, splits, st);
   }
   if (rc != KAN_OK) return rc;
   return check_launch("gemm");
