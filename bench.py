@@ -889,10 +889,11 @@ def bench_infer(args):
 
 
 def bench_stream(args):
-    """HBM streaming ceiling of this GPU for buffers of c3's size: float4
+    """HBM streaming ceilings of this GPU for buffers of c3's size: float4
     write, read and copy kernels (kan_hip_stream_probe) over a buffer of the
-    c3 augmented basis' size (65536 x 14336 fp32 = 3.76 GB), each timed with
-    the library's HIP events; the basis kernels' GB/s are judged against
+    c3 augmented basis' size (65536 x 14336 fp32 = 3.76 GB), and the write
+    pattern of the basis kernel on that layout (row segments), each timed
+    with the library's HIP events; the basis kernels' GB/s are judged against
     these."""
     import torch
     from torchsplinekan_amd import _C, _lib
@@ -901,7 +902,8 @@ def bench_stream(args):
     a = torch.empty(nbytes // 4, dtype=torch.float32, device=dev)
     b = torch.zeros(nbytes // 4, dtype=torch.float32, device=dev)
     out = {}
-    for mode, name, moved in ((0, "write", nbytes), (1, "read", nbytes), (2, "copy", 2 * nbytes)):
+    for mode, name, moved in ((0, "write", nbytes), (1, "read", nbytes), (2, "copy", 2 * nbytes),
+                              (3, "basis_row_segments", nbytes)):
         for _ in range(args.warmup):
             _C.stream_probe(mode, a, b)
         torch.cuda.synchronize()

@@ -384,9 +384,11 @@ int kan_hip_timing_read(int kernel_class, double* total_ms, int64_t* launches, d
 /* Streaming probe (measurement support, no reference counterpart): float4
  * kernels that write a (mode 0), read a (mode 1; b receives nothing in
  * practice but must be a valid 4-byte buffer) or copy a to b (mode 2), over
- * `bytes` (a multiple of 16; 16-byte aligned buffers).  Timed as kernel
- * class 6 with the bytes moved as work; the HBM ceiling the memory-bound
- * kernels are compared with. */
+ * `bytes` (a multiple of 16; 16-byte aligned buffers); mode 3 writes a in
+ * the row-segment pattern of the basis kernel at c3's layout (whole rows of
+ * 14336 floats that fit in `bytes`).  Timed as kernel class 6 with the bytes
+ * moved as work; the HBM ceilings the memory-bound kernels are compared
+ * with. */
 int kan_hip_stream_probe(int mode, void* a, void* b, int64_t bytes, void* stream);
 
 #ifdef __cplusplus

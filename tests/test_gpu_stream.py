@@ -1,7 +1,8 @@
 """The streaming probe (kan_hip_stream_probe, measurement support): write
 fills the buffer with the (1, 2, 3, 4) float4 pattern, copy reproduces the
 source exactly, read leaves its operands untouched; sizes that are not whole
-float4 are refused before any launch."""
+float4 are refused before any launch; the row-segment mode writes exactly
+the whole rows that fit."""
 
 import pytest
 import torch
@@ -27,3 +28,15 @@ def test_stream_probe_modes():
     assert torch.equal(src, before) and torch.equal(b, before)
     assert _lib.LIB.kan_hip_stream_probe(0, a.data_ptr(), b.data_ptr(), 20, None) == \
         _lib.KAN_ERR_INVALID
+    assert _lib.LIB.kan_hip_stream_probe(4, a.data_ptr(), b.data_ptr(), 16, None) == \
+        _lib.KAN_ERR_INVALID
+    # mode 3: every float of the whole rows (13 * 1024 segment values of 4-float
+    # pattern, then 1024 values of 5.0) is written, nothing past them
+    ld, rows = 14336, 37
+    c = torch.zeros(rows * ld + 100, device="cuda")
+    _C.stream_probe(3, c, c)
+    torch.cuda.synchronize()
+    body = c[:rows * ld].view(rows, ld)
+    assert torch.equal(body[:, :13312], torch.tensor([1.0, 2.0, 3.0, 4.0], device="cuda")
+                       .repeat(rows, 3328))
+    assert bool((body[:, 13312:] == 5.0).all()) and bool((c[rows * ld:] == 0).all())

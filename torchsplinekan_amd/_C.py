@@ -321,7 +321,8 @@ def kan_apply(x, grid, base_weight, spline_weight, spline_scaler, spline_order: 
 
 def stream_probe(mode: int, a: torch.Tensor, b: torch.Tensor) -> None:
     """Streaming probe over a's bytes (measurement support): mode 0 writes a,
-    1 reads a, 2 copies a into b (b at least as large as a for mode 2)."""
+    1 reads a, 2 copies a into b (b at least as large as a for mode 2), 3
+    writes a in the basis kernel's row-segment pattern (rows of 14336 floats)."""
     _req(a.is_cuda and b.is_cuda and a.is_contiguous() and b.is_contiguous(),
          "stream_probe: contiguous device tensors")
     nbytes = a.numel() * a.element_size() // 16 * 16
