@@ -592,10 +592,10 @@ def run_c4(args, dev, steps, warmup):
     # products, 6 n O I (R+1) flops; parameter kernel for the first layer,
     # whose input needs no gradient: 4 n O I (R+1))
     if f64:
-        roof = _mfma_roofline(kern, "edge_grad", "edge_param_grad_kernel + "
-                              "edge_input_grad_kernel (fp64): mean|phi| backward",
+        roof = _mfma_roofline(kern, "edge_grad", "edge_param_mfma64_kernel + "
+                              "edge_input_mfma64_kernel (fp64 MFMA): mean|phi| backward, "
+                              "4 n O I (R+1) flops per launch",
                               None, None, PEAK_FP64_TFLOPS)
-        roof["bound"] = "fp64"
     else:
         roof = _mfma_roofline(kern, "edge_grad", "edge_bwd_mfma_kernel (both gradient sides, "
                               "dL/dy folded in; edge_bwd_stage_kernel for the 64-wide layer) + "

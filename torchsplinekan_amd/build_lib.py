@@ -18,7 +18,7 @@ BUILD_DIR = os.path.join(PKG_DIR, "_build")
 LIB_NAME = "libkan_hip.so"
 LIB_PATH = os.path.join(PKG_DIR, LIB_NAME)
 SOURCES = ["kan_capi.hip", "kan_basis.hip", "kan_gemm.hip", "kan_edge.hip", "kan_edge_mfma.hip",
-           "kan_refit.hip", "kan_stream.hip", "kan_reg.hip"]
+           "kan_edge_mfma64.hip", "kan_refit.hip", "kan_stream.hip", "kan_reg.hip"]
 ARCH = "gfx950"
 
 COMMON_FLAGS = [

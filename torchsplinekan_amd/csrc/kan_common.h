@@ -250,6 +250,21 @@ int launch_matmul(int layout, int64_t M, int64_t N, int64_t K, const T* A, int64
 template <typename T>
 int gemm_pick_splits(int64_t M, int64_t N, int64_t K, int64_t max_slice_elems = -1);
 
+// fp64 edge statistic on MFMA (kan_edge_mfma64.hip), for R + 1 <= 16; the
+// VALU kernels of kan_edge.hip serve wider rows.
+bool edge_mfma64_applies(int64_t R);
+int edge_mfma64_splits(int64_t n, int64_t I, int64_t O, bool backward);
+int launch_edge_forward_mfma64(const double* s, const double* H, const double* bw,
+                               const double* W, double* a, double* part, int splits, int64_t n,
+                               int64_t I, int64_t O, int64_t R, hipStream_t st);
+int launch_edge_param_mfma64(const double* ga, const double* s, const double* H,
+                             const double* bw, const double* W, double* dbw, double* dW,
+                             double* part, int splits, int64_t n, int64_t I, int64_t O, int64_t R,
+                             hipStream_t st);
+int launch_edge_input_mfma64(const double* ga, const double* s, const double* H,
+                             const double* bw, const double* W, double* ds, double* dH,
+                             int64_t n, int64_t I, int64_t O, int64_t R, hipStream_t st);
+
 template <typename T>
 int launch_edge_forward(const T* s, const T* H, const T* bw, const T* W, T* a, T* part,
                         int splits, int64_t n, int64_t I, int64_t O, int64_t R, hipStream_t st);

@@ -17,6 +17,8 @@
 // partial slice and a finalize kernel adds the slices in fixed order, so the
 // result is deterministic (no atomics).  sign(0) = 0 (kan_reg_cuda.cu:25-28).
 
+#include <type_traits>
+
 #include "kan_common.h"
 
 namespace kan {
@@ -374,6 +376,7 @@ inline int fin_blocks(int64_t total) {
 
 int edge_pick_splits(int dtype, int64_t n, int64_t I, int64_t O, int64_t R, bool backward) {
   if (dtype == KAN_DTYPE_F32) return edge_mfma_splits(n, I, O, R, backward);
+  if (edge_mfma64_applies(R)) return edge_mfma64_splits(n, I, O, backward);
   const int64_t blocks = ceil_div(O, kEdgeThreads) * I;
   const int64_t target = 4LL * device_cu_count();
   int64_t s = ceil_div(target, blocks > 0 ? blocks : 1);
@@ -389,6 +392,15 @@ int launch_edge_forward(const T* s, const T* H, const T* bw, const T* W, T* a, T
                         int splits, int64_t n, int64_t I, int64_t O, int64_t R, hipStream_t st) {
   if (O == 0 || I == 0) return KAN_OK;
   if (splits > 1 && part == nullptr) return set_error(KAN_ERR_WORKSPACE, "edge_abs_mean: missing workspace");
+  if constexpr (std::is_same<T, double>::value) {
+    if (edge_mfma64_applies(R)) {
+      const int rc = launch_edge_forward_mfma64(s, H, bw, W, a, part, splits, n, I, O, R, st);
+      if (rc != KAN_OK || splits == 1) return rc;
+      hipLaunchKernelGGL((edge_forward_finalize<T>), dim3(fin_blocks(O * I)), dim3(256), 0, st,
+                         part, a, splits, O * I, n);
+      return check_launch("edge_abs_mean_finalize");
+    }
+  }
   const int64_t per_split = round_up(ceil_div(n, splits), kEdgeTile);
   dim3 grid((unsigned)ceil_div(O, kEdgeThreads), (unsigned)I, (unsigned)splits);
   const bool fin = splits == 1;
@@ -413,14 +425,25 @@ int launch_edge_backward(const T* ga, const T* s, const T* H, const T* bw, const
   if ((dbw != nullptr || dW != nullptr) && O > 0 && I > 0) {
     if (splits > 1 && part == nullptr)
       return set_error(KAN_ERR_WORKSPACE, "edge_abs_mean_backward: missing workspace");
-    const int64_t per_split = round_up(ceil_div(n, splits), kEdgeTile);
-    dim3 grid((unsigned)ceil_div(O, kEdgeThreads), (unsigned)I, (unsigned)splits);
     const bool fin = splits == 1;
-    TimedLaunch timed(kClassEdgeGrad, st, 4.0 * (double)n * (double)O * (double)I * (double)R1);
-    KAN_EDGE_DISPATCH(R1, hipLaunchKernelGGL((edge_param_grad_kernel<T, RP>), grid,
-                                             dim3(kEdgeThreads), 0, st, ga, s, H, bw, W, dbw, dW,
-                                             part, n, (int)I, (int)O, (int)R, per_split, fin));
-    int rc = check_launch("edge_abs_mean_backward(params)");
+    int rc = KAN_OK;
+    bool done = false;
+    if constexpr (std::is_same<T, double>::value) {
+      if (edge_mfma64_applies(R)) {
+        rc = launch_edge_param_mfma64(ga, s, H, bw, W, dbw, dW, part, splits, n, I, O, R, st);
+        done = true;
+      }
+    }
+    if (!done) {
+      const int64_t per_split = round_up(ceil_div(n, splits), kEdgeTile);
+      dim3 grid((unsigned)ceil_div(O, kEdgeThreads), (unsigned)I, (unsigned)splits);
+      TimedLaunch timed(kClassEdgeGrad, st, 4.0 * (double)n * (double)O * (double)I * (double)R1);
+      KAN_EDGE_DISPATCH(R1, hipLaunchKernelGGL((edge_param_grad_kernel<T, RP>), grid,
+                                               dim3(kEdgeThreads), 0, st, ga, s, H, bw, W, dbw,
+                                               dW, part, n, (int)I, (int)O, (int)R, per_split,
+                                               fin));
+      rc = check_launch("edge_abs_mean_backward(params)");
+    }
     if (rc != KAN_OK) return rc;
     if (!fin) {
       hipLaunchKernelGGL((edge_param_finalize<T>), dim3(fin_blocks(O * I * R1)), dim3(256), 0, st,
@@ -430,6 +453,10 @@ int launch_edge_backward(const T* ga, const T* s, const T* H, const T* bw, const
     }
   }
   if ((ds != nullptr || dH != nullptr) && n > 0 && I > 0) {
+    if constexpr (std::is_same<T, double>::value) {
+      if (edge_mfma64_applies(R))
+        return launch_edge_input_mfma64(ga, s, H, bw, W, ds, dH, n, I, O, R, st);
+    }
     dim3 grid((unsigned)ceil_div(n, kEdgeThreads), (unsigned)I);
     TimedLaunch timed(kClassEdgeGrad, st, 4.0 * (double)n * (double)O * (double)I * (double)R1);
     KAN_EDGE_DISPATCH(R1, hipLaunchKernelGGL((edge_input_grad_kernel<T, RP>), grid,

@@ -327,7 +327,7 @@ class KANLinear(nn.Module):
         interior [t_k, t_{k+G}], moved out to min(x) - margin (max(x) + margin)
         on a side where samples lie beyond it, and clipped to the outermost
         current knots, past which the current spline is identically zero
-        (spline_kan/kan_linear.py:562-570)."""
+        (spline_kan/kan_linear.py:567-572)."""
         k, g = self.spline_order, self.grid
         interior = g[:, [k, k + self.grid_size]]
         xmin, xmax = torch.aminmax(x_flat, dim=0)
