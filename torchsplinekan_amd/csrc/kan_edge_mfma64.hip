@@ -44,13 +44,14 @@ __device__ __forceinline__ double sign_d(double v) {
 
 // Tilings chosen by a sweep on MI355X at c4's layers (n = 16384, R + 1 = 12):
 // the forward prefetches the next sample tile (it holds 4 waves per SIMD
-// with it); the parameter kernel does not (at 1-2 waves per SIMD the
+// with it) and takes 8 output tiles per block, 4 for layers of at most 64
+// outputs (8 left half the block idle there); the parameter kernel does not (at 1-2 waves per SIMD the
 // prefetch cost a third of its rate) and takes 4 output tiles per block at
 // 4 waves per SIMD (8 tiles: 2 waves, 6 % slower, and half the block idle
 // at O = 64); the input kernel takes 4 sample tiles per wave, at 4 waves per
 // SIMD where a block has more than 4 output tiles to loop over.
 constexpr int kE64Threads = 256;  // 4 waves
-constexpr int kE64OT = 8;         // output tiles of 16 per forward block
+constexpr int kE64OT = 8;         // output tiles of 16 per forward block (4 where O <= 64)
 constexpr int kE64Out = kE64OT * 16;
 constexpr int kE64POT = 4;        // output tiles of 16 per parameter block
 constexpr int kE64NT = 4;         // sample tiles of 16 per wave (input product)
@@ -105,27 +106,28 @@ __device__ __forceinline__ E64Block e64_block(int I, int ochunks) {
   return b;
 }
 
-// Forward: a[o, i] (or the split's partial sum) for the block's kE64Out outputs.
-template <int KS>
+// Forward: a[o, i] (or the split's partial sum) for the block's 16 * OT outputs.
+template <int KS, int OT>
 __global__ __launch_bounds__(kE64Threads) void edge_fwd_mfma64_kernel(
     const double* __restrict__ s, const double* __restrict__ H, const double* __restrict__ bw,
     const double* __restrict__ W, double* __restrict__ out, int64_t n, int I, int O, int R,
     int64_t per_split, int ochunks, int final_out) {
-  __shared__ double ws[kE64Out][kE64Stride];
-  __shared__ double red[4][kE64Out];
+  constexpr int OUT = OT * 16;
+  __shared__ double ws[OUT][kE64Stride];
+  __shared__ double red[4][OUT];
   const E64Block blk = e64_block(I, ochunks);
-  const int o0 = blk.oc * kE64Out;
-  stage_wc(ws, nullptr, nullptr, bw, W, o0, kE64Out, O, I, blk.i, R, 0.0);
+  const int o0 = blk.oc * OUT;
+  stage_wc(ws, nullptr, nullptr, bw, W, o0, OUT, O, I, blk.i, R, 0.0);
   __syncthreads();
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, q = lane >> 4, r = lane & 15;
-  double b[kE64OT][KS];
+  double b[OT][KS];
 #pragma unroll
-  for (int t = 0; t < kE64OT; ++t)
+  for (int t = 0; t < OT; ++t)
 #pragma unroll
     for (int k = 0; k < KS; ++k) b[t][k] = ws[16 * t + r][4 * k + q];
-  double acc_abs[kE64OT];
+  double acc_abs[OT];
 #pragma unroll
-  for (int t = 0; t < kE64OT; ++t) acc_abs[t] = 0.0;
+  for (int t = 0; t < OT; ++t) acc_abs[t] = 0.0;
   const int64_t nb = (int64_t)blk.split * per_split;
   const int64_t ne = min(n, nb + per_split);
   double a[KS];
@@ -136,7 +138,7 @@ __global__ __launch_bounds__(kE64Threads) void edge_fwd_mfma64_kernel(
 #pragma unroll
     for (int k = 0; k < KS; ++k) an[k] = hc_at(s, H, n0 + 64 + r, ne, I, blk.i, R, 4 * k + q);
 #pragma unroll
-    for (int t = 0; t < kE64OT; ++t) {
+    for (int t = 0; t < OT; ++t) {
       f64x4 acc = zero4d();
 #pragma unroll
       for (int k = 0; k < KS; ++k) acc = mfma64(a[k], b[t][k], acc);
@@ -148,14 +150,14 @@ __global__ __launch_bounds__(kE64Threads) void edge_fwd_mfma64_kernel(
   // lanes r, r + 16, r + 32, r + 48 hold the same output column: add them,
   // then the waves' sample shares in wave order
 #pragma unroll
-  for (int t = 0; t < kE64OT; ++t) {
+  for (int t = 0; t < OT; ++t) {
     double v = acc_abs[t];
     v += __shfl_xor(v, 16);
     v += __shfl_xor(v, 32);
     if (q == 0) red[wave][16 * t + r] = v;
   }
   __syncthreads();
-  for (int ol = threadIdx.x; ol < kE64Out; ol += blockDim.x) {
+  for (int ol = threadIdx.x; ol < OUT; ol += blockDim.x) {
     const int o = o0 + ol;
     if (o >= O) continue;
     const double v = ((red[0][ol] + red[1][ol]) + red[2][ol]) + red[3][ol];
@@ -326,8 +328,10 @@ bool edge_mfma64_applies(int64_t R) { return R + 1 <= 16; }
 // per wave.  The backward's count sizes the [splits, O, I, R + 1] partials
 // of edge_param_finalize, the forward's the [splits, O, I] ones of
 // edge_forward_finalize.
+static int fwd_tiles(int64_t O) { return O <= 64 ? 4 : kE64OT; }
+
 int edge_mfma64_splits(int64_t n, int64_t I, int64_t O, bool backward) {
-  const int64_t blocks = I * ceil_div(O, backward ? 16 * kE64POT : kE64Out);
+  const int64_t blocks = I * ceil_div(O, 16 * (backward ? kE64POT : fwd_tiles(O)));
   const int64_t target = 8LL * device_cu_count();
   int64_t s = ceil_div(target, blocks > 0 ? blocks : 1);
   const int64_t cap = ceil_div(n, 4 * 16 * 4);
@@ -340,16 +344,22 @@ int edge_mfma64_splits(int64_t n, int64_t I, int64_t O, bool backward) {
 int launch_edge_forward_mfma64(const double* s, const double* H, const double* bw,
                                const double* W, double* a, double* part, int splits, int64_t n,
                                int64_t I, int64_t O, int64_t R, hipStream_t st) {
-  const int64_t ochunks = ceil_div(O, kE64Out);
+  const int ot = fwd_tiles(O);
+  const int64_t ochunks = ceil_div(O, 16 * ot);
   const int64_t blocks = I * ochunks * splits;
   if (blocks > 2147483647LL) return set_error(KAN_ERR_LIMIT, "edge_abs_mean: too many blocks");
   const int64_t per_split = round_up(ceil_div(n, splits), 64);
   const bool fin = splits == 1;
   const int R1 = (int)R + 1;
   TimedLaunch timed(kClassEdge, st, 2.0 * (double)n * (double)O * (double)I * (double)R1);
-  KAN_E64_KS(R1, hipLaunchKernelGGL((edge_fwd_mfma64_kernel<KS>), dim3((unsigned)blocks),
-                                    dim3(kE64Threads), 0, st, s, H, bw, W, fin ? a : part, n,
-                                    (int)I, (int)O, (int)R, per_split, (int)ochunks, (int)fin));
+  if (ot == 4)
+    KAN_E64_KS(R1, hipLaunchKernelGGL((edge_fwd_mfma64_kernel<KS, 4>), dim3((unsigned)blocks),
+                                      dim3(kE64Threads), 0, st, s, H, bw, W, fin ? a : part, n,
+                                      (int)I, (int)O, (int)R, per_split, (int)ochunks, (int)fin));
+  else
+    KAN_E64_KS(R1, hipLaunchKernelGGL((edge_fwd_mfma64_kernel<KS, kE64OT>), dim3((unsigned)blocks),
+                                      dim3(kE64Threads), 0, st, s, H, bw, W, fin ? a : part, n,
+                                      (int)I, (int)O, (int)R, per_split, (int)ochunks, (int)fin));
   return check_launch("edge_abs_mean (fp64 MFMA)");
 }
 
