@@ -902,8 +902,16 @@ def bench_stream(args):
     a = torch.empty(nbytes // 4, dtype=torch.float32, device=dev)
     b = torch.zeros(nbytes // 4, dtype=torch.float32, device=dev)
     out = {}
+    rows = nbytes // (14336 * 4)
     for mode, name, moved in ((0, "write", nbytes), (1, "read", nbytes), (2, "copy", 2 * nbytes),
-                              (3, "basis_row_segments", nbytes)):
+                              (3, "basis_row_segments", nbytes),
+                              (4, "one_segment_per_workgroup_write", nbytes),
+                              (5, "one_segment_per_workgroup_read", nbytes + rows * 1024 * 4),
+                              (6, "basis_row_segments_one_step", nbytes),
+                              (7, "workgroup_segments_4_rows", nbytes),
+                              (8, "workgroup_segments_16_rows", nbytes),
+                              (9, "one_segment_per_wave_workgroup_write", nbytes),
+                              (10, "two_segments_per_workgroup_read", nbytes + rows * 1024 * 4)):
         for _ in range(args.warmup):
             _C.stream_probe(mode, a, b)
         torch.cuda.synchronize()

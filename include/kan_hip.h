@@ -386,7 +386,13 @@ int kan_hip_timing_read(int kernel_class, double* total_ms, int64_t* launches, d
  * practice but must be a valid 4-byte buffer) or copy a to b (mode 2), over
  * `bytes` (a multiple of 16; 16-byte aligned buffers); mode 3 writes a in
  * the row-segment pattern of the basis kernel at c3's layout (whole rows of
- * 14336 floats that fit in `bytes`).  Timed as kernel class 6 with the bytes
+ * 14336 floats that fit in `bytes`); modes 4 (write), 5 (read a, write
+ * [rows, 1024] floats of b) and 6 (write) are candidate patterns on that
+ * layout: one row segment per workgroup, and mode 3 with one step per
+ * workgroup; 7 and 8 write 4 and 16 rows per workgroup, one whole-workgroup
+ * segment at a time; 9 writes one segment per one-wave workgroup; 10 reads
+ * two adjacent segments per workgroup (b as in mode 5).  Timed as kernel
+ * class 6 with the bytes
  * moved as work; the HBM ceilings the memory-bound kernels are compared
  * with. */
 int kan_hip_stream_probe(int mode, void* a, void* b, int64_t bytes, void* stream);

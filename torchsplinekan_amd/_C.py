@@ -322,11 +322,15 @@ def kan_apply(x, grid, base_weight, spline_weight, spline_scaler, spline_order: 
 def stream_probe(mode: int, a: torch.Tensor, b: torch.Tensor) -> None:
     """Streaming probe over a's bytes (measurement support): mode 0 writes a,
     1 reads a, 2 copies a into b (b at least as large as a for mode 2), 3
-    writes a in the basis kernel's row-segment pattern (rows of 14336 floats)."""
+    writes a in the basis kernel's row-segment pattern (rows of 14336 floats);
+    4-10 are candidate patterns on that layout (4, 6, 7, 8 and 9 write a, 5
+    and 10 read a and write [rows, 1024] floats of b)."""
     _req(a.is_cuda and b.is_cuda and a.is_contiguous() and b.is_contiguous(),
          "stream_probe: contiguous device tensors")
     nbytes = a.numel() * a.element_size() // 16 * 16
     _req(mode != 2 or b.numel() * b.element_size() >= nbytes, "stream_probe: b too small")
+    _req(mode not in (5, 10) or b.numel() * b.element_size() >= nbytes // 14,
+         "stream_probe: b too small")
     with torch.cuda.device(a.device):
         check(LIB.kan_hip_stream_probe(int(mode), ptr(a), ptr(b), nbytes, stream_of(a.device)))
 

@@ -518,12 +518,12 @@ int kan_hip_timing_read(int kernel_class, double* total_ms, int64_t* launches, d
 }
 
 int kan_hip_stream_probe(int mode, void* a, void* b, int64_t bytes, void* stream) {
-  if (mode < 0 || mode > 3)
+  if (mode < 0 || mode > 10)
     return set_error(KAN_ERR_INVALID,
-                     "stream_probe: mode must be 0 (write), 1 (read), 2 (copy) or 3 (row segments)");
+                     "stream_probe: mode must be 0 (write), 1 (read), 2 (copy) or 3-10 (row segments)");
   if (bytes < 0 || bytes % 16 != 0)
     return set_error(KAN_ERR_INVALID, "stream_probe: bytes must be a non-negative multiple of 16");
-  if (bytes > 0 && (a == nullptr || ((mode == 1 || mode == 2) && b == nullptr) ||
+  if (bytes > 0 && (a == nullptr || ((mode == 1 || mode == 2 || mode == 5 || mode == 10) && b == nullptr) ||
                     ((uintptr_t)a % 16) != 0 || (mode == 2 && ((uintptr_t)b % 16) != 0)))
     return set_error(KAN_ERR_INVALID, "stream_probe: buffers must be non-null and 16-byte aligned");
   return launch_stream_probe(mode, a, b, bytes, (hipStream_t)stream);
