@@ -10,8 +10,8 @@ output:
   * the regulariser, from the oracle's edge means over every edge;
   * parameter gradients on sampled edges over all samples, and the input
     gradient on sampled rows, through both the layer output and the edge
-    statistic, with sign flips of phi at float32 rounding level bounded term
-    by term (tests/_slack.py).
+    statistic, with sign flips of phi at the device's rounding level bounded
+    term by term (tests/_slack.py).
 Each link of the chain is checked, so the whole backward is: the gradient
 a layer receives is the previous check's input gradient.
 """
@@ -85,9 +85,10 @@ def capture(net):
 
 
 def check_layers(net, cap, mu, k, tol, n_rows=32, n_edges=48, n_xrows=12, say=print,
-                 amb_frac=1e-4):
+                 amb_frac=1e-4, unit=_slack.U32):
     """Per-layer checks of a captured step (see the module docstring); returns
-    the oracle's total regulariser.  Every check asserts against `tol`."""
+    the oracle's total regulariser.  Every check asserts against `tol`;
+    `unit` is the device's unit roundoff (2^-24 float32, 2^-53 float64)."""
     reg_total = 0.0
     for li, (layer, (xl, yl, rl)) in enumerate(zip(net.layers, cap)):
         grid, bw, sw, sc = params(layer)
@@ -112,7 +113,7 @@ def check_layers(net, cap, mu, k, tol, n_rows=32, n_edges=48, n_xrows=12, say=pr
         ga = ko.regularization_grad(a, mu, mu)
         D = np64(yl.grad)
         edges = sample_edges(O, I, n_edges, seed=li)
-        res, n_amb = _slack.edge_param_grads(D, ga, s, H, bw, sw, sc, edges)
+        res, n_amb = _slack.edge_param_grads(D, ga, s, H, bw, sw, sc, edges, unit=unit)
         oo, ii = map(list, zip(*edges))
         for name, key, got in (("dbase_w", "base_weight", layer.base_weight.grad[oo, ii]),
                                ("dcoef", "spline_weight", layer.spline_weight.grad[oo, ii]),
@@ -126,7 +127,7 @@ def check_layers(net, cap, mu, k, tol, n_rows=32, n_edges=48, n_xrows=12, say=pr
         if xl.requires_grad:
             xrows = rows[:n_xrows]
             ref, slack, n_amb = _slack.edge_input_grads(D, ga, x, grid, k, s, H, bw, sw, sc,
-                                                        xrows)
+                                                        xrows, unit=unit)
             e = _slack.within(np64(xl.grad[xrows]), ref, slack, tol)
             say(f"layer {li}: dx on {len(xrows)} rows {e:.2e} "
                 f"({n_amb} of {len(xrows) * O * I} terms ambiguous)")

@@ -50,16 +50,16 @@ def edge_terms(s, H, bw, W, n_idx, o_idx, i_idx):
     return phi, mag
 
 
-def edge_param_grads(D, ga, s, H, bw, sw, sc, edges, extra=16):
+def edge_param_grads(D, ga, s, H, bw, sw, sc, edges, extra=16, unit=U32):
     """Parameter gradients of y = s bw^T + <H, sw*sc> and of the edge
     statistic together, for sampled edges [(o, i), ...], over all samples:
     -> dict name -> (ref [E, ...], slack [E, ...]) for "spline_weight"
     [E, R], "spline_scaler" [E], "base_weight" [E], and the count of
     ambiguous terms.  D [N, O] = dL/dy (None: no output term), ga [O, I]
-    = dL/da (None: no statistic)."""
+    = dL/da (None: no statistic); `unit` is the device's unit roundoff."""
     N, I, R = H.shape
     W = sw * sc[:, :, None]
-    c = rounding_factor(R, extra) * U32
+    c = rounding_factor(R, extra) * unit
     out = {k: ([], []) for k in ("spline_weight", "spline_scaler", "base_weight")}
     n_amb = 0
     nn_ = np.arange(N)
@@ -87,15 +87,16 @@ def edge_param_grads(D, ga, s, H, bw, sw, sc, edges, extra=16):
     return res, n_amb
 
 
-def edge_input_grads(D, ga, x, grid, k, s, H, bw, sw, sc, rows, extra=16):
+def edge_input_grads(D, ga, x, grid, k, s, H, bw, sw, sc, rows, extra=16, unit=U32):
     """Gradient with respect to the layer input x for sampled rows, through
     the layer output and the edge statistic: dx[n, i] = silu'(x)
     sum_o g bw + sum_r dB_r(x) sum_o g W, g = D[n, o] + ga sign(phi) / N
-    -> (ref [len(rows), I], slack [len(rows), I], ambiguous count)."""
+    -> (ref [len(rows), I], slack [len(rows), I], ambiguous count); `unit`
+    is the device's unit roundoff."""
     N, I, R = H.shape
     W = sw * sc[:, :, None]
     O = W.shape[0]
-    c = rounding_factor(R, extra) * U32
+    c = rounding_factor(R, extra) * unit
     xr = x[rows]
     dB = ko.basis_derivative(xr, grid, k)           # [n, I, R]
     sp = ko.silu_grad(xr)                           # [n, I]

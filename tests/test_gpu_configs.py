@@ -190,6 +190,41 @@ def test_c4_regularised_network_matches_oracle(bench):
     assert e < TOL
 
 
+@pytest.mark.timeout(1200)
+def test_c4_regularised_network_fp64_matches_oracle(bench):
+    """c4 in float64 (the edge statistic on the fp64 MFMA kernels, the layer
+    products on the fp64 GEMM): each layer against the oracle given its own
+    device input, at 1e-10, with sign ambiguity bounded at float64's unit
+    roundoff; the network output through the whole fp64 chain from x."""
+    dev = torch.device("cuda", 0)
+    net, xd, td = bench.build_c4(dev, 16384, torch.float64)
+    N = xd.shape[0]
+    k = 3
+    mu = 1e-2
+    tol = 1e-10
+    _say("c4 fp64: KAN([256,512,512,64]) G8 update_grid knots, forward_with_regularization")
+    with _netcheck.capture(net) as cap:
+        for p in net.parameters():
+            p.grad = None
+        y, reg = net.forward_with_regularization(xd, mu, mu, reg_impl="auto")
+        (F.mse_loss(y, td) + reg).backward()
+        torch.cuda.synchronize()
+    assert all(l.last_backend == "cuda" for l in net.layers) and len(cap) == 3
+    rows = np.unique(np.linspace(0, N - 1, 32).astype(int))
+    h = np64(xd)[rows]
+    for layer in net.layers:
+        grid, bw, sw, sc = _netcheck.params(layer)
+        h, _ = ko.kan_forward(h, grid, bw, sw, sc, k)
+    e = normwise(np64(y[rows]), h)
+    _say(f"c4 fp64: network output rows through the fp64 chain from x {e:.2e}")
+    assert e < tol
+    reg_total = _netcheck.check_layers(net, cap, mu, k, tol, say=lambda m: _say("c4 fp64 " + m),
+                                       unit=2.0 ** -53)
+    e = abs(reg.item() - reg_total) / abs(reg_total)
+    _say(f"c4 fp64: total regulariser {e:.2e}")
+    assert e < tol
+
+
 @pytest.mark.timeout(900)
 def test_c2_network_matches_oracle(bench):
     """Each layer against the oracle given its own device input and the
