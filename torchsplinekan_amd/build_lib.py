@@ -35,6 +35,7 @@ COMMON_FLAGS = [
 # instead of accumulation registers save a copy per value and registers.
 SOURCE_FLAGS = {
     "kan_edge_mfma.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+    "kan_edge_mfma64.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
 }
 
 

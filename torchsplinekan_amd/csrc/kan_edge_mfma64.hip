@@ -45,11 +45,12 @@ __device__ __forceinline__ double sign_d(double v) {
 // Tilings chosen by a sweep on MI355X at c4's layers (n = 16384, R + 1 = 12):
 // the forward prefetches the next sample tile (it holds 4 waves per SIMD
 // with it) and takes 8 output tiles per block, 4 for layers of at most 64
-// outputs (8 left half the block idle there); the parameter kernel does not (at 1-2 waves per SIMD the
-// prefetch cost a third of its rate) and takes 4 output tiles per block at
-// 4 waves per SIMD (8 tiles: 2 waves, 6 % slower, and half the block idle
-// at O = 64); the input kernel takes 4 sample tiles per wave, at 4 waves per
-// SIMD where a block has more than 4 output tiles to loop over.
+// outputs (8 left half the block idle there); the parameter kernel does not
+// prefetch (at 1-2 waves per SIMD that cost a third of its rate) and takes
+// 4 output tiles per block at 4 waves per SIMD (3 for even k-step counts,
+// which would spill at 4; 8 tiles: 2 waves, 6 % slower, and half the block
+// idle at O = 64); the input kernel takes 4 sample tiles per wave, at 4
+// waves per SIMD where a block has more than 4 output tiles to loop over.
 constexpr int kE64Threads = 256;  // 4 waves
 constexpr int kE64OT = 8;         // output tiles of 16 per forward block (4 where O <= 64)
 constexpr int kE64Out = kE64OT * 16;
@@ -169,7 +170,7 @@ __global__ __launch_bounds__(kE64Threads) void edge_fwd_mfma64_kernel(
 
 // Parameters: dWc[o, c] over the block's samples for its 16 * kE64POT outputs.
 template <int KS>
-__global__ __launch_bounds__(kE64Threads, 4) void edge_param_mfma64_kernel(
+__global__ __launch_bounds__(kE64Threads, KS % 2 == 1 ? 4 : 3) void edge_param_mfma64_kernel(
     const double* __restrict__ ga, const double* __restrict__ s, const double* __restrict__ H,
     const double* __restrict__ bw, const double* __restrict__ W, double* __restrict__ dbw,
     double* __restrict__ dW, double* __restrict__ part, int64_t n, int I, int O, int R,
