@@ -1127,16 +1127,13 @@ __global__ __launch_bounds__(kEdgeMfThreads) void edge_bwd_mfma_kernel(
 #pragma unroll
           for (int v = 0; v < 4; ++v) gv[t][v] += dq[t][v];
       }
-      // g[n = 4q + v, o = 16t + r] -> tile t at [o][n] (one 16-byte store per lane)
+      // g[n = 4q + v, o = 16t + r] -> tile t at [n][o] (four scalar stores
+      // per lane and tile, bank-conflict free; the reads below then take
+      // one 16-byte load per tile, all in flight before the first wait)
 #pragma unroll
-      for (int t = 0; t < kOT; ++t) {
-        f32x4 gq;
-        gq[0] = gv[t][0];
-        gq[1] = gv[t][1];
-        gq[2] = gv[t][2];
-        gq[3] = gv[t][3];
-        *reinterpret_cast<f32x4*>(tb + t * 16 * TS + r * TS + 4 * q) = gq;
-      }
+      for (int t = 0; t < kOT; ++t)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) tb[t * 16 * TS + (4 * q + v) * TS + r] = gv[t][v];
 #pragma unroll
       for (int v = 0; v < 4; ++v)
 #pragma unroll
@@ -1145,9 +1142,11 @@ __global__ __launch_bounds__(kEdgeMfThreads) void edge_bwd_mfma_kernel(
       // g[n = r, o = 16t + 4q + v]
       float gt[kOT][4];
 #pragma unroll
-      for (int t = 0; t < kOT; ++t)
+      for (int t = 0; t < kOT; ++t) {
+        const f32x4 gq = *reinterpret_cast<const f32x4*>(tb + t * 16 * TS + r * TS + 4 * q);
 #pragma unroll
-        for (int v = 0; v < 4; ++v) gt[t][v] = tb[t * 16 * TS + (4 * q + v) * TS + r];
+        for (int v = 0; v < 4; ++v) gt[t][v] = gq[v];
+      }
       edge_wave_sync();  // (the next tile's stores come after these reads)
       f32x4 d0 = zero4(), d1 = zero4();
 #pragma unroll
@@ -1352,16 +1351,12 @@ __global__ __launch_bounds__(kEdgeMfThreads, VEC && KS <= 3 ? 3 : 1) void edge_b
             gv[t][v] = g_sign(gav[t], acc[t][v]);
             if constexpr (HASD) gv[t][v] += dq[t][v];
           }
-        // g[n = 4q + v, o = 16t + r] -> tile t at [o][n]
+        // g[n = 4q + v, o = 16t + r] -> tile t at [n][o] (as in
+        // edge_bwd_mfma_kernel)
 #pragma unroll
-        for (int t = 0; t < OT; ++t) {
-          f32x4 gq;
-          gq[0] = gv[t][0];
-          gq[1] = gv[t][1];
-          gq[2] = gv[t][2];
-          gq[3] = gv[t][3];
-          *reinterpret_cast<f32x4*>(tb + t * 16 * TS + r * TS + 4 * q) = gq;
-        }
+        for (int t = 0; t < OT; ++t)
+#pragma unroll
+          for (int v = 0; v < 4; ++v) tb[t * 16 * TS + (4 * q + v) * TS + r] = gv[t][v];
 #pragma unroll
         for (int v = 0; v < 4; ++v)
 #pragma unroll
@@ -1370,9 +1365,11 @@ __global__ __launch_bounds__(kEdgeMfThreads, VEC && KS <= 3 ? 3 : 1) void edge_b
         // g[n = r, o = 16t + 4q + v]
         float gt[OT][4];
 #pragma unroll
-        for (int t = 0; t < OT; ++t)
+        for (int t = 0; t < OT; ++t) {
+          const f32x4 gq = *reinterpret_cast<const f32x4*>(tb + t * 16 * TS + r * TS + 4 * q);
 #pragma unroll
-          for (int v = 0; v < 4; ++v) gt[t][v] = tb[t * 16 * TS + (4 * q + v) * TS + r];
+          for (int v = 0; v < 4; ++v) gt[t][v] = gq[v];
+        }
         edge_wave_sync();  // (the next tile's stores come after these reads)
         f32x4 d0 = zero4(), d1 = zero4();
 #pragma unroll
