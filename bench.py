@@ -86,6 +86,9 @@ def parse():
                     help="c3 only: skip the c2, c4 and c5 figures of the JSON line")
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="target CPU time of each baseline sample (3 timed repetitions)")
+    ap.add_argument("--no-graph", action="store_true",
+                    help="c2: time eager steps instead of replays of the step captured in a "
+                         "HIP graph")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a plain 1 GiB device-to-device copy (3 times); the HBM "
                          "counters of this known-size copy scale the counter readings of the "
@@ -354,12 +357,14 @@ def _layer_tensors(layer):
 # timed GPU steps
 # ---------------------------------------------------------------------------
 
-def timed_steps(step, steps, warmup, classes, params=()):
+def timed_steps(step, steps, warmup, classes, params=(), timed=None):
     """warmup untimed steps, then `steps` timed ones between two device
     synchronisations with nothing else running (the library's per-launch
     timing off), then one more step for the memory figures and `steps`
     instrumented ones for the per-kernel times (HIP events the library
-    records around each launch on its own stream):
+    records around each launch on its own stream).  timed: what the timed
+    steps call instead of step (a graph replay of it); warmup, memory and
+    the instrumented pass run step itself.
     -> (wall seconds of the timed steps, {class: (ms, launches, work)},
         memory figures)."""
     import torch
@@ -367,10 +372,14 @@ def timed_steps(step, steps, warmup, classes, params=()):
     for _ in range(warmup):
         step()
     _lib.timing_enable(False)
+    run = timed or step
+    if timed is not None:
+        for _ in range(warmup):
+            run()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(steps):
-        step()
+        run()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     mem = measure_memory(step, params)
@@ -532,9 +541,55 @@ def run_c3(args, dev, steps, warmup, need_dx=True, f64=False):
     return line
 
 
+def capture_step(step):
+    """The step captured once in a HIP graph (torch.cuda.CUDAGraph, warmed up
+    on a side stream of default priority) -> a function that replays it.
+    Every launch of the native path goes to the current stream and nothing in
+    it synchronises with the host, so a replay runs the step's kernels
+    without its host work (tests/test_gpu_graph.py checks replays of c2's
+    step, F.mse_loss included, against eager steps bit for bit; torch's
+    multi-block means over larger outputs are not replay-safe on this ROCm
+    build, so a step with one stays eager)."""
+    import torch
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(2):
+            step()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step()
+    return graph.replay
+
+
+def graph_step(args, step, steps, warmup):
+    """(replay, extra fields of the JSON line): unless --no-graph, the eager
+    step's time per step (warmup, then `steps` timed) and a replay of the
+    step captured in a HIP graph; (None, {}) with --no-graph."""
+    import torch
+    if args.no_graph:
+        return None, {}
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    eager = (time.perf_counter() - t0) * 1e3 / steps
+    return capture_step(step), {"step": "HIP graph replay of the captured step",
+                                "eager_ms_per_step": eager}
+
+
 def run_c2(args, dev, steps, warmup):
     """c2: KAN([784, 256, 10]) G5 k3 fp32, N = 4096, fwd + MSE + bwd (x
-    without grad, the network input of a classifier)."""
+    without grad, the network input of a classifier).  Its kernels take
+    about 0.5 ms per step, close to what the host needs to issue them from
+    Python, so on a slow host eager steps measure the host: the timed steps
+    replay the step captured in a HIP graph (the same kernels on the same
+    inputs, nothing skipped), and the eager figure is reported beside it
+    (eager_ms_per_step; --no-graph times eager steps)."""
     import torch
     import torch.nn.functional as F
     N = args.n or 4096
@@ -546,19 +601,21 @@ def run_c2(args, dev, steps, warmup):
             p.grad = None
         F.mse_loss(net(xd), td).backward()
 
+    replay, extra = graph_step(args, step, steps, warmup)
     wall, kern, mem = timed_steps(step, steps, warmup,
                                   ("contraction", "basis", "basis_grad", "other"),
-                                  list(net.parameters()))
+                                  list(net.parameters()), timed=replay)
     if any(l.last_backend != "cuda" for l in net.layers):
         raise RuntimeError("c2 did not run on the native backend")
     line = _line("fwd+bwd samples/s, KAN([784,256,10]) G5 k3 N=4096", N, steps, warmup, wall,
                  "c2: KAN([784,256,10], G=5, k=3) fp32, N=%d, fwd + MSE + bwd (x without "
-                 "grad)" % N,
+                 "grad)%s" % (N, "" if replay is None else ", replayed from a HIP graph"),
                  _mfma_roofline(kern, "contraction", "contraction: gemm_pipe_kernel (fp32 MFMA; "
                                 "forward and parameter products of the first layer) and the "
                                 "thin-product kernels (thin_wide_cols/thin_wide_rows/"
                                 "thin_short_k: forward, parameter and input products of the "
-                                "10-wide output layer)", *recorded_traffic("c2")), kern, mem)
+                                "10-wide output layer)", *recorded_traffic("c2")), kern, mem,
+                 **extra)
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline_layers(
             [_layer_tensors(l) for l in net.layers], x, target, False, args.cpu_seconds, 1024,
