@@ -177,10 +177,11 @@ def test_forward_with_regularization_fused_matches_dense(C, dtype):
 # (N, I, O, R): every tiling of the folded backward (O = 4, 7 -> 2x4, 33, 64 ->
 # 4x4, 100 -> 4x2, 200 -> 4x1, 300 and 512 -> 8x1; odd widths leave partial
 # output tiles), ragged sample counts, sample splits across blocks (4097, 6000)
-# and R + 1 at 5, 12 and 16.
+# and R + 1 at 2, 5, 12 and 16.
 LINEAR_SHAPES = [(37, 5, 4, 4), (90, 3, 7, 6), (300, 7, 64, 11), (250, 4, 33, 11),
                  (1000, 9, 100, 15), (513, 3, 200, 11), (700, 2, 300, 8), (4097, 5, 512, 11),
-                 (6000, 3, 64, 11), (2000, 8, 64, 11), (500, 12, 10, 3), (777, 16, 24, 14)]
+                 (6000, 3, 64, 11), (2000, 8, 64, 11), (500, 12, 10, 3), (777, 16, 24, 14),
+                 (90, 3, 20, 1)]
 
 
 @pytest.mark.parametrize("shape", LINEAR_SHAPES)
