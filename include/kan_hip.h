@@ -306,6 +306,28 @@ int kan_hip_edge_linear_backward(int dtype, const void* grad_a, const void* grad
                                  int64_t n, int64_t in_features, int64_t out_features,
                                  int64_t num_basis, void* stream);
 
+/* Forward of one regularised layer's output and edge statistic together:
+ * y [n, O] = s bw^T + H W^T (flattened over I and R) and a [O, I] =
+ * (1/n) sum_m |phi[m,o,i]|.  The output is the sum over features of the
+ * edge values, y[m,o] = sum_i phi[m,o,i], so one pass over phi gives both.
+ * Replaces the two F.linear calls and EdgeAbsMean's forward of
+ * forward_with_regularization (spline_kan/kan_linear.py:384-387,
+ * spline_kan/fused.py:64-73, csrc/kan_reg_cuda.cu:34-109), which form phi's
+ * products twice.  float32, n, in_features, out_features > 0,
+ * num_basis + 1 <= 16 (kan_hip_edge_linear_forward_supported returns 1
+ * exactly then); s and base_weight both given or both NULL.  Workspace
+ * (partial sums of a per 128 samples): kan_hip_edge_linear_forward_workspace. */
+int kan_hip_edge_linear_forward_supported(int dtype, int64_t n, int64_t in_features,
+                                          int64_t out_features, int64_t num_basis);
+int kan_hip_edge_linear_forward_workspace(int dtype, int64_t n, int64_t in_features,
+                                          int64_t out_features, int64_t num_basis,
+                                          size_t* bytes);
+int kan_hip_edge_linear_forward(int dtype, const void* s, const void* basis,
+                                const void* base_weight, const void* weight, void* y, void* a,
+                                void* workspace, size_t workspace_bytes, int64_t n,
+                                int64_t in_features, int64_t out_features, int64_t num_basis,
+                                void* stream);
+
 /* Double backward of the edge statistic, used when the regulariser's
  * backward is itself recorded (create_graph=True).  With the sign pattern
  * S = sign(phi) of the forward operands held fixed (its derivative is zero

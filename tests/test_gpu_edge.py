@@ -211,6 +211,39 @@ def test_edge_linear_backward_matches_oracle(C, shape):
                       which=(False, False, True, True))
 
 
+# (N, I, O, R) of the one-pass forward (128 x 128 blocks): partial sample
+# and output blocks, a single block, several of each, outputs past 512, every
+# k-step count (R + 1 = 2, 5, 8, 12, 15, 16), 16-byte staging (I % 4 == 0)
+# and scalar staging with a partial last feature group (I % 4 != 0).
+YLIN_SHAPES = [(37, 5, 4, 4), (300, 7, 64, 11), (1000, 9, 100, 15), (513, 3, 200, 11),
+               (4097, 8, 512, 11), (777, 16, 130, 14), (90, 3, 20, 1), (129, 12, 257, 7),
+               (2000, 4, 600, 4), (256, 6, 128, 11), (128, 1, 1, 3)]
+
+
+@pytest.mark.parametrize("shape", YLIN_SHAPES)
+def test_edge_linear_forward_matches_oracle(C, shape):
+    """kan_hip_edge_linear_forward: the layer output y = s bw^T + H W^T and
+    the edge statistic a = mean_n |phi| from one pass over phi, against the
+    float64 products and the oracle's edge_abs_mean (fp32 1e-5 normwise);
+    repeated calls are bit-identical; without a base branch as well."""
+    N, I, O, R = shape
+    print(f"edge linear forward {shape}", flush=True)
+    s, H, bw, W, _ = _edge_inputs(N, I, O, R, torch.float32, seed=3 * N + O)
+    assert C.edge_linear_forward_supported(H.cuda(), W.cuda())
+    for base in (True, False):
+        sd, bwd = (s.cuda(), bw.cuda()) if base else (None, None)
+        y, a = C.edge_linear_forward(sd, H.cuda(), bwd, W.cuda())
+        y2, a2 = C.edge_linear_forward(sd, H.cuda(), bwd, W.cuda())
+        assert torch.equal(y, y2) and torch.equal(a, a2)
+        ry = np64(H).reshape(N, I * R) @ np64(W).reshape(O, I * R).T
+        if base:
+            ry = ry + np64(s) @ np64(bw).T
+        ra = ko.edge_abs_mean(np64(s) if base else None, np64(H), np64(bw) if base else None,
+                              np64(W))
+        assert normwise(np64(y), ry) < 1e-5, ("y", base)
+        assert normwise(np64(a), ra) < 1e-5, ("a", base)
+
+
 def test_edge_linear_supported_range(C):
     mk = lambda N, I, O, R, dt=torch.float32: (torch.empty(N, I, R, dtype=dt, device="cuda"),
                                                torch.empty(O, I, R, dtype=dt, device="cuda"))
@@ -219,6 +252,9 @@ def test_edge_linear_supported_range(C):
     assert C.edge_linear_supported(*mk(10, 3, 70, 11))
     assert not C.edge_linear_supported(*mk(10, 3, 64, 16))    # R + 1 > 16
     assert not C.edge_linear_supported(*mk(10, 3, 64, 11, torch.float64))
+    assert C.edge_linear_forward_supported(*mk(10, 3, 1300, 15))
+    assert not C.edge_linear_forward_supported(*mk(10, 3, 64, 16))    # R + 1 > 16
+    assert not C.edge_linear_forward_supported(*mk(10, 3, 64, 11, torch.float64))
 
 
 def _reg_grads(net, x, impl, create_graph=False):
@@ -236,17 +272,20 @@ def _reg_grads(net, x, impl, create_graph=False):
     return list(gs) + list(second)
 
 
+@pytest.mark.parametrize("widths,N", [([16, 64, 100, 12], 3000), ([8, 300, 6], 16384)])
 @pytest.mark.parametrize("x_grad", [True, False])
 @pytest.mark.parametrize("route", ["folded", "unfolded", "dense"])
-def test_regularized_layers_match_oracle(C, monkeypatch, x_grad, route):
-    """KAN([16, 64, 100, 12]) fp32, forward_with_regularization + loss +
+def test_regularized_layers_match_oracle(C, monkeypatch, x_grad, route, widths, N):
+    """KAN([16, 64, 100, 12]) at N = 3000 and KAN([8, 300, 6]) at N = 16384,
+    fp32, forward_with_regularization + loss +
     backward through each route, every layer held to the fp64 oracle
     (tests/_netcheck.py: outputs, regulariser, parameter gradients on
     sampled edges, input gradients on sampled rows) at 1e-5 with sign flips
     of phi at fp32 rounding level counted and bounded term by term:
     * "folded": output and edge statistic through EdgeLinear (one folded
       native backward launch per layer; the weight-only branch for the first
-      layer when x needs no gradient);
+      layer when x needs no gradient; the 300-wide layer's forward from one
+      pass over phi, kan_hip_edge_linear_forward);
     * "unfolded": the separate native output products and edge backward,
       summed by autograd;
     * "dense": the PyTorch dense path (reg_impl="dense").
@@ -254,10 +293,12 @@ def test_regularized_layers_match_oracle(C, monkeypatch, x_grad, route):
     the counted flips."""
     from torchsplinekan_amd import KAN
     from torchsplinekan_amd import fused as fz
-    print(f"regularised KAN([16,64,100,12]) route={route} x_grad={x_grad}", flush=True)
+    print(f"regularised KAN({widths}) N={N} route={route} x_grad={x_grad}", flush=True)
     torch.manual_seed(1)
-    net = KAN([16, 64, 100, 12], grid_size=7, backend="cuda").to("cuda")
-    x = (torch.rand(3000, 16, device="cuda") * 2.2 - 1.1).requires_grad_(x_grad)
+    net = KAN(widths, grid_size=7, backend="cuda").to("cuda")
+    x = (torch.rand(N, widths[0], device="cuda") * 2.2 - 1.1).requires_grad_(x_grad)
+    if route == "folded" and widths[1] >= 256:
+        assert fz._one_pass_forward(N, widths[1])
     if route == "unfolded":
         monkeypatch.setattr(fz, "edge_linear_applies", lambda *a: False)
     impl = "dense" if route == "dense" else "fused"

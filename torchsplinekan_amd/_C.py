@@ -786,6 +786,44 @@ def edge_linear_supported(H: torch.Tensor, W: torch.Tensor) -> bool:
                                                   N, I, W.shape[0], R))
 
 
+def edge_linear_forward_supported(H: torch.Tensor, W: torch.Tensor) -> bool:
+    """True where edge_linear_forward applies to these operands (float32,
+    num_basis + 1 <= 16, at least one sample, input and output)."""
+    if not (H.is_cuda and H.dim() == 3 and W.dim() == 3):
+        return False
+    N, I, R = H.shape
+    return bool(LIB.kan_hip_edge_linear_forward_supported(
+        dtype_code(H.dtype) if H.dtype in _F else -1, N, I, W.shape[0], R))
+
+
+def edge_linear_forward(s, H, base_weight, W):
+    """(y, a) of one regularised layer in one pass over phi (device, float32;
+    see edge_linear_forward_supported): y = s bw^T + H W^T [N, O] (flattened
+    over I and R) and a = mean_n |phi| [O, I], phi[n,o,i] = s bw + <H, W>.
+    The reference forms y with two F.linear calls and a with EdgeAbsMean
+    (spline_kan/kan_linear.py:384-387, spline_kan/fused.py:64-73)."""
+    hb = _cmp.has_base(base_weight)
+    _check_edge_inputs(s, H, base_weight, W, hb)
+    _req(edge_linear_forward_supported(H, W), "edge_linear_forward: configuration not supported")
+    N, I, R = H.shape
+    O = W.shape[0]
+    H, W = H.contiguous(), W.contiguous()
+    sc = s.contiguous() if hb else None
+    bw = base_weight.contiguous() if hb else None
+    y = torch.empty(N, O, dtype=H.dtype, device=H.device)
+    a = torch.empty(O, I, dtype=H.dtype, device=H.device)
+    code = dtype_code(H.dtype)
+    nbytes = _lib.ctypes.c_size_t(0)
+    with torch.cuda.device(H.device):
+        check(LIB.kan_hip_edge_linear_forward_workspace(code, N, I, O, R,
+                                                        _lib.ctypes.byref(nbytes)))
+        ws = torch.empty(max(int(nbytes.value), 1), dtype=torch.uint8, device=H.device)
+        check(LIB.kan_hip_edge_linear_forward(
+            code, ptr(sc), ptr(H), ptr(bw), ptr(W), ptr(y), ptr(a), ptr(ws), int(nbytes.value),
+            N, I, O, R, stream_of(H.device)))
+    return y, a
+
+
 def edge_linear_backward(grad_a, grad_y, s, H, base_weight, W, need_s: bool, need_H: bool,
                          need_bw: bool, need_W: bool):
     """Gradients of one regularised layer's output y = s bw^T + H W^T and its

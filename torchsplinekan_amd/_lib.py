@@ -82,6 +82,11 @@ SIGNATURES = {
     "kan_hip_edge_linear_supported": (_int, [_int, _i64, _i64, _i64, _i64]),
     "kan_hip_edge_linear_backward": (_int, [_int] + [_vp] * 11 + [_sz, _i64, _i64, _i64, _i64,
                                                                 _vp]),
+    "kan_hip_edge_linear_forward_supported": (_int, [_int, _i64, _i64, _i64, _i64]),
+    "kan_hip_edge_linear_forward_workspace": (_int, [_int, _i64, _i64, _i64, _i64,
+                                                     ctypes.POINTER(_sz)]),
+    "kan_hip_edge_linear_forward": (_int, [_int] + [_vp] * 7 + [_sz, _i64, _i64, _i64, _i64,
+                                                               _vp]),
     "kan_hip_refit_gram": (_int, [_int, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64,
                                   _vp]),
     "kan_hip_stream_probe": (_int, [_int, _vp, _vp, _i64, _vp]),

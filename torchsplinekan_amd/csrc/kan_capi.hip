@@ -1049,6 +1049,37 @@ int kan_hip_edge_linear_backward(int dtype, const void* ga, const void* gy, cons
       static_cast<hipStream_t>(stream));
 }
 
+int kan_hip_edge_linear_forward_supported(int dtype, int64_t n, int64_t I, int64_t O, int64_t R) {
+  return dtype == KAN_DTYPE_F32 && edge_ylin_supported(n, I, O, R) ? 1 : 0;
+}
+
+int kan_hip_edge_linear_forward_workspace(int dtype, int64_t n, int64_t I, int64_t O, int64_t R,
+                                          size_t* bytes) {
+  KAN_TRY(need_ptr(bytes, "edge_linear_forward_workspace", "bytes"));
+  if (!kan_hip_edge_linear_forward_supported(dtype, n, I, O, R))
+    return set_error(KAN_ERR_LIMIT, "edge_linear_forward: needs float32, n, in_features, out_features > 0 and num_basis + 1 <= 16");
+  *bytes = edge_ylin_ws_bytes(n, I, O);
+  return KAN_OK;
+}
+
+int kan_hip_edge_linear_forward(int dtype, const void* s, const void* H, const void* bw,
+                                const void* W, void* y, void* a, void* ws, size_t ws_bytes,
+                                int64_t n, int64_t I, int64_t O, int64_t R, void* stream) {
+  KAN_TRY(check_edge("edge_linear_forward", dtype, s, H, bw, W, n, I, O, R));
+  KAN_TRY(need_ptr(y, "edge_linear_forward", "y"));
+  KAN_TRY(need_ptr(a, "edge_linear_forward", "a"));
+  if (!kan_hip_edge_linear_forward_supported(dtype, n, I, O, R))
+    return set_error(KAN_ERR_LIMIT, "edge_linear_forward: needs float32, n, in_features, out_features > 0 and num_basis + 1 <= 16");
+  const size_t need = edge_ylin_ws_bytes(n, I, O);
+  if (ws_bytes < need || ws == nullptr)
+    return set_error(KAN_ERR_WORKSPACE, "edge_linear_forward: workspace of %zu bytes is smaller than the %zu required", ws_bytes, need);
+  return launch_edge_ylin_forward(static_cast<const float*>(s), static_cast<const float*>(H),
+                                  static_cast<const float*>(bw), static_cast<const float*>(W),
+                                  static_cast<float*>(y), static_cast<float*>(a),
+                                  static_cast<float*>(ws), n, I, O, R,
+                                  static_cast<hipStream_t>(stream));
+}
+
 int kan_hip_edge_reg_workspace(int dtype, int64_t count, size_t* bytes) {
   KAN_TRY(check_dtype(dtype, "edge_reg_workspace"));
   KAN_TRY(need_ptr(bytes, "edge_reg_workspace", "bytes"));

@@ -305,5 +305,12 @@ int launch_edge_linear_backward_mfma(const float* ga, const float* D, const floa
                                      const float* H, const float* bw, const float* W, float* ds,
                                      float* dH, float* dbw, float* dW, float* part, int splits,
                                      int64_t n, int64_t I, int64_t O, int64_t R, hipStream_t st);
+// Forward of the same layer: y = s bw^T + <H, W> and a = mean_n |phi| from one
+// pass over phi (edge_ylin_fwd_kernel), with part holding edge_ylin_ws_bytes.
+bool edge_ylin_supported(int64_t n, int64_t I, int64_t O, int64_t R);
+size_t edge_ylin_ws_bytes(int64_t n, int64_t I, int64_t O);
+int launch_edge_ylin_forward(const float* s, const float* H, const float* bw, const float* W,
+                             float* y, float* a, float* part, int64_t n, int64_t I, int64_t O,
+                             int64_t R, hipStream_t st);
 
 }  // namespace kan

@@ -439,6 +439,17 @@ struct StageLoader {
                                        : kBufOob);
     }
   }
+  // the registers of a chunk that lies wholly past the range (read as zeros)
+  __device__ __forceinline__ void clear() {
+    if constexpr (VEC) {
+#pragma unroll
+      for (int j = 0; j < KS; ++j) hv4[j] = u32x4{0u, 0u, 0u, 0u};
+    } else {
+#pragma unroll
+      for (int j = 0; j < SG::kEPT; ++j) hv[j] = 0.0f;
+      sv = 0.0f;
+    }
+  }
   __device__ __forceinline__ void store(float* __restrict__ buf, int R, int nf, float inv_fr,
                                         float inv_nf) const {
     const int t = (int)threadIdx.x;
@@ -556,6 +567,168 @@ __global__ __launch_bounds__(kEdgeMfThreads) void edge_fwd_stage_kernel(
       if (final_out) out[e] = cs / (float)g.n;
       else out[(int64_t)split * g.O * g.I + e] = cs;
     }
+  }
+}
+
+// Layer output and edge statistic of a regularised layer in one pass.  The
+// output y[n, o] = s bw^T + H W^T (flattened over I and R) is the sum over
+// features of the very edge values whose absolute means the statistic
+// takes, y = sum_i phi_i, so phi is formed once: a block owns 128 samples x
+// 128 outputs (4 waves as 2 sample halves x 2 output halves, 4 x 4 tiles of
+// 16 each) and walks the features in groups of kStF, staging the H rows of
+// its samples and the W rows of its outputs through LDS in the row layout of
+// the staged kernels ([H | s | zero slot]; the W side is the same layout
+// with bw for s).  Per feature a wave forms phi on its 16 tiles, adds it to
+// the output accumulators and |phi| to the feature's column sums; after each
+// group the two sample halves add their column sums in LDS, in wave order,
+// and write one partial row per feature, apart[block row][i][o], which
+// edge_ylin_finalize adds in order.  Features are summed into y in index
+// order, so both results are deterministic.
+template <int KS, bool VEC>
+__global__ __launch_bounds__(kEdgeMfThreads, 2) void edge_ylin_fwd_kernel(
+    const float* __restrict__ s, const float* __restrict__ H, const float* __restrict__ bw,
+    const float* __restrict__ W, float* __restrict__ y, float* __restrict__ apart, int64_t n,
+    int I, int O, int R, int oblocks) {
+  typedef StageGeom<KS> SG;
+  constexpr int kRows = 2 * kStRows;  // samples (and outputs) of a block
+  __shared__ float lh[kRows * SG::kS];
+  __shared__ float lw[kRows * SG::kS];
+  __shared__ float red[2][kStF][64];
+  const int bid = xcd_remap((int)blockIdx.x, (int)gridDim.x);
+  const int ob = bid % oblocks;
+  const int64_t nblk = bid / oblocks;
+  const int64_t n0 = nblk * kRows;
+  const int o0 = ob * kRows;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int q = lane >> 4, r = lane & 15;
+  const int wn = wave >> 1, wo = wave & 1;
+  const int groups = (I + kStF - 1) / kStF;
+
+  // zero slots (never written by the stores) read as zero
+  for (int e = threadIdx.x; e < kRows * SG::kS; e += kEdgeMfThreads) {
+    lh[e] = 0.0f;
+    lw[e] = 0.0f;
+  }
+  StageLoader<KS, VEC> ldh[2], ldw[2];
+  auto load_group = [&](int g) {
+    const int i0 = g * kStF, nf = min(kStF, I - i0);
+    const float inv_fr = 1.0f / (float)(VEC ? R : nf * R), inv_nf = 1.0f / (float)nf;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      if (n0 + h * kStRows < n) ldh[h].load(s, H, n0 + h * kStRows, n, I, R, i0, nf, inv_fr, inv_nf);
+      else ldh[h].clear();
+      if (o0 + h * kStRows < O) ldw[h].load(bw, W, o0 + h * kStRows, O, I, R, i0, nf, inv_fr, inv_nf);
+      else ldw[h].clear();
+    }
+  };
+  f32x4 yacc[4][4];
+#pragma unroll
+  for (int tn = 0; tn < 4; ++tn)
+#pragma unroll
+    for (int to = 0; to < 4; ++to) yacc[tn][to] = zero4();
+  load_group(0);
+  for (int g = 0; g < groups; ++g) {
+    const int i0 = g * kStF, nf = min(kStF, I - i0);
+    const float inv_fr = 1.0f / (float)(VEC ? R : nf * R), inv_nf = 1.0f / (float)nf;
+    __syncthreads();  // the previous group's rows are no longer read
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      ldh[h].store(lh + h * kStRows * SG::kS, R, nf, inv_fr, inv_nf);
+      ldw[h].store(lw + h * kStRows * SG::kS, R, nf, inv_fr, inv_nf);
+    }
+    if (g + 1 < groups) load_group(g + 1);
+    __syncthreads();
+    float asum[kStF][4];
+#pragma unroll
+    for (int f = 0; f < kStF; ++f) {
+#pragma unroll
+      for (int to = 0; to < 4; ++to) asum[f][to] = 0.0f;
+      if (f < nf) {
+        // LDS column of operand column c = 4 k + q: s, H(i0 + f, c - 1) or the zero slot
+        float a[4][KS], w[4][KS];
+#pragma unroll
+        for (int k = 0; k < KS; ++k) {
+          const int c = 4 * k + q;
+          const int col = c == 0 ? 4 * R + f : (c <= R ? f * R + c - 1 : 4 * R + 4);
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            a[t][k] = lh[(wn * 64 + t * 16 + r) * SG::kS + col];
+            w[t][k] = lw[(wo * 64 + t * 16 + r) * SG::kS + col];
+          }
+        }
+        // per sample tile, the four output tiles' MFMA chains interleaved
+#pragma unroll
+        for (int tn = 0; tn < 4; ++tn) {
+          f32x4 phi[4];
+#pragma unroll
+          for (int to = 0; to < 4; ++to) phi[to] = zero4();
+#pragma unroll
+          for (int k = 0; k < KS; ++k)
+#pragma unroll
+            for (int to = 0; to < 4; ++to) phi[to] = mfma16(a[tn][k], w[to][k], phi[to]);
+#pragma unroll
+          for (int to = 0; to < 4; ++to) {
+            yacc[tn][to] += phi[to];
+            asum[f][to] += (fabsf(phi[to][0]) + fabsf(phi[to][1])) +
+                           (fabsf(phi[to][2]) + fabsf(phi[to][3]));
+          }
+        }
+      }
+    }
+    // column sums over the wave's 64 samples (lanes q hold rows 4q..4q+3 of
+    // each tile), then the two sample halves in wave order
+#pragma unroll
+    for (int f = 0; f < kStF; ++f)
+#pragma unroll
+      for (int to = 0; to < 4; ++to) {
+        const float s1 = asum[f][to] + __shfl_xor(asum[f][to], 16);
+        asum[f][to] = s1 + __shfl_xor(s1, 32);
+      }
+    if (wn == 0 && q == 0) {
+#pragma unroll
+      for (int f = 0; f < kStF; ++f)
+#pragma unroll
+        for (int to = 0; to < 4; ++to) red[wo][f][to * 16 + r] = asum[f][to];
+    }
+    __syncthreads();
+    if (wn == 1 && q == 0) {
+#pragma unroll
+      for (int f = 0; f < kStF; ++f) {
+        if (f >= nf) continue;
+        float* dst = apart + ((int64_t)nblk * I + i0 + f) * O;
+#pragma unroll
+        for (int to = 0; to < 4; ++to) {
+          const int o = o0 + wo * 64 + to * 16 + r;
+          if (o < O) dst[o] = red[wo][f][to * 16 + r] + asum[f][to];
+        }
+      }
+    }
+  }
+  // y: lane (q, r) of tile (tn, to) holds rows 4q + v, column r
+#pragma unroll
+  for (int tn = 0; tn < 4; ++tn)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int64_t nn = n0 + wn * 64 + tn * 16 + 4 * q + v;
+      if (nn >= n) continue;
+#pragma unroll
+      for (int to = 0; to < 4; ++to) {
+        const int o = o0 + wo * 64 + to * 16 + r;
+        if (o < O) y[nn * O + o] = yacc[tn][to][v];
+      }
+    }
+}
+
+// a[o, i] = (sum over block rows b, in order, of apart[b][i][o]) / n
+__global__ void edge_ylin_finalize(const float* __restrict__ apart, float* __restrict__ a,
+                                   int nblk, int I, int O, int64_t n) {
+  const int64_t count = (int64_t)I * O;
+  for (int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; e < count;
+       e += (int64_t)gridDim.x * blockDim.x) {
+    float v = apart[e];
+    for (int b = 1; b < nblk; ++b) v += apart[(int64_t)b * count + e];
+    const int64_t i = e / O, o = e - i * O;
+    a[o * I + i] = v / (float)n;
   }
 }
 
@@ -1758,6 +1931,49 @@ int launch_edge_linear_backward_mfma(const float* ga, const float* D, const floa
                ? KAN_OK
                : launch_edge_params(ga, D, s, H, bw, W, dbw, dW, part, splits, n, I, O, R, st);
   return launch_edge_fused(ga, D, s, H, bw, W, ds, dH, dbw, dW, part, splits, n, I, O, R, st);
+}
+
+bool edge_ylin_supported(int64_t n, int64_t I, int64_t O, int64_t R) {
+  return n > 0 && I > 0 && O > 0 && R >= 1 && R + 1 <= 16;
+}
+
+size_t edge_ylin_ws_bytes(int64_t n, int64_t I, int64_t O) {
+  return sizeof(float) * (size_t)ceil_div(n, (int64_t)(2 * kStRows)) * (size_t)I * (size_t)O;
+}
+
+int launch_edge_ylin_forward(const float* s, const float* H, const float* bw, const float* W,
+                             float* y, float* a, float* part, int64_t n, int64_t I, int64_t O,
+                             int64_t R, hipStream_t st) {
+  if (!edge_ylin_supported(n, I, O, R))
+    return set_error(KAN_ERR_LIMIT,
+                     "edge_linear_forward: needs n, in_features, out_features > 0 and "
+                     "num_basis + 1 <= 16");
+  if ((s == nullptr) != (bw == nullptr))
+    return set_error(KAN_ERR_INVALID, "edge_linear_forward: s and base_weight must both be given or both be empty");
+  const int64_t nblk = ceil_div(n, (int64_t)(2 * kStRows));
+  const int64_t oblocks = ceil_div(O, (int64_t)(2 * kStRows));
+  const int64_t blocks = nblk * oblocks;
+  if (blocks > 2147483647LL || nblk > 2147483647LL)
+    return set_error(KAN_ERR_LIMIT, "edge_linear_forward: too many blocks");
+  auto al = [](const float* q) { return (reinterpret_cast<uintptr_t>(q) & 15) == 0; };
+  const bool vec = I % kStF == 0 && al(H) && al(W) && (s == nullptr || (al(s) && al(bw)));
+  const int R1 = (int)R + 1;
+  {
+    TimedLaunch timed(kClassEdge, st, 2.0 * (double)n * (double)O * (double)I * (double)R1);
+#define KAN_YLIN(VV)                                                                           \
+  KAN_EDGE_MF_DISPATCH4(R1, hipLaunchKernelGGL((edge_ylin_fwd_kernel<KS, VV>),                 \
+                                               dim3((unsigned)blocks), dim3(kEdgeMfThreads), 0, \
+                                               st, s, H, bw, W, y, part, n, (int)I, (int)O,    \
+                                               (int)R, (int)oblocks))
+    if (vec) KAN_YLIN(true);
+    else KAN_YLIN(false);
+#undef KAN_YLIN
+    const int rc = check_launch("edge_linear_forward");
+    if (rc != KAN_OK) return rc;
+  }
+  hipLaunchKernelGGL(edge_ylin_finalize, dim3(fin_blocks_f32(O * I)), dim3(256), 0, st, part, a,
+                     (int)nblk, (int)I, (int)O, n);
+  return check_launch("edge_linear_forward(finalize)");
 }
 
 int launch_edge_backward_mfma(const float* ga, const float* s, const float* H, const float* bw,

@@ -113,6 +113,17 @@ class EdgeAbsMean(torch.autograd.Function):
                 dbw if need_bw and has_base else None, dW if need_W else None)
 
 
+def _one_pass_forward(B: int, O: int) -> bool:
+    """Whether EdgeLinear's forward takes y and a from one pass over phi
+    (_C.edge_linear_forward, 128 x 128 sample x output blocks) rather than
+    the edge statistic's kernel plus the engine's two output products.
+    Measured at N = 16384, G = 8: 256->512 0.81 -> 0.65 ms and 512->512
+    1.55 -> 1.28 ms, but 512->64 0.28 -> 0.89 ms (half-empty output
+    blocks, 128 workgroups) and 64->128 0.125 -> 0.142 ms; so at least 256
+    outputs and one block per CU."""
+    return O >= 256 and -(-B // 128) * -(-O // 128) >= 256
+
+
 class EdgeLinear(torch.autograd.Function):
     """(y, a) of one regularised layer from the same operands:
     y = s bw^T + H W^T (flattened over I and R) and a = mean_n |phi|.
@@ -124,14 +135,19 @@ class EdgeLinear(torch.autograd.Function):
     (_C.edge_linear_backward: dL/dy added to g inside the fused edge kernel)
     returns all four (only the weight gradients: the parameter kernel with
     dL/dy added the same way).  Recorded backwards (create_graph) use the
-    separate differentiable pieces."""
+    separate differentiable pieces.  The forward of a wide layer takes y and
+    a from one pass over phi as well (_C.edge_linear_forward: y is the sum
+    over features of the edge values whose absolute means a holds)."""
 
     @staticmethod
     def forward(ctx, s, H, bw, W):
         B, I, R = H.shape
         O = W.shape[0]
-        y = _C.matmul(s, bw.t()) + _C.matmul(H.reshape(B, I * R), W.reshape(O, I * R).t())
-        a = _C.edge_abs_mean(s, H, bw, W)
+        if _one_pass_forward(B, O) and _C.edge_linear_forward_supported(H, W):
+            y, a = _C.edge_linear_forward(s, H, bw, W)
+        else:
+            y = _C.matmul(s, bw.t()) + _C.matmul(H.reshape(B, I * R), W.reshape(O, I * R).t())
+            a = _C.edge_abs_mean(s, H, bw, W)
         ctx.save_for_backward(s, H, bw, W)
         return y, a
 
