@@ -22,6 +22,7 @@
 
 #include <cstdlib>
 #include <cstring>
+#include <type_traits>
 
 #include "kan_common.h"
 
@@ -450,9 +451,12 @@ struct StageLoader {
       sv = 0.0f;
     }
   }
+  // SKEW: row j of the chunk starts at j kS + 4 (j / 16) instead of j kS
+  template <bool SKEW = false>
   __device__ __forceinline__ void store(float* __restrict__ buf, int R, int nf, float inv_fr,
                                         float inv_nf) const {
     const int t = (int)threadIdx.x;
+    auto row_at = [](int row) { return row * SG::kS + (SKEW ? 4 * (row >> 4) : 0); };
     if constexpr (VEC) {
 #pragma unroll
       for (int j = 0; j < KS; ++j) {
@@ -460,9 +464,9 @@ struct StageLoader {
         int off;
         if (v < kStRows * R) {
           const int row = small_div_f(v, inv_fr);
-          off = row * SG::kS + 4 * (v - row * R);
+          off = row_at(row) + 4 * (v - row * R);
         } else {
-          off = (v - kStRows * R) * SG::kS + 4 * R;
+          off = row_at(v - kStRows * R) + 4 * R;
         }
         if (v < kStRows * (R + 1)) *reinterpret_cast<u32x4*>(buf + off) = hv4[j];
       }
@@ -473,12 +477,12 @@ struct StageLoader {
         const int e = t + kEdgeMfThreads * j;
         if (e < elems) {
           const int row = small_div_f(e, inv_fr);
-          buf[row * SG::kS + (e - row * FR)] = hv[j];
+          buf[row_at(row) + (e - row * FR)] = hv[j];
         }
       }
       if (t < kStRows * nf) {
         const int row = small_div_f(t, inv_nf);
-        buf[row * SG::kS + 4 * R + (t - row * nf)] = sv;
+        buf[row_at(row) + 4 * R + (t - row * nf)] = sv;
       }
     }
   }
@@ -570,6 +574,74 @@ __global__ __launch_bounds__(kEdgeMfThreads) void edge_fwd_stage_kernel(
   }
 }
 
+// Staging of 64-row chunks for edge_ylin_fwd_kernel with 16-byte loads
+// (I % kStF == 0, aligned operands): the chunk holds 64 R H vectors (each
+// row's 4 features x R floats are contiguous) and 64 s vectors; vector
+// v = thread + 256 jj.  Since 64 R is a multiple of 64, each
+// wave's vectors of one jj are all H, all s or all past the end, so the
+// choice is a scalar branch.  Per-lane offsets are the same for every
+// feature group, for both halves and for both operands (H rows and W rows
+// are both I R floats apart, s and bw rows I), so they are computed once.
+template <int KS>
+struct YlinVecLoader {
+  typedef StageGeom<KS> SG;
+  typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+  uint32_t goff[KS];  // byte offset in the chunk's H (or s) resource
+  int loff[KS];       // float offset in the staged half
+  u32x4 hv4[KS];
+  __device__ __forceinline__ static int kind(int jj, int wave, int R) {
+    const int vw = kEdgeMfThreads * jj + 64 * wave;  // the wave's first vector
+    return vw < kStRows * R ? 0 : (vw < kStRows * (R + 1) ? 1 : 2);
+  }
+  __device__ __forceinline__ void init(int I, int R, int wave) {
+    const int t = (int)threadIdx.x;
+    const float inv_r = 1.0f / (float)R;
+#pragma unroll
+    for (int jj = 0; jj < KS; ++jj) {
+      const int v = t + kEdgeMfThreads * jj;
+      const int kd = kind(jj, wave, R);
+      int row = 0, l = 0;
+      uint32_t g = 0;
+      if (kd == 0) {
+        row = small_div_f(v, inv_r);
+        const int piece = v - row * R;
+        g = (uint32_t)(((int64_t)row * I * R + 4 * piece) * 4);
+        l = 4 * piece;
+      } else if (kd == 1) {
+        row = v - kStRows * R;
+        g = (uint32_t)((int64_t)row * I * 4);
+        l = 4 * R;
+      }
+      goff[jj] = g;
+      loff[jj] = row * SG::kS + 4 * (row >> 4) + l;
+    }
+  }
+  // rows [c0, c0 + 64) of X [rows, I, R] / xs [rows, I] at features i0.., rows
+  // at or past ne read as zero
+  __device__ __forceinline__ void load(const float* __restrict__ xs, const float* __restrict__ X,
+                                       int64_t c0, int64_t ne, int I, int R, int i0, int wave) {
+    const int64_t IR = (int64_t)I * R;
+    const int64_t rows = ne - c0 < kStRows ? (ne - c0 > 0 ? ne - c0 : 0) : kStRows;
+    const __amdgpu_buffer_rsrc_t rh = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(X + c0 * IR + (int64_t)i0 * R), (short)0, (int)(rows * IR * 4),
+        kBufWord3);
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(xs != nullptr ? xs + c0 * I + i0 : X), (short)0,
+        xs != nullptr ? (int)(rows * (int64_t)I * 4) : 0, kBufWord3);
+#pragma unroll
+    for (int jj = 0; jj < KS; ++jj) {
+      const int kd = kind(jj, wave, R);
+      if (kd == 0) hv4[jj] = __builtin_amdgcn_raw_buffer_load_b128(rh, (int)goff[jj], 0, 0);
+      else if (kd == 1) hv4[jj] = __builtin_amdgcn_raw_buffer_load_b128(rs, (int)goff[jj], 0, 0);
+    }
+  }
+  __device__ __forceinline__ void store(float* __restrict__ buf, int R, int wave) const {
+#pragma unroll
+    for (int jj = 0; jj < KS; ++jj)
+      if (kind(jj, wave, R) != 2) *reinterpret_cast<u32x4*>(buf + loff[jj]) = hv4[jj];
+  }
+};
+
 // Layer output and edge statistic of a regularised layer in one pass.  The
 // output y[n, o] = s bw^T + H W^T (flattened over I and R) is the sum over
 // features of the very edge values whose absolute means the statistic
@@ -591,8 +663,13 @@ __global__ __launch_bounds__(kEdgeMfThreads, 2) void edge_ylin_fwd_kernel(
     int I, int O, int R, int oblocks) {
   typedef StageGeom<KS> SG;
   constexpr int kRows = 2 * kStRows;  // samples (and outputs) of a block
-  __shared__ float lh[kRows * SG::kS];
-  __shared__ float lw[kRows * SG::kS];
+  // row j of a staged half starts at j kS + 4 (j / 16): within a 16-row
+  // tile the rows fall in distinct banks (kS = 4 x odd), and the skew keeps a
+  // lane's reads of two tiles (16 kS apart, a multiple of the 64 banks) off
+  // one bank when the compiler pairs them into one instruction
+  constexpr int kHalf = kStRows * SG::kS + 4 * (kStRows / 16);
+  __shared__ float lh[2 * kHalf];
+  __shared__ float lw[2 * kHalf];
   __shared__ float red[2][kStF][64];
   const int bid = xcd_remap((int)blockIdx.x, (int)gridDim.x);
   const int ob = bid % oblocks;
@@ -605,20 +682,38 @@ __global__ __launch_bounds__(kEdgeMfThreads, 2) void edge_ylin_fwd_kernel(
   const int groups = (I + kStF - 1) / kStF;
 
   // zero slots (never written by the stores) read as zero
-  for (int e = threadIdx.x; e < kRows * SG::kS; e += kEdgeMfThreads) {
+  for (int e = threadIdx.x; e < 2 * kHalf; e += kEdgeMfThreads) {
     lh[e] = 0.0f;
     lw[e] = 0.0f;
   }
-  StageLoader<KS, VEC> ldh[2], ldw[2];
-  auto load_group = [&](int g) {
-    const int i0 = g * kStF, nf = min(kStF, I - i0);
-    const float inv_fr = 1.0f / (float)(VEC ? R : nf * R), inv_nf = 1.0f / (float)nf;
+  // 16-byte staging (YlinVecLoader) or the staged kernels' scalar loader
+  typedef typename std::conditional<VEC, YlinVecLoader<KS>, StageLoader<KS, false>>::type Loader;
+  Loader ldh[2], ldw[2];
+  if constexpr (VEC) {
+    ldh[0].init(I, R, wave);
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-      if (n0 + h * kStRows < n) ldh[h].load(s, H, n0 + h * kStRows, n, I, R, i0, nf, inv_fr, inv_nf);
-      else ldh[h].clear();
-      if (o0 + h * kStRows < O) ldw[h].load(bw, W, o0 + h * kStRows, O, I, R, i0, nf, inv_fr, inv_nf);
-      else ldw[h].clear();
+#pragma unroll
+      for (int jj = 0; jj < KS; ++jj) {
+        ldh[h].goff[jj] = ldw[h].goff[jj] = ldh[0].goff[jj];
+        ldh[h].loff[jj] = ldw[h].loff[jj] = ldh[0].loff[jj];
+      }
+    }
+  }
+  auto load_group = [&](int g) {
+    const int i0 = g * kStF, nf = min(kStF, I - i0);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      if constexpr (VEC) {
+        ldh[h].load(s, H, n0 + h * kStRows, n, I, R, i0, wave);
+        ldw[h].load(bw, W, o0 + h * kStRows, O, I, R, i0, wave);
+      } else {
+        const float inv_fr = 1.0f / (float)(nf * R), inv_nf = 1.0f / (float)nf;
+        if (n0 + h * kStRows < n) ldh[h].load(s, H, n0 + h * kStRows, n, I, R, i0, nf, inv_fr, inv_nf);
+        else ldh[h].clear();
+        if (o0 + h * kStRows < O) ldw[h].load(bw, W, o0 + h * kStRows, O, I, R, i0, nf, inv_fr, inv_nf);
+        else ldw[h].clear();
+      }
     }
   };
   f32x4 yacc[4][4];
@@ -627,14 +722,30 @@ __global__ __launch_bounds__(kEdgeMfThreads, 2) void edge_ylin_fwd_kernel(
 #pragma unroll
     for (int to = 0; to < 4; ++to) yacc[tn][to] = zero4();
   load_group(0);
+  // operand columns: c = 4 k + q reads column colk[k] + f inck[k] of feature
+  // f's group row (s: 4R + f; H(f, c - 1): f R + c - 1; past R: the zero slot)
+  int colk[KS], inck[KS];
+#pragma unroll
+  for (int k = 0; k < KS; ++k) {
+    const int c = 4 * k + q;
+    colk[k] = c == 0 ? 4 * R : (c <= R ? c - 1 : 4 * R + 4);
+    inck[k] = c == 0 ? 1 : (c <= R ? R : 0);
+  }
+  const float* pa = lh + wn * kHalf + r * SG::kS;
+  const float* pw = lw + wo * kHalf + r * SG::kS;
   for (int g = 0; g < groups; ++g) {
     const int i0 = g * kStF, nf = min(kStF, I - i0);
-    const float inv_fr = 1.0f / (float)(VEC ? R : nf * R), inv_nf = 1.0f / (float)nf;
     __syncthreads();  // the previous group's rows are no longer read
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-      ldh[h].store(lh + h * kStRows * SG::kS, R, nf, inv_fr, inv_nf);
-      ldw[h].store(lw + h * kStRows * SG::kS, R, nf, inv_fr, inv_nf);
+      if constexpr (VEC) {
+        ldh[h].store(lh + h * kHalf, R, wave);
+        ldw[h].store(lw + h * kHalf, R, wave);
+      } else {
+        const float inv_fr = 1.0f / (float)(nf * R), inv_nf = 1.0f / (float)nf;
+        ldh[h].template store<true>(lh + h * kHalf, R, nf, inv_fr, inv_nf);
+        ldw[h].template store<true>(lw + h * kHalf, R, nf, inv_fr, inv_nf);
+      }
     }
     if (g + 1 < groups) load_group(g + 1);
     __syncthreads();
@@ -644,16 +755,14 @@ __global__ __launch_bounds__(kEdgeMfThreads, 2) void edge_ylin_fwd_kernel(
 #pragma unroll
       for (int to = 0; to < 4; ++to) asum[f][to] = 0.0f;
       if (f < nf) {
-        // LDS column of operand column c = 4 k + q: s, H(i0 + f, c - 1) or the zero slot
         float a[4][KS], w[4][KS];
 #pragma unroll
         for (int k = 0; k < KS; ++k) {
-          const int c = 4 * k + q;
-          const int col = c == 0 ? 4 * R + f : (c <= R ? f * R + c - 1 : 4 * R + 4);
+          const int col = colk[k] + f * inck[k];
 #pragma unroll
           for (int t = 0; t < 4; ++t) {
-            a[t][k] = lh[(wn * 64 + t * 16 + r) * SG::kS + col];
-            w[t][k] = lw[(wo * 64 + t * 16 + r) * SG::kS + col];
+            a[t][k] = pa[t * (16 * SG::kS + 4) + col];
+            w[t][k] = pw[t * (16 * SG::kS + 4) + col];
           }
         }
         // per sample tile, the four output tiles' MFMA chains interleaved
