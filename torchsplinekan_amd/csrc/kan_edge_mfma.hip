@@ -828,16 +828,23 @@ __global__ __launch_bounds__(kEdgeMfThreads, 2) void edge_ylin_fwd_kernel(
     }
 }
 
-// a[o, i] = (sum over block rows b, in order, of apart[b][i][o]) / n
+// a[o, i] = (sum over block rows b of apart[b][i][o]) / n, as four
+// interleaved partial sums (b mod 4, each in order) added in a fixed order,
+// so that four loads are in flight per thread
 __global__ void edge_ylin_finalize(const float* __restrict__ apart, float* __restrict__ a,
                                    int nblk, int I, int O, int64_t n) {
   const int64_t count = (int64_t)I * O;
   for (int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; e < count;
        e += (int64_t)gridDim.x * blockDim.x) {
-    float v = apart[e];
-    for (int b = 1; b < nblk; ++b) v += apart[(int64_t)b * count + e];
+    float p[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    int b = 0;
+    for (; b + 4 <= nblk; b += 4) {
+#pragma unroll
+      for (int u = 0; u < 4; ++u) p[u] += apart[(int64_t)(b + u) * count + e];
+    }
+    for (int u = 0; b < nblk; ++b, ++u) p[u] += apart[(int64_t)b * count + e];
     const int64_t i = e / O, o = e - i * O;
-    a[o * I + i] = v / (float)n;
+    a[o * I + i] = ((p[0] + p[1]) + (p[2] + p[3])) / (float)n;
   }
 }
 
