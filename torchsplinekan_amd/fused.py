@@ -113,15 +113,22 @@ class EdgeAbsMean(torch.autograd.Function):
                 dbw if need_bw and has_base else None, dW if need_W else None)
 
 
-def _one_pass_forward(B: int, O: int) -> bool:
+_CU_COUNT = {}
+
+
+def _one_pass_forward(B: int, O: int, device) -> bool:
     """Whether EdgeLinear's forward takes y and a from one pass over phi
     (_C.edge_linear_forward, 128 x 128 sample x output blocks) rather than
-    the edge statistic's kernel plus the engine's two output products.
-    Measured at N = 16384, G = 8: 256->512 0.81 -> 0.65 ms and 512->512
-    1.55 -> 1.28 ms, but 512->64 0.28 -> 0.89 ms (half-empty output
-    blocks, 128 workgroups) and 64->128 0.125 -> 0.142 ms; so at least 256
-    outputs and one block per CU."""
-    return O >= 256 and -(-B // 128) * -(-O // 128) >= 256
+    the edge statistic's kernel plus the engine's two output products:
+    where the blocks fill the chip once (one per CU).  A sweep at G = 8
+    (in_features 64-512, out_features 64-1024, N 2048-65536) found the one
+    pass faster in every such case (time ratio 0.58-0.99; 512->512 at
+    N = 16384: 1.56 -> 1.19 ms) and slower in nearly every other (512->64
+    at N = 16384, 128 blocks: 0.28 -> 0.85 ms)."""
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    if idx not in _CU_COUNT:
+        _CU_COUNT[idx] = torch.cuda.get_device_properties(idx).multi_processor_count
+    return -(-B // 128) * -(-O // 128) >= _CU_COUNT[idx]
 
 
 class EdgeLinear(torch.autograd.Function):
@@ -143,7 +150,7 @@ class EdgeLinear(torch.autograd.Function):
     def forward(ctx, s, H, bw, W):
         B, I, R = H.shape
         O = W.shape[0]
-        if _one_pass_forward(B, O) and _C.edge_linear_forward_supported(H, W):
+        if _one_pass_forward(B, O, H.device) and _C.edge_linear_forward_supported(H, W):
             y, a = _C.edge_linear_forward(s, H, bw, W)
         else:
             y = _C.matmul(s, bw.t()) + _C.matmul(H.reshape(B, I * R), W.reshape(O, I * R).t())
