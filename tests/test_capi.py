@@ -153,6 +153,43 @@ def test_edge_linear_supported(lib):
     assert L.kan_hip_edge_linear_supported(f64, 100, 8, 64, 11) == 0
 
 
+def test_edge_linear_forward_queries_and_refusals(lib):
+    """The one-pass forward's range, workspace size (partial sums of the
+    statistic per 128 samples: 4 * ceil(n / 128) * I * O bytes) and the
+    refusals that come before any launch (no device call)."""
+    L, f32, f64 = lib.LIB, lib.KAN_DTYPE_F32, lib.KAN_DTYPE_F64
+    assert L.kan_hip_edge_linear_forward_supported(f32, 16384, 512, 512, 11) == 1
+    assert L.kan_hip_edge_linear_forward_supported(f32, 1, 1, 1300, 15) == 1
+    assert L.kan_hip_edge_linear_forward_supported(f32, 100, 8, 64, 16) == 0
+    assert L.kan_hip_edge_linear_forward_supported(f32, 0, 8, 64, 11) == 0
+    assert L.kan_hip_edge_linear_forward_supported(f32, 100, 8, 0, 11) == 0
+    assert L.kan_hip_edge_linear_forward_supported(f64, 100, 8, 64, 11) == 0
+    nb = ctypes.c_size_t(0)
+    assert L.kan_hip_edge_linear_forward_workspace(f32, 16384, 512, 512, 11,
+                                                   ctypes.byref(nb)) == lib.KAN_OK
+    assert nb.value == 4 * 128 * 512 * 512
+    assert L.kan_hip_edge_linear_forward_workspace(f32, 129, 3, 200, 7,
+                                                   ctypes.byref(nb)) == lib.KAN_OK
+    assert nb.value == 4 * 2 * 3 * 200
+    assert L.kan_hip_edge_linear_forward_workspace(f64, 129, 3, 200, 7,
+                                                   ctypes.byref(nb)) == lib.KAN_ERR_LIMIT
+    assert L.kan_hip_edge_linear_forward_workspace(f32, 129, 3, 200, 7, None) == \
+        lib.KAN_ERR_INVALID
+    # refusals before any launch (the pointers are never dereferenced)
+    need = 4 * 2 * 3 * 200
+    p = 4096
+    fwd = L.kan_hip_edge_linear_forward
+    assert fwd(f32, p, p, p, p, None, p, p, need, 129, 3, 200, 7, None) == lib.KAN_ERR_INVALID
+    assert "must not be NULL" in lib.last_error()
+    assert fwd(f32, p, p, None, p, p, p, p, need, 129, 3, 200, 7, None) == lib.KAN_ERR_INVALID
+    assert "both be given" in lib.last_error()
+    assert fwd(f32, p, p, p, p, p, p, p, need - 4, 129, 3, 200, 7, None) == lib.KAN_ERR_WORKSPACE
+    assert fwd(f32, p, p, p, p, p, p, None, need, 129, 3, 200, 7, None) == lib.KAN_ERR_WORKSPACE
+    assert fwd(f64, p, p, p, p, p, p, p, need, 129, 3, 200, 7, None) == lib.KAN_ERR_LIMIT
+    assert fwd(f32, p, p, p, p, p, p, p, need, 129, 3, 200, 16, None) == lib.KAN_ERR_LIMIT
+    assert "num_basis + 1 <= 16" in lib.last_error()
+
+
 def test_c_header_compiles_as_c(tmp_path):
     """The header is plain C (no C++ or torch types in the signatures)."""
     import shutil
