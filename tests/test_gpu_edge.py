@@ -298,7 +298,7 @@ def test_regularized_layers_match_oracle(C, monkeypatch, x_grad, route, widths, 
     net = KAN(widths, grid_size=7, backend="cuda").to("cuda")
     x = (torch.rand(N, widths[0], device="cuda") * 2.2 - 1.1).requires_grad_(x_grad)
     if route == "folded" and widths[1] >= 256:
-        assert fz._one_pass_forward(N, widths[1], x.device)
+        assert fz._one_pass_forward(N, widths[1], 7 + 3, x.device)
     if route == "unfolded":
         monkeypatch.setattr(fz, "edge_linear_applies", lambda *a: False)
     impl = "dense" if route == "dense" else "fused"

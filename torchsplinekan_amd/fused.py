@@ -116,7 +116,7 @@ class EdgeAbsMean(torch.autograd.Function):
 _CU_COUNT = {}
 
 
-def _one_pass_forward(B: int, O: int, device) -> bool:
+def _one_pass_forward(B: int, O: int, R: int, device) -> bool:
     """Whether EdgeLinear's forward takes y and a from one pass over phi
     (_C.edge_linear_forward, 128 x 128 sample x output blocks) rather than
     the edge statistic's kernel plus the engine's two output products:
@@ -124,11 +124,15 @@ def _one_pass_forward(B: int, O: int, device) -> bool:
     (in_features 64-512, out_features 64-1024, N 2048-65536) found the one
     pass faster in every such case (time ratio 0.58-0.99; 512->512 at
     N = 16384: 1.56 -> 1.19 ms) and slower in nearly every other (512->64
-    at N = 16384, 128 blocks: 0.28 -> 0.85 ms)."""
+    at N = 16384, 128 blocks: 0.28 -> 0.85 ms).  Its workspace (one partial
+    row of the statistic per 128 samples, ceil(B / 128) * I * O values)
+    grows with the batch, so it is taken only while that stays within the
+    size of the basis H [B, I, R] the layer holds anyway (O <= 128 R)."""
     idx = device.index if device.index is not None else torch.cuda.current_device()
     if idx not in _CU_COUNT:
         _CU_COUNT[idx] = torch.cuda.get_device_properties(idx).multi_processor_count
-    return -(-B // 128) * -(-O // 128) >= _CU_COUNT[idx]
+    nblk = -(-B // 128)
+    return nblk * -(-O // 128) >= _CU_COUNT[idx] and nblk * O <= B * R
 
 
 class EdgeLinear(torch.autograd.Function):
@@ -150,7 +154,7 @@ class EdgeLinear(torch.autograd.Function):
     def forward(ctx, s, H, bw, W):
         B, I, R = H.shape
         O = W.shape[0]
-        if _one_pass_forward(B, O, H.device) and _C.edge_linear_forward_supported(H, W):
+        if _one_pass_forward(B, O, R, H.device) and _C.edge_linear_forward_supported(H, W):
             y, a = _C.edge_linear_forward(s, H, bw, W)
         else:
             y = _C.matmul(s, bw.t()) + _C.matmul(H.reshape(B, I * R), W.reshape(O, I * R).t())
