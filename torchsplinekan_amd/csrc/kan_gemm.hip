@@ -284,8 +284,35 @@ __device__ __forceinline__ void read_frag(const T* __restrict__ lds, int row, in
   }
 }
 
-// Writes the wave's accumulators to C (+ split slice), bounds-checked.
-template <class C, typename Acc>
+// Fragments of an MN-contiguous operand for all F of a wave's MFMA tiles
+// at once, with the tiles' rows interleaved: tile t's row r is the wave's
+// row F r + t (a permutation of the rows, undone where the output is
+// stored), so the F values a lane needs at one k are contiguous in the
+// [BK][rows + 4] layout and come from one 8- or 16-byte read instead of F
+// scalar reads.  f[t][s] = value of tile t at k = kofs + s.
+template <typename T, int ROWS, int BK, int F>
+__device__ __forceinline__ void read_frag_il(const T* __restrict__ lds, int row0, int kofs,
+                                             T (&f)[F][4]) {
+  static_assert(F == 2 || F == 4, "2 or 4 tiles per wave");
+  constexpr int kS = Slab<ROWS, BK, false>::kStride;
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    if constexpr (F == 4) {
+      const Vec4<T> v = *reinterpret_cast<const Vec4<T>*>(lds + (kofs + s) * kS + row0);
+#pragma unroll
+      for (int t = 0; t < 4; ++t) f[t][s] = v.v[t];
+    } else {
+      typedef T T2 __attribute__((ext_vector_type(2)));
+      const T2 v = *reinterpret_cast<const T2*>(lds + (kofs + s) * kS + row0);
+      f[0][s] = v[0];
+      f[1][s] = v[1];
+    }
+  }
+}
+
+// Writes the wave's accumulators to C (+ split slice), bounds-checked.  AIL /
+// BIL: the rows / columns of the MFMA tiles are interleaved (read_frag_il).
+template <class C, typename Acc, bool AIL = false, bool BIL = false>
 __device__ __forceinline__ void store_tile(const GemmParams<typename C::T>& p, const TileCoords& tc,
                                            const Acc (&acc)[C::FM][C::FN], int wm, int wn,
                                            int lane) {
@@ -295,11 +322,13 @@ __device__ __forceinline__ void store_tile(const GemmParams<typename C::T>& p, c
   for (int i = 0; i < C::FM; ++i) {
 #pragma unroll
     for (int j = 0; j < C::FN; ++j) {
-      const int64_t col = tc.n0 + wn * C::TN + j * C::MF + M::out_col(lane);
+      const int cl = M::out_col(lane);
+      const int64_t col = tc.n0 + wn * C::TN + (BIL ? C::FN * cl + j : j * C::MF + cl);
       if (col >= p.N) continue;
 #pragma unroll
       for (int v = 0; v < M::kNAcc; ++v) {
-        const int64_t row = tc.m0 + wm * C::TM + i * C::MF + M::out_row(lane, v);
+        const int rl = M::out_row(lane, v);
+        const int64_t row = tc.m0 + wm * C::TM + (AIL ? C::FM * rl + i : i * C::MF + rl);
         if (row < p.M) Cp[row * p.ldc + col] = acc[i][j][v];
       }
     }
@@ -734,7 +763,10 @@ __global__ __launch_bounds__(C::kThreads, C::MINB) void gemm_pipe_kernel(GemmPar
   // memory operations per slab (stores, loads) and per k-group (fragment reads)
   constexpr int kDSW = LA::kPer + LB::kPer;
   constexpr int kGLD = LA::kPer + LB::kPer;
-  constexpr int kDSR = (AK ? FM : 4 * FM) + (BKC ? FN : 4 * FN);
+  // MN-contiguous operands take their fragments interleaved (read_frag_il):
+  // one read per k step for all of the wave's tiles
+  constexpr bool AIL = !AK, BIL = !BKC;
+  constexpr int kDSR = (AK ? FM : 4) + (BKC ? FN : 4);
   constexpr int kMF = 4 * FM * FN;  // MFMAs per k-group
   __shared__ __align__(16) T lds_a[2][SA::kElems];
   __shared__ __align__(16) T lds_b[2][SB::kElems];
@@ -756,12 +788,20 @@ __global__ __launch_bounds__(C::kThreads, C::MINB) void gemm_pipe_kernel(GemmPar
   LB lb;
   T fa[2][FM][4], fb[2][FN][4];
   auto fread = [&](const T* a_lds, const T* b_lds, int g, int slot) {
+    if constexpr (AIL) {
+      read_frag_il<T, BM, BK, FM>(a_lds, wm * C::TM + FM * rl, M::kofs(g, q), fa[slot]);
+    } else {
 #pragma unroll
-    for (int i = 0; i < FM; ++i)
-      read_frag<T, BM, BK, AK>(a_lds, wm * C::TM + i * C::MF + rl, M::kofs(g, q), fa[slot][i]);
+      for (int i = 0; i < FM; ++i)
+        read_frag<T, BM, BK, AK>(a_lds, wm * C::TM + i * C::MF + rl, M::kofs(g, q), fa[slot][i]);
+    }
+    if constexpr (BIL) {
+      read_frag_il<T, BN, BK, FN>(b_lds, wn * C::TN + FN * rl, M::kofs(g, q), fb[slot]);
+    } else {
 #pragma unroll
-    for (int j = 0; j < FN; ++j)
-      read_frag<T, BN, BK, BKC>(b_lds, wn * C::TN + j * C::MF + rl, M::kofs(g, q), fb[slot][j]);
+      for (int j = 0; j < FN; ++j)
+        read_frag<T, BN, BK, BKC>(b_lds, wn * C::TN + j * C::MF + rl, M::kofs(g, q), fb[slot][j]);
+    }
   };
   auto mfmas = [&](int slot) {
 #pragma unroll
@@ -844,8 +884,9 @@ __global__ __launch_bounds__(C::kThreads, C::MINB) void gemm_pipe_kernel(GemmPar
   }
   if constexpr (EPIK == 0) {
     (void)e;
-    store_tile<C>(p, tc, acc, wm, wn, lane);
+    store_tile<C, typename M::acc_t, AIL, BIL>(p, tc, acc, wm, wn, lane);
   } else {
+    static_assert(!AIL && !BIL, "the epilogues read the accumulators in tile order");
     static_assert(C::WM * C::WN * 32 * (C::TN + 1) <= 2 * SA::kElems,
                   "dx staging must fit in the A slab buffers");
     constexpr int kSide = 2 * SB::kElems / (C::WM * C::WN);
