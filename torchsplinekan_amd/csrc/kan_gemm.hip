@@ -376,6 +376,8 @@ __global__ __launch_bounds__(C::kThreads, C::MINB) void gemm_kernel(GemmParams<t
     }
   };
   T fa[FM][4], fb[FN][4];
+  // MN-contiguous operands: interleaved fragment reads (read_frag_il)
+  constexpr bool AIL = !AK, BIL = !BKC;
 
   if (tc.nkt > 0) {
     gload(0);
@@ -388,12 +390,20 @@ __global__ __launch_bounds__(C::kThreads, C::MINB) void gemm_kernel(GemmParams<t
       if (more) gload(kt + 1);
 #pragma unroll
       for (int g = 0; g < NG; ++g) {
+        if constexpr (AIL) {
+          read_frag_il<T, BM, BK, FM>(lds_a[cur], wm * C::TM + FM * rl, M::kofs(g, q), fa);
+        } else {
 #pragma unroll
-        for (int i = 0; i < FM; ++i)
-          read_frag<T, BM, BK, AK>(lds_a[cur], wm * C::TM + i * C::MF + rl, M::kofs(g, q), fa[i]);
+          for (int i = 0; i < FM; ++i)
+            read_frag<T, BM, BK, AK>(lds_a[cur], wm * C::TM + i * C::MF + rl, M::kofs(g, q), fa[i]);
+        }
+        if constexpr (BIL) {
+          read_frag_il<T, BN, BK, FN>(lds_b[cur], wn * C::TN + FN * rl, M::kofs(g, q), fb);
+        } else {
 #pragma unroll
-        for (int j = 0; j < FN; ++j)
-          read_frag<T, BN, BK, BKC>(lds_b[cur], wn * C::TN + j * C::MF + rl, M::kofs(g, q), fb[j]);
+          for (int j = 0; j < FN; ++j)
+            read_frag<T, BN, BK, BKC>(lds_b[cur], wn * C::TN + j * C::MF + rl, M::kofs(g, q), fb[j]);
+        }
 #pragma unroll
         for (int s = 0; s < 4; ++s)
 #pragma unroll
@@ -408,7 +418,7 @@ __global__ __launch_bounds__(C::kThreads, C::MINB) void gemm_kernel(GemmParams<t
       __syncthreads();
     }
   }
-  store_tile<C>(p, tc, acc, wm, wn, lane);
+  store_tile<C, typename M::acc_t, AIL, BIL>(p, tc, acc, wm, wn, lane);
 }
 
 // ---- fp32: software-pipelined main loop ------------------------------------
