@@ -127,6 +127,15 @@ using CfgF64 = Cfg<double, 128, 128, 16, 2, 2, 16, 1>;
 // fp64, 256 x 128 block tiles: 8 waves of 64 x 64, two per SIMD (while one
 // wave waits at the slab barrier the other issues MFMAs)
 using CfgF64Big = Cfg<double, 256, 128, 16, 4, 2, 16, 1>;
+// fp64 on the software-pipelined kernel: 128 x 128 tiles, 32-deep slabs (two
+// k-groups), 8 waves of 64 x 32 (two per SIMD); 147 KB of LDS, one block per CU
+using CfgF64Pipe = Cfg<double, 128, 128, 32, 2, 4, 16, 1>;
+
+// Configurations that run on gemm_pipe_kernel (the rest on gemm_kernel).
+template <class C>
+struct RunsPipe {
+  static constexpr bool value = std::is_same<typename C::T, float>::value || C::BK == 32;
+};
 
 template <typename T>
 struct GemmParams {
@@ -759,10 +768,13 @@ __device__ __forceinline__ void ecomp_epilogue(const GemmParams<float>& p, const
 }
 
 template <class C, bool AK, bool BKC, int EPIK>
-__global__ __launch_bounds__(C::kThreads, C::MINB) void gemm_pipe_kernel(GemmParams<float> p,
-                                                                         DxParams e) {
-  typedef float T;
-  typedef Mfma<float, C::MF> M;
+__global__ __launch_bounds__(C::kThreads, C::MINB) void gemm_pipe_kernel(
+    GemmParams<typename C::T> p, DxParams e) {
+  typedef typename C::T T;
+  typedef Mfma<T, C::MF> M;
+  // fp32 loads whole slabs through buffer resources; fp64 (a four-element
+  // chunk is 32 bytes) through plain 16-byte loads
+  constexpr bool kF32 = std::is_same<T, float>::value;
   constexpr int BM = C::BM, BN = C::BN, BK = C::BK, NT = C::kThreads;
   constexpr int FM = C::FM, FN = C::FN, NG = BK / M::kKG;
   static_assert(NG % 2 == 0, "slab must hold an even number of k-groups");
@@ -770,13 +782,17 @@ __global__ __launch_bounds__(C::kThreads, C::MINB) void gemm_pipe_kernel(GemmPar
   typedef Slab<BN, BK, BKC> SB;
   typedef SlabLoader<T, BM, BK, AK, NT> LA;
   typedef SlabLoader<T, BN, BK, BKC, NT> LB;
-  // memory operations per slab (stores, loads) and per k-group (fragment reads)
-  constexpr int kDSW = LA::kPer + LB::kPer;
-  constexpr int kGLD = LA::kPer + LB::kPer;
+  // memory instructions (16 bytes each) per slab (stores, loads) and per
+  // k-group (fragment reads); a chunk of four elements is kW of them
+  constexpr int kW = (int)sizeof(T) / 4;
+  constexpr int kDSW = (LA::kPer + LB::kPer) * kW;
+  constexpr int kGLD = (LA::kPer + LB::kPer) * kW;
   // MN-contiguous operands take their fragments interleaved (read_frag_il):
-  // one read per k step for all of the wave's tiles
+  // F contiguous elements per k step for all of the wave's F tiles
   constexpr bool AIL = !AK, BIL = !BKC;
-  constexpr int kDSR = (AK ? FM : 4) + (BKC ? FN : 4);
+  constexpr int kRdA = AK ? FM * kW : 4 * ((FM * (int)sizeof(T) + 15) / 16);
+  constexpr int kRdB = BKC ? FN * kW : 4 * ((FN * (int)sizeof(T) + 15) / 16);
+  constexpr int kDSR = kRdA + kRdB;
   constexpr int kMF = 4 * FM * FN;  // MFMAs per k-group
   __shared__ __align__(16) T lds_a[2][SA::kElems];
   __shared__ __align__(16) T lds_b[2][SB::kElems];
@@ -825,9 +841,12 @@ __global__ __launch_bounds__(C::kThreads, C::MINB) void gemm_pipe_kernel(GemmPar
   // (guarded; also whole slabs whose offsets do not fit a buffer resource)
   auto gload = [&](int slab, auto full_c) {
     const int64_t k0 = tc.kbeg + (int64_t)slab * BK;
-    if constexpr (decltype(full_c)::value == 1) {
+    if constexpr (decltype(full_c)::value == 1 && kF32) {
       la.load_buf(p.A, p.lda, tc.m0, k0);
       lb.load_buf(p.B, p.ldb, tc.n0, k0);
+    } else if constexpr (decltype(full_c)::value == 1) {
+      la.load_full(p.A, p.lda, tc.m0, k0);
+      lb.load_full(p.B, p.ldb, tc.n0, k0);
     } else {
       la.load_guarded(p.A, p.lda, tc.m0, p.M, k0, tc.kend);
       lb.load_guarded(p.B, p.ldb, tc.n0, p.N, k0, tc.kend);
@@ -868,7 +887,7 @@ __global__ __launch_bounds__(C::kThreads, C::MINB) void gemm_pipe_kernel(GemmPar
     }
   };
   auto run = [&](auto full_c) {
-    if constexpr (decltype(full_c)::value == 1) {
+    if constexpr (decltype(full_c)::value == 1 && kF32) {
       la.init_buf(p.lda);
       lb.init_buf(p.ldb);
     }
@@ -887,7 +906,7 @@ __global__ __launch_bounds__(C::kThreads, C::MINB) void gemm_pipe_kernel(GemmPar
     slab(kt, IC<0>(), IC<0>(), IC<0>(), full_c, IC<-1>());
   };
   if (tc.nkt > 0) {
-    const bool full = p.vec && p.buf && (tc.m0 + BM <= p.M) && (tc.n0 + BN <= p.N) &&
+    const bool full = p.vec && (p.buf || !kF32) && (tc.m0 + BM <= p.M) && (tc.n0 + BN <= p.N) &&
                       ((tc.kend - tc.kbeg) % BK == 0);
     if (full) run(IC<1>());
     else run(IC<0>());
@@ -896,6 +915,7 @@ __global__ __launch_bounds__(C::kThreads, C::MINB) void gemm_pipe_kernel(GemmPar
     (void)e;
     store_tile<C, typename M::acc_t, AIL, BIL>(p, tc, acc, wm, wn, lane);
   } else {
+    static_assert(kF32, "the epilogues are fp32");
     static_assert(!AIL && !BIL, "the epilogues read the accumulators in tile order");
     static_assert(C::WM * C::WN * 32 * (C::TN + 1) <= 2 * SA::kElems,
                   "dx staging must fit in the A slab buffers");
@@ -962,7 +982,10 @@ struct CfgModelF64 {
 };
 // (measured at c3's shapes: 0.81-0.83 of the FP64 peak for the 8-wave tile,
 // 0.75-0.82 for the 4-wave one, whose parameter product lost most)
-constexpr CfgModelF64 kModelF64[2] = {{256, 128, 16, 1, 0.84}, {128, 128, 16, 1, 0.80}};
+// (the pipelined 128 x 128 x 32 measured 0.91-0.95 of the FP64 peak at c3's
+// three product shapes, where the other two measured 0.80-0.82)
+constexpr CfgModelF64 kModelF64[3] = {
+    {256, 128, 16, 1, 0.84}, {128, 128, 16, 1, 0.80}, {128, 128, 32, 1, 0.93}};
 constexpr double kPeakPerCuF64 = 78.6e12 / 256.0;
 constexpr double kKOverheadF64 = 256.0;
 
@@ -998,15 +1021,22 @@ double est_seconds_f64(const CfgModelF64& c, int64_t M, int64_t N, int64_t K, in
 // model.
 int forced_cfg_f32() { return kan_hip_get_route(KAN_ROUTE_GEMM_TILE); }
 
-// fp64 configuration (0 = 256 x 128 with 8 waves, 1 = 128 x 128 with 4) for
-// a split count; the route forces 0 for "256" and 1 for "128".
+// fp64 configuration (0 = 256 x 128 with 8 waves, 1 = 128 x 128 with 4,
+// 2 = the pipelined 128 x 128 x 32) for a split count; the route forces 0
+// for "256", 1 for "128" and 2 for "256x64" (the third fp32 tile's value).
 int pick_cfg_f64(int64_t M, int64_t N, int64_t K, int splits) {
   const int forced = kan_hip_get_route(KAN_ROUTE_GEMM_TILE);
-  if (forced == 0 || forced == 1) return forced;
-  return est_seconds_f64(kModelF64[0], M, N, K, splits) <=
-                 est_seconds_f64(kModelF64[1], M, N, K, splits)
-             ? 0
-             : 1;
+  if (forced >= 0 && forced <= 2) return forced;
+  int best = 0;
+  double best_t = est_seconds_f64(kModelF64[0], M, N, K, splits);
+  for (int c = 1; c <= 2; ++c) {
+    const double t = est_seconds_f64(kModelF64[c], M, N, K, splits);
+    if (t < best_t) {
+      best = c;
+      best_t = t;
+    }
+  }
+  return best;
 }
 
 // fp32 configuration (0 = big, 1 = small, 2 = narrow, 3 = 4-wave big, only
@@ -1045,7 +1075,7 @@ int launch_cfg(GemmParams<typename C::T> p, int splits, hipStream_t st, const Dx
     return span * (int64_t)sizeof(typename C::T) < (int64_t)1 << 31;
   };
   p.buf = span_ok(AK, C::BM, p.lda) && span_ok(BKC, C::BN, p.ldb);
-  if constexpr (std::is_same<typename C::T, float>::value) {
+  if constexpr (RunsPipe<C>::value) {
     DxParams e{};
     if (dx != nullptr) e = *dx;
     hipLaunchKernelGGL((gemm_pipe_kernel<C, AK, BKC, EPIK>), dim3((unsigned)blocks),
@@ -1561,10 +1591,10 @@ int launch_gemm(int layout, int64_t M, int64_t N, int64_t K, const T* A, int64_t
     else if (cfg == 2) rc = launch_layout<CfgF32Narrow>(layout, p, splits, st);
     else rc = launch_layout<CfgF32Small>(layout, p, splits, st);
   } else {
-    if (pick_cfg_f64(M, N, K, splits < 1 ? 1 : splits) == 0)
-      rc = launch_layout<CfgF64Big>(layout, p, splits, st);
-    else
-      rc = launch_layout<CfgF64>(layout, p, splits, st);
+    const int cfg = pick_cfg_f64(M, N, K, splits < 1 ? 1 : splits);
+    if (cfg == 0) rc = launch_layout<CfgF64Big>(layout, p, splits, st);
+    else if (cfg == 2) rc = launch_layout<CfgF64Pipe>(layout, p, splits, st);
+    else rc = launch_layout<CfgF64>(layout, p, splits, st);
   }
   if (rc != KAN_OK) return rc;
   return check_launch("gemm");
