@@ -487,7 +487,7 @@ def run_c3(args, dev, steps, warmup, need_dx=True, f64=False):
     traffic, source = recorded_traffic(tag)
     roof = _mfma_roofline(kernels, "contraction",
                           "%s (%s MFMA contraction; average over the forward, parameter%s "
-                          "launches)" % ("gemm_kernel" if f64 else "gemm_pipe_kernel",
+                          "launches)" % ("gemm_pipe_kernel",
                                          "fp64" if f64 else "fp32",
                                          " and input" if need_dx else ""),
                           traffic, source, PEAK_FP64_TFLOPS if f64 else PEAK_FP32_MFMA_TFLOPS)
