@@ -6,6 +6,7 @@ oracle at the north star's fp32 bar (normwise relative 1e-5):
   of y, dx, dcoef, dscaler and dbase_w (tests/_fullcheck.py: the oracle in
   row chunks; each tensor held to the bar block by block, so one faulty
   output tile of the c3 schedule cannot hide in the whole-tensor norm).
+  The same step in float64: every element, block by block, at 1e-12.
 * c5: KANLinear 4096 -> 256 G65 k3, N = 8192 (N I (G + 2k) = 2.38e9, past
   the reference's 32-bit guard): the same whole-tensor checks, exact zero
   basis rows outside the knot span, and the edge statistic on the c5 basis
@@ -57,9 +58,10 @@ _params = _netcheck.params
 basis_threaded = _netcheck.basis_threaded
 
 
-def _check_whole_step(L, xd, td, x_cpu, k, tag):
+def _check_whole_step(L, xd, td, x_cpu, k, tag, tol=TOL):
     """One training step of a single KANLinear (the bench's step); every
-    element of its outputs against the oracle (tests/_fullcheck.py)."""
+    element of its outputs against the oracle (tests/_fullcheck.py), each
+    tensor block by block within tol."""
     from tests import _fullcheck
     for p in L.parameters():
         p.grad = None
@@ -74,7 +76,7 @@ def _check_whole_step(L, xd, td, x_cpu, k, tag):
     for name, (worst, block, whole) in errs.items():
         _say(f"{tag}: {name} whole-tensor {whole:.2e}, worst block {worst:.2e} at {block}")
     for name, (worst, block, whole) in errs.items():
-        assert worst < TOL, (name, worst, block)
+        assert worst < tol, (name, worst, block)
 
 
 @pytest.mark.timeout(900)
@@ -83,6 +85,17 @@ def test_c3_training_step_matches_oracle(bench):
     L, xd, td, cpu = bench.build_c3(dev, 65536, need_dx=True)
     _say("c3: KANLinear 1024->1024 G10 k3 N=65536 fwd+MSE+bwd with dx, every element")
     _check_whole_step(L, xd, td, cpu[0], 3, tag="c3")
+
+
+@pytest.mark.timeout(900)
+def test_c3_fp64_training_step_matches_oracle(bench):
+    """c3 in float64 (bench.py --dtype f64: the same draws cast after they
+    are made), its three products on the fp64 MFMA tiles the cost model
+    picks at this size: every element at the fp64 bar, 1e-12."""
+    dev = torch.device("cuda", 0)
+    L, xd, td, cpu = bench.build_c3(dev, 65536, need_dx=True, dtype=torch.float64)
+    _say("c3-f64: KANLinear 1024->1024 G10 k3 N=65536 fp64 fwd+MSE+bwd with dx, every element")
+    _check_whole_step(L, xd, td, cpu[0], 3, tag="c3-f64", tol=1e-12)
 
 
 @pytest.mark.timeout(900)
