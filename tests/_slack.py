@@ -206,6 +206,85 @@ def edge_backward_full(ga, s, H, bw, W, D=None, chunk=256, extra=16, unit=U32):
     return (ds, dH, dbw, dW), (sds, sH, sbw, sW), n_amb
 
 
+def layer_grads_full(D, ga, x, grid, k, s, H, bw, sw, sc, need_dx=True, extra=16, unit=U32,
+                     workers=16):
+    """Every gradient of one regularised layer step, over all samples and
+    edges, with its slack: the layer output y = s bw^T + <H, sw*sc> with
+    D = dL/dy [N, O] (None: no output term) and its edge statistic with
+    ga = dL/da [O, I] (None: no statistic).  Feature by feature (the [N, O]
+    tensors of phi, its rounding bound, g = D + ga sign(phi) / N with 0 on
+    the ambiguous set, and the slack weight |ga| / N on that set, contracted
+    with the feature's operands), features in threads with one BLAS thread
+    each.  -> ({name: (ref, slack)} for "base_weight" [O, I] (with a base
+    branch), "spline_weight" [O, I, R], "spline_scaler" [O, I] and, with
+    need_dx, "x" [N, I]; the ambiguous count)."""
+    from concurrent.futures import ThreadPoolExecutor
+    from threadpoolctl import threadpool_limits
+    N, I, R = H.shape
+    O = sw.shape[0]
+    W = sw * sc[:, :, None]
+    c = rounding_factor(R, extra) * unit
+    hb = bw is not None
+    out = {"spline_weight": (np.empty((O, I, R)), np.empty((O, I, R))),
+           "spline_scaler": (np.empty((O, I)), np.empty((O, I)))}
+    if hb:
+        out["base_weight"] = (np.empty((O, I)), np.empty((O, I)))
+    if need_dx:
+        out["x"] = (np.empty((N, I)), np.empty((N, I)))
+        sp = ko.silu_grad(x)
+
+    def one(i):
+        Hi, Wi = H[:, i, :], W[:, i, :]
+        aH, aW = np.abs(Hi), np.abs(Wi)
+        g = np.zeros((N, O)) if D is None else D.copy()
+        gA = np.zeros((N, O))
+        n_amb = 0
+        if ga is not None:
+            phi = Hi @ Wi.T
+            mag = aH @ aW.T
+            if hb:
+                sb = np.outer(s[:, i], bw[:, i])
+                phi += sb
+                mag += np.abs(sb)
+            amb = np.abs(phi) <= c * mag
+            n_amb = int(amb.sum())
+            S = np.sign(phi)
+            S[amb] = 0.0
+            g += S * (ga[:, i] / N)[None, :]
+            gA = amb * (np.abs(ga[:, i]) / N)[None, :]
+        dWi, sWi = g.T @ Hi, gA.T @ aH
+        out["spline_weight"][0][:, i] = sc[:, i, None] * dWi
+        out["spline_weight"][1][:, i] = np.abs(sc[:, i, None]) * sWi
+        out["spline_scaler"][0][:, i] = (sw[:, i, :] * dWi).sum(1)
+        out["spline_scaler"][1][:, i] = (np.abs(sw[:, i, :]) * sWi).sum(1)
+        if hb:
+            out["base_weight"][0][:, i] = g.T @ s[:, i]
+            out["base_weight"][1][:, i] = gA.T @ np.abs(s[:, i])
+        if need_dx:
+            dB = ko.basis_derivative(x[:, i:i + 1], grid[i:i + 1], k)[:, 0, :]
+            r = (dB * (g @ Wi)).sum(1)
+            sl = (np.abs(dB) * (gA @ aW)).sum(1)
+            if hb:
+                r += sp[:, i] * (g @ bw[:, i])
+                sl += np.abs(sp[:, i]) * (gA @ np.abs(bw[:, i]))
+            out["x"][0][:, i] = r
+            out["x"][1][:, i] = sl
+        return n_amb
+
+    with threadpool_limits(limits=1, user_api="blas"):
+        with ThreadPoolExecutor(max(1, workers)) as ex:
+            n_amb = sum(ex.map(one, range(I)))
+    return out, n_amb
+
+
+def slack_adjusted(dev, ref, slack):
+    """dev with each entry's difference from ref shrunk by its slack (to ref
+    itself where |dev - ref| <= slack), for blockwise error measures."""
+    dev = np.asarray(dev, dtype=np.float64)
+    d = dev - ref
+    return ref + np.sign(d) * np.maximum(np.abs(d) - slack, 0.0)
+
+
 def within(dev, ref, slack, tol):
     """max over entries of (|dev - ref| - slack) / max|ref| (<= tol passes)."""
     dev = np.asarray(dev, dtype=np.float64)

@@ -13,11 +13,13 @@ oracle at the north star's fp32 bar (normwise relative 1e-5):
   (2.28e9 elements) with its backward.
 * c4: KAN([256, 512, 512, 64]) G8 with update_grid knots on the Gaussian
   mixture, forward_with_regularization(1e-2, 1e-2, "auto") + MSE + backward:
-  per layer, outputs on rows, the regulariser from the oracle's edge means
-  over all edges, parameter gradients on sampled edges and input gradients
-  on sampled rows, with sign flips of phi at fp32 rounding level bounded
-  term by term (tests/_slack.py); the network output on rows through the
-  full oracle chain; layer 0's knots against the oracle's grid_from_samples.
+  per layer, given its own device input, every element of its output, its
+  parameter gradients and its input gradient, block by block
+  (tests/_netcheck.py, full mode), and the regulariser from the oracle's
+  edge means over all edges, with sign flips of phi at fp32 rounding level
+  bounded term by term (tests/_slack.py); the network output on rows
+  through the full oracle chain; layer 0's knots against the oracle's
+  grid_from_samples.  The same in float64 at 1e-10.
 * c2: KAN([784, 256, 10]) G5, N = 4096 + MSE: every output and gradient
   against the full oracle chain.
 
@@ -197,7 +199,8 @@ def test_c4_regularised_network_matches_oracle(bench):
     e = normwise(np64(y[rows]), h)
     _say(f"c4: network output rows through the fp64 chain from x {e:.2e}")
     assert e < CHAIN_TOL
-    reg_total = _netcheck.check_layers(net, cap, mu, k, TOL, say=lambda m: _say("c4 " + m))
+    reg_total = _netcheck.check_layers(net, cap, mu, k, TOL, say=lambda m: _say("c4 " + m),
+                                       full=True)
     e = abs(reg.item() - reg_total) / abs(reg_total)
     _say(f"c4: total regulariser {e:.2e}")
     assert e < TOL
@@ -206,9 +209,10 @@ def test_c4_regularised_network_matches_oracle(bench):
 @pytest.mark.timeout(1200)
 def test_c4_regularised_network_fp64_matches_oracle(bench):
     """c4 in float64 (the edge statistic on the fp64 MFMA kernels, the layer
-    products on the fp64 GEMM): each layer against the oracle given its own
-    device input, at 1e-10, with sign ambiguity bounded at float64's unit
-    roundoff; the network output through the whole fp64 chain from x."""
+    products on the fp64 GEMM): every element of each layer's outputs and
+    gradients against the oracle given its own device input, at 1e-10, with
+    sign ambiguity bounded at float64's unit roundoff; the network output
+    through the whole fp64 chain from x."""
     dev = torch.device("cuda", 0)
     net, xd, td = bench.build_c4(dev, 16384, torch.float64)
     N = xd.shape[0]
@@ -232,7 +236,7 @@ def test_c4_regularised_network_fp64_matches_oracle(bench):
     _say(f"c4 fp64: network output rows through the fp64 chain from x {e:.2e}")
     assert e < tol
     reg_total = _netcheck.check_layers(net, cap, mu, k, tol, say=lambda m: _say("c4 fp64 " + m),
-                                       unit=2.0 ** -53)
+                                       unit=2.0 ** -53, full=True)
     e = abs(reg.item() - reg_total) / abs(reg_total)
     _say(f"c4 fp64: total regulariser {e:.2e}")
     assert e < tol

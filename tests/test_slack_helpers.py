@@ -123,3 +123,47 @@ def test_full_edge_backward_equals_the_oracle():
     assert got[0] is None and got[2] is None and slack[0] is None
     ref0 = ko.edge_abs_mean_backward(ga, None, H, None, sw)
     assert np.abs(got[1] - ref0[1]).max() < 1e-13 and np.abs(got[3] - ref0[3]).max() < 1e-13
+
+
+def test_full_layer_grads_equal_the_sampled_helpers():
+    """layer_grads_full (every edge and row, features in threads) equals the
+    sampled helpers entry for entry, slack included, with and without the
+    output term, the statistic and the base branch; a planted phi = 0 is
+    found as ambiguous by both."""
+    x, grid, bw, sw, sc, D, ga, k = _layer(N=50, I=6, O=5, seed=7)
+    N, I = x.shape
+    O = sw.shape[0]
+    H = ko.basis_dense(x, grid, k)
+    s = ko.silu(x)
+    # plant phi[n0, o0, i0] = 0 exactly (base term cancels the spline term)
+    n0, o0, i0 = 3, 2, 4
+    bw = bw.copy()
+    bw[o0, i0] = -(H[n0, i0] @ (sw[o0, i0] * sc[o0, i0])) / s[n0, i0]
+    edges = [(o, i) for o in range(O) for i in range(I)]
+    rows = list(range(N))
+    for Dv, gav, base in ((D, ga, True), (None, ga, True), (D, None, True), (D, ga, False)):
+        b = bw if base else None
+        sv = s if base else None
+        full, n_full = _slack.layer_grads_full(Dv, gav, x, grid, k, sv, H, b, sw, sc, workers=3)
+        res, n_par = _slack.edge_param_grads(Dv, gav, sv, H, b, sw, sc, edges)
+        assert n_full == n_par
+        if gav is not None and base:
+            assert n_full >= 1   # the planted term
+        oo, ii = map(np.array, zip(*edges))
+        for name, (ref, slack) in res.items():
+            fr, fs = full[name]
+            assert np.abs(fr[oo, ii] - ref).max() < 1e-13, name
+            assert np.abs(fs[oo, ii] - slack).max() < 1e-13, name
+        rx, sx, _ = _slack.edge_input_grads(Dv, gav, x, grid, k, sv, H, b, sw, sc, rows)
+        assert np.abs(full["x"][0] - rx).max() < 1e-12
+        assert np.abs(full["x"][1] - sx).max() < 1e-13
+        assert ("base_weight" in full) == base
+
+
+def test_slack_adjusted_differences():
+    ref = np.array([1.0, -2.0, 3.0, 0.0])
+    dev = np.array([1.5, -2.1, 2.0, 0.0])
+    slack = np.array([0.2, 0.5, 0.0, 1.0])
+    got = _slack.slack_adjusted(dev, ref, slack)
+    assert np.allclose(got, [1.3, -2.0, 2.0, 0.0])
+
