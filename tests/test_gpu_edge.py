@@ -279,9 +279,10 @@ def test_regularized_layers_match_oracle(C, monkeypatch, x_grad, route, widths, 
     """KAN([16, 64, 100, 12]) at N = 3000 and KAN([8, 300, 6]) at N = 16384,
     fp32, forward_with_regularization + loss +
     backward through each route, every layer held to the fp64 oracle
-    (tests/_netcheck.py: outputs, regulariser, parameter gradients on
-    sampled edges, input gradients on sampled rows) at 1e-5 with sign flips
-    of phi at fp32 rounding level counted and bounded term by term:
+    (tests/_netcheck.py, full mode: every element of the outputs, the
+    parameter gradients and the input gradients, block by block, and the
+    regulariser) at 1e-5 with sign flips of phi at fp32 rounding level
+    counted and bounded term by term:
     * "folded": output and edge statistic through EdgeLinear (one folded
       native backward launch per layer; the weight-only branch for the first
       layer when x needs no gradient; the 300-wide layer's forward from one
@@ -308,8 +309,8 @@ def test_regularized_layers_match_oracle(C, monkeypatch, x_grad, route, widths, 
         torch.cuda.synchronize()
     assert all(l.last_backend == ("reference" if route == "dense" else "cuda")
                for l in net.layers)
-    reg = _netcheck.check_layers(net, cap, 1e-2, 3, 1e-5, n_rows=24, n_edges=40, n_xrows=8,
-                                 say=lambda m: print("  " + m, flush=True))
+    reg = _netcheck.check_layers(net, cap, 1e-2, 3, 1e-5,
+                                 say=lambda m: print("  " + m, flush=True), full=True)
     assert abs(r.item() - reg) < 1e-5 * abs(reg)
     if x_grad:
         assert x.grad is not None
