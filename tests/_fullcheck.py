@@ -103,3 +103,73 @@ def check_layer_step(layer, x_cpu, y_dev, gx_dev, D, k, say, chunk=None):
     out["dscaler"] = block_error(np64(layer.spline_scaler.grad), gsc, 64, 64)
     out["dbase_w"] = block_error(np64(layer.base_weight.grad), gbw, 64, 64)
     return out
+
+
+def check_edge_full(x, grid, k, bw, W, ga, dev, extra=16, unit=None, rows_per_block=256,
+                    outs_per_block=64):
+    """Every element of the edge statistic a [O, I] and of its backward
+    (ds [N, I], dH [N, I, R], dbw [O, I], dW [O, I, R]) against the oracle,
+    one input feature at a time: the oracle's basis of that feature from x,
+    phi = [s_i | H_i] [bw_i | W_i]^T, g = ga sign(phi) / N with 0 on the
+    set of ambiguous signs, and each entry's slack for those signs taken off
+    (tests/_slack.py).  dev holds the device results as host arrays under
+    "a", "ds", "dH", "dbw", "dW".  Each tensor is held block by block: a
+    block is one feature's rows_per_block samples (ds, dH) or outs_per_block
+    outputs (a, dbw, dW), with the floor of block_error.  Features run in
+    threads with one BLAS thread each, so nothing of size [N, I, R] is formed
+    on the host beyond dev itself.  -> ({name: (worst block error,
+    (first row or output of the block, feature), whole-tensor error)},
+    ambiguous count)."""
+    from concurrent.futures import ThreadPoolExecutor
+    from threadpoolctl import threadpool_limits
+    from tests import _slack
+    unit = _slack.U32 if unit is None else unit
+    N, I = x.shape
+    O, _, R = W.shape
+    c = _slack.rounding_factor(R, extra) * unit
+    bsz = {"a": outs_per_block, "ds": rows_per_block, "dH": rows_per_block,
+           "dbw": outs_per_block, "dW": outs_per_block}
+    extent = {"a": O, "ds": N, "dH": N, "dbw": O, "dW": O}
+    num = {name: np.zeros((-(-extent[name] // bs), I)) for name, bs in bsz.items()}
+    den = {name: np.zeros_like(num[name]) for name in bsz}
+
+    def blocks(a2, bs):
+        """Sums of squares of a over blocks of bs leading indices."""
+        rows = np.square(a2).reshape(a2.shape[0], -1).sum(1)
+        return np.add.reduceat(rows, np.arange(0, a2.shape[0], bs))
+
+    def one(i):
+        Hi = ko.basis_dense(x[:, i:i + 1], grid[i:i + 1], k)[:, 0, :]
+        si = ko.silu(x[:, i])
+        Wi, bwi = W[:, i, :], bw[:, i]
+        sb = np.outer(si, bwi)
+        phi = Hi @ Wi.T + sb
+        mag = np.abs(Hi) @ np.abs(Wi).T + np.abs(sb)
+        amb = np.abs(phi) <= c * mag
+        S = np.sign(phi)
+        S[amb] = 0.0
+        g = S * (ga[:, i] / N)[None, :]
+        gA = amb * (np.abs(ga[:, i]) / N)[None, :]
+        refs = {"a": (np.abs(phi).sum(0) / N, 0.0, dev["a"][:, i]),
+                "ds": (g @ bwi, gA @ np.abs(bwi), dev["ds"][:, i]),
+                "dH": (g @ Wi, gA @ np.abs(Wi), dev["dH"][:, i, :]),
+                "dbw": (g.T @ si, gA.T @ np.abs(si), dev["dbw"][:, i]),
+                "dW": (g.T @ Hi, gA.T @ np.abs(Hi), dev["dW"][:, i, :])}
+        for name, (ref, slack, got) in refs.items():
+            adj = _slack.slack_adjusted(np.asarray(got, dtype=np.float64), ref, slack)
+            num[name][:, i] = blocks(adj - ref, bsz[name])
+            den[name][:, i] = blocks(ref, bsz[name])
+        return int(amb.sum())
+
+    with threadpool_limits(limits=1, user_api="blas"):
+        with ThreadPoolExecutor(WORKERS) as ex:
+            n_amb = sum(ex.map(one, range(I)))
+    out = {}
+    for name, bs in bsz.items():
+        floor = 1e-4 * den[name].mean()
+        err = np.sqrt(num[name] / np.maximum(den[name], floor))
+        w = np.unravel_index(int(np.argmax(err)), err.shape)
+        whole = float(np.sqrt(num[name].sum() / den[name].sum()))
+        out[name] = (float(err[w]), (int(w[0]) * bs, int(w[1])), whole)
+    return out, n_amb
+

@@ -8,6 +8,7 @@ import numpy as np
 import torch
 import torch.nn.functional as F
 
+from oracle import kan_oracle as ko
 from tests import _fullcheck
 from tests._util import np64
 from torchsplinekan_amd import KANLinear
@@ -60,3 +61,34 @@ def test_check_layer_step_passes_and_catches():
     errs = _fullcheck.check_layer_step(L, x, y, gx, D, 3, lambda m: None, chunk=256)
     assert errs["dcoef"][0] > 1e-5
     assert errs["y"][0] < 1e-12 and errs["dbase_w"][0] < 1e-12
+
+
+def test_edge_full_check_equals_the_oracle_and_finds_a_planted_fault():
+    """check_edge_full (per feature, blockwise, slack taken off) reports
+    errors at rounding level for the oracle's own statistic and backward,
+    fed back as the device results, and fails a fault of 1e-4 of the
+    largest entry planted in one entry of dH, ds, dW, dbw or a."""
+    r = np.random.default_rng(3)
+    N, I, O, G, k = 600, 7, 70, 6, 3
+    x = r.uniform(-1.1, 1.1, size=(N, I))
+    grid = ko.uniform_grid(I, G, k)
+    W = r.normal(0, 0.2, size=(O, I, G + k))
+    bw = r.normal(0, 0.3, size=(O, I))
+    ga = r.normal(size=(O, I))
+    H = ko.basis_dense(x, grid, k)
+    s = ko.silu(x)
+    ds, dH, dbw, dW = ko.edge_abs_mean_backward(ga, s, H, bw, W)
+    dev = {"a": ko.edge_abs_mean(s, H, bw, W), "ds": ds, "dH": dH, "dbw": dbw, "dW": dW}
+    res, n_amb = _fullcheck.check_edge_full(x, grid, k, bw, W, ga, dev, rows_per_block=64,
+                                            outs_per_block=16)
+    assert n_amb == 0
+    for name, (worst, _, whole) in res.items():
+        assert worst < 1e-13, name
+    for name, idx in (("dH", (123, 4, 2)), ("ds", (321, 6)), ("dW", (33, 1, 5)),
+                      ("dbw", (69, 0)), ("a", (7, 3))):
+        bad = {key: v.copy() for key, v in dev.items()}
+        bad[name][idx] += 1e-4 * np.abs(dev[name]).max()
+        res, _ = _fullcheck.check_edge_full(x, grid, k, bw, W, ga, bad, rows_per_block=64,
+                                            outs_per_block=16)
+        assert res[name][0] > 1e-5, name
+        assert all(res[other][0] < 1e-13 for other in res if other != name)
