@@ -243,6 +243,50 @@ def test_pinn_two_layer_matches_reference_backend(C):
         assert normwise(np64(p.grad), np64(q.grad)) < 1e-10, n
 
 
+@pytest.mark.timeout(900)
+def test_pinn_workload_matches_reference_backend(C):
+    """bench.py's PINN workload itself (KAN([2, 128, 128, 1]) G8 k3 fp64,
+    N = 16384, the same draws): one step, u -> grad u -> Laplacian through
+    create_graph -> MSE -> backward, on the native path against the
+    reference backend on the CPU (autograd through the dense recurrences):
+    the Laplacian, the loss and every parameter gradient at the fp64 bar."""
+    from torchsplinekan_amd import KAN
+    N, widths, G, k = 16384, [2, 128, 128, 1], 8, 3
+    g = torch.Generator().manual_seed(0)
+    x = torch.rand(N, 2, generator=g, dtype=torch.float64) * 1.8 - 0.9
+    f = torch.sin(3 * x[:, :1]) * torch.cos(2 * x[:, 1:])
+    torch.manual_seed(0)
+    net = KAN(widths, grid_size=G, spline_order=k, backend="cuda").double()
+    with torch.no_grad():
+        for layer in net.layers:
+            layer.spline_weight.normal_(0.0, 0.1, generator=g)
+    ref = KAN(widths, grid_size=G, spline_order=k, backend="reference").double()
+    ref.load_state_dict(net.state_dict())
+    net = net.cuda()
+
+    def step(model, xx, ff):
+        xg = xx.clone().requires_grad_()
+        u = model(xg)
+        gu = torch.autograd.grad(u.sum(), xg, create_graph=True)[0]
+        lap = (torch.autograd.grad(gu[:, 0].sum(), xg, create_graph=True)[0][:, 0]
+               + torch.autograd.grad(gu[:, 1].sum(), xg, create_graph=True)[0][:, 1])
+        loss = ((lap.unsqueeze(1) - ff) ** 2).mean()
+        loss.backward()
+        return lap.detach(), loss.detach()
+
+    lap_d, loss_d = step(net, x.cuda(), f.cuda())
+    assert all(l.last_backend == "cuda" for l in net.layers)
+    lap_r, loss_r = step(ref, x, f)
+    e = normwise(np64(lap_d), np64(lap_r))
+    el = abs(loss_d.item() - loss_r.item()) / abs(loss_r.item())
+    print(f"pinn workload: Laplacian {e:.2e}, loss {el:.2e}", flush=True)
+    assert e < 1e-10 and el < 1e-10
+    for (n, p), (_, q) in zip(net.named_parameters(), ref.named_parameters()):
+        e = normwise(np64(p.grad), np64(q.grad))
+        print(f"pinn workload: {n} grad {e:.2e}", flush=True)
+        assert e < 1e-10, n
+
+
 def _view(t, trans):
     """t itself, or the same values as the transpose of a row-major buffer."""
     return t.t().contiguous().t() if trans else t
