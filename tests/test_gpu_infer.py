@@ -51,6 +51,39 @@ def test_infer_matches_oracle(C, dtype, tol, N, I, O, G, k, base, scaler):
     assert normwise(np64(y), np64(yf)) < tol
 
 
+@pytest.mark.timeout(900)
+def test_infer_c3_layer_every_output(C):
+    """bench.py's inference workload itself: c3's layer (KANLinear 1024 ->
+    1024 G10 k3 fp32, the same draws) exported, at N = 65536, through
+    kan_hip_infer with the packed weight: every output against the oracle,
+    in 256 x 256 blocks (tests/_fullcheck.py, block_error), at 1e-5."""
+    from torchsplinekan_amd import KANLinear
+    from tests._fullcheck import block_error
+    from tests._netcheck import basis_threaded
+    N, I, O, G, k = 65536, 1024, 1024, 10, 3
+    g = torch.Generator().manual_seed(0)
+    L = KANLinear(I, O, grid_size=G, spline_order=k, backend="cuda")
+    with torch.no_grad():
+        L.spline_weight.normal_(0.0, 0.1, generator=g)
+        L.spline_scaler.uniform_(0.5, 1.5, generator=g)
+    E = L.export_inference().cuda()
+    x = torch.rand(N, I, generator=g) * 2.2 - 1.1
+    with torch.no_grad():
+        y = E(x.cuda())
+    assert E.last_backend == "cuda"
+    grid, bw, sw = np64(E.grid), np64(E.base_weight), np64(E.spline_weight)
+    sc = np64(E.spline_scaler) if getattr(E, "spline_scaler", None) is not None else None
+    xs = x.double().numpy()
+    ref = np.empty((N, O))
+    for n0 in range(0, N, 4096):
+        xc = xs[n0:n0 + 4096]
+        ref[n0:n0 + 4096] = ko.kan_forward(xc, grid, bw, sw, sc, k,
+                                           basis=basis_threaded(xc, grid, k))[0]
+    worst, block, whole = block_error(np64(y), ref, 256, 256)
+    print(f"infer c3 layer: whole {whole:.2e}, worst block {worst:.2e} at {block}", flush=True)
+    assert worst < 1e-5
+
+
 def test_frozen_eval_layer_keeps_packed_weight(C):
     from torchsplinekan_amd import KANLinear
     torch.manual_seed(0)
