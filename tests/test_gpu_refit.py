@@ -77,6 +77,50 @@ def test_update_grid_on_device_matches_oracle(dtype, tol):
     assert normwise(np64(L.spline_weight), sw_ref) < tol
 
 
+@pytest.mark.timeout(900)
+def test_update_grid_refit_workload_matches_oracle():
+    """bench.py's refit workload itself (KANLinear 512 -> 512 G8 k3 fp32,
+    update_grid on N = 16384 samples of the Gaussian mixture, the same
+    draws): every knot and every refitted coefficient against the oracle's
+    update_grid, run one feature at a time (the refit is separable over
+    features) in threads; knots at 1e-6, coefficients block by block (64
+    outputs x 16 features) at 1e-5."""
+    from concurrent.futures import ThreadPoolExecutor
+    from threadpoolctl import threadpool_limits
+    from torchsplinekan_amd import KANLinear
+    from tests._fullcheck import block_error
+    from tests._netcheck import WORKERS
+    N, I, O, G, k = 16384, 512, 512, 8, 3
+    g = torch.Generator().manual_seed(0)
+    means = torch.tensor([-0.8, -0.5, 0.5, 0.8])
+    x = means[torch.randint(0, 4, (N, I), generator=g)] + 0.1 * torch.randn(N, I, generator=g)
+    coef = torch.randn(O, I, G + k, generator=g) * 0.1
+    L = KANLinear(I, O, grid_size=G, spline_order=k, backend="cuda")
+    with torch.no_grad():
+        L.spline_weight.copy_(coef)
+    grid0, eps = L.grid.detach().numpy().copy(), L._ref.grid_eps
+    L = L.cuda()
+    L.update_grid(x.cuda())
+    torch.cuda.synchronize()
+    xs, cs = x.numpy(), coef.numpy()
+
+    def one(i):
+        return ko.update_grid(xs[:, i:i + 1], grid0[i:i + 1], cs[:, i:i + 1], G, k, eps, 0.01)
+
+    with threadpool_limits(limits=1, user_api="blas"):
+        with ThreadPoolExecutor(WORKERS) as ex:
+            parts = list(ex.map(one, range(I)))
+    grid_ref = np.concatenate([p[0] for p in parts], axis=0)
+    sw_ref = np.concatenate([p[1] for p in parts], axis=1)
+    e = normwise(np64(L.grid), grid_ref)
+    worst, block, whole = block_error(np64(L.spline_weight).reshape(O, -1),
+                                      sw_ref.reshape(O, -1), 64, 16 * (G + k))
+    print(f"refit workload: knots {e:.2e}; coefficients whole {whole:.2e}, worst block "
+          f"{worst:.2e} at {block}", flush=True)
+    assert e < 1e-6
+    assert worst < 1e-5
+
+
 @pytest.mark.parametrize("tag,dtype,tol", [("32", torch.float32, 1e-5), ("64", torch.float64, 1e-10)])
 def test_update_grid_golden_on_device(tag, dtype, tol):
     from torchsplinekan_amd import KANLinear
