@@ -76,8 +76,9 @@ int64_t kan_hip_get_basis_impl(void);
  *   KAN_ROUTE_GEMM_TILE  (KAN_HIP_GEMM_TILE)  -1 cost model (default), 0 256x256
  *                        ("256"), 1 128x128 ("128"), 2 256x64 ("256x64"),
  *                        3 4-wave 256x256 ("256w4"); float64 products take
- *                        0 as 256x128, 1 as 128x128 and 2 as the pipelined
- *                        128x128 tile with 32-deep slabs
+ *                        0 as 256x128, 1 as 128x128, 2 as the pipelined
+ *                        128x128 tile with 32-deep slabs and 3 as the
+ *                        pipelined 64x64 tile
  * kan_hip_set_route returns KAN_ERR_INVALID for an unknown route or value;
  * kan_hip_get_route returns -2 for an unknown route. */
 #define KAN_ROUTE_FUSED_DX 0

@@ -341,14 +341,16 @@ def test_matmul_tile_configs_match_torch(C, routes, tile, M, K, N):
             assert normwise(np64(c), ref) < 1e-5, (ta, tb)
 
 
-@pytest.mark.parametrize("tile", [0, 1, 2], ids=["256x128", "128x128", "128x128x32-pipelined"])
+@pytest.mark.parametrize("tile", [0, 1, 2, 3], ids=["256x128", "128x128", "128x128x32-pipelined",
+                                             "64x64x32-pipelined"])
 @pytest.mark.parametrize("M,K,N", [(256, 512, 256), (128, 64, 128), (300, 37, 129),
                                    (1000, 777, 555), (513, 1000, 300), (257, 4100, 33),
                                    (65, 33000, 70)])
 def test_matmul_fp64_tile_configs_match_torch(C, routes, tile, M, K, N):
     """The float64 tile configurations forced through the gemm_tile route
     (0: 256x128 tiles of 8 waves, 1: 128x128 of 4 waves, both with 16-deep
-    slabs; 2: the software-pipelined 128x128 tile with 32-deep slabs): whole
+    slabs; 2: the software-pipelined 128x128 tile with 32-deep slabs; 3: the
+    pipelined 64x64 tile, two blocks per CU): whole
     tiles, ragged rows and columns, K tails past both slab depths, split-K on
     long contractions, all four transposition pairs, against the float64
     product at 1e-12; two calls agree bit for bit."""

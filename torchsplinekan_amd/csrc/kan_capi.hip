@@ -42,8 +42,8 @@ std::map<std::pair<int, const void*>, int> g_resident;  // (device, kernel) -> b
 //    an edge-statistic layer in one kernel where it applies.
 //  * GEMM_TILE (KAN_HIP_GEMM_TILE=256, 128, 256x64 or 256w4): forces the fp32
 //    tile configuration (values 0-3; float64 products take 0 as 256x128,
-//    1 as 128x128 and 2 as the pipelined 128x128 tile); otherwise the cost
-//    model picks it.
+//    1 as 128x128, 2 as the pipelined 128x128 tile and 3 as the pipelined
+//    64x64 tile); otherwise the cost model picks it.
 constexpr int64_t kCompactMinR = 25;
 
 int route_from_env(int route) {

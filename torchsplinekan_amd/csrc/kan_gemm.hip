@@ -130,6 +130,10 @@ using CfgF64Big = Cfg<double, 256, 128, 16, 4, 2, 16, 1>;
 // fp64 on the software-pipelined kernel: 128 x 128 tiles, 32-deep slabs (two
 // k-groups), 8 waves of 64 x 32 (two per SIMD); 147 KB of LDS, one block per CU
 using CfgF64Pipe = Cfg<double, 128, 128, 32, 2, 4, 16, 1>;
+// fp64 on the pipelined kernel with 64 x 64 tiles: 4 waves of 32 x 32, two
+// blocks per CU (73 KB of LDS each), for products with a side of at most 64
+// (a 64-wide layer's products fill half of a 128 x 128 tile)
+using CfgF64Small = Cfg<double, 64, 64, 32, 2, 2, 16, 2>;
 
 // Configurations that run on gemm_pipe_kernel (the rest on gemm_kernel).
 template <class C>
@@ -974,20 +978,27 @@ constexpr CfgModel kModelF32[4] = {
 constexpr double kPeakPerCuF32 = 157.3e12 / 256.0;  // FP32 MFMA flop/s per CU
 constexpr double kStreamBytesPerS = 5.0e12;          // split-K partial-sum traffic
 
-// fp64 (one configuration): whole waves of resident blocks times one block's
-// k range plus a 256-k start-up and write-out term.
+// fp64: whole waves of resident blocks times one block's k range plus its
+// configuration's start-up and write-out term.
 struct CfgModelF64 {
   int bm, bn, bk, blocks_per_cu;
   double eff;
+  double k_overhead;  // a block's start-up and write-out, in k of its own MFMA work
 };
 // (measured at c3's shapes: 0.81-0.83 of the FP64 peak for the 8-wave tile,
 // 0.75-0.82 for the 4-wave one, whose parameter product lost most)
 // (the pipelined 128 x 128 x 32 measured 0.91-0.95 of the FP64 peak at c3's
-// three product shapes, where the other two measured 0.80-0.82)
-constexpr CfgModelF64 kModelF64[3] = {
-    {256, 128, 16, 1, 0.84}, {128, 128, 16, 1, 0.80}, {128, 128, 32, 1, 0.93}};
+// three product shapes, where the other two measured 0.80-0.82; the
+// pipelined 64 x 64 x 32 measured 0.65-0.68 on the products of a 64-wide
+// layer, 16384 samples by 512 features, where the 128 x 128 tile, half of it
+// past the 64 outputs, measured 0.31-0.33.  The pipelined tiles' start-up
+// and write-out terms come from that layer's input-side product, K = 64:
+// 16 us per 128 x 128 block against 7 us of MFMA work, 7 us per pair of
+// 64 x 64 blocks against 4.5 us.)
+constexpr CfgModelF64 kModelF64[4] = {
+    {256, 128, 16, 1, 0.84, 256.0}, {128, 128, 16, 1, 0.80, 256.0},
+    {128, 128, 32, 1, 0.93, 96.0}, {64, 64, 32, 2, 0.75, 48.0}};
 constexpr double kPeakPerCuF64 = 78.6e12 / 256.0;
-constexpr double kKOverheadF64 = 256.0;
 
 double split_traffic_s(int64_t M, int64_t N, int splits, size_t elem) {
   return splits > 1 ? 2.0 * (double)splits * (double)(M * N) * (double)elem / kStreamBytesPerS
@@ -996,8 +1007,8 @@ double split_traffic_s(int64_t M, int64_t N, int splits, size_t elem) {
 
 // Estimated seconds for M x N x K with `splits` K-slices on fp32 tiles of c,
 // plus the split-K partial traffic (written once, read once by the sum).
-double est_seconds(const CfgModel& c, int64_t M, int64_t N, int64_t K, int splits) {
-  const int64_t cus = device_cu_count();
+double est_seconds(const CfgModel& c, int64_t M, int64_t N, int64_t K, int splits,
+                   int64_t cus) {
   const int64_t tiles = ceil_div(M, c.bm) * ceil_div(N, c.bn) * splits;
   const int64_t per_cu = ceil_div(tiles, cus);
   const int64_t kper = round_up(ceil_div(K > 0 ? K : 1, splits), c.bk);
@@ -1006,12 +1017,12 @@ double est_seconds(const CfgModel& c, int64_t M, int64_t N, int64_t K, int split
   return (double)per_cu * block + split_traffic_s(M, N, splits, 4);
 }
 
-double est_seconds_f64(const CfgModelF64& c, int64_t M, int64_t N, int64_t K, int splits) {
-  const int64_t cus = device_cu_count();
+double est_seconds_f64(const CfgModelF64& c, int64_t M, int64_t N, int64_t K, int splits,
+                       int64_t cus) {
   const int64_t tiles = ceil_div(M, c.bm) * ceil_div(N, c.bn) * splits;
   const int64_t waves = ceil_div(tiles, cus * c.blocks_per_cu);
   const int64_t kper = round_up(ceil_div(K > 0 ? K : 1, splits), c.bk);
-  const double block_s = 2.0 * c.bm * c.bn * ((double)kper + kKOverheadF64) * c.blocks_per_cu /
+  const double block_s = 2.0 * c.bm * c.bn * ((double)kper + c.k_overhead) * c.blocks_per_cu /
                          (kPeakPerCuF64 * c.eff);
   return (double)waves * block_s + split_traffic_s(M, N, splits, 8);
 }
@@ -1022,15 +1033,20 @@ double est_seconds_f64(const CfgModelF64& c, int64_t M, int64_t N, int64_t K, in
 int forced_cfg_f32() { return kan_hip_get_route(KAN_ROUTE_GEMM_TILE); }
 
 // fp64 configuration (0 = 256 x 128 with 8 waves, 1 = 128 x 128 with 4,
-// 2 = the pipelined 128 x 128 x 32) for a split count; the route forces 0
-// for "256", 1 for "128" and 2 for "256x64" (the third fp32 tile's value).
-int pick_cfg_f64(int64_t M, int64_t N, int64_t K, int splits) {
+// 2 = the pipelined 128 x 128 x 32, 3 = the pipelined 64 x 64 x 32) for a
+// split count; the route forces 0 for "256", 1 for "128", 2 for "256x64"
+// and 3 for "256w4" (the fp32 tiles' values).
+int pick_cfg_f64(int64_t M, int64_t N, int64_t K, int splits, int64_t cus = 0) {
   const int forced = kan_hip_get_route(KAN_ROUTE_GEMM_TILE);
-  if (forced >= 0 && forced <= 2) return forced;
-  int best = 0;
-  double best_t = est_seconds_f64(kModelF64[0], M, N, K, splits);
-  for (int c = 1; c <= 2; ++c) {
-    const double t = est_seconds_f64(kModelF64[c], M, N, K, splits);
+  if (forced >= 0 && forced <= 3) return forced;
+  // The cost model chooses between the two pipelined tiles: the older ones
+  // (0, 1) measured slower than one of them at every shape timed (c3's
+  // products, a 64-wide layer's, PINN's), and are reached only by the route.
+  if (cus <= 0) cus = device_cu_count();
+  int best = 2;
+  double best_t = est_seconds_f64(kModelF64[2], M, N, K, splits, cus);
+  for (int c = 3; c <= 3; ++c) {
+    const double t = est_seconds_f64(kModelF64[c], M, N, K, splits, cus);
     if (t < best_t) {
       best = c;
       best_t = t;
@@ -1042,14 +1058,15 @@ int pick_cfg_f64(int64_t M, int64_t N, int64_t K, int splits) {
 // fp32 configuration (0 = big, 1 = small, 2 = narrow, 3 = 4-wave big, only
 // when forced) for a given split count; the narrow one only where N fits its
 // 64 columns.
-int pick_cfg_f32(int64_t M, int64_t N, int64_t K, int splits) {
+int pick_cfg_f32(int64_t M, int64_t N, int64_t K, int splits, int64_t cus = 0) {
   const int forced = forced_cfg_f32();
   if (forced >= 0) return forced;
+  if (cus <= 0) cus = device_cu_count();
   const int last = N <= 64 ? 2 : 1;
   int best = 0;
-  double best_t = est_seconds(kModelF32[0], M, N, K, splits);
+  double best_t = est_seconds(kModelF32[0], M, N, K, splits, cus);
   for (int c = 1; c <= last; ++c) {
-    const double t = est_seconds(kModelF32[c], M, N, K, splits);
+    const double t = est_seconds(kModelF32[c], M, N, K, splits, cus);
     if (t < best_t) {
       best = c;
       best_t = t;
@@ -1540,6 +1557,7 @@ inline bool gemm_is_thin(int64_t M, int64_t N, int64_t K) {
 template <typename T>
 int gemm_pick_splits(int64_t M, int64_t N, int64_t K, int64_t max_slice_elems) {
   if (gemm_is_thin(M, N, K)) return K <= kThinMax ? 1 : thin_splits(M, N, K);
+  const int64_t cus = device_cu_count();  // (once: the model is evaluated ~200 times)
   int best = 1;
   double best_t = 0.0;
   for (int s = 1; s <= 64; ++s) {
@@ -1547,10 +1565,10 @@ int gemm_pick_splits(int64_t M, int64_t N, int64_t K, int64_t max_slice_elems) {
     double t;
     if (std::is_same<T, float>::value) {
       if (s > 1 && K / s < 8 * kModelF32[0].bk) break;
-      t = est_seconds(kModelF32[pick_cfg_f32(M, N, K, s)], M, N, K, s);
+      t = est_seconds(kModelF32[pick_cfg_f32(M, N, K, s, cus)], M, N, K, s, cus);
     } else {
       if (s > 1 && K / s < 8 * kModelF64[1].bk) break;
-      t = est_seconds_f64(kModelF64[pick_cfg_f64(M, N, K, s)], M, N, K, s);
+      t = est_seconds_f64(kModelF64[pick_cfg_f64(M, N, K, s, cus)], M, N, K, s, cus);
     }
     if (s == 1 || t < best_t * (1.0 - 1e-9)) {
       best = s;
@@ -1594,6 +1612,7 @@ int launch_gemm(int layout, int64_t M, int64_t N, int64_t K, const T* A, int64_t
     const int cfg = pick_cfg_f64(M, N, K, splits < 1 ? 1 : splits);
     if (cfg == 0) rc = launch_layout<CfgF64Big>(layout, p, splits, st);
     else if (cfg == 2) rc = launch_layout<CfgF64Pipe>(layout, p, splits, st);
+    else if (cfg == 3) rc = launch_layout<CfgF64Small>(layout, p, splits, st);
     else rc = launch_layout<CfgF64>(layout, p, splits, st);
   }
   if (rc != KAN_OK) return rc;
